@@ -1,0 +1,314 @@
+"""Benchmark of the LegoLink KV link step on one MI355X.
+
+One step = one link of the workload: the fused gather -> RoPE re-rotation ->
+scatter over every layer (repair rows masked) plus the repaired-row write-back,
+with every input already resident in HBM.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload c2]
+
+The default workload is the Qwen2.5-7B-shaped 32,768-token link (pool 262,144
+fully fragmented slots, 16 blocks, 240 repair rows).  ``--cpu-baseline`` (on by
+default) times the reference's eager torch link path on the host cores on a
+bounded sample of the same workload.  ``--copy-calibration`` instead times a
+plain device copy of known size, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT / "sglang-legolink_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "linked KV GB/s (rd+wr) and % of 8 TB/s HBM; tokens linked/s, Qwen2.5-7B"
+TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic_kv_link_c2.json"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
+    parser.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    parser.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    parser.add_argument("--cpu-reps", type=int, default=3)
+    parser.add_argument("--layers-per-wave", type=int, default=0)
+    parser.add_argument("--waves-per-block", type=int, default=4)
+    parser.add_argument("--copy-calibration", type=int, default=0,
+                        help="time a plain device copy of this many MiB instead of the link")
+    return parser.parse_args()
+
+
+def copy_calibration(args: argparse.Namespace) -> None:
+    import torch
+
+    device = torch.device("cuda", 0)
+    nbytes = args.copy_calibration << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize(device)
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize(device)
+    elapsed = (time.perf_counter() - start) / args.steps
+    print(json.dumps({"copy_bytes": nbytes, "read_kib": nbytes / 1024, "write_kib": nbytes / 1024,
+                      "ms_per_copy": elapsed * 1e3, "gbps_rd_wr": 2 * nbytes / elapsed / 1e9}), flush=True)
+
+
+def cpu_baseline(workload, args) -> dict:
+    """The reference's eager torch link path (index_select -> remap -> index_copy_,
+    then the repair write-back) on the host cores, on a bounded sample."""
+
+    import numpy as np
+    import torch
+
+    from legolink_amd.rope import build_cos_sin_cache
+    from legolink_amd.workloads import scaled_single_request
+    from oracle import r1_torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    lengths, total = [], 0
+    for length in workload.block_lengths:
+        if total >= args.cpu_sample_tokens:
+            break
+        lengths.append(length)
+        total += length
+    shape = workload.shape
+    slots = 4 * total
+    sample = scaled_single_request(shape=shape, num_slots=slots, block_lengths=lengths,
+                                   imp_per_seam=int(workload.notes.get("imp_per_seam", 16)),
+                                   delta_range=None, seed=workload.seed, name="cpu_sample")
+    log(f"cpu baseline: {sample.tokens} tokens, pool {slots} slots, {shape.layers} layers, {cores} threads")
+    generator = torch.Generator().manual_seed(1)
+    tile = torch.randn(1 << 20, generator=generator).to(torch.bfloat16)
+    row = shape.kv_heads * shape.head_dim
+
+    def filled() -> torch.Tensor:
+        flat = tile.repeat((slots * row + tile.numel() - 1) // tile.numel())[: slots * row]
+        return flat.view(slots, shape.kv_heads, shape.head_dim).clone()
+
+    keys = [filled() for _ in range(shape.layers)]
+    values = [filled() for _ in range(shape.layers)]
+    table = build_cos_sin_cache(sample.max_position + 1, sample.rotary_dim, theta=sample.theta)
+    src = torch.from_numpy(sample.source_slots)
+    dst = torch.from_numpy(sample.destination_slots)
+    local = torch.from_numpy(sample.local_positions)
+    glob = torch.from_numpy(sample.global_positions)
+    repair_slots = torch.from_numpy(sample.repair_destination_slots)
+    repaired = torch.randn(shape.layers, sample.repair_rows, shape.kv_heads, shape.head_dim,
+                           generator=generator).to(torch.bfloat16)
+
+    def step() -> None:
+        r1_torch.link_batched_layers(keys, values, src, dst, local, glob, table,
+                                     prefix_token_count=sample.prefix_token_count,
+                                     rotary_dim=sample.rotary_dim, is_neox_style=True)
+        r1_torch.scatter_rows(keys, values, repair_slots, repaired, repaired)
+
+    step()
+    times = []
+    for _ in range(max(1, args.cpu_reps)):
+        start = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - start)
+    seconds = float(np.median(times))
+    total_bytes = sample.algorithmic_bytes()["total_bytes"]
+    return {
+        "value": total_bytes / seconds / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "tokens_linked_per_s": sample.tokens / seconds,
+        "seconds_per_link": seconds,
+        "sample": (
+            f"eager torch link path of the reference (per layer index_select -> R1 RoPE remap -> "
+            f"index_copy_, then repair-row index_copy_) on the first {len(lengths)} blocks of the "
+            f"workload ({sample.tokens} tokens, {sample.repair_rows} repair rows) in a "
+            f"{slots}-slot bf16 pool, {shape.layers} layers x {shape.kv_heads} KV heads x "
+            f"{shape.head_dim}; 1 warm-up + {len(times)} timed reps, median"
+        ),
+    }
+
+
+def load_traffic(link_launch_bytes: int) -> float | None:
+    """HBM bytes per link launch from the committed rocprofv3 counter summary."""
+
+    if not TRAFFIC_FILE.is_file():
+        return None
+    data = json.loads(TRAFFIC_FILE.read_text())
+    try:
+        return float(data["hbm_bytes_per_launch"])
+    except (KeyError, TypeError, ValueError):
+        return None
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures the link step on one GPU only; this build runs no multi-GPU "
+              "configuration (the link shards by KV head / request with no exchange step).",
+              file=sys.stderr)
+        return 2
+    if args.copy_calibration:
+        copy_calibration(args)
+        return 0
+
+    import numpy as np
+    import torch
+
+    from legolink_amd import kv_link
+    from legolink_amd.rope import build_cos_sin_cache
+    from legolink_amd.workloads import make_workload
+
+    device = torch.device("cuda", 0)
+    host_start = time.perf_counter()
+    workload = make_workload(args.workload)
+    shape = workload.shape
+    log(f"workload {workload.name}: {workload.description}")
+    keys, values = [], []
+    generator = torch.Generator(device=device).manual_seed(20260824)
+    for _ in range(shape.layers):
+        keys.append(torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                                device=device, generator=generator))
+        values.append(torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                                  device=device, generator=generator))
+    table = build_cos_sin_cache(workload.max_position + 1, workload.rotary_dim, theta=workload.theta).to(device)
+    index_start = time.perf_counter()
+    src = torch.from_numpy(workload.source_slots).to(device)
+    dst = torch.from_numpy(workload.destination_slots).to(device)
+    local = torch.from_numpy(workload.local_positions).to(device)
+    glob = torch.from_numpy(workload.global_positions).to(device)
+    mask = torch.from_numpy(workload.repair_mask).to(device)
+    repair_slots = torch.from_numpy(workload.repair_destination_slots).to(device)
+    torch.cuda.synchronize(device)
+    index_upload_ms = (time.perf_counter() - index_start) * 1e3
+    repaired_k = torch.randn(shape.layers, workload.repair_rows, shape.kv_heads, shape.head_dim,
+                             dtype=torch.bfloat16, device=device, generator=generator)
+    repaired_v = torch.randn_like(repaired_k)
+    setup_s = time.perf_counter() - host_start
+    launch = kv_link.describe_link_launch(
+        key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
+        local_positions=local, global_positions=glob, cos_sin_cache=table,
+        prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
+        is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
+        layers_per_wave=args.layers_per_wave,
+    )
+    log(f"setup {setup_s:.1f}s; link launch {launch}")
+
+    def link() -> None:
+        kv_link.fused_kv_link_layers_inplace(
+            key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
+            local_positions=local, global_positions=glob, cos_sin_cache=table,
+            prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
+            is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
+            layers_per_wave=args.layers_per_wave,
+        )
+
+    def scatter() -> None:
+        kv_link.scatter_kv_rows_inplace(
+            key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
+            repaired_keys=repaired_k, repaired_values=repaired_v,
+        )
+
+    for _ in range(args.warmup):
+        link()
+        scatter()
+    torch.cuda.synchronize(device)
+    log(f"warmup {args.warmup} steps done; timing {args.steps} steps")
+
+    stream = torch.cuda.current_stream(device)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+               torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize(device)
+    wall_start = time.perf_counter()
+    for start, middle, end in events:
+        start.record(stream)
+        link()
+        middle.record(stream)
+        scatter()
+        end.record(stream)
+    torch.cuda.synchronize(device)
+    wall_s = time.perf_counter() - wall_start
+    link_ms = [s.elapsed_time(m) for s, m, _ in events]
+    scatter_ms = [m.elapsed_time(e) for _, m, e in events]
+    gpu_ms = events[0][0].elapsed_time(events[-1][2]) / args.steps
+    ms_per_step = wall_s * 1e3 / args.steps
+    log(f"timed: {ms_per_step:.4f} ms/step wall, {gpu_ms:.4f} ms/step events, "
+        f"link {np.mean(link_ms):.4f} ms, scatter {np.mean(scatter_ms):.4f} ms")
+
+    bytes_info = workload.algorithmic_bytes()
+    total_bytes = bytes_info["total_bytes"]
+    value = total_bytes / (ms_per_step / 1e3) / 1e9
+    link_avg_ms = float(np.mean(link_ms))
+    achieved = bytes_info["link_bytes"] / (link_avg_ms / 1e3) / 1e9
+    traffic = load_traffic(bytes_info["link_bytes"])
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 K/V pool, seeded slot permutation and block layout",
+        "config": {
+            "workload": f"{workload.name}: {workload.description}",
+            "layers": shape.layers,
+            "kv_heads": shape.kv_heads,
+            "head_dim": shape.head_dim,
+            "pool_slots": workload.num_slots,
+            "linked_tokens": workload.tokens,
+            "repair_rows": workload.repair_rows,
+            "blocks": len(workload.block_lengths),
+            "requests": workload.requests,
+            "prefix_token_count": workload.prefix_token_count,
+            "algorithmic_bytes_per_step": total_bytes,
+        },
+        "tokens_linked_per_s": round(workload.tokens / (ms_per_step / 1e3), 1),
+        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "link_kernel_ms": round(link_avg_ms, 5),
+        "scatter_kernel_ms": round(float(np.mean(scatter_ms)), 5),
+        "event_ms_per_step": round(gpu_ms, 5),
+        "index_upload_ms": round(index_upload_ms, 3),
+        "launch": launch,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "kv_link_vec_kernel" if launch["kernel"] == "vector" else "kv_link_generic_kernel",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": bytes_info["link_bytes"],
+        },
+        "cpu_baseline": None,
+    }
+    del keys, values
+    torch.cuda.empty_cache()
+    if args.cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(workload, args)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,216 @@
+/*
+ * legolink_kv.h - C ABI of the MI355X (gfx950) LegoLink KV link library
+ * (liblegolink_kv.so).
+ *
+ * The library moves registered KV blocks of a paged KV pool into a new
+ * request's slots: it gathers source rows, re-rotates K from each token's
+ * compile-time RoPE position to its request-global position, and scatters
+ * the result into destination rows; V rows and non-rotated K rows are moved
+ * bit-exactly.  A second entry writes repaired boundary rows (imp_indices)
+ * into the pool.
+ *
+ * Pool layout (unchanged from the reference, patched_sglang_files/python/
+ * sglang/srt/legolink_triton.py:184-193 and pic_runtime.py:6283-6289): every
+ * layer owns one dense [num_slots, num_heads, key_head_dim] K buffer and one
+ * dense [num_slots, num_heads, value_head_dim] V buffer, both fp16 or bf16.
+ * Layers are separate allocations, so the entries take host arrays of
+ * per-layer device pointers.
+ *
+ * Conventions
+ *   - Every integer field is int64_t, so the structs have no padding and a
+ *     ctypes / cgo / JNI mirror is a flat list of 8-byte fields.
+ *   - Device pointers are plain addresses in the device's HIP address space.
+ *     Host pointers are marked "host".
+ *   - Work is enqueued on `stream` (a hipStream_t) and is asynchronous.  No
+ *     entry allocates memory, synchronises or keeps state between calls
+ *     other than the thread-local error string.  Entries are reentrant.
+ *   - A return value of 0 is success; a negative value is one of the LL_ERR_*
+ *     codes below, and ll_last_error() then holds a message.
+ *   - Rows whose slot index lies outside [0, num_slots) and remapped tokens
+ *     whose positions lie outside [0, cos_sin_rows) are neither read nor
+ *     written (the kernels bound-check every index they dereference).
+ *   - Preconditions that are NOT checked: source rows and destination rows
+ *     are disjoint, and destination slots are pairwise distinct.
+ *     Overlapping or repeated destinations race, as in the reference.
+ */
+#ifndef LEGOLINK_KV_H
+#define LEGOLINK_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LL_ABI_VERSION 1
+
+/* hipStream_t, declared without pulling in the HIP headers. */
+struct ihipStream_t;
+typedef struct ihipStream_t *ll_stream_t;
+
+/* Element type codes (the *_dtype fields). */
+enum {
+  LL_DTYPE_FLOAT16 = 1,
+  LL_DTYPE_BFLOAT16 = 2,
+  LL_DTYPE_FLOAT32 = 3,
+  LL_DTYPE_INT32 = 4,
+  LL_DTYPE_INT64 = 5,
+  LL_DTYPE_UINT8 = 6 /* uint8 or bool repair mask */
+};
+
+/* Kernel selection (ll_kv_link_args.kernel). */
+enum {
+  LL_KERNEL_AUTO = 0,   /* vectorised kernel when the shape allows, else generic */
+  LL_KERNEL_VECTOR = 1, /* 16-byte row-chunk kernel; LL_ERR_UNSUPPORTED_KERNEL if the shape does not fit */
+  LL_KERNEL_GENERIC = 2 /* element-wise kernel for every eligible shape */
+};
+
+/*
+ * Status codes.  Each eligibility code corresponds 1:1 to a reason string of
+ * check_fused_kv_link_eligibility (legolink_triton.py:159-247); ll_status_reason()
+ * returns that string.
+ */
+enum {
+  LL_OK = 0,
+  LL_ERR_INVALID_ARGUMENT = -1,                /* "invalid_argument" (NULL pointer, bad struct_size, negative count) */
+  LL_ERR_MHA_3D_KV_BUFFERS_REQUIRED = -2,      /* "mha_3d_kv_buffers_required" */
+  LL_ERR_KV_HEAD_LAYOUT_MISMATCH = -3,         /* "kv_head_layout_mismatch" */
+  LL_ERR_KV_DTYPE_MISMATCH = -4,               /* "kv_dtype_mismatch" */
+  LL_ERR_FP16_OR_BF16_REQUIRED = -5,           /* "fp16_or_bf16_required" */
+  LL_ERR_CONTIGUOUS_KV_BUFFERS_REQUIRED = -6,  /* "contiguous_kv_buffers_required" */
+  LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE = -7,     /* "head_dimension_out_of_range" */
+  LL_ERR_EMPTY_LINK = -8,                      /* "empty_link" */
+  LL_ERR_TOKEN_MAP_LENGTH_MISMATCH = -9,       /* "token_map_length_mismatch" */
+  LL_ERR_REPAIR_MASK_LENGTH_MISMATCH = -10,    /* "repair_mask_length_mismatch" */
+  LL_ERR_BOOLEAN_REPAIR_MASK_REQUIRED = -11,   /* "boolean_repair_mask_required" */
+  LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED = -12,    /* "integer_token_maps_required" */
+  LL_ERR_EVEN_ROTARY_DIM_REQUIRED = -13,       /* "even_rotary_dim_required" */
+  LL_ERR_ROTARY_DIM_EXCEEDS_HEAD_DIM = -14,    /* "rotary_dim_exceeds_head_dim" */
+  LL_ERR_UNSUPPORTED_COS_SIN_CACHE = -15,      /* "unsupported_cos_sin_cache" */
+  LL_ERR_UNSUPPORTED_COS_SIN_DTYPE = -16,      /* "unsupported_cos_sin_dtype" */
+  LL_ERR_PREFIX_OUT_OF_RANGE = -17,            /* "prefix_token_count_out_of_range" (reference raises ValueError) */
+  LL_ERR_LAUNCH_CONFIG = -18,                  /* "invalid_launch_config" (reference raises ValueError) */
+  LL_ERR_UNSUPPORTED_KERNEL = -19,             /* "unsupported_kernel_for_shape" (LL_KERNEL_VECTOR forced on an unfit shape) */
+  LL_ERR_HIP = -20                             /* "hip_error" (launch failed; message from the HIP runtime) */
+};
+
+/*
+ * Link: for every token t in [0, num_tokens) and every layer l:
+ *     if repair_mask != NULL and repair_mask[t] != 0: nothing is written;
+ *     V_l[destination_slots[t]] = V_l[source_slots[t]]                    (bit copy)
+ *     K_l[destination_slots[t]] = K_l[source_slots[t]]   if t <  prefix_token_count (bit copy)
+ *     K_l[destination_slots[t]] = rerotate(K_l[source_slots[t]],
+ *                                          local_positions[t] -> global_positions[t])
+ *                                                        if t >= prefix_token_count
+ * rerotate applies, per rotary pair i of every head, the delta rotation
+ *     dc = gc*lc + gs*ls,  ds = gs*lc - gc*ls
+ *     first'  = first*dc - second*ds,  second' = second*dc + first*ds
+ * with (lc, ls) = cos_sin_cache[local][i], cos_sin_cache[local][i + rotary_dim/2]
+ * and  (gc, gs) the same at the global position; pairs are (i, i + rotary_dim/2)
+ * for neox style and (2i, 2i + 1) otherwise.  Dims >= rotary_dim are copied.
+ * Rounding (legolink_triton.py:413-470): bf16 K with an fp32 cache uses fp32
+ * with every multiply and add rounded to nearest even (no fused multiply-add)
+ * and one round-to-nearest-even to bf16 at the store; bf16 K with a bf16 or fp16
+ * cache rounds every product and sum to bf16; fp16 K computes in fp32 and rounds
+ * once to fp16.
+ *
+ * Replaces, with num_layers == 1, fused_kv_link_inplace
+ * (patched_sglang_files/python/sglang/srt/legolink_triton.py:550-645), and with
+ * num_layers == L the per-layer loop that calls it
+ * (patched_sglang_files/python/sglang/srt/pic_runtime.py:5168-5208): one launch
+ * covers up to 64 layers.
+ */
+typedef struct ll_kv_link_args {
+  int64_t struct_size;             /* sizeof(ll_kv_link_args) */
+  int64_t num_layers;              /* >= 1 */
+  void *const *key_layers;         /* host array [num_layers] of device pointers */
+  void *const *value_layers;       /* host array [num_layers] of device pointers */
+  int64_t num_slots;               /* rows of every layer buffer */
+  int64_t num_heads;               /* KV heads per row (this rank's shard) */
+  int64_t key_head_dim;            /* 1..256 */
+  int64_t value_head_dim;          /* 1..256 */
+  int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16 */
+  int64_t num_tokens;              /* linked tokens, >= 1 */
+  const void *source_slots;        /* device [num_tokens], int32 or int64 */
+  int64_t source_slots_dtype;
+  const void *destination_slots;   /* device [num_tokens], int32 or int64 */
+  int64_t destination_slots_dtype;
+  const void *local_positions;     /* device [num_tokens], int32 or int64: compile-time RoPE positions */
+  int64_t local_positions_dtype;
+  const void *global_positions;    /* device [num_tokens], int32 or int64: request-global positions */
+  int64_t global_positions_dtype;
+  const void *repair_mask;         /* device [num_tokens] uint8/bool, or NULL */
+  int64_t repair_mask_dtype;
+  const void *cos_sin_cache;       /* device [cos_sin_rows, cos_sin_cols]: cos in [0, r/2), sin in [r/2, r) */
+  int64_t cos_sin_dtype;           /* LL_DTYPE_FLOAT32, LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16 */
+  int64_t cos_sin_rows;
+  int64_t cos_sin_cols;
+  int64_t cos_sin_stride_row;      /* elements */
+  int64_t cos_sin_stride_col;      /* elements */
+  int64_t rotary_dim;              /* even, 2..key_head_dim */
+  int64_t is_neox_style;           /* 1: pairs (i, i + r/2); 0: pairs (2i, 2i + 1) */
+  int64_t prefix_token_count;      /* tokens [0, prefix) are copied unrotated; 0..num_tokens */
+  int64_t kernel;                  /* LL_KERNEL_* */
+  int64_t waves_per_block;         /* 0 = default; else 1, 2, 4 or 8 */
+  int64_t layers_per_wave;         /* 0 = auto; else >= 1 */
+} ll_kv_link_args;
+
+/*
+ * Repaired-row write-back: for every layer l and row r in [0, num_rows):
+ *     K_l[destination_slots[r]] = repaired_key[l][r]    (bit copy, all heads)
+ *     V_l[destination_slots[r]] = repaired_value[l][r]
+ * repaired_key[l] is the dense [num_rows, num_heads, key_head_dim] block at
+ * element offset l * repaired_key_layer_stride (likewise for V).
+ *
+ * Replaces the repair pass's KV write of the imp_indices rows
+ * (patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py:2235-2239,
+ * whose semantics the reference restates as write_repaired_kv in
+ * tests/pic/reference/repair_reference.py:14-25).
+ */
+typedef struct ll_kv_scatter_args {
+  int64_t struct_size;             /* sizeof(ll_kv_scatter_args) */
+  int64_t num_layers;
+  void *const *key_layers;         /* host array [num_layers] of device pointers */
+  void *const *value_layers;       /* host array [num_layers] of device pointers */
+  int64_t num_slots;
+  int64_t num_heads;
+  int64_t key_head_dim;
+  int64_t value_head_dim;
+  int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16 */
+  int64_t num_rows;                /* >= 0; 0 is a no-op */
+  const void *destination_slots;   /* device [num_rows], int32 or int64 */
+  int64_t destination_slots_dtype;
+  const void *repaired_key;        /* device */
+  int64_t repaired_key_layer_stride;   /* elements */
+  const void *repaired_value;      /* device */
+  int64_t repaired_value_layer_stride; /* elements */
+  int64_t waves_per_block;         /* 0 = default; else 1, 2, 4 or 8 */
+} ll_kv_scatter_args;
+
+/* Which kernel and launch shape ll_kv_link would use (no GPU work). */
+typedef struct ll_launch_info {
+  int64_t kernel;                  /* LL_KERNEL_VECTOR or LL_KERNEL_GENERIC */
+  int64_t launches;                /* kernel launches (one per group of <= 64 layers) */
+  int64_t grid_x;                  /* of the first launch */
+  int64_t grid_y;
+  int64_t block_threads;
+  int64_t layers_per_wave;
+} ll_launch_info;
+
+int ll_kv_link(const ll_kv_link_args *args, ll_stream_t stream);
+int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info);
+int ll_kv_scatter_rows(const ll_kv_scatter_args *args, ll_stream_t stream);
+
+/* Reason string of a status code ("supported" for LL_OK). */
+const char *ll_status_reason(int status);
+/* Message of the last failing call on this thread ("" if none). */
+const char *ll_last_error(void);
+int ll_abi_version(void);
+int64_t ll_kv_link_args_size(void);
+int64_t ll_kv_scatter_args_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEGOLINK_KV_H */

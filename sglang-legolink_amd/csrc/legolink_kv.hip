@@ -1,0 +1,799 @@
+// LegoLink KV link kernels for MI355X (gfx950) and their C ABI.
+//
+// Two kernels implement the link (gather -> RoPE delta re-rotation -> scatter):
+//
+//   kv_link_vec_kernel      the production kernel.  The per-layer K/V rows of
+//                           all tokens are flattened into 16-byte chunks; one
+//                           lane owns one chunk of one token's row and walks
+//                           that chunk through a run of layers.  The token's
+//                           fp32 RoPE delta is computed once per lane and
+//                           reused for every layer (and both V/K moves use one
+//                           global_load_dwordx4 / global_store_dwordx4 per lane
+//                           per layer).  Neox pairs (i, i + D/2) sit in lanes
+//                           q and q ^ (D/16) of the same head, so the partner
+//                           half arrives by a DPP row rotation (D = 128) or a
+//                           lane swizzle (other D) instead of a second load.
+//   kv_link_generic_kernel  one thread per rotary pair / pass-through element /
+//                           V element; every shape the operator accepts
+//                           (partial rotary, K/V head dims that differ,
+//                           bf16/fp16 caches, strided caches).
+//
+// kv_scatter_kernel writes repaired boundary rows into the pool.
+//
+// Rounding follows patched_sglang_files/python/sglang/srt/legolink_triton.py:
+// 413-470: multiplies and adds are separate round-to-nearest-even fp32 ops (the
+// file is compiled with contraction off, so no FMA is formed) and K is rounded
+// once to bf16/fp16 at the store.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "legolink_kv.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kMaxLayersPerLaunch = 64;
+constexpr int kWave = 64;
+constexpr int kLayerUnroll = 4;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Kernel parameters (passed by value in the kernarg segment; the per-layer
+// pointer tables make one launch cover up to kMaxLayersPerLaunch layers
+// without a device-side table allocation).
+// ---------------------------------------------------------------------------
+struct LinkParams {
+  char *k_layers[kMaxLayersPerLaunch];
+  char *v_layers[kMaxLayersPerLaunch];
+  const void *src;
+  const void *dst;
+  const void *lpos;
+  const void *gpos;
+  const unsigned char *mask;
+  const void *cs;
+  long long num_tokens;
+  long long num_slots;
+  long long cs_rows;
+  long long cs_stride_row;
+  long long cs_stride_col;
+  long long prefix;
+  long long k_row_bytes;
+  long long v_row_bytes;
+  long long chunks_per_row;  // vector kernel: 16-byte chunks per K row (== per V row)
+  int num_layers;            // layers in this launch
+  int layers_per_wave;
+  int num_heads;
+  int kdim;
+  int vdim;
+  int rotary_dim;
+  int idx64;                 // bit0 src, bit1 dst, bit2 local, bit3 global are int64
+  int neox;
+};
+
+struct ScatterParams {
+  char *k_layers[kMaxLayersPerLaunch];
+  char *v_layers[kMaxLayersPerLaunch];
+  const void *dst;
+  const char *rk;
+  const char *rv;
+  long long num_rows;
+  long long num_slots;
+  long long rk_layer_stride_bytes;
+  long long rv_layer_stride_bytes;
+  long long k_row_bytes;
+  long long v_row_bytes;
+  int idx64;
+};
+
+// ---------------------------------------------------------------------------
+// Element conversions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ long long load_index(const void *p, bool is64, long long i) {
+  return is64 ? static_cast<const long long *>(p)[i]
+              : static_cast<long long>(static_cast<const int *>(p)[i]);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
+  return __uint_as_float(bits << 16);
+}
+
+// float -> bf16 bits, round to nearest even; NaN becomes the quiet NaN 0x7fc0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// Round an fp32 value to the nearest bf16 and widen it back.
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+template <bool kBF16>
+__device__ __forceinline__ float lo_elem(uint32_t w) {
+  if constexpr (kBF16) return __uint_as_float(w << 16);
+  else return f16_bits_to_f32(w & 0xffffu);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ float hi_elem(uint32_t w) {
+  if constexpr (kBF16) return __uint_as_float(w & 0xffff0000u);
+  else return f16_bits_to_f32(w >> 16);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (kBF16) return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+  else return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane partner exchange: lane i receives lane i ^ kXor (kXor < 64).
+// ---------------------------------------------------------------------------
+template <int kXor>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  if constexpr (kXor == 8) {
+    // DPP row_ror:8 rotates each 16-lane row by 8, i.e. lane i <- lane i ^ 8.
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false));
+  } else {
+    return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), kXor, kWave));
+  }
+}
+
+template <int kXor>
+__device__ __forceinline__ u32x4 xor_lane4(u32x4 v) {
+  u32x4 r;
+  r.x = xor_lane<kXor>(v.x);
+  r.y = xor_lane<kXor>(v.y);
+  r.z = xor_lane<kXor>(v.z);
+  r.w = xor_lane<kXor>(v.w);
+  return r;
+}
+
+// Neox: x holds 8 elements of this lane's half, y the same 8 dims of the other
+// half.  out = x*dc + y*dsn, with dsn = -ds in the first half and +ds in the
+// second half:  first' = first*dc - second*ds,  second' = second*dc + first*ds.
+template <bool kBF16>
+__device__ __forceinline__ u32x4 rotate_neox(u32x4 x, u32x4 y, const float *dc,
+                                             const float *dsn) {
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float x0 = lo_elem<kBF16>(x[w]);
+    const float x1 = hi_elem<kBF16>(x[w]);
+    const float y0 = lo_elem<kBF16>(y[w]);
+    const float y1 = hi_elem<kBF16>(y[w]);
+    const float r0 = x0 * dc[2 * w] + y0 * dsn[2 * w];
+    const float r1 = x1 * dc[2 * w + 1] + y1 * dsn[2 * w + 1];
+    out[w] = pack2<kBF16>(r0, r1);
+  }
+  return out;
+}
+
+// GPT-J style: every 32-bit word holds one (first, second) pair.
+template <bool kBF16>
+__device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const float *ds) {
+  u32x4 out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float a = lo_elem<kBF16>(x[w]);
+    const float b = hi_elem<kBF16>(x[w]);
+    const float r0 = a * dc[w] - b * ds[w];
+    const float r1 = b * dc[w] + a * ds[w];
+    out[w] = pack2<kBF16>(r0, r1);
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Vectorised link kernel.
+//   grid.x * (blockDim.x / 64) waves cover num_tokens * chunks_per_row chunks,
+//   grid.y splits the launch's layers into runs of layers_per_wave.
+// Requirements (checked on the host): key_head_dim == value_head_dim ==
+// rotary_dim == kD, fp32 cos/sin cache with unit column stride and 16-byte
+// aligned rows, 16-byte aligned layer buffers.
+// ---------------------------------------------------------------------------
+template <bool kBF16, int kD, bool kNeox>
+__global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
+  constexpr int kChunksPerHead = kD / 8;
+  constexpr int kPairs = kNeox ? 8 : 4;  // rotary pairs touched by one lane
+  constexpr int kHalf = kD / 2;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long wave =
+      static_cast<long long>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const long long g = wave * kWave + lane;
+  const long long C = p.chunks_per_row;
+  const bool in_range = g < p.num_tokens * C;
+  const long long t = in_range ? g / C : 0;
+  const long long c = in_range ? g - t * C : 0;
+  // Chunk index inside the head; chunks_per_row is a multiple of
+  // kChunksPerHead and kChunksPerHead divides 64, so this is lane-aligned.
+  const int q = lane % kChunksPerHead;
+
+  const long long src = load_index(p.src, p.idx64 & 1, t);
+  const long long dst = load_index(p.dst, p.idx64 & 2, t);
+  bool ok = in_range && src >= 0 && src < p.num_slots && dst >= 0 && dst < p.num_slots;
+  if (p.mask != nullptr) ok = ok && (p.mask[t] == 0);
+  const bool remap = t >= p.prefix;
+
+  float dc[kPairs];
+  float ds[kPairs];
+#pragma unroll
+  for (int e = 0; e < kPairs; ++e) {
+    dc[e] = 1.0f;
+    ds[e] = 0.0f;
+  }
+  if (remap && in_range) {
+    const long long lp = load_index(p.lpos, p.idx64 & 4, t);
+    const long long gp = load_index(p.gpos, p.idx64 & 8, t);
+    if (lp < 0 || lp >= p.cs_rows || gp < 0 || gp >= p.cs_rows) {
+      ok = false;
+    } else {
+      const int pb = kNeox ? (q % (kChunksPerHead / 2)) * 8 : q * 4;
+      const float *lrow = static_cast<const float *>(p.cs) + lp * p.cs_stride_row + pb;
+      const float *grow = static_cast<const float *>(p.cs) + gp * p.cs_stride_row + pb;
+#pragma unroll
+      for (int e = 0; e < kPairs; e += 4) {
+        const f32x4 lc = *reinterpret_cast<const f32x4 *>(lrow + e);
+        const f32x4 ls = *reinterpret_cast<const f32x4 *>(lrow + kHalf + e);
+        const f32x4 gc = *reinterpret_cast<const f32x4 *>(grow + e);
+        const f32x4 gs = *reinterpret_cast<const f32x4 *>(grow + kHalf + e);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          dc[e + k] = gc[k] * lc[k] + gs[k] * ls[k];
+          ds[e + k] = gs[k] * lc[k] - gc[k] * ls[k];
+        }
+      }
+    }
+  }
+  float dsn[kPairs];
+  if constexpr (kNeox) {
+    const bool second_half = q >= kChunksPerHead / 2;
+#pragma unroll
+    for (int e = 0; e < kPairs; ++e) dsn[e] = second_half ? ds[e] : -ds[e];
+  }
+
+  const int l0 = blockIdx.y * p.layers_per_wave;
+  const int l1 = min(l0 + p.layers_per_wave, p.num_layers);
+  const long long k_src = src * p.k_row_bytes + c * 16;
+  const long long k_dst = dst * p.k_row_bytes + c * 16;
+  const long long v_src = src * p.v_row_bytes + c * 16;
+  const long long v_dst = dst * p.v_row_bytes + c * 16;
+
+  for (int l = l0; l < l1; l += kLayerUnroll) {
+    u32x4 kin[kLayerUnroll];
+    u32x4 vin[kLayerUnroll];
+#pragma unroll
+    for (int u = 0; u < kLayerUnroll; ++u) {
+      kin[u] = u32x4{0u, 0u, 0u, 0u};
+      vin[u] = u32x4{0u, 0u, 0u, 0u};
+      if (ok && l + u < l1) {
+        kin[u] = *reinterpret_cast<const u32x4 *>(p.k_layers[l + u] + k_src);
+        vin[u] = *reinterpret_cast<const u32x4 *>(p.v_layers[l + u] + v_src);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kLayerUnroll; ++u) {
+      u32x4 kout = kin[u];
+      if constexpr (kNeox) {
+        // Every lane takes part in the exchange (uniform control flow here).
+        const u32x4 partner = xor_lane4<kChunksPerHead / 2>(kin[u]);
+        if (remap) kout = rotate_neox<kBF16>(kin[u], partner, dc, dsn);
+      } else {
+        if (remap) kout = rotate_gptj<kBF16>(kin[u], dc, ds);
+      }
+      if (ok && l + u < l1) {
+        *reinterpret_cast<u32x4 *>(p.k_layers[l + u] + k_dst) = kout;
+        *reinterpret_cast<u32x4 *>(p.v_layers[l + u] + v_dst) = vin[u];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic link kernel: grid.y = layer, blocks stride over tokens, threads over
+// the token's work items (rotary pairs, pass-through K dims, V dims).
+// kKey: 1 = fp16, 2 = bf16.  kCache: 1 = fp16, 2 = bf16, 3 = fp32.
+// ---------------------------------------------------------------------------
+template <int kCache>
+__device__ __forceinline__ float load_cache(const void *cs, long long offset) {
+  if constexpr (kCache == 3) return static_cast<const float *>(cs)[offset];
+  else if constexpr (kCache == 2)
+    return bf16_bits_to_f32(static_cast<const uint16_t *>(cs)[offset]);
+  else return f16_bits_to_f32(static_cast<const uint16_t *>(cs)[offset]);
+}
+
+template <int kKey>
+__device__ __forceinline__ float key_to_f32(uint16_t bits) {
+  if constexpr (kKey == 2) return bf16_bits_to_f32(bits);
+  else return f16_bits_to_f32(bits);
+}
+
+template <int kKey>
+__device__ __forceinline__ uint16_t f32_to_key(float f) {
+  if constexpr (kKey == 2) return static_cast<uint16_t>(f32_to_bf16_bits(f));
+  else return static_cast<uint16_t>(f32_to_f16_bits(f));
+}
+
+template <int kKey, int kCache>
+__global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p) {
+  const int layer = blockIdx.y;
+  const uint16_t *kbase = reinterpret_cast<const uint16_t *>(p.k_layers[layer]);
+  uint16_t *kout = reinterpret_cast<uint16_t *>(p.k_layers[layer]);
+  const uint16_t *vbase = reinterpret_cast<const uint16_t *>(p.v_layers[layer]);
+  uint16_t *vout = reinterpret_cast<uint16_t *>(p.v_layers[layer]);
+  const int half = p.rotary_dim / 2;
+  const int rot_items = p.num_heads * half;
+  const int pass_dims = p.kdim - p.rotary_dim;
+  const int pass_items = p.num_heads * pass_dims;
+  const int v_items = p.num_heads * p.vdim;
+  const int items = rot_items + pass_items + v_items;
+  const long long k_row = static_cast<long long>(p.num_heads) * p.kdim;
+  const long long v_row = static_cast<long long>(p.num_heads) * p.vdim;
+
+  for (long long t = blockIdx.x; t < p.num_tokens; t += gridDim.x) {
+    const long long src = load_index(p.src, p.idx64 & 1, t);
+    const long long dst = load_index(p.dst, p.idx64 & 2, t);
+    if (src < 0 || src >= p.num_slots || dst < 0 || dst >= p.num_slots) continue;
+    if (p.mask != nullptr && p.mask[t] != 0) continue;
+    const bool remap = t >= p.prefix;
+    long long lp = 0, gp = 0;
+    if (remap) {
+      lp = load_index(p.lpos, p.idx64 & 4, t);
+      gp = load_index(p.gpos, p.idx64 & 8, t);
+      if (lp < 0 || lp >= p.cs_rows || gp < 0 || gp >= p.cs_rows) continue;
+    }
+    const uint16_t *ks = kbase + src * k_row;
+    uint16_t *kd = kout + dst * k_row;
+    for (int w = threadIdx.x; w < items; w += blockDim.x) {
+      if (w < rot_items) {
+        const int h = w / half;
+        const int i = w - h * half;
+        const int d1 = p.neox ? i : 2 * i;
+        const int d2 = p.neox ? i + half : 2 * i + 1;
+        const uint16_t b1 = ks[h * p.kdim + d1];
+        const uint16_t b2 = ks[h * p.kdim + d2];
+        uint16_t o1 = b1, o2 = b2;
+        if (remap) {
+          const float lc = load_cache<kCache>(p.cs, lp * p.cs_stride_row + i * p.cs_stride_col);
+          const float ls =
+              load_cache<kCache>(p.cs, lp * p.cs_stride_row + (i + half) * p.cs_stride_col);
+          const float gc = load_cache<kCache>(p.cs, gp * p.cs_stride_row + i * p.cs_stride_col);
+          const float gs =
+              load_cache<kCache>(p.cs, gp * p.cs_stride_row + (i + half) * p.cs_stride_col);
+          const float x1 = key_to_f32<kKey>(b1);
+          const float x2 = key_to_f32<kKey>(b2);
+          if constexpr (kKey == 2 && kCache != 3) {
+            // bf16 K with a bf16/fp16 cache: every product and sum rounded to bf16.
+            const float dcb = round_bf16(round_bf16(gc * lc) + round_bf16(gs * ls));
+            const float dsb = round_bf16(round_bf16(gs * lc) - round_bf16(gc * ls));
+            const float first_cos = round_bf16(x1 * dcb);
+            const float second_sin = round_bf16(x2 * dsb);
+            const float second_cos = round_bf16(x2 * dcb);
+            const float first_sin = round_bf16(x1 * dsb);
+            o1 = static_cast<uint16_t>(f32_to_bf16_bits(first_cos - second_sin));
+            o2 = static_cast<uint16_t>(f32_to_bf16_bits(second_cos + first_sin));
+          } else {
+            const float dc = gc * lc + gs * ls;
+            const float ds = gs * lc - gc * ls;
+            o1 = f32_to_key<kKey>(x1 * dc - x2 * ds);
+            o2 = f32_to_key<kKey>(x2 * dc + x1 * ds);
+          }
+        }
+        kd[h * p.kdim + d1] = o1;
+        kd[h * p.kdim + d2] = o2;
+      } else if (w < rot_items + pass_items) {
+        const int j = w - rot_items;
+        const int h = j / pass_dims;
+        const int d = p.rotary_dim + (j - h * pass_dims);
+        kd[h * p.kdim + d] = ks[h * p.kdim + d];
+      } else {
+        const long long j = w - rot_items - pass_items;
+        vout[dst * v_row + j] = vbase[src * v_row + j];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Repaired-row scatter: grid.y = layer; threads stride over the layer's
+// (row, chunk) items, K rows first, then V rows.
+// ---------------------------------------------------------------------------
+template <typename Chunk>
+__global__ void __launch_bounds__(512) kv_scatter_kernel(const ScatterParams p) {
+  const int layer = blockIdx.y;
+  constexpr int kBytes = sizeof(Chunk);
+  const long long kc = p.k_row_bytes / kBytes;
+  const long long vc = p.v_row_bytes / kBytes;
+  const long long k_items = p.num_rows * kc;
+  const long long total = k_items + p.num_rows * vc;
+  const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += stride) {
+    const bool is_k = i < k_items;
+    const long long j = is_k ? i : i - k_items;
+    const long long per_row = is_k ? kc : vc;
+    const long long r = j / per_row;
+    const long long c = j - r * per_row;
+    const long long slot = load_index(p.dst, p.idx64 & 2, r);
+    if (slot < 0 || slot >= p.num_slots) continue;
+    if (is_k) {
+      const Chunk v = *reinterpret_cast<const Chunk *>(
+          p.rk + layer * p.rk_layer_stride_bytes + r * p.k_row_bytes + c * kBytes);
+      *reinterpret_cast<Chunk *>(p.k_layers[layer] + slot * p.k_row_bytes + c * kBytes) = v;
+    } else {
+      const Chunk v = *reinterpret_cast<const Chunk *>(
+          p.rv + layer * p.rv_layer_stride_bytes + r * p.v_row_bytes + c * kBytes);
+      *reinterpret_cast<Chunk *>(p.v_layers[layer] + slot * p.v_row_bytes + c * kBytes) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+bool is_index_dtype(int64_t dt) { return dt == LL_DTYPE_INT32 || dt == LL_DTYPE_INT64; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate_link(const ll_kv_link_args *a) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_kv_link_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_kv_link_args));
+  if (a->num_layers < 1 || a->key_layers == nullptr || a->value_layers == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "num_layers must be >= 1 with key/value layer tables");
+  for (int64_t l = 0; l < a->num_layers; ++l)
+    if (a->key_layers[l] == nullptr || a->value_layers[l] == nullptr)
+      return fail(LL_ERR_INVALID_ARGUMENT, "layer %lld buffer is NULL", static_cast<long long>(l));
+  if (a->num_slots < 0) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots is negative");
+  if (a->num_heads < 1)
+    return fail(LL_ERR_MHA_3D_KV_BUFFERS_REQUIRED, "num_heads must be >= 1");
+  if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
+    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "kv_dtype must be fp16 or bf16");
+  if (a->key_head_dim < 1 || a->value_head_dim < 1 || a->key_head_dim > 256 ||
+      a->value_head_dim > 256)
+    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head dims must be in 1..256");
+  if (a->num_tokens < 0) return fail(LL_ERR_INVALID_ARGUMENT, "num_tokens is negative");
+  if (a->num_tokens == 0) return fail(LL_ERR_EMPTY_LINK, "no tokens to link");
+  if (a->source_slots == nullptr || a->destination_slots == nullptr ||
+      a->local_positions == nullptr || a->global_positions == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "token map pointer is NULL");
+  if (a->repair_mask != nullptr && a->repair_mask_dtype != LL_DTYPE_UINT8)
+    return fail(LL_ERR_BOOLEAN_REPAIR_MASK_REQUIRED, "repair mask must be uint8/bool");
+  if (!is_index_dtype(a->source_slots_dtype) || !is_index_dtype(a->destination_slots_dtype) ||
+      !is_index_dtype(a->local_positions_dtype) || !is_index_dtype(a->global_positions_dtype))
+    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "token maps must be int32 or int64");
+  if (a->rotary_dim <= 0 || (a->rotary_dim % 2) != 0)
+    return fail(LL_ERR_EVEN_ROTARY_DIM_REQUIRED, "rotary_dim must be positive and even");
+  if (a->rotary_dim > a->key_head_dim)
+    return fail(LL_ERR_ROTARY_DIM_EXCEEDS_HEAD_DIM, "rotary_dim exceeds key_head_dim");
+  if (a->cos_sin_cache == nullptr || a->cos_sin_rows < 0 || a->cos_sin_cols < a->rotary_dim)
+    return fail(LL_ERR_UNSUPPORTED_COS_SIN_CACHE, "cos/sin cache must hold >= rotary_dim columns");
+  if (a->cos_sin_dtype != LL_DTYPE_FLOAT32 && a->cos_sin_dtype != LL_DTYPE_BFLOAT16 &&
+      a->cos_sin_dtype != LL_DTYPE_FLOAT16)
+    return fail(LL_ERR_UNSUPPORTED_COS_SIN_DTYPE, "cos/sin cache must be fp32, bf16 or fp16");
+  if (a->prefix_token_count < 0 || a->prefix_token_count > a->num_tokens)
+    return fail(LL_ERR_PREFIX_OUT_OF_RANGE, "prefix_token_count is outside the linked token range");
+  if (a->kernel < LL_KERNEL_AUTO || a->kernel > LL_KERNEL_GENERIC)
+    return fail(LL_ERR_LAUNCH_CONFIG, "unknown kernel selector %lld",
+                static_cast<long long>(a->kernel));
+  if (a->waves_per_block != 0 && a->waves_per_block != 1 && a->waves_per_block != 2 &&
+      a->waves_per_block != 4 && a->waves_per_block != 8)
+    return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0, 1, 2, 4 or 8");
+  if (a->layers_per_wave < 0) return fail(LL_ERR_LAUNCH_CONFIG, "layers_per_wave is negative");
+  return LL_OK;
+}
+
+bool vector_kernel_fits(const ll_kv_link_args *a) {
+  const int64_t d = a->key_head_dim;
+  if (!(d == 32 || d == 64 || d == 128 || d == 256)) return false;
+  if (a->value_head_dim != d || a->rotary_dim != d) return false;
+  if (a->cos_sin_dtype != LL_DTYPE_FLOAT32 || a->cos_sin_stride_col != 1) return false;
+  if ((a->cos_sin_stride_row % 4) != 0 || !aligned16(a->cos_sin_cache)) return false;
+  for (int64_t l = 0; l < a->num_layers; ++l)
+    if (!aligned16(a->key_layers[l]) || !aligned16(a->value_layers[l])) return false;
+  return true;
+}
+
+struct LinkPlan {
+  int kernel;  // LL_KERNEL_VECTOR / LL_KERNEL_GENERIC
+  int block_threads;
+  long long grid_x;
+  int layers_per_wave;  // vector kernel
+  int launches;
+};
+
+constexpr long long kTargetWaves = 16384;  // >= 64 waves per CU on 256 CUs
+
+int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
+  const bool fits = vector_kernel_fits(a);
+  if (a->kernel == LL_KERNEL_VECTOR && !fits)
+    return fail(LL_ERR_UNSUPPORTED_KERNEL,
+                "vector kernel needs key_head_dim == value_head_dim == rotary_dim in "
+                "{32,64,128,256}, an fp32 unit-stride cache and 16-byte aligned buffers");
+  plan->kernel = (a->kernel == LL_KERNEL_GENERIC || !fits) ? LL_KERNEL_GENERIC : LL_KERNEL_VECTOR;
+  const int waves_per_block = a->waves_per_block ? static_cast<int>(a->waves_per_block) : 4;
+  plan->block_threads = waves_per_block * kWave;
+  const int layers_first = static_cast<int>(
+      a->num_layers < kMaxLayersPerLaunch ? a->num_layers : kMaxLayersPerLaunch);
+  plan->launches = static_cast<int>((a->num_layers + kMaxLayersPerLaunch - 1) / kMaxLayersPerLaunch);
+  if (plan->kernel == LL_KERNEL_VECTOR) {
+    const long long chunks = a->num_heads * a->key_head_dim / 8;
+    const long long waves_x = (a->num_tokens * chunks + kWave - 1) / kWave;
+    plan->grid_x = (waves_x + waves_per_block - 1) / waves_per_block;
+    int lpw = static_cast<int>(a->layers_per_wave);
+    if (lpw == 0) {
+      long long groups = (kTargetWaves + waves_x - 1) / waves_x;
+      if (groups < 1) groups = 1;
+      if (groups > layers_first) groups = layers_first;
+      lpw = static_cast<int>((layers_first + groups - 1) / groups);
+    }
+    if (lpw > layers_first) lpw = layers_first;
+    plan->layers_per_wave = lpw;
+  } else {
+    plan->grid_x = a->num_tokens < 65536 ? a->num_tokens : 65536;
+    plan->layers_per_wave = 1;
+  }
+  if (plan->grid_x > 0x7fffffffLL) return fail(LL_ERR_LAUNCH_CONFIG, "link too large for one grid");
+  return LL_OK;
+}
+
+template <bool kBF16, int kD>
+void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+  if (neox) kv_link_vec_kernel<kBF16, kD, true><<<grid, block, 0, s>>>(p);
+  else kv_link_vec_kernel<kBF16, kD, false><<<grid, block, 0, s>>>(p);
+}
+
+template <bool kBF16>
+void launch_vec(int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+  switch (d) {
+    case 32: launch_vec_neox<kBF16, 32>(grid, block, s, p, neox); break;
+    case 64: launch_vec_neox<kBF16, 64>(grid, block, s, p, neox); break;
+    case 128: launch_vec_neox<kBF16, 128>(grid, block, s, p, neox); break;
+    default: launch_vec_neox<kBF16, 256>(grid, block, s, p, neox); break;
+  }
+}
+
+template <int kKey>
+void launch_generic(int cache_dtype, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p) {
+  switch (cache_dtype) {
+    case LL_DTYPE_FLOAT32: kv_link_generic_kernel<kKey, 3><<<grid, block, 0, s>>>(p); break;
+    case LL_DTYPE_BFLOAT16: kv_link_generic_kernel<kKey, 2><<<grid, block, 0, s>>>(p); break;
+    default: kv_link_generic_kernel<kKey, 1><<<grid, block, 0, s>>>(p); break;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ll_abi_version(void) { return LL_ABI_VERSION; }
+int64_t ll_kv_link_args_size(void) { return static_cast<int64_t>(sizeof(ll_kv_link_args)); }
+int64_t ll_kv_scatter_args_size(void) { return static_cast<int64_t>(sizeof(ll_kv_scatter_args)); }
+const char *ll_last_error(void) { return g_last_error.c_str(); }
+
+const char *ll_status_reason(int status) {
+  switch (status) {
+    case LL_OK: return "supported";
+    case LL_ERR_INVALID_ARGUMENT: return "invalid_argument";
+    case LL_ERR_MHA_3D_KV_BUFFERS_REQUIRED: return "mha_3d_kv_buffers_required";
+    case LL_ERR_KV_HEAD_LAYOUT_MISMATCH: return "kv_head_layout_mismatch";
+    case LL_ERR_KV_DTYPE_MISMATCH: return "kv_dtype_mismatch";
+    case LL_ERR_FP16_OR_BF16_REQUIRED: return "fp16_or_bf16_required";
+    case LL_ERR_CONTIGUOUS_KV_BUFFERS_REQUIRED: return "contiguous_kv_buffers_required";
+    case LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE: return "head_dimension_out_of_range";
+    case LL_ERR_EMPTY_LINK: return "empty_link";
+    case LL_ERR_TOKEN_MAP_LENGTH_MISMATCH: return "token_map_length_mismatch";
+    case LL_ERR_REPAIR_MASK_LENGTH_MISMATCH: return "repair_mask_length_mismatch";
+    case LL_ERR_BOOLEAN_REPAIR_MASK_REQUIRED: return "boolean_repair_mask_required";
+    case LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED: return "integer_token_maps_required";
+    case LL_ERR_EVEN_ROTARY_DIM_REQUIRED: return "even_rotary_dim_required";
+    case LL_ERR_ROTARY_DIM_EXCEEDS_HEAD_DIM: return "rotary_dim_exceeds_head_dim";
+    case LL_ERR_UNSUPPORTED_COS_SIN_CACHE: return "unsupported_cos_sin_cache";
+    case LL_ERR_UNSUPPORTED_COS_SIN_DTYPE: return "unsupported_cos_sin_dtype";
+    case LL_ERR_PREFIX_OUT_OF_RANGE: return "prefix_token_count_out_of_range";
+    case LL_ERR_LAUNCH_CONFIG: return "invalid_launch_config";
+    case LL_ERR_UNSUPPORTED_KERNEL: return "unsupported_kernel_for_shape";
+    case LL_ERR_HIP: return "hip_error";
+    default: return "unknown_status";
+  }
+}
+
+int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info) {
+  int rc = validate_link(args);
+  if (rc != LL_OK) return rc;
+  if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
+  LinkPlan plan;
+  rc = plan_link(args, &plan);
+  if (rc != LL_OK) return rc;
+  const int layers_first = static_cast<int>(
+      args->num_layers < kMaxLayersPerLaunch ? args->num_layers : kMaxLayersPerLaunch);
+  info->kernel = plan.kernel;
+  info->launches = plan.launches;
+  info->grid_x = plan.grid_x;
+  info->grid_y = plan.kernel == LL_KERNEL_VECTOR
+                     ? (layers_first + plan.layers_per_wave - 1) / plan.layers_per_wave
+                     : layers_first;
+  info->block_threads = plan.block_threads;
+  info->layers_per_wave = plan.layers_per_wave;
+  return LL_OK;
+}
+
+int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
+  int rc = validate_link(a);
+  if (rc != LL_OK) return rc;
+  LinkPlan plan;
+  rc = plan_link(a, &plan);
+  if (rc != LL_OK) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  LinkParams p;
+  memset(&p, 0, sizeof(p));
+  p.src = a->source_slots;
+  p.dst = a->destination_slots;
+  p.lpos = a->local_positions;
+  p.gpos = a->global_positions;
+  p.mask = static_cast<const unsigned char *>(a->repair_mask);
+  p.cs = a->cos_sin_cache;
+  p.num_tokens = a->num_tokens;
+  p.num_slots = a->num_slots;
+  p.cs_rows = a->cos_sin_rows;
+  p.cs_stride_row = a->cos_sin_stride_row;
+  p.cs_stride_col = a->cos_sin_stride_col;
+  p.prefix = a->prefix_token_count;
+  p.k_row_bytes = a->num_heads * a->key_head_dim * 2;
+  p.v_row_bytes = a->num_heads * a->value_head_dim * 2;
+  p.chunks_per_row = a->num_heads * a->key_head_dim / 8;
+  p.num_heads = static_cast<int>(a->num_heads);
+  p.kdim = static_cast<int>(a->key_head_dim);
+  p.vdim = static_cast<int>(a->value_head_dim);
+  p.rotary_dim = static_cast<int>(a->rotary_dim);
+  p.idx64 = (a->source_slots_dtype == LL_DTYPE_INT64 ? 1 : 0) |
+            (a->destination_slots_dtype == LL_DTYPE_INT64 ? 2 : 0) |
+            (a->local_positions_dtype == LL_DTYPE_INT64 ? 4 : 0) |
+            (a->global_positions_dtype == LL_DTYPE_INT64 ? 8 : 0);
+  p.neox = a->is_neox_style ? 1 : 0;
+  const bool bf16 = a->kv_dtype == LL_DTYPE_BFLOAT16;
+  const dim3 block(plan.block_threads);
+
+  for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
+    const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch
+                                       ? a->num_layers - base
+                                       : kMaxLayersPerLaunch);
+    for (int l = 0; l < n; ++l) {
+      p.k_layers[l] = static_cast<char *>(a->key_layers[base + l]);
+      p.v_layers[l] = static_cast<char *>(a->value_layers[base + l]);
+    }
+    p.num_layers = n;
+    if (plan.kernel == LL_KERNEL_VECTOR) {
+      const int lpw = plan.layers_per_wave < n ? plan.layers_per_wave : n;
+      p.layers_per_wave = lpw;
+      const dim3 grid(static_cast<unsigned>(plan.grid_x), static_cast<unsigned>((n + lpw - 1) / lpw));
+      if (bf16) launch_vec<true>(p.kdim, grid, block, s, p, p.neox != 0);
+      else launch_vec<false>(p.kdim, grid, block, s, p, p.neox != 0);
+    } else {
+      p.layers_per_wave = 1;
+      const dim3 grid(static_cast<unsigned>(plan.grid_x), static_cast<unsigned>(n));
+      if (bf16) launch_generic<2>(static_cast<int>(a->cos_sin_dtype), grid, block, s, p);
+      else launch_generic<1>(static_cast<int>(a->cos_sin_dtype), grid, block, s, p);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+      return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return LL_OK;
+}
+
+int ll_kv_scatter_rows(const ll_kv_scatter_args *a, ll_stream_t stream) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_kv_scatter_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_kv_scatter_args));
+  if (a->num_layers < 1 || a->key_layers == nullptr || a->value_layers == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "num_layers must be >= 1 with key/value layer tables");
+  for (int64_t l = 0; l < a->num_layers; ++l)
+    if (a->key_layers[l] == nullptr || a->value_layers[l] == nullptr)
+      return fail(LL_ERR_INVALID_ARGUMENT, "layer %lld buffer is NULL", static_cast<long long>(l));
+  if (a->num_slots < 0 || a->num_rows < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "num_slots and num_rows must be >= 0");
+  if (a->num_heads < 1)
+    return fail(LL_ERR_MHA_3D_KV_BUFFERS_REQUIRED, "num_heads must be >= 1");
+  if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
+    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "kv_dtype must be fp16 or bf16");
+  if (a->key_head_dim < 1 || a->value_head_dim < 1 || a->key_head_dim > 256 ||
+      a->value_head_dim > 256)
+    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head dims must be in 1..256");
+  if (a->waves_per_block != 0 && a->waves_per_block != 1 && a->waves_per_block != 2 &&
+      a->waves_per_block != 4 && a->waves_per_block != 8)
+    return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0, 1, 2, 4 or 8");
+  if (a->num_rows == 0) return LL_OK;
+  if (a->destination_slots == nullptr || a->repaired_key == nullptr ||
+      a->repaired_value == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "destination_slots / repaired rows pointer is NULL");
+  if (!is_index_dtype(a->destination_slots_dtype))
+    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "destination slots must be int32 or int64");
+  if (a->repaired_key_layer_stride < 0 || a->repaired_value_layer_stride < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "repaired layer strides must be >= 0");
+
+  ScatterParams p;
+  memset(&p, 0, sizeof(p));
+  p.dst = a->destination_slots;
+  p.rk = static_cast<const char *>(a->repaired_key);
+  p.rv = static_cast<const char *>(a->repaired_value);
+  p.num_rows = a->num_rows;
+  p.num_slots = a->num_slots;
+  p.rk_layer_stride_bytes = a->repaired_key_layer_stride * 2;
+  p.rv_layer_stride_bytes = a->repaired_value_layer_stride * 2;
+  p.k_row_bytes = a->num_heads * a->key_head_dim * 2;
+  p.v_row_bytes = a->num_heads * a->value_head_dim * 2;
+  p.idx64 = a->destination_slots_dtype == LL_DTYPE_INT64 ? 2 : 0;
+
+  bool vec = (p.k_row_bytes % 16) == 0 && (p.v_row_bytes % 16) == 0 &&
+             (p.rk_layer_stride_bytes % 16) == 0 && (p.rv_layer_stride_bytes % 16) == 0 &&
+             aligned16(p.rk) && aligned16(p.rv);
+  for (int64_t l = 0; l < a->num_layers && vec; ++l)
+    vec = aligned16(a->key_layers[l]) && aligned16(a->value_layers[l]);
+  const long long chunk = vec ? 16 : 2;
+  const long long items = a->num_rows * (p.k_row_bytes + p.v_row_bytes) / chunk;
+  const int waves_per_block = a->waves_per_block ? static_cast<int>(a->waves_per_block) : 4;
+  const int threads = waves_per_block * kWave;
+  long long gx = (items + threads - 1) / threads;
+  if (gx > 65536) gx = 65536;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
+    const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch
+                                       ? a->num_layers - base
+                                       : kMaxLayersPerLaunch);
+    for (int l = 0; l < n; ++l) {
+      p.k_layers[l] = static_cast<char *>(a->key_layers[base + l]);
+      p.v_layers[l] = static_cast<char *>(a->value_layers[base + l]);
+    }
+    // Staged rows of layer base + l start at (base + l) * stride.
+    ScatterParams q = p;
+    q.rk = p.rk + base * p.rk_layer_stride_bytes;
+    q.rv = p.rv + base * p.rv_layer_stride_bytes;
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n));
+    if (vec) kv_scatter_kernel<u32x4><<<grid, dim3(threads), 0, s>>>(q);
+    else kv_scatter_kernel<uint16_t><<<grid, dim3(threads), 0, s>>>(q);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+      return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return LL_OK;
+}
+
+}  // extern "C"

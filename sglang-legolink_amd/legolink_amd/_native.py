@@ -1,0 +1,243 @@
+"""ctypes binding of ``liblegolink_kv.so`` (the C ABI in ``include/legolink_kv.h``).
+
+The library is built in-tree for gfx950 (``legolink_amd.build``).  It links
+against ``libamdhip64.so.7``; torch is imported before the library is opened so
+that the dynamic loader binds those symbols to the HIP runtime torch already
+loaded, and device pointers and streams handed over from torch are valid in
+the library.
+
+There is no fallback: when the library is missing every entry raises
+``NativeLibraryUnavailable``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+LIB_PATH = LIB_DIR / "liblegolink_kv.so"
+ABI_VERSION = 1
+
+# Element type codes (include/legolink_kv.h).
+DTYPE_FLOAT16 = 1
+DTYPE_BFLOAT16 = 2
+DTYPE_FLOAT32 = 3
+DTYPE_INT32 = 4
+DTYPE_INT64 = 5
+DTYPE_UINT8 = 6
+
+KERNEL_AUTO = 0
+KERNEL_VECTOR = 1
+KERNEL_GENERIC = 2
+
+# Status codes.
+LL_OK = 0
+LL_ERR_INVALID_ARGUMENT = -1
+LL_ERR_PREFIX_OUT_OF_RANGE = -17
+LL_ERR_LAUNCH_CONFIG = -18
+LL_ERR_UNSUPPORTED_KERNEL = -19
+LL_ERR_HIP = -20
+
+EXPORTED_SYMBOLS = (
+    "ll_kv_link",
+    "ll_kv_link_describe",
+    "ll_kv_scatter_rows",
+    "ll_status_reason",
+    "ll_last_error",
+    "ll_abi_version",
+    "ll_kv_link_args_size",
+    "ll_kv_scatter_args_size",
+)
+
+_i64 = ctypes.c_int64
+_ptr = ctypes.c_void_p
+
+
+class LinkArgs(ctypes.Structure):
+    """Mirror of ``ll_kv_link_args``."""
+
+    _fields_ = [
+        ("struct_size", _i64),
+        ("num_layers", _i64),
+        ("key_layers", _ptr),
+        ("value_layers", _ptr),
+        ("num_slots", _i64),
+        ("num_heads", _i64),
+        ("key_head_dim", _i64),
+        ("value_head_dim", _i64),
+        ("kv_dtype", _i64),
+        ("num_tokens", _i64),
+        ("source_slots", _ptr),
+        ("source_slots_dtype", _i64),
+        ("destination_slots", _ptr),
+        ("destination_slots_dtype", _i64),
+        ("local_positions", _ptr),
+        ("local_positions_dtype", _i64),
+        ("global_positions", _ptr),
+        ("global_positions_dtype", _i64),
+        ("repair_mask", _ptr),
+        ("repair_mask_dtype", _i64),
+        ("cos_sin_cache", _ptr),
+        ("cos_sin_dtype", _i64),
+        ("cos_sin_rows", _i64),
+        ("cos_sin_cols", _i64),
+        ("cos_sin_stride_row", _i64),
+        ("cos_sin_stride_col", _i64),
+        ("rotary_dim", _i64),
+        ("is_neox_style", _i64),
+        ("prefix_token_count", _i64),
+        ("kernel", _i64),
+        ("waves_per_block", _i64),
+        ("layers_per_wave", _i64),
+    ]
+
+
+class ScatterArgs(ctypes.Structure):
+    """Mirror of ``ll_kv_scatter_args``."""
+
+    _fields_ = [
+        ("struct_size", _i64),
+        ("num_layers", _i64),
+        ("key_layers", _ptr),
+        ("value_layers", _ptr),
+        ("num_slots", _i64),
+        ("num_heads", _i64),
+        ("key_head_dim", _i64),
+        ("value_head_dim", _i64),
+        ("kv_dtype", _i64),
+        ("num_rows", _i64),
+        ("destination_slots", _ptr),
+        ("destination_slots_dtype", _i64),
+        ("repaired_key", _ptr),
+        ("repaired_key_layer_stride", _i64),
+        ("repaired_value", _ptr),
+        ("repaired_value_layer_stride", _i64),
+        ("waves_per_block", _i64),
+    ]
+
+
+class LaunchInfo(ctypes.Structure):
+    """Mirror of ``ll_launch_info``."""
+
+    _fields_ = [
+        ("kernel", _i64),
+        ("launches", _i64),
+        ("grid_x", _i64),
+        ("grid_y", _i64),
+        ("block_threads", _i64),
+        ("layers_per_wave", _i64),
+    ]
+
+
+class NativeLibraryUnavailable(RuntimeError):
+    """``liblegolink_kv.so`` is not built or cannot be loaded."""
+
+
+class NativeCallError(RuntimeError):
+    """A library entry returned a negative status."""
+
+    def __init__(self, status: int, reason: str, message: str) -> None:
+        super().__init__(f"{reason}: {message}" if message else reason)
+        self.status = status
+        self.reason = reason
+        self.detail = message
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Open the library once, verify its ABI, and return the handle."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (binds libamdhip64.so.7 to torch's copy first)
+
+        if not LIB_PATH.is_file():
+            raise NativeLibraryUnavailable(
+                f"{LIB_PATH} is not built; build it with "
+                "`python -m legolink_amd.build` (hipcc --offload-arch=gfx950)"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as error:
+            raise NativeLibraryUnavailable(f"cannot load {LIB_PATH}: {error}") from error
+        lib.ll_kv_link.argtypes = [ctypes.POINTER(LinkArgs), _ptr]
+        lib.ll_kv_link.restype = ctypes.c_int
+        lib.ll_kv_link_describe.argtypes = [ctypes.POINTER(LinkArgs), ctypes.POINTER(LaunchInfo)]
+        lib.ll_kv_link_describe.restype = ctypes.c_int
+        lib.ll_kv_scatter_rows.argtypes = [ctypes.POINTER(ScatterArgs), _ptr]
+        lib.ll_kv_scatter_rows.restype = ctypes.c_int
+        lib.ll_status_reason.argtypes = [ctypes.c_int]
+        lib.ll_status_reason.restype = ctypes.c_char_p
+        lib.ll_last_error.argtypes = []
+        lib.ll_last_error.restype = ctypes.c_char_p
+        lib.ll_abi_version.argtypes = []
+        lib.ll_abi_version.restype = ctypes.c_int
+        lib.ll_kv_link_args_size.argtypes = []
+        lib.ll_kv_link_args_size.restype = _i64
+        lib.ll_kv_scatter_args_size.argtypes = []
+        lib.ll_kv_scatter_args_size.restype = _i64
+        if lib.ll_abi_version() != ABI_VERSION:
+            raise NativeLibraryUnavailable(
+                f"{LIB_PATH} has ABI {lib.ll_abi_version()}, expected {ABI_VERSION}; rebuild it"
+            )
+        if lib.ll_kv_link_args_size() != ctypes.sizeof(LinkArgs) or (
+            lib.ll_kv_scatter_args_size() != ctypes.sizeof(ScatterArgs)
+        ):
+            raise NativeLibraryUnavailable(f"{LIB_PATH} struct layout differs; rebuild it")
+        _lib = lib
+        return lib
+
+
+def library_available() -> bool:
+    try:
+        load_library()
+    except NativeLibraryUnavailable:
+        return False
+    return True
+
+
+def status_reason(status: int) -> str:
+    return load_library().ll_status_reason(int(status)).decode()
+
+
+def _check(status: int) -> None:
+    if status != LL_OK:
+        lib = load_library()
+        raise NativeCallError(
+            status, lib.ll_status_reason(status).decode(), lib.ll_last_error().decode()
+        )
+
+
+def pointer_table(pointers: list[int]) -> ctypes.Array:
+    """Host array of device pointers for the per-layer tables."""
+
+    table = (ctypes.c_void_p * len(pointers))()
+    for index, value in enumerate(pointers):
+        table[index] = int(value)
+    return table
+
+
+def kv_link(args: LinkArgs, stream: int) -> None:
+    args.struct_size = ctypes.sizeof(LinkArgs)
+    _check(load_library().ll_kv_link(ctypes.byref(args), _ptr(int(stream))))
+
+
+def kv_link_describe(args: LinkArgs) -> LaunchInfo:
+    args.struct_size = ctypes.sizeof(LinkArgs)
+    info = LaunchInfo()
+    _check(load_library().ll_kv_link_describe(ctypes.byref(args), ctypes.byref(info)))
+    return info
+
+
+def kv_scatter_rows(args: ScatterArgs, stream: int) -> None:
+    args.struct_size = ctypes.sizeof(ScatterArgs)
+    _check(load_library().ll_kv_scatter_rows(ctypes.byref(args), _ptr(int(stream))))

@@ -1,0 +1,668 @@
+"""HIP LegoLink KV link operator: gather, RoPE delta re-rotation and scatter.
+
+Drop-in counterpart of ``patched_sglang_files/python/sglang/srt/legolink_triton.py``:
+the same public names, keyword arguments, eligibility reasons, exception types
+and traffic model, backed by the hand-written gfx950 kernels in
+``liblegolink_kv.so`` instead of a Triton JIT kernel.
+
+Two entries go beyond the reference operator:
+
+* ``fused_kv_link_layers_inplace`` links every layer of the pool in one launch
+  (the reference calls its operator once per layer, pic_runtime.py:5168-5208);
+* ``scatter_kv_rows_inplace`` writes repaired boundary rows into the pool
+  (the repair pass's K/V write, flashinfer_sparse_repair.py:2235-2239).
+
+Every tensor stays owned by the caller; nothing here allocates device memory.
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+import torch
+
+from . import _native
+
+# Reason reported when the HIP library cannot be loaded; the reference reports
+# "triton_not_installed" in the same position (legolink_triton.py:174-175).
+NATIVE_UNAVAILABLE_REASON = "hip_kv_link_not_built"
+
+
+@dataclass(frozen=True)
+class LegoLinkFusionEligibility:
+    supported: bool
+    reason: str
+
+
+@dataclass(frozen=True)
+class LegoLinkLaunchConfig:
+    block_size: int
+    num_warps: int
+    num_stages: int
+    source: str
+
+
+_KV_DTYPES = {torch.float16: _native.DTYPE_FLOAT16, torch.bfloat16: _native.DTYPE_BFLOAT16}
+_CACHE_DTYPES = {
+    torch.float16: _native.DTYPE_FLOAT16,
+    torch.bfloat16: _native.DTYPE_BFLOAT16,
+    torch.float32: _native.DTYPE_FLOAT32,
+}
+_INDEX_DTYPES = {torch.int32: _native.DTYPE_INT32, torch.int64: _native.DTYPE_INT64}
+
+
+def resolve_fused_kv_launch_config(
+    *,
+    work_items: int,
+    device: torch.device | None = None,
+    capability: tuple[int, int] | None = None,
+    block_size: int | None = None,
+    num_warps: int | None = None,
+    num_stages: int | None = None,
+) -> LegoLinkLaunchConfig:
+    """Resolve and validate the launch keywords (legolink_triton.py:38-99).
+
+    Same validation rules, defaults and environment overrides
+    (``SGLANG_PIC_TRITON_BLOCK_SIZE`` / ``_NUM_WARPS`` / ``_NUM_STAGES``) as the
+    reference.  On gfx950 ``num_warps`` is the number of 64-lane waves per
+    workgroup; ``block_size`` and ``num_stages`` are validated and recorded but
+    do not shape the HIP kernels (their work unit is a 16-byte row chunk and
+    they keep four layers of loads in flight per lane).
+    """
+
+    del work_items, device, capability  # one gfx950 default for every shape
+    defaults = (256, 4, 2)
+    source = "gfx950_default"
+    env_values = (
+        os.getenv("SGLANG_PIC_TRITON_BLOCK_SIZE"),
+        os.getenv("SGLANG_PIC_TRITON_NUM_WARPS"),
+        os.getenv("SGLANG_PIC_TRITON_NUM_STAGES"),
+    )
+    explicit_values = (block_size, num_warps, num_stages)
+    resolved = []
+    overridden = False
+    for explicit, environment, default in zip(explicit_values, env_values, defaults, strict=True):
+        if explicit is not None:
+            resolved.append(int(explicit))
+            overridden = True
+        elif environment not in (None, ""):
+            resolved.append(int(environment))
+            overridden = True
+        else:
+            resolved.append(default)
+    if overridden:
+        source = "explicit_or_environment_override"
+    resolved_block_size, resolved_num_warps, resolved_num_stages = resolved
+    if (
+        resolved_block_size <= 0
+        or resolved_block_size > 1024
+        or resolved_block_size & (resolved_block_size - 1)
+    ):
+        raise ValueError("block_size must be a power of two between 1 and 1024")
+    if resolved_num_warps not in (1, 2, 4, 8):
+        raise ValueError("num_warps must be one of 1, 2, 4, or 8")
+    if not 1 <= resolved_num_stages <= 5:
+        raise ValueError("num_stages must be between 1 and 5")
+    return LegoLinkLaunchConfig(resolved_block_size, resolved_num_warps, resolved_num_stages, source)
+
+
+def hip_legolink_available() -> bool:
+    """True when the HIP library loads and a ROCm device is visible."""
+
+    return _native.library_available() and torch.cuda.is_available()
+
+
+# Name kept for callers written against the reference module.
+triton_legolink_available = hip_legolink_available
+
+
+def estimate_kv_traffic_bytes(
+    *,
+    token_count: int,
+    key_row_bytes: int,
+    value_row_bytes: int,
+    remapped_token_count: int,
+    repair_token_count: int = 0,
+) -> dict[str, int | float]:
+    """Lower-bound HBM traffic of the eager torch path and of the fused link.
+
+    Same model and keys as legolink_triton.py:107-156: the fused link reads and
+    writes K and V of every copied (non-repair) token once; position maps and
+    the cos/sin table are excluded.
+    """
+
+    token_count = max(int(token_count), 0)
+    remapped_token_count = max(min(int(remapped_token_count), token_count), 0)
+    repair_token_count = max(min(int(repair_token_count), token_count), 0)
+    copied_token_count = token_count - repair_token_count
+    key_bytes = token_count * max(int(key_row_bytes), 0)
+    value_bytes = token_count * max(int(value_row_bytes), 0)
+    remapped_key_bytes = remapped_token_count * max(int(key_row_bytes), 0)
+    copied_key_bytes = copied_token_count * max(int(key_row_bytes), 0)
+    copied_value_bytes = copied_token_count * max(int(value_row_bytes), 0)
+    # Eager torch gathers K/V, materialises the remapped K, and reads those
+    # temporaries again for index_copy_.
+    torch_read_bytes = 2 * (key_bytes + value_bytes) + remapped_key_bytes
+    torch_write_bytes = 2 * (key_bytes + value_bytes) + remapped_key_bytes
+    torch_bytes = torch_read_bytes + torch_write_bytes
+    fused_read_bytes = copied_key_bytes + copied_value_bytes
+    fused_write_bytes = copied_key_bytes + copied_value_bytes
+    fused_bytes = fused_read_bytes + fused_write_bytes
+    reduction = 1.0 - (fused_bytes / torch_bytes) if torch_bytes else 0.0
+    return {
+        "torch_lower_bound_bytes": torch_bytes,
+        "triton_lower_bound_bytes": fused_bytes,
+        "torch_estimated_hbm_read_bytes": torch_read_bytes,
+        "torch_estimated_hbm_write_bytes": torch_write_bytes,
+        "triton_estimated_hbm_read_bytes": fused_read_bytes,
+        "triton_estimated_hbm_write_bytes": fused_write_bytes,
+        "torch_estimated_hbm_traffic_bytes": torch_bytes,
+        "triton_estimated_hbm_traffic_bytes": fused_bytes,
+        "estimated_reduction_ratio": reduction,
+        "copied_token_count": copied_token_count,
+        "repair_token_count": repair_token_count,
+    }
+
+
+def _eligibility(
+    key_buffers: Sequence[torch.Tensor],
+    value_buffers: Sequence[torch.Tensor],
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    rotary_dim: int,
+    repair_mask: torch.Tensor | None,
+) -> LegoLinkFusionEligibility:
+    """The reference's checks in the reference's order (legolink_triton.py:159-247),
+    applied to every layer, followed by the checks the raw-pointer kernels need."""
+
+    if not _native.library_available():
+        return LegoLinkFusionEligibility(False, NATIVE_UNAVAILABLE_REASON)
+    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+    tensors = (
+        *key_buffers,
+        *value_buffers,
+        source_slots,
+        destination_slots,
+        local_positions,
+        global_positions,
+        cos_sin_cache,
+    )
+    if not all(tensor.is_cuda for tensor in tensors):
+        return LegoLinkFusionEligibility(False, "cuda_tensors_required")
+    for key, value in zip(key_buffers, value_buffers, strict=True):
+        if key.ndim != 3 or value.ndim != 3:
+            return LegoLinkFusionEligibility(False, "mha_3d_kv_buffers_required")
+        if key.shape[:2] != value.shape[:2] or key.shape != key_buffer.shape or (
+            value.shape != value_buffer.shape
+        ):
+            return LegoLinkFusionEligibility(False, "kv_head_layout_mismatch")
+        if key.dtype != value.dtype or key.dtype != key_buffer.dtype:
+            return LegoLinkFusionEligibility(False, "kv_dtype_mismatch")
+    if key_buffer.dtype not in (torch.float16, torch.bfloat16):
+        return LegoLinkFusionEligibility(False, "fp16_or_bf16_required")
+    if not all(buffer.is_contiguous() for buffer in (*key_buffers, *value_buffers)):
+        return LegoLinkFusionEligibility(False, "contiguous_kv_buffers_required")
+    key_head_dim = int(key_buffer.shape[-1])
+    value_head_dim = int(value_buffer.shape[-1])
+    if key_head_dim <= 0 or value_head_dim <= 0 or key_head_dim > 256 or value_head_dim > 256:
+        return LegoLinkFusionEligibility(False, "head_dimension_out_of_range")
+    token_count = int(source_slots.numel())
+    if token_count == 0:
+        return LegoLinkFusionEligibility(False, "empty_link")
+    if any(
+        int(tensor.numel()) != token_count
+        for tensor in (destination_slots, local_positions, global_positions)
+    ):
+        return LegoLinkFusionEligibility(False, "token_map_length_mismatch")
+    if repair_mask is not None:
+        if not repair_mask.is_cuda:
+            return LegoLinkFusionEligibility(False, "cuda_repair_mask_required")
+        if int(repair_mask.numel()) != token_count:
+            return LegoLinkFusionEligibility(False, "repair_mask_length_mismatch")
+        if repair_mask.dtype not in (torch.bool, torch.uint8):
+            return LegoLinkFusionEligibility(False, "boolean_repair_mask_required")
+        if not repair_mask.is_contiguous():
+            return LegoLinkFusionEligibility(False, "contiguous_repair_mask_required")
+    if any(
+        tensor.dtype not in (torch.int32, torch.int64)
+        for tensor in (source_slots, destination_slots, local_positions, global_positions)
+    ):
+        return LegoLinkFusionEligibility(False, "integer_token_maps_required")
+    rotary_dim = int(rotary_dim)
+    if rotary_dim <= 0 or rotary_dim % 2:
+        return LegoLinkFusionEligibility(False, "even_rotary_dim_required")
+    if rotary_dim > key_head_dim:
+        return LegoLinkFusionEligibility(False, "rotary_dim_exceeds_head_dim")
+    if cos_sin_cache.ndim != 2 or int(cos_sin_cache.shape[1]) < rotary_dim:
+        return LegoLinkFusionEligibility(False, "unsupported_cos_sin_cache")
+    if cos_sin_cache.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return LegoLinkFusionEligibility(False, "unsupported_cos_sin_dtype")
+    # The kernels read the token maps as dense arrays on the pool's device.
+    device = key_buffer.device
+    if any(
+        tensor.device != device
+        for tensor in (*tensors, *(() if repair_mask is None else (repair_mask,)))
+    ):
+        return LegoLinkFusionEligibility(False, "same_device_required")
+    if not all(
+        tensor.is_contiguous()
+        for tensor in (source_slots, destination_slots, local_positions, global_positions)
+    ):
+        return LegoLinkFusionEligibility(False, "contiguous_token_maps_required")
+    return LegoLinkFusionEligibility(True, "supported")
+
+
+def check_fused_kv_link_eligibility(
+    *,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    rotary_dim: int,
+    repair_mask: torch.Tensor | None = None,
+) -> LegoLinkFusionEligibility:
+    """Can the HIP link run on these tensors? (legolink_triton.py:159-247)."""
+
+    return _eligibility(
+        [key_buffer],
+        [value_buffer],
+        source_slots,
+        destination_slots,
+        local_positions,
+        global_positions,
+        cos_sin_cache,
+        rotary_dim,
+        repair_mask,
+    )
+
+
+def _validate_index_ranges(
+    num_slots: int,
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cache_rows: int,
+    prefix_token_count: int,
+) -> None:
+    """Optional host check (synchronises): the kernels skip out-of-range rows."""
+
+    for name, tensor, limit in (
+        ("source_slots", source_slots, num_slots),
+        ("destination_slots", destination_slots, num_slots),
+        ("local_positions", local_positions[prefix_token_count:], cache_rows),
+        ("global_positions", global_positions[prefix_token_count:], cache_rows),
+    ):
+        if tensor.numel() and (int(tensor.min()) < 0 or int(tensor.max()) >= limit):
+            raise IndexError(f"{name} has values outside [0, {limit})")
+
+
+def _link_args(
+    key_buffers: Sequence[torch.Tensor],
+    value_buffers: Sequence[torch.Tensor],
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    prefix_token_count: int,
+    rotary_dim: int,
+    is_neox_style: bool,
+    repair_mask: torch.Tensor | None,
+    waves_per_block: int,
+    layers_per_wave: int,
+    kernel: int,
+) -> tuple[_native.LinkArgs, tuple[Any, ...]]:
+    key_table = _native.pointer_table([buffer.data_ptr() for buffer in key_buffers])
+    value_table = _native.pointer_table([buffer.data_ptr() for buffer in value_buffers])
+    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+    args = _native.LinkArgs()
+    args.num_layers = len(key_buffers)
+    args.key_layers = ctypes_address(key_table)
+    args.value_layers = ctypes_address(value_table)
+    args.num_slots = int(key_buffer.shape[0])
+    args.num_heads = int(key_buffer.shape[1])
+    args.key_head_dim = int(key_buffer.shape[2])
+    args.value_head_dim = int(value_buffer.shape[2])
+    args.kv_dtype = _KV_DTYPES[key_buffer.dtype]
+    args.num_tokens = int(source_slots.numel())
+    args.source_slots = source_slots.data_ptr()
+    args.source_slots_dtype = _INDEX_DTYPES[source_slots.dtype]
+    args.destination_slots = destination_slots.data_ptr()
+    args.destination_slots_dtype = _INDEX_DTYPES[destination_slots.dtype]
+    args.local_positions = local_positions.data_ptr()
+    args.local_positions_dtype = _INDEX_DTYPES[local_positions.dtype]
+    args.global_positions = global_positions.data_ptr()
+    args.global_positions_dtype = _INDEX_DTYPES[global_positions.dtype]
+    args.repair_mask = None if repair_mask is None else repair_mask.data_ptr()
+    args.repair_mask_dtype = _native.DTYPE_UINT8
+    args.cos_sin_cache = cos_sin_cache.data_ptr()
+    args.cos_sin_dtype = _CACHE_DTYPES[cos_sin_cache.dtype]
+    args.cos_sin_rows = int(cos_sin_cache.shape[0])
+    args.cos_sin_cols = int(cos_sin_cache.shape[1])
+    args.cos_sin_stride_row = int(cos_sin_cache.stride(0))
+    args.cos_sin_stride_col = int(cos_sin_cache.stride(1))
+    args.rotary_dim = int(rotary_dim)
+    args.is_neox_style = 1 if is_neox_style else 0
+    args.prefix_token_count = int(prefix_token_count)
+    args.kernel = int(kernel)
+    args.waves_per_block = int(waves_per_block)
+    args.layers_per_wave = int(layers_per_wave)
+    # The pointer tables must outlive the call.
+    return args, (key_table, value_table)
+
+
+def ctypes_address(array: Any) -> int:
+    import ctypes
+
+    return ctypes.addressof(array)
+
+
+def _raise_unavailable(reason: str) -> None:
+    raise RuntimeError(f"HIP LegoLink fusion is unavailable: {reason}")
+
+
+def fused_kv_link_layers_inplace(
+    *,
+    key_buffers: Sequence[torch.Tensor],
+    value_buffers: Sequence[torch.Tensor],
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    prefix_token_count: int,
+    rotary_dim: int,
+    is_neox_style: bool,
+    repair_mask: torch.Tensor | None = None,
+    block_size: int | None = None,
+    num_warps: int | None = None,
+    num_stages: int | None = None,
+    layers_per_wave: int = 0,
+    kernel: int = _native.KERNEL_AUTO,
+    validate_indices: bool = False,
+) -> None:
+    """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
+    64 layers.  Per layer the result equals ``fused_kv_link_inplace``."""
+
+    key_buffers = list(key_buffers)
+    value_buffers = list(value_buffers)
+    if not key_buffers or len(key_buffers) != len(value_buffers):
+        raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
+    eligibility = _eligibility(
+        key_buffers,
+        value_buffers,
+        source_slots,
+        destination_slots,
+        local_positions,
+        global_positions,
+        cos_sin_cache,
+        rotary_dim,
+        repair_mask,
+    )
+    if not eligibility.supported:
+        _raise_unavailable(eligibility.reason)
+    if not 0 <= int(prefix_token_count) <= int(source_slots.numel()):
+        raise ValueError("prefix_token_count is outside the linked token range")
+    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+    work_items = int(key_buffer.shape[1]) * (
+        int(rotary_dim) // 2
+        + int(key_buffer.shape[2])
+        - int(rotary_dim)
+        + int(value_buffer.shape[2])
+    )
+    launch_config = resolve_fused_kv_launch_config(
+        work_items=work_items,
+        device=key_buffer.device,
+        block_size=block_size,
+        num_warps=num_warps,
+        num_stages=num_stages,
+    )
+    if validate_indices:
+        _validate_index_ranges(
+            int(key_buffer.shape[0]),
+            source_slots,
+            destination_slots,
+            local_positions,
+            global_positions,
+            int(cos_sin_cache.shape[0]),
+            int(prefix_token_count),
+        )
+    if repair_mask is not None and repair_mask.dtype == torch.bool:
+        repair_mask = repair_mask.view(torch.uint8)
+    args, keepalive = _link_args(
+        key_buffers,
+        value_buffers,
+        source_slots,
+        destination_slots,
+        local_positions,
+        global_positions,
+        cos_sin_cache,
+        prefix_token_count,
+        rotary_dim,
+        is_neox_style,
+        repair_mask,
+        launch_config.num_warps,
+        layers_per_wave,
+        kernel,
+    )
+    with torch.cuda.device(key_buffer.device):
+        stream = torch.cuda.current_stream(key_buffer.device).cuda_stream
+        try:
+            _native.kv_link(args, stream)
+        except _native.NativeCallError as error:
+            if error.status == _native.LL_ERR_PREFIX_OUT_OF_RANGE:
+                raise ValueError("prefix_token_count is outside the linked token range") from error
+            if error.status in (_native.LL_ERR_LAUNCH_CONFIG, _native.LL_ERR_UNSUPPORTED_KERNEL):
+                raise ValueError(str(error)) from error
+            if error.status == _native.LL_ERR_HIP:
+                raise RuntimeError(f"HIP LegoLink link launch failed: {error.detail}") from error
+            _raise_unavailable(error.reason)
+    del keepalive
+
+
+def fused_kv_link_inplace(
+    *,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    prefix_token_count: int,
+    rotary_dim: int,
+    is_neox_style: bool,
+    repair_mask: torch.Tensor | None = None,
+    block_size: int | None = None,
+    num_warps: int | None = None,
+    num_stages: int | None = None,
+) -> None:
+    """Link one layer in place (legolink_triton.py:550-645).
+
+    For every linked token t (skipped when ``repair_mask[t]`` is set):
+    V[dst[t]] = V[src[t]]; K[dst[t]] = K[src[t]] for t < prefix_token_count,
+    otherwise K[src[t]] re-rotated from ``local_positions[t]`` to
+    ``global_positions[t]``.  Raises RuntimeError with the eligibility reason
+    and ValueError for a bad prefix or launch configuration, like the reference.
+    """
+
+    fused_kv_link_layers_inplace(
+        key_buffers=[key_buffer],
+        value_buffers=[value_buffer],
+        source_slots=source_slots,
+        destination_slots=destination_slots,
+        local_positions=local_positions,
+        global_positions=global_positions,
+        cos_sin_cache=cos_sin_cache,
+        prefix_token_count=prefix_token_count,
+        rotary_dim=rotary_dim,
+        is_neox_style=is_neox_style,
+        repair_mask=repair_mask,
+        block_size=block_size,
+        num_warps=num_warps,
+        num_stages=num_stages,
+    )
+
+
+def describe_link_launch(
+    *,
+    key_buffers: Sequence[torch.Tensor],
+    value_buffers: Sequence[torch.Tensor],
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    local_positions: torch.Tensor,
+    global_positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    prefix_token_count: int,
+    rotary_dim: int,
+    is_neox_style: bool,
+    repair_mask: torch.Tensor | None = None,
+    num_warps: int = 4,
+    layers_per_wave: int = 0,
+    kernel: int = _native.KERNEL_AUTO,
+) -> dict[str, int]:
+    """Kernel and launch shape the link would use (no GPU work, no device needed)."""
+
+    if repair_mask is not None and repair_mask.dtype == torch.bool:
+        repair_mask = repair_mask.view(torch.uint8)
+    args, keepalive = _link_args(
+        list(key_buffers),
+        list(value_buffers),
+        source_slots,
+        destination_slots,
+        local_positions,
+        global_positions,
+        cos_sin_cache,
+        prefix_token_count,
+        rotary_dim,
+        is_neox_style,
+        repair_mask,
+        num_warps,
+        layers_per_wave,
+        kernel,
+    )
+    info = _native.kv_link_describe(args)
+    del keepalive
+    return {
+        "kernel": "vector" if info.kernel == _native.KERNEL_VECTOR else "generic",
+        "launches": int(info.launches),
+        "grid_x": int(info.grid_x),
+        "grid_y": int(info.grid_y),
+        "block_threads": int(info.block_threads),
+        "layers_per_wave": int(info.layers_per_wave),
+    }
+
+
+def scatter_kv_rows_inplace(
+    *,
+    key_buffers: Sequence[torch.Tensor],
+    value_buffers: Sequence[torch.Tensor],
+    destination_slots: torch.Tensor,
+    repaired_keys: torch.Tensor,
+    repaired_values: torch.Tensor,
+    num_warps: int = 4,
+) -> None:
+    """Write repaired rows: K_l[destination_slots[r]] = repaired_keys[l, r] (and V).
+
+    ``repaired_keys`` is [num_layers, rows, heads, key_head_dim] (or
+    [rows, heads, key_head_dim] for a single layer) with dense rows; the layer
+    stride may be anything.  Same semantics as write_repaired_kv
+    (tests/pic/reference/repair_reference.py:14-25) applied to every layer.
+    """
+
+    key_buffers = list(key_buffers)
+    value_buffers = list(value_buffers)
+    if not key_buffers or len(key_buffers) != len(value_buffers):
+        raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
+    if repaired_keys.ndim == 3:
+        repaired_keys = repaired_keys.unsqueeze(0)
+    if repaired_values.ndim == 3:
+        repaired_values = repaired_values.unsqueeze(0)
+    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+    layers = len(key_buffers)
+    rows = int(destination_slots.numel())
+    if not _native.library_available():
+        _raise_unavailable(NATIVE_UNAVAILABLE_REASON)
+    tensors = (*key_buffers, *value_buffers, destination_slots, repaired_keys, repaired_values)
+    if not all(tensor.is_cuda and tensor.device == key_buffer.device for tensor in tensors):
+        _raise_unavailable("cuda_tensors_required")
+    for key, value in zip(key_buffers, value_buffers, strict=True):
+        if key.ndim != 3 or value.ndim != 3:
+            _raise_unavailable("mha_3d_kv_buffers_required")
+        if key.shape != key_buffer.shape or value.shape != value_buffer.shape or (
+            key.shape[:2] != value.shape[:2]
+        ):
+            _raise_unavailable("kv_head_layout_mismatch")
+        if key.dtype != key_buffer.dtype or value.dtype != key_buffer.dtype:
+            _raise_unavailable("kv_dtype_mismatch")
+        if not key.is_contiguous() or not value.is_contiguous():
+            _raise_unavailable("contiguous_kv_buffers_required")
+    if key_buffer.dtype not in _KV_DTYPES:
+        _raise_unavailable("fp16_or_bf16_required")
+    if destination_slots.dtype not in _INDEX_DTYPES or not destination_slots.is_contiguous():
+        _raise_unavailable("integer_token_maps_required")
+    expected_k = (layers, rows, int(key_buffer.shape[1]), int(key_buffer.shape[2]))
+    expected_v = (layers, rows, int(value_buffer.shape[1]), int(value_buffer.shape[2]))
+    if tuple(repaired_keys.shape) != expected_k or tuple(repaired_values.shape) != expected_v:
+        raise ValueError(
+            f"repaired rows must be {expected_k} / {expected_v}, got "
+            f"{tuple(repaired_keys.shape)} / {tuple(repaired_values.shape)}"
+        )
+    if repaired_keys.dtype != key_buffer.dtype or repaired_values.dtype != key_buffer.dtype:
+        _raise_unavailable("kv_dtype_mismatch")
+    if not repaired_keys[0].is_contiguous() or not repaired_values[0].is_contiguous():
+        raise ValueError("repaired rows of each layer must be dense")
+    if rows == 0:
+        return
+    key_table = _native.pointer_table([buffer.data_ptr() for buffer in key_buffers])
+    value_table = _native.pointer_table([buffer.data_ptr() for buffer in value_buffers])
+    args = _native.ScatterArgs()
+    args.num_layers = layers
+    args.key_layers = ctypes_address(key_table)
+    args.value_layers = ctypes_address(value_table)
+    args.num_slots = int(key_buffer.shape[0])
+    args.num_heads = int(key_buffer.shape[1])
+    args.key_head_dim = int(key_buffer.shape[2])
+    args.value_head_dim = int(value_buffer.shape[2])
+    args.kv_dtype = _KV_DTYPES[key_buffer.dtype]
+    args.num_rows = rows
+    args.destination_slots = destination_slots.data_ptr()
+    args.destination_slots_dtype = _INDEX_DTYPES[destination_slots.dtype]
+    args.repaired_key = repaired_keys.data_ptr()
+    args.repaired_key_layer_stride = int(repaired_keys.stride(0)) if layers > 1 else 0
+    args.repaired_value = repaired_values.data_ptr()
+    args.repaired_value_layer_stride = int(repaired_values.stride(0)) if layers > 1 else 0
+    args.waves_per_block = int(num_warps)
+    with torch.cuda.device(key_buffer.device):
+        stream = torch.cuda.current_stream(key_buffer.device).cuda_stream
+        try:
+            _native.kv_scatter_rows(args, stream)
+        except _native.NativeCallError as error:
+            if error.status == _native.LL_ERR_HIP:
+                raise RuntimeError(f"HIP LegoLink scatter launch failed: {error.detail}") from error
+            _raise_unavailable(error.reason)
+    del key_table, value_table
+
+
+def fusion_metadata(**kwargs: Any) -> dict[str, Any]:
+    """Bounded metadata for trace records (legolink_triton.py:648-660)."""
+
+    boundary_repair_aware = bool(kwargs.get("boundary_repair_aware", False))
+    return {
+        "implementation": (
+            "hip_fused_gather_rope_scatter_boundary_repair_aware"
+            if boundary_repair_aware
+            else "hip_fused_gather_rope_scatter"
+        ),
+        "kernel_launches_per_layer": 1,
+        **kwargs,
+    }

@@ -1,0 +1,321 @@
+"""GPU parity of the HIP link and repair-row scatter against the CPU oracle.
+
+Bar: bit-exact on every element (V and copied K are bit copies; re-rotated K
+follows the fused rounding exactly, which implies <= 1 bf16 ulp).
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from legolink_amd import _native, kv_link
+from legolink_amd.rope import build_cos_sin_cache
+from legolink_amd.workloads import make_workload
+from oracle import kv_link_oracle as ko
+from tests import rope_math
+from tests.gpu_helpers import TORCH_TO_CODE, bits, cache_host, check_workload, make_pool, report
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+AUTO, VECTOR, GENERIC = _native.KERNEL_AUTO, _native.KERNEL_VECTOR, _native.KERNEL_GENERIC
+
+# name, kv dtype, cache dtype, heads, key dim, value dim, rotary dim, neox, kernel, index dtype,
+# prefix, mask fraction, layers, tokens, expected kernel
+CASES = [
+    ("qwen7b_vec", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 0.0, 3, 200, "vector"),
+    ("qwen7b_vec_prefix_mask", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 37, 0.2, 3, 200, "vector"),
+    ("qwen7b_generic_prefix_mask", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, GENERIC, torch.int64, 37, 0.2, 3, 200, "generic"),
+    ("qwen3_32b_heads8", torch.bfloat16, torch.float32, 8, 128, 128, 128, True, VECTOR, torch.int64, 5, 0.1, 2, 150, "vector"),
+    ("tp_shard_one_head_int32", torch.bfloat16, torch.float32, 1, 128, 128, 128, True, AUTO, torch.int32, 3, 0.1, 3, 333, "vector"),
+    ("three_heads_straddling_waves", torch.bfloat16, torch.float32, 3, 128, 128, 128, True, AUTO, torch.int64, 0, 0.1, 2, 171, "vector"),
+    ("head_dim_64", torch.bfloat16, torch.float32, 2, 64, 64, 64, True, AUTO, torch.int64, 0, 0.1, 2, 190, "vector"),
+    ("head_dim_256", torch.bfloat16, torch.float32, 2, 256, 256, 256, True, AUTO, torch.int64, 0, 0.1, 2, 90, "vector"),
+    ("head_dim_32", torch.bfloat16, torch.float32, 4, 32, 32, 32, True, AUTO, torch.int64, 0, 0.1, 2, 150, "vector"),
+    ("gptj_vec", torch.bfloat16, torch.float32, 4, 128, 128, 128, False, AUTO, torch.int64, 10, 0.1, 2, 150, "vector"),
+    ("gptj_generic", torch.bfloat16, torch.float32, 4, 128, 128, 128, False, GENERIC, torch.int64, 10, 0.1, 2, 150, "generic"),
+    ("fp16_vec", torch.float16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 0.1, 2, 150, "vector"),
+    ("fp16_generic", torch.float16, torch.float32, 4, 128, 128, 128, True, GENERIC, torch.int64, 0, 0.1, 2, 150, "generic"),
+    ("fp16_gptj_d64", torch.float16, torch.float32, 2, 64, 64, 64, False, AUTO, torch.int32, 0, 0.1, 2, 150, "vector"),
+    ("bf16_key_bf16_cache", torch.bfloat16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
+    ("bf16_key_fp16_cache", torch.bfloat16, torch.float16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
+    ("fp16_key_bf16_cache", torch.float16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
+    ("partial_rotary", torch.bfloat16, torch.float32, 4, 128, 128, 64, True, AUTO, torch.int64, 0, 0.1, 2, 150, "generic"),
+    ("value_dim_differs", torch.bfloat16, torch.float32, 2, 128, 64, 128, True, AUTO, torch.int64, 0, 0.1, 2, 150, "generic"),
+    ("odd_dims_gptj", torch.bfloat16, torch.float32, 3, 40, 24, 16, False, AUTO, torch.int64, 2, 0.1, 2, 150, "generic"),
+    ("prefix_is_everything", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 150, 0.0, 2, 150, "vector"),
+    ("all_masked", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 1.0, 2, 150, "vector"),
+    ("single_token", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 0.0, 2, 1, "vector"),
+    ("seventy_layers", torch.bfloat16, torch.float32, 2, 128, 128, 128, True, AUTO, torch.int64, 3, 0.1, 70, 64, "vector"),
+]
+
+
+def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense"):
+    (name, dtype, cache_dtype, heads, kdim, vdim, rotary, neox, kernel, index_dtype, prefix,
+     mask_fraction, layers, tokens, expected_kernel) = case
+    report(f"case {name}: layers={layers} heads={heads} kdim={kdim} vdim={vdim} rotary={rotary} "
+           f"neox={neox} tokens={tokens} kernel={kernel}")
+    slots = 2 * tokens + 41
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(slots)
+    src_np, dst_np = perm[:tokens], perm[tokens : 2 * tokens]
+    max_position = 70_000
+    local_np = rng.integers(0, max_position, size=tokens)
+    global_np = rng.integers(0, max_position, size=tokens)
+    mask_np = (rng.random(tokens) < mask_fraction).astype(np.uint8)
+    keys, values = make_pool(layers, slots, heads, kdim, vdim, dtype, device, seed)
+    table = build_cos_sin_cache(max_position, rotary, theta=1e6).to(cache_dtype)
+    if cache_layout == "strided":
+        wide = torch.zeros(max_position, 2 * rotary + 4, dtype=cache_dtype)
+        wide[:, 1 : 1 + 2 * rotary : 2] = table
+        table_dev = wide.to(device)[:, 1 : 1 + 2 * rotary : 2]
+        assert table_dev.stride(1) == 2
+    else:
+        table_dev = table.to(device)
+    maps = [torch.from_numpy(a).to(index_dtype).to(device) for a in (src_np, dst_np, local_np, global_np)]
+    mask = torch.from_numpy(mask_np).to(device).to(mask_dtype) if mask_fraction > 0 else None
+    key_np = [bits(k) for k in keys]
+    value_np = [bits(v) for v in values]
+    expected_k, expected_v = ko.link_pool(
+        key_np, value_np, src_np, dst_np, local_np, global_np, cache_host(table),
+        key_dtype=TORCH_TO_CODE[dtype], cache_dtype=TORCH_TO_CODE[cache_dtype],
+        rotary_dim=rotary, neox=neox, prefix=prefix, repair_mask=mask_np if mask is not None else None,
+    )
+    launch = kv_link.describe_link_launch(
+        key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+        local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
+        prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
+        kernel=kernel,
+    )
+    assert launch["kernel"] == expected_kernel, launch
+    kv_link.fused_kv_link_layers_inplace(
+        key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+        local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
+        prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
+        kernel=kernel,
+    )
+    torch.cuda.synchronize(device)
+    for layer in range(layers):
+        got_k, got_v = bits(keys[layer]), bits(values[layer])
+        if dtype == torch.float16:
+            # NaN payloads are not part of the contract; inputs here hold none.
+            assert not np.isnan(got_k.view(np.float16)).any()
+        assert np.array_equal(got_v, expected_v[layer]), f"{name}: V layer {layer}"
+        diff = np.argwhere(got_k != expected_k[layer])
+        assert diff.size == 0, f"{name}: K layer {layer} differs at {diff[:5].tolist()}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])
+def test_link_matches_oracle(gpu_device, case):
+    _run_case(gpu_device, case)
+
+
+def test_bool_mask_and_strided_cache(gpu_device):
+    case = ("bool_mask_strided_cache", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO,
+            torch.int64, 7, 0.3, 2, 160, "generic")
+    _run_case(gpu_device, case, mask_dtype=torch.bool, cache_layout="strided")
+
+
+def test_per_layer_entry_equals_all_layer_entry(gpu_device):
+    layers, slots, tokens = 4, 700, 300
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(slots)
+    src = torch.from_numpy(perm[:tokens]).to(gpu_device)
+    dst = torch.from_numpy(perm[tokens : 2 * tokens]).to(gpu_device)
+    local = torch.from_numpy(rng.integers(0, 4096, size=tokens)).to(gpu_device)
+    glob = torch.from_numpy(rng.integers(0, 4096, size=tokens)).to(gpu_device)
+    table = build_cos_sin_cache(4096, 128).to(gpu_device)
+    keys_a, values_a = make_pool(layers, slots, 4, 128, 128, torch.bfloat16, gpu_device, 5)
+    keys_b = [k.clone() for k in keys_a]
+    values_b = [v.clone() for v in values_a]
+    for key, value in zip(keys_a, values_a):
+        kv_link.fused_kv_link_inplace(
+            key_buffer=key, value_buffer=value, source_slots=src, destination_slots=dst,
+            local_positions=local, global_positions=glob, cos_sin_cache=table,
+            prefix_token_count=11, rotary_dim=128, is_neox_style=True,
+        )
+    kv_link.fused_kv_link_layers_inplace(
+        key_buffers=keys_b, value_buffers=values_b, source_slots=src, destination_slots=dst,
+        local_positions=local, global_positions=glob, cos_sin_cache=table,
+        prefix_token_count=11, rotary_dim=128, is_neox_style=True,
+    )
+    torch.cuda.synchronize(gpu_device)
+    for a, b in zip(keys_a + values_a, keys_b + values_b):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_out_of_range_rows_are_skipped_or_rejected(gpu_device):
+    slots, tokens = 100, 40
+    keys, values = make_pool(2, slots, 4, 128, 128, torch.bfloat16, gpu_device, 9)
+    rng = np.random.default_rng(9)
+    perm = rng.permutation(slots)
+    src_np, dst_np = perm[:tokens].copy(), perm[tokens : 2 * tokens].copy()
+    local_np = rng.integers(0, 512, size=tokens)
+    global_np = rng.integers(0, 512, size=tokens)
+    src_np[3] = slots + 5          # source outside the pool
+    dst_np[7] = -1                 # negative destination
+    global_np[11] = 512            # position outside the table
+    table = build_cos_sin_cache(512, 128)
+    bad = {3, 7, 11}
+    good = np.array([t for t in range(tokens) if t not in bad])
+    expected_k, expected_v = ko.link_pool(
+        [bits(k) for k in keys], [bits(v) for v in values], src_np[good], dst_np[good],
+        local_np[good], global_np[good], table.numpy(), key_dtype=ko.BF16, cache_dtype=ko.F32,
+        rotary_dim=128, neox=True, prefix=0,
+    )
+    maps = [torch.from_numpy(a).to(gpu_device) for a in (src_np, dst_np, local_np, global_np)]
+    with pytest.raises(IndexError):
+        kv_link.fused_kv_link_layers_inplace(
+            key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+            local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table.to(gpu_device),
+            prefix_token_count=0, rotary_dim=128, is_neox_style=True, validate_indices=True,
+        )
+    kv_link.fused_kv_link_layers_inplace(
+        key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+        local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table.to(gpu_device),
+        prefix_token_count=0, rotary_dim=128, is_neox_style=True,
+    )
+    torch.cuda.synchronize(gpu_device)
+    for layer in range(2):
+        assert np.array_equal(bits(keys[layer]), expected_k[layer])
+        assert np.array_equal(bits(values[layer]), expected_v[layer])
+
+
+def test_reference_relocation_case(gpu_device):
+    """tests/pic/test_kv_relocation.py:47-103 on the HIP op: bit-exact against the
+    oracle and within the reference's own atol 2e-2 of the fp64 relocation."""
+
+    case = GOLDEN["kv_relocation"]
+    slots, heads, rotary = case["gpu_pool_slots"], case["heads"], case["rotary_dim"]
+    generator = torch.Generator(device=gpu_device).manual_seed(20260824)
+    key = torch.randn(slots, heads, rotary, device=gpu_device, dtype=torch.bfloat16, generator=generator)
+    value = torch.randn(slots, heads, rotary, device=gpu_device, dtype=torch.bfloat16, generator=generator)
+    source = torch.tensor(case["source_slots"], device=gpu_device)
+    destination = torch.tensor(case["gpu_destination"], device=gpu_device)
+    local = torch.tensor(case["local"], device=gpu_device)
+    glob = torch.tensor(case["global"], device=gpu_device)
+    table = build_cos_sin_cache(16, rotary, theta=10_000.0)
+    # Source rows hold K rotated to their local positions (compile-time keys).
+    raw = key[source].float().cpu().numpy().astype(np.float64)
+    compiled = rope_math.rotate(raw, np.array(case["local"]), rotary, theta=10_000.0)
+    key[source] = torch.from_numpy(compiled).to(torch.bfloat16).to(gpu_device)
+    key_before, value_before = bits(key), bits(value)
+    expected_k, expected_v = ko.link_pool(
+        [key_before], [value_before], np.array(case["source_slots"]), np.array(case["gpu_destination"]),
+        np.array(case["local"]), np.array(case["global"]), table.numpy(), key_dtype=ko.BF16,
+        cache_dtype=ko.F32, rotary_dim=rotary, neox=True, prefix=0,
+    )
+    kv_link.fused_kv_link_inplace(
+        key_buffer=key, value_buffer=value, source_slots=source, destination_slots=destination,
+        local_positions=local, global_positions=glob, cos_sin_cache=table.to(gpu_device),
+        prefix_token_count=0, rotary_dim=rotary, is_neox_style=True,
+    )
+    torch.cuda.synchronize(gpu_device)
+    assert np.array_equal(bits(key), expected_k[0])
+    assert np.array_equal(bits(value), expected_v[0])
+    # The re-rotated keys are the raw keys rotated straight to the global positions.
+    truth = rope_math.rotate(raw, np.array(case["global"]), rotary, theta=10_000.0)
+    got = key[destination].float().cpu().numpy()
+    atol = case["gpu_atol"]
+    assert np.all(np.abs(got - truth) <= atol + atol * np.abs(truth))
+
+
+def test_repair_writeback_cases(gpu_device):
+    """tests/pic/test_kv_writeback.py:12-55 through the HIP scatter (bf16 pools)."""
+
+    single = GOLDEN["repair_writeback"]["single"]
+    generator = torch.Generator(device=gpu_device).manual_seed(20260824)
+    shape = (single["pool_slots"], single["heads"], single["head_dim"])
+    key = torch.randn(*shape, device=gpu_device, dtype=torch.bfloat16, generator=generator)
+    value = torch.randn(*shape, device=gpu_device, dtype=torch.bfloat16, generator=generator)
+    dest = torch.tensor(single["destination"], device=gpu_device)
+    rk = torch.randn(len(single["destination"]), *shape[1:], device=gpu_device, dtype=torch.bfloat16, generator=generator)
+    rv = torch.randn_like(rk)
+    key_before, value_before = bits(key), bits(value)
+    ek, ev = ko.scatter_rows([key_before], [value_before], np.array(single["destination"]),
+                             bits(rk)[None], bits(rv)[None])
+    kv_link.scatter_kv_rows_inplace(key_buffers=[key], value_buffers=[value], destination_slots=dest,
+                                    repaired_keys=rk, repaired_values=rv)
+    torch.cuda.synchronize(gpu_device)
+    assert np.array_equal(bits(key), ek[0]) and np.array_equal(bits(value), ev[0])
+    source = np.array(single["source_slots"])
+    assert np.array_equal(bits(key)[source], key_before[source])
+    assert np.array_equal(bits(value)[source], value_before[source])
+
+    multi = GOLDEN["repair_writeback"]["multi"]
+    key = torch.zeros(multi["pool_slots"], multi["heads"], multi["head_dim"], device=gpu_device, dtype=torch.bfloat16)
+    value = torch.zeros_like(key)
+    slots = [s for row in multi["row_slots"] for s in row]
+    rk = torch.arange(len(slots) * multi["head_dim"], dtype=torch.float32).view(len(slots), 1, multi["head_dim"]).to(torch.bfloat16).to(gpu_device)
+    rv = (rk.float() + multi["value_offset"]).to(torch.bfloat16)
+    kv_link.scatter_kv_rows_inplace(key_buffers=[key], value_buffers=[value],
+                                    destination_slots=torch.tensor(slots, device=gpu_device),
+                                    repaired_keys=rk, repaired_values=rv)
+    torch.cuda.synchronize(gpu_device)
+    assert torch.equal(key[torch.tensor(slots)], rk)
+    assert torch.equal(value[torch.tensor(slots)], rv)
+    assert torch.count_nonzero(key[torch.tensor(multi["untouched"])]) == 0
+
+
+def test_scatter_unaligned_rows_use_the_element_path(gpu_device):
+    layers, slots, rows = 3, 64, 10
+    keys, values = make_pool(layers, slots, 3, 7, 5, torch.bfloat16, gpu_device, 21)
+    dest = torch.randperm(slots, device=gpu_device)[:rows]
+    rk = torch.randn(layers, rows, 3, 7, device=gpu_device, dtype=torch.bfloat16)
+    rv = torch.randn(layers, rows, 3, 5, device=gpu_device, dtype=torch.bfloat16)
+    ek, ev = ko.scatter_rows([bits(k) for k in keys], [bits(v) for v in values], dest.cpu().numpy(),
+                             bits(rk), bits(rv))
+    kv_link.scatter_kv_rows_inplace(key_buffers=keys, value_buffers=values, destination_slots=dest,
+                                    repaired_keys=rk, repaired_values=rv)
+    torch.cuda.synchronize(gpu_device)
+    for layer in range(layers):
+        assert np.array_equal(bits(keys[layer]), ek[layer])
+        assert np.array_equal(bits(values[layer]), ev[layer])
+
+
+def test_eligibility_reasons_on_device(gpu_device):
+    keys, values = make_pool(1, 32, 2, 8, 8, torch.bfloat16, gpu_device, 1)
+    maps = dict(
+        source_slots=torch.arange(4, device=gpu_device),
+        destination_slots=torch.arange(4, 8, device=gpu_device),
+        local_positions=torch.arange(4, device=gpu_device),
+        global_positions=torch.arange(4, 8, device=gpu_device),
+    )
+    table = build_cos_sin_cache(16, 8).to(gpu_device)
+
+    def reason(**overrides):
+        kwargs = dict(key_buffer=keys[0], value_buffer=values[0], cos_sin_cache=table, rotary_dim=8, **maps)
+        kwargs.update(overrides)
+        return kv_link.check_fused_kv_link_eligibility(**kwargs).reason
+
+    assert reason() == "supported"
+    assert reason(key_buffer=keys[0].float()) == "kv_dtype_mismatch"
+    assert reason(key_buffer=keys[0].float(), value_buffer=values[0].float()) == "fp16_or_bf16_required"
+    assert reason(rotary_dim=7) == "even_rotary_dim_required"
+    assert reason(rotary_dim=10) == "rotary_dim_exceeds_head_dim"
+    assert reason(source_slots=maps["source_slots"].float()) == "integer_token_maps_required"
+    assert reason(repair_mask=torch.zeros(3, dtype=torch.uint8, device=gpu_device)) == "repair_mask_length_mismatch"
+    assert reason(cos_sin_cache=table.double()) == "unsupported_cos_sin_dtype"
+    assert reason(source_slots=maps["source_slots"][:0]) == "empty_link"
+    with pytest.raises(RuntimeError, match="HIP LegoLink fusion is unavailable: even_rotary_dim_required"):
+        kv_link.fused_kv_link_inplace(key_buffer=keys[0], value_buffer=values[0], cos_sin_cache=table,
+                                      rotary_dim=7, prefix_token_count=0, is_neox_style=True, **maps)
+    with pytest.raises(ValueError, match="prefix_token_count is outside"):
+        kv_link.fused_kv_link_inplace(key_buffer=keys[0], value_buffer=values[0], cos_sin_cache=table,
+                                      rotary_dim=8, prefix_token_count=5, is_neox_style=True, **maps)
+
+
+@pytest.mark.parametrize("name,sample", [("c1", None), ("c2", None), ("c5", None), ("c4", None), ("c3", 16384)])
+def test_full_size_workload(gpu_device, name, sample):
+    result = check_workload(make_workload(name), gpu_device, sample_tokens=sample)
+    assert result["mismatches"] == 0
+
+
+def test_full_size_workload_generic_kernel(gpu_device):
+    result = check_workload(make_workload("c1"), gpu_device, kernel=GENERIC)
+    assert result["mismatches"] == 0
