@@ -1,8 +1,10 @@
 """Benchmark of the LegoLink KV link step on one MI355X.
 
 One step = one link of the workload: the fused gather -> RoPE re-rotation ->
-scatter over every layer (repair rows masked) plus the repaired-row write-back,
-with every input already resident in HBM.  Prints one JSON line.
+scatter over every layer (repair rows left out) plus the repaired-row
+write-back, with every input already resident in HBM.  The link and the
+write-back are prepared once (validation, argument blocks) and launched per
+step; preparation is reported separately.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload c2]
 
@@ -42,10 +44,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     parser.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
-    parser.add_argument("--cpu-sample-tokens", type=int, default=8192)
-    parser.add_argument("--cpu-reps", type=int, default=3)
+    parser.add_argument("--cpu-sample-tokens", type=int, default=32768)
+    parser.add_argument("--cpu-reps", type=int, default=25)
     parser.add_argument("--layers-per-wave", type=int, default=0)
     parser.add_argument("--waves-per-block", type=int, default=4)
+    parser.add_argument("--repair-rows", choices=["compact", "mask"], default="compact",
+                        help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
                         help="time a plain device copy of this many MiB instead of the link")
     return parser.parse_args()
@@ -188,42 +192,44 @@ def main() -> int:
         values.append(torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
                                   device=device, generator=generator))
     table = build_cos_sin_cache(workload.max_position + 1, workload.rotary_dim, theta=workload.theta).to(device)
-    index_start = time.perf_counter()
-    src = torch.from_numpy(workload.source_slots).to(device)
-    dst = torch.from_numpy(workload.destination_slots).to(device)
-    local = torch.from_numpy(workload.local_positions).to(device)
-    glob = torch.from_numpy(workload.global_positions).to(device)
-    mask = torch.from_numpy(workload.repair_mask).to(device)
-    repair_slots = torch.from_numpy(workload.repair_destination_slots).to(device)
-    torch.cuda.synchronize(device)
-    index_upload_ms = (time.perf_counter() - index_start) * 1e3
     repaired_k = torch.randn(shape.layers, workload.repair_rows, shape.kv_heads, shape.head_dim,
                              dtype=torch.bfloat16, device=device, generator=generator)
     repaired_v = torch.randn_like(repaired_k)
+    torch.cuda.synchronize(device)
     setup_s = time.perf_counter() - host_start
-    launch = kv_link.describe_link_launch(
+
+    # Host preparation of one link: token maps to the device, argument blocks
+    # validated and built.  Timed separately; not part of the step.
+    prepare_start = time.perf_counter()
+    if args.repair_rows == "compact":
+        keep = workload.repair_mask == 0
+        maps = [workload.source_slots[keep], workload.destination_slots[keep],
+                workload.local_positions[keep], workload.global_positions[keep]]
+        prefix = int(np.count_nonzero(keep[: workload.prefix_token_count]))
+        mask = None
+    else:
+        maps = [workload.source_slots, workload.destination_slots, workload.local_positions,
+                workload.global_positions]
+        prefix = workload.prefix_token_count
+        mask = torch.from_numpy(workload.repair_mask).to(device)
+    packed = torch.from_numpy(np.stack(maps)).to(device)
+    src, dst, local, glob = packed[0], packed[1], packed[2], packed[3]
+    repair_slots = torch.from_numpy(workload.repair_destination_slots).to(device)
+    link = kv_link.PreparedKVLink(
         key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
         local_positions=local, global_positions=glob, cos_sin_cache=table,
-        prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
+        prefix_token_count=prefix, rotary_dim=workload.rotary_dim,
         is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
         layers_per_wave=args.layers_per_wave,
     )
-    log(f"setup {setup_s:.1f}s; link launch {launch}")
-
-    def link() -> None:
-        kv_link.fused_kv_link_layers_inplace(
-            key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
-            local_positions=local, global_positions=glob, cos_sin_cache=table,
-            prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
-            is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
-            layers_per_wave=args.layers_per_wave,
-        )
-
-    def scatter() -> None:
-        kv_link.scatter_kv_rows_inplace(
-            key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
-            repaired_keys=repaired_k, repaired_values=repaired_v,
-        )
+    scatter = kv_link.PreparedKVScatter(
+        key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
+        repaired_keys=repaired_k, repaired_values=repaired_v,
+    )
+    torch.cuda.synchronize(device)
+    host_prepare_ms = (time.perf_counter() - prepare_start) * 1e3
+    launch = link.launch
+    log(f"setup {setup_s:.1f}s; host prepare {host_prepare_ms:.2f} ms; link launch {launch}")
 
     for _ in range(args.warmup):
         link()
@@ -288,7 +294,8 @@ def main() -> int:
         "link_kernel_ms": round(link_avg_ms, 5),
         "scatter_kernel_ms": round(float(np.mean(scatter_ms)), 5),
         "event_ms_per_step": round(gpu_ms, 5),
-        "index_upload_ms": round(index_upload_ms, 3),
+        "host_prepare_ms": round(host_prepare_ms, 3),
+        "repair_rows_mode": args.repair_rows,
         "launch": launch,
         "roofline": {
             "bound": "hbm",

@@ -17,6 +17,7 @@ Every tensor stays owned by the caller; nothing here allocates device memory.
 
 from __future__ import annotations
 
+import ctypes
 import os
 from dataclasses import dataclass
 from typing import Any, Sequence
@@ -68,8 +69,8 @@ def resolve_fused_kv_launch_config(
     (``SGLANG_PIC_TRITON_BLOCK_SIZE`` / ``_NUM_WARPS`` / ``_NUM_STAGES``) as the
     reference.  On gfx950 ``num_warps`` is the number of 64-lane waves per
     workgroup; ``block_size`` and ``num_stages`` are validated and recorded but
-    do not shape the HIP kernels (their work unit is a 16-byte row chunk and
-    they keep four layers of loads in flight per lane).
+    do not shape the HIP kernels (their work unit is a 16-byte row chunk of one
+    layer row, and each wave walks a short run of layers).
     """
 
     del work_items, device, capability  # one gfx950 default for every shape
@@ -361,13 +362,149 @@ def _link_args(
 
 
 def ctypes_address(array: Any) -> int:
-    import ctypes
-
     return ctypes.addressof(array)
 
 
 def _raise_unavailable(reason: str) -> None:
     raise RuntimeError(f"HIP LegoLink fusion is unavailable: {reason}")
+
+
+class PreparedKVLink:
+    """A validated link: the argument block is built once and every call
+    enqueues the kernel with one C call (a few microseconds of host time).
+
+    Arguments are those of ``fused_kv_link_layers_inplace``; the tensors are
+    referenced, not copied, so their contents may change between calls (the
+    kernel reads them when it runs) but their storage must stay alive and in
+    place.
+    """
+
+    def __init__(
+        self,
+        *,
+        key_buffers: Sequence[torch.Tensor],
+        value_buffers: Sequence[torch.Tensor],
+        source_slots: torch.Tensor,
+        destination_slots: torch.Tensor,
+        local_positions: torch.Tensor,
+        global_positions: torch.Tensor,
+        cos_sin_cache: torch.Tensor,
+        prefix_token_count: int,
+        rotary_dim: int,
+        is_neox_style: bool,
+        repair_mask: torch.Tensor | None = None,
+        block_size: int | None = None,
+        num_warps: int | None = None,
+        num_stages: int | None = None,
+        layers_per_wave: int = 0,
+        kernel: int = _native.KERNEL_AUTO,
+        validate_indices: bool = False,
+    ) -> None:
+        key_buffers = list(key_buffers)
+        value_buffers = list(value_buffers)
+        if not key_buffers or len(key_buffers) != len(value_buffers):
+            raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
+        eligibility = _eligibility(
+            key_buffers,
+            value_buffers,
+            source_slots,
+            destination_slots,
+            local_positions,
+            global_positions,
+            cos_sin_cache,
+            rotary_dim,
+            repair_mask,
+        )
+        if not eligibility.supported:
+            _raise_unavailable(eligibility.reason)
+        if not 0 <= int(prefix_token_count) <= int(source_slots.numel()):
+            raise ValueError("prefix_token_count is outside the linked token range")
+        key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+        work_items = int(key_buffer.shape[1]) * (
+            int(rotary_dim) // 2
+            + int(key_buffer.shape[2])
+            - int(rotary_dim)
+            + int(value_buffer.shape[2])
+        )
+        self.launch_config = resolve_fused_kv_launch_config(
+            work_items=work_items,
+            device=key_buffer.device,
+            block_size=block_size,
+            num_warps=num_warps,
+            num_stages=num_stages,
+        )
+        if validate_indices:
+            _validate_index_ranges(
+                int(key_buffer.shape[0]),
+                source_slots,
+                destination_slots,
+                local_positions,
+                global_positions,
+                int(cos_sin_cache.shape[0]),
+                int(prefix_token_count),
+            )
+        if repair_mask is not None and repair_mask.dtype == torch.bool:
+            repair_mask = repair_mask.view(torch.uint8)
+        self._args, self._tables = _link_args(
+            key_buffers,
+            value_buffers,
+            source_slots,
+            destination_slots,
+            local_positions,
+            global_positions,
+            cos_sin_cache,
+            prefix_token_count,
+            rotary_dim,
+            is_neox_style,
+            repair_mask,
+            self.launch_config.num_warps,
+            layers_per_wave,
+            kernel,
+        )
+        self._args.struct_size = ctypes.sizeof(_native.LinkArgs)
+        # Keep every tensor the argument block points at alive.
+        self._tensors = (
+            key_buffers, value_buffers, source_slots, destination_slots,
+            local_positions, global_positions, cos_sin_cache, repair_mask,
+        )
+        self.device = key_buffer.device
+        try:
+            info = _native.kv_link_describe(self._args)
+        except _native.NativeCallError as error:
+            self._raise_for(error)
+        self.launch = {
+            "kernel": "vector" if info.kernel == _native.KERNEL_VECTOR else "generic",
+            "launches": int(info.launches),
+            "grid_x": int(info.grid_x),
+            "grid_y": int(info.grid_y),
+            "block_threads": int(info.block_threads),
+            "layers_per_wave": int(info.layers_per_wave),
+        }
+        self._lib = _native.load_library()
+        self._args_ref = ctypes.byref(self._args)
+
+    @staticmethod
+    def _raise_for(error: _native.NativeCallError) -> None:
+        if error.status == _native.LL_ERR_PREFIX_OUT_OF_RANGE:
+            raise ValueError("prefix_token_count is outside the linked token range") from error
+        if error.status in (_native.LL_ERR_LAUNCH_CONFIG, _native.LL_ERR_UNSUPPORTED_KERNEL):
+            raise ValueError(str(error)) from error
+        if error.status == _native.LL_ERR_HIP:
+            raise RuntimeError(f"HIP LegoLink link launch failed: {error.detail}") from error
+        _raise_unavailable(error.reason)
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> None:
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        status = self._lib.ll_kv_link(self._args_ref, ctypes.c_void_p(stream.cuda_stream))
+        if status != _native.LL_OK:
+            self._raise_for(
+                _native.NativeCallError(
+                    status,
+                    self._lib.ll_status_reason(status).decode(),
+                    self._lib.ll_last_error().decode(),
+                )
+            )
 
 
 def fused_kv_link_layers_inplace(
@@ -391,82 +528,29 @@ def fused_kv_link_layers_inplace(
     validate_indices: bool = False,
 ) -> None:
     """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
-    64 layers.  Per layer the result equals ``fused_kv_link_inplace``."""
+    64 layers, on the current stream.  Per layer the result equals
+    ``fused_kv_link_inplace``."""
 
-    key_buffers = list(key_buffers)
-    value_buffers = list(value_buffers)
-    if not key_buffers or len(key_buffers) != len(value_buffers):
-        raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
-    eligibility = _eligibility(
-        key_buffers,
-        value_buffers,
-        source_slots,
-        destination_slots,
-        local_positions,
-        global_positions,
-        cos_sin_cache,
-        rotary_dim,
-        repair_mask,
-    )
-    if not eligibility.supported:
-        _raise_unavailable(eligibility.reason)
-    if not 0 <= int(prefix_token_count) <= int(source_slots.numel()):
-        raise ValueError("prefix_token_count is outside the linked token range")
-    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
-    work_items = int(key_buffer.shape[1]) * (
-        int(rotary_dim) // 2
-        + int(key_buffer.shape[2])
-        - int(rotary_dim)
-        + int(value_buffer.shape[2])
-    )
-    launch_config = resolve_fused_kv_launch_config(
-        work_items=work_items,
-        device=key_buffer.device,
+    prepared = PreparedKVLink(
+        key_buffers=key_buffers,
+        value_buffers=value_buffers,
+        source_slots=source_slots,
+        destination_slots=destination_slots,
+        local_positions=local_positions,
+        global_positions=global_positions,
+        cos_sin_cache=cos_sin_cache,
+        prefix_token_count=prefix_token_count,
+        rotary_dim=rotary_dim,
+        is_neox_style=is_neox_style,
+        repair_mask=repair_mask,
         block_size=block_size,
         num_warps=num_warps,
         num_stages=num_stages,
+        layers_per_wave=layers_per_wave,
+        kernel=kernel,
+        validate_indices=validate_indices,
     )
-    if validate_indices:
-        _validate_index_ranges(
-            int(key_buffer.shape[0]),
-            source_slots,
-            destination_slots,
-            local_positions,
-            global_positions,
-            int(cos_sin_cache.shape[0]),
-            int(prefix_token_count),
-        )
-    if repair_mask is not None and repair_mask.dtype == torch.bool:
-        repair_mask = repair_mask.view(torch.uint8)
-    args, keepalive = _link_args(
-        key_buffers,
-        value_buffers,
-        source_slots,
-        destination_slots,
-        local_positions,
-        global_positions,
-        cos_sin_cache,
-        prefix_token_count,
-        rotary_dim,
-        is_neox_style,
-        repair_mask,
-        launch_config.num_warps,
-        layers_per_wave,
-        kernel,
-    )
-    with torch.cuda.device(key_buffer.device):
-        stream = torch.cuda.current_stream(key_buffer.device).cuda_stream
-        try:
-            _native.kv_link(args, stream)
-        except _native.NativeCallError as error:
-            if error.status == _native.LL_ERR_PREFIX_OUT_OF_RANGE:
-                raise ValueError("prefix_token_count is outside the linked token range") from error
-            if error.status in (_native.LL_ERR_LAUNCH_CONFIG, _native.LL_ERR_UNSUPPORTED_KERNEL):
-                raise ValueError(str(error)) from error
-            if error.status == _native.LL_ERR_HIP:
-                raise RuntimeError(f"HIP LegoLink link launch failed: {error.detail}") from error
-            _raise_unavailable(error.reason)
-    del keepalive
+    prepared()
 
 
 def fused_kv_link_inplace(
@@ -562,6 +646,112 @@ def describe_link_launch(
     }
 
 
+class PreparedKVScatter:
+    """A validated repaired-row write-back; each call enqueues one kernel launch
+    per 64 layers.
+
+    ``repaired_keys`` is [num_layers, rows, heads, key_head_dim] (or
+    [rows, heads, key_head_dim] for a single layer) with dense rows; the layer
+    stride may be anything.  Semantics of write_repaired_kv
+    (tests/pic/reference/repair_reference.py:14-25) applied to every layer:
+    K_l[destination_slots[r]] = repaired_keys[l, r], V likewise.
+    """
+
+    def __init__(
+        self,
+        *,
+        key_buffers: Sequence[torch.Tensor],
+        value_buffers: Sequence[torch.Tensor],
+        destination_slots: torch.Tensor,
+        repaired_keys: torch.Tensor,
+        repaired_values: torch.Tensor,
+        num_warps: int = 4,
+    ) -> None:
+        key_buffers = list(key_buffers)
+        value_buffers = list(value_buffers)
+        if not key_buffers or len(key_buffers) != len(value_buffers):
+            raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
+        if repaired_keys.ndim == 3:
+            repaired_keys = repaired_keys.unsqueeze(0)
+        if repaired_values.ndim == 3:
+            repaired_values = repaired_values.unsqueeze(0)
+        key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+        layers = len(key_buffers)
+        rows = int(destination_slots.numel())
+        if not _native.library_available():
+            _raise_unavailable(NATIVE_UNAVAILABLE_REASON)
+        tensors = (*key_buffers, *value_buffers, destination_slots, repaired_keys, repaired_values)
+        if not all(tensor.is_cuda and tensor.device == key_buffer.device for tensor in tensors):
+            _raise_unavailable("cuda_tensors_required")
+        for key, value in zip(key_buffers, value_buffers, strict=True):
+            if key.ndim != 3 or value.ndim != 3:
+                _raise_unavailable("mha_3d_kv_buffers_required")
+            if key.shape != key_buffer.shape or value.shape != value_buffer.shape or (
+                key.shape[:2] != value.shape[:2]
+            ):
+                _raise_unavailable("kv_head_layout_mismatch")
+            if key.dtype != key_buffer.dtype or value.dtype != key_buffer.dtype:
+                _raise_unavailable("kv_dtype_mismatch")
+            if not key.is_contiguous() or not value.is_contiguous():
+                _raise_unavailable("contiguous_kv_buffers_required")
+        if key_buffer.dtype not in _KV_DTYPES:
+            _raise_unavailable("fp16_or_bf16_required")
+        if destination_slots.dtype not in _INDEX_DTYPES or not destination_slots.is_contiguous():
+            _raise_unavailable("integer_token_maps_required")
+        expected_k = (layers, rows, int(key_buffer.shape[1]), int(key_buffer.shape[2]))
+        expected_v = (layers, rows, int(value_buffer.shape[1]), int(value_buffer.shape[2]))
+        if tuple(repaired_keys.shape) != expected_k or tuple(repaired_values.shape) != expected_v:
+            raise ValueError(
+                f"repaired rows must be {expected_k} / {expected_v}, got "
+                f"{tuple(repaired_keys.shape)} / {tuple(repaired_values.shape)}"
+            )
+        if repaired_keys.dtype != key_buffer.dtype or repaired_values.dtype != key_buffer.dtype:
+            _raise_unavailable("kv_dtype_mismatch")
+        if not repaired_keys[0].is_contiguous() or not repaired_values[0].is_contiguous():
+            raise ValueError("repaired rows of each layer must be dense")
+        self.rows = rows
+        self.device = key_buffer.device
+        self._tables = (
+            _native.pointer_table([buffer.data_ptr() for buffer in key_buffers]),
+            _native.pointer_table([buffer.data_ptr() for buffer in value_buffers]),
+        )
+        args = _native.ScatterArgs()
+        args.struct_size = ctypes.sizeof(_native.ScatterArgs)
+        args.num_layers = layers
+        args.key_layers = ctypes_address(self._tables[0])
+        args.value_layers = ctypes_address(self._tables[1])
+        args.num_slots = int(key_buffer.shape[0])
+        args.num_heads = int(key_buffer.shape[1])
+        args.key_head_dim = int(key_buffer.shape[2])
+        args.value_head_dim = int(value_buffer.shape[2])
+        args.kv_dtype = _KV_DTYPES[key_buffer.dtype]
+        args.num_rows = rows
+        args.destination_slots = destination_slots.data_ptr()
+        args.destination_slots_dtype = _INDEX_DTYPES[destination_slots.dtype]
+        args.repaired_key = repaired_keys.data_ptr()
+        args.repaired_key_layer_stride = int(repaired_keys.stride(0)) if layers > 1 else 0
+        args.repaired_value = repaired_values.data_ptr()
+        args.repaired_value_layer_stride = int(repaired_values.stride(0)) if layers > 1 else 0
+        args.waves_per_block = int(num_warps)
+        self._args = args
+        self._args_ref = ctypes.byref(args)
+        self._tensors = tensors
+        self._lib = _native.load_library()
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> None:
+        if self.rows == 0:
+            return
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        status = self._lib.ll_kv_scatter_rows(self._args_ref, ctypes.c_void_p(stream.cuda_stream))
+        if status != _native.LL_OK:
+            reason = self._lib.ll_status_reason(status).decode()
+            detail = self._lib.ll_last_error().decode()
+            if status == _native.LL_ERR_HIP:
+                raise RuntimeError(f"HIP LegoLink scatter launch failed: {detail}")
+            _raise_unavailable(reason)
+
+
 def scatter_kv_rows_inplace(
     *,
     key_buffers: Sequence[torch.Tensor],
@@ -571,86 +761,17 @@ def scatter_kv_rows_inplace(
     repaired_values: torch.Tensor,
     num_warps: int = 4,
 ) -> None:
-    """Write repaired rows: K_l[destination_slots[r]] = repaired_keys[l, r] (and V).
+    """Write repaired rows on the current stream: K_l[destination_slots[r]] =
+    repaired_keys[l, r] (and V).  See ``PreparedKVScatter``."""
 
-    ``repaired_keys`` is [num_layers, rows, heads, key_head_dim] (or
-    [rows, heads, key_head_dim] for a single layer) with dense rows; the layer
-    stride may be anything.  Same semantics as write_repaired_kv
-    (tests/pic/reference/repair_reference.py:14-25) applied to every layer.
-    """
-
-    key_buffers = list(key_buffers)
-    value_buffers = list(value_buffers)
-    if not key_buffers or len(key_buffers) != len(value_buffers):
-        raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
-    if repaired_keys.ndim == 3:
-        repaired_keys = repaired_keys.unsqueeze(0)
-    if repaired_values.ndim == 3:
-        repaired_values = repaired_values.unsqueeze(0)
-    key_buffer, value_buffer = key_buffers[0], value_buffers[0]
-    layers = len(key_buffers)
-    rows = int(destination_slots.numel())
-    if not _native.library_available():
-        _raise_unavailable(NATIVE_UNAVAILABLE_REASON)
-    tensors = (*key_buffers, *value_buffers, destination_slots, repaired_keys, repaired_values)
-    if not all(tensor.is_cuda and tensor.device == key_buffer.device for tensor in tensors):
-        _raise_unavailable("cuda_tensors_required")
-    for key, value in zip(key_buffers, value_buffers, strict=True):
-        if key.ndim != 3 or value.ndim != 3:
-            _raise_unavailable("mha_3d_kv_buffers_required")
-        if key.shape != key_buffer.shape or value.shape != value_buffer.shape or (
-            key.shape[:2] != value.shape[:2]
-        ):
-            _raise_unavailable("kv_head_layout_mismatch")
-        if key.dtype != key_buffer.dtype or value.dtype != key_buffer.dtype:
-            _raise_unavailable("kv_dtype_mismatch")
-        if not key.is_contiguous() or not value.is_contiguous():
-            _raise_unavailable("contiguous_kv_buffers_required")
-    if key_buffer.dtype not in _KV_DTYPES:
-        _raise_unavailable("fp16_or_bf16_required")
-    if destination_slots.dtype not in _INDEX_DTYPES or not destination_slots.is_contiguous():
-        _raise_unavailable("integer_token_maps_required")
-    expected_k = (layers, rows, int(key_buffer.shape[1]), int(key_buffer.shape[2]))
-    expected_v = (layers, rows, int(value_buffer.shape[1]), int(value_buffer.shape[2]))
-    if tuple(repaired_keys.shape) != expected_k or tuple(repaired_values.shape) != expected_v:
-        raise ValueError(
-            f"repaired rows must be {expected_k} / {expected_v}, got "
-            f"{tuple(repaired_keys.shape)} / {tuple(repaired_values.shape)}"
-        )
-    if repaired_keys.dtype != key_buffer.dtype or repaired_values.dtype != key_buffer.dtype:
-        _raise_unavailable("kv_dtype_mismatch")
-    if not repaired_keys[0].is_contiguous() or not repaired_values[0].is_contiguous():
-        raise ValueError("repaired rows of each layer must be dense")
-    if rows == 0:
-        return
-    key_table = _native.pointer_table([buffer.data_ptr() for buffer in key_buffers])
-    value_table = _native.pointer_table([buffer.data_ptr() for buffer in value_buffers])
-    args = _native.ScatterArgs()
-    args.num_layers = layers
-    args.key_layers = ctypes_address(key_table)
-    args.value_layers = ctypes_address(value_table)
-    args.num_slots = int(key_buffer.shape[0])
-    args.num_heads = int(key_buffer.shape[1])
-    args.key_head_dim = int(key_buffer.shape[2])
-    args.value_head_dim = int(value_buffer.shape[2])
-    args.kv_dtype = _KV_DTYPES[key_buffer.dtype]
-    args.num_rows = rows
-    args.destination_slots = destination_slots.data_ptr()
-    args.destination_slots_dtype = _INDEX_DTYPES[destination_slots.dtype]
-    args.repaired_key = repaired_keys.data_ptr()
-    args.repaired_key_layer_stride = int(repaired_keys.stride(0)) if layers > 1 else 0
-    args.repaired_value = repaired_values.data_ptr()
-    args.repaired_value_layer_stride = int(repaired_values.stride(0)) if layers > 1 else 0
-    args.waves_per_block = int(num_warps)
-    with torch.cuda.device(key_buffer.device):
-        stream = torch.cuda.current_stream(key_buffer.device).cuda_stream
-        try:
-            _native.kv_scatter_rows(args, stream)
-        except _native.NativeCallError as error:
-            if error.status == _native.LL_ERR_HIP:
-                raise RuntimeError(f"HIP LegoLink scatter launch failed: {error.detail}") from error
-            _raise_unavailable(error.reason)
-    del key_table, value_table
+    PreparedKVScatter(
+        key_buffers=key_buffers,
+        value_buffers=value_buffers,
+        destination_slots=destination_slots,
+        repaired_keys=repaired_keys,
+        repaired_values=repaired_values,
+        num_warps=num_warps,
+    )()
 
 
 def fusion_metadata(**kwargs: Any) -> dict[str, Any]:

@@ -1,0 +1,135 @@
+"""Registered KV blocks: the supplier of the link's source slots.
+
+A small registry with the LegoLink block registry's interface names
+(patched_sglang_files/python/sglang/srt/mem_cache/radix_cache.py:
+``register_legolink_block`` :755, ``get_legolink_block_tokens`` :950,
+``lookup_legolink_blocks`` :995, ``acquire_legolink_blocks`` :1246,
+``release_legolink_blocks`` :1330) and the handle fields the link reads
+(``LegoLinkBlockHandle`` :289-334: token ids, ``kv_slots``,
+``compile_local_positions``, pin count).  The radix tree, eviction policy,
+compatibility keys and statistics of the reference registry manage block
+lifetime, not link arithmetic, and are not restated.
+"""
+
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass, field
+from typing import Iterable, Optional, Sequence
+
+import torch
+
+
+@dataclass
+class LegoLinkBlockHandle:
+    cache_key: str
+    token_ids: tuple[int, ...]
+    kv_slots: torch.Tensor                 # int64 [token_count], pool slots holding the block's K/V
+    compile_local_positions: tuple[int, ...]  # RoPE positions the cached K carries
+    block_id: str = ""
+    pin_count: int = 0
+    generation: int = 0
+    valid: bool = True
+    stale_reason: Optional[str] = None
+
+    @property
+    def token_count(self) -> int:
+        return len(self.token_ids)
+
+
+@dataclass
+class LegoLinkLookupResult:
+    matched_blocks: dict[str, LegoLinkBlockHandle] = field(default_factory=dict)
+    kv_slot_ranges: dict[str, torch.Tensor] = field(default_factory=dict)
+    missing_blocks: list[str] = field(default_factory=list)
+    stale_blocks: list[str] = field(default_factory=list)
+    matched_handles: list[LegoLinkBlockHandle] = field(default_factory=list)
+
+
+class LegoLinkBlockRegistry:
+    """cache_key -> handle.  Callers on several threads are serialised by a lock."""
+
+    def __init__(self) -> None:
+        self._blocks: dict[str, LegoLinkBlockHandle] = {}
+        self._lock = threading.Lock()
+        self._generation = 0
+
+    def register_legolink_block(
+        self,
+        cache_key: str,
+        token_ids: Sequence[int],
+        kv_slots: torch.Tensor,
+        *,
+        compile_local_positions: Optional[Sequence[int]] = None,
+        block_id: Optional[str] = None,
+    ) -> LegoLinkBlockHandle:
+        token_ids = tuple(int(token) for token in token_ids)
+        slots = torch.as_tensor(kv_slots).long().reshape(-1).clone()
+        if int(slots.numel()) != len(token_ids):
+            raise ValueError("LegoLink KV slot count must equal the exact logical token length.")
+        positions = (
+            tuple(range(len(token_ids)))
+            if compile_local_positions is None
+            else tuple(int(p) for p in compile_local_positions)
+        )
+        if len(positions) != len(token_ids):
+            raise ValueError("compile_local_positions must hold one position per token.")
+        with self._lock:
+            resident = self._blocks.get(str(cache_key))
+            if resident is not None and resident.valid:
+                raise ValueError(f"LegoLink block {cache_key} is already registered.")
+            self._generation += 1
+            handle = LegoLinkBlockHandle(
+                cache_key=str(cache_key),
+                token_ids=token_ids,
+                kv_slots=slots,
+                compile_local_positions=positions,
+                block_id=str(block_id or cache_key),
+                generation=self._generation,
+            )
+            self._blocks[str(cache_key)] = handle
+            return handle
+
+    def get_legolink_block_tokens(self, cache_key: str) -> Optional[tuple[int, ...]]:
+        handle = self._blocks.get(str(cache_key))
+        return handle.token_ids if handle is not None and handle.valid else None
+
+    def lookup_legolink_blocks(self, cache_keys: Iterable[str]) -> LegoLinkLookupResult:
+        result = LegoLinkLookupResult()
+        with self._lock:
+            for cache_key in (str(key) for key in cache_keys):
+                handle = self._blocks.get(cache_key)
+                if handle is None:
+                    result.missing_blocks.append(cache_key)
+                elif not handle.valid:
+                    result.stale_blocks.append(cache_key)
+                else:
+                    result.matched_blocks[cache_key] = handle
+                    result.kv_slot_ranges[cache_key] = handle.kv_slots
+                    result.matched_handles.append(handle)
+        return result
+
+    def acquire_legolink_blocks(self, handles: Iterable[LegoLinkBlockHandle]) -> list[LegoLinkBlockHandle]:
+        handles = list(handles)
+        with self._lock:
+            for handle in handles:
+                handle.pin_count += 1
+        return handles
+
+    def release_legolink_blocks(self, handles: Iterable[LegoLinkBlockHandle]) -> None:
+        with self._lock:
+            for handle in handles:
+                if handle.pin_count <= 0:
+                    raise ValueError(f"LegoLink block {handle.cache_key} is not pinned.")
+                handle.pin_count -= 1
+
+    def evict_legolink_block(self, cache_key: str) -> bool:
+        """Invalidate an unpinned block; pinned blocks stay resident."""
+
+        with self._lock:
+            handle = self._blocks.get(str(cache_key))
+            if handle is None or handle.pin_count > 0:
+                return False
+            handle.valid = False
+            handle.stale_reason = "evicted"
+            return True

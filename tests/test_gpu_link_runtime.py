@@ -1,0 +1,233 @@
+"""GPU tests of the link executor (registry -> plan -> HIP link -> repair write)."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from legolink_amd import kv_link
+from legolink_amd.link_plan import resolve_link_plan
+from legolink_amd.link_runtime import KVLinkExecutor, KVPool
+from legolink_amd.registry import LegoLinkBlockRegistry
+from legolink_amd.rope import RotarySpec, build_cos_sin_cache
+from oracle import kv_link_oracle as ko
+from tests import rope_math
+from tests.gpu_helpers import bits, report
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+
+
+def _bf16(array: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(ko.f32_to_bf16_bits(array.astype(np.float32)).view(np.int16)).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", GOLDEN["first_block_remap"]["cases"], ids=lambda c: str(c["blocks"]))
+def test_first_block_remap_cases(gpu_device, case):
+    """tests/pic/test_first_block_rope_remap.py:126-249 through the HIP executor:
+    every block lands rotated to its request-global positions; a block already
+    at its compile positions is copied bit for bit."""
+
+    report(f"first-block case {case['blocks']}")
+    heads = GOLDEN["first_block_remap"]["heads"]
+    rotary = GOLDEN["first_block_remap"]["rotary_dim"]
+    theta = GOLDEN["first_block_remap"]["theta"]
+    rng = np.random.default_rng(20260824)
+    registry = LegoLinkBlockRegistry()
+    pool = KVPool.allocate(num_slots=256, num_layers=1, num_heads=heads, head_dim=rotary, device=gpu_device)
+    pool.k_buffer[0].zero_()
+    pool.v_buffer[0].zero_()
+    raws, slot = {}, 128
+    for index, (_, count) in enumerate(case["blocks"]):
+        key = f"block-{index}"
+        raw = rng.standard_normal((count, heads, rotary))
+        compiled = rope_math.rotate(raw, np.arange(count), rotary, theta=theta)
+        slots = torch.arange(slot, slot + count)
+        pool.k_buffer[0][slots] = _bf16(compiled).to(gpu_device)
+        pool.v_buffer[0][slots] = _bf16(rng.standard_normal((count, heads, rotary))).to(gpu_device)
+        registry.register_legolink_block(key, list(range(count)), slots.to(gpu_device))
+        raws[key] = (raw, compiled)
+        slot += count
+    total = max(start + count for start, count in case["blocks"])
+    destination = torch.arange(total, device=gpu_device)
+    plan = {"cache_keys": list(raws),
+            "block_ranges": [{"start_token": s, "end_token": s + c} for s, c in case["blocks"]]}
+    rotary_spec = RotarySpec(build_cos_sin_cache(4096, rotary, theta=theta), rotary_dim=rotary)
+    executor = KVLinkExecutor(registry, rotary_spec, end_layer=1)
+    record = executor.copy_linked_kv(pool, destination, plan)
+    torch.cuda.synchronize(gpu_device)
+    assert record["rope_remapped"] == case["expected_remapped"]
+    for index, (start, count) in enumerate(case["blocks"]):
+        raw, compiled = raws[f"block-{index}"]
+        got = pool.k_buffer[0][start : start + count].float().cpu().numpy()
+        want = rope_math.rotate(raw, start + np.arange(count), rotary, theta=theta)
+        assert np.abs(got - want).max() < 0.05
+        if not case["expected_remapped"][index]:
+            assert np.array_equal(bits(pool.k_buffer[0][start : start + count]),
+                                  ko.f32_to_bf16_bits(compiled.astype(np.float32)))
+
+
+def _flow(device, *, boundary_repair_aware, compact, seed=3):
+    """Register 5 blocks, derive a plan, link, write repaired rows."""
+
+    rng = np.random.default_rng(seed)
+    layers, heads, dim, slots = 6, 4, 128, 8192
+    lengths = [300, 77, 512, 129, 64]
+    registry = LegoLinkBlockRegistry()
+    generator = torch.Generator(device=device).manual_seed(seed)
+    pool = KVPool([torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=device, generator=generator)
+                   for _ in range(layers)],
+                  [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=device, generator=generator)
+                   for _ in range(layers)])
+    perm = rng.permutation(slots)
+    cursor = 0
+    blocks = {}
+    for index, length in enumerate(lengths):
+        key = f"blk{index}"
+        tokens = rng.integers(0, 50_000, size=length).tolist()
+        # Block 3 was compiled behind a 900-token prefix.
+        positions = (np.arange(length) + 900).tolist() if index == 3 else None
+        registry.register_legolink_block(key, tokens, torch.from_numpy(perm[cursor : cursor + length]).to(device),
+                                         compile_local_positions=positions)
+        blocks[key] = tokens
+        cursor += length
+    plan = {"cache_keys": ["blk2", "blk0", "blk4", "blk3", "blk1"], "recompute_initial_tokens": 16,
+            "physical_prefix_token_count": 5}
+    host_tokens = rng.integers(0, 50_000, size=5 + 40).tolist()
+    linked = resolve_link_plan(registry.get_legolink_block_tokens, host_tokens, plan)
+    destination = torch.from_numpy(perm[cursor : cursor + len(linked)]).to(device)
+    rotary = RotarySpec(build_cos_sin_cache(2048, dim), rotary_dim=dim)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers)
+    before_k = [bits(k) for k in pool.k_buffer]
+    before_v = [bits(v) for v in pool.v_buffer]
+    prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=boundary_repair_aware,
+                                     compact_repair_rows=compact)
+    prepared.launch()
+    repair_rows = int(prepared.repair_offsets.size)
+    repaired_k = torch.randn(layers, repair_rows, heads, dim, dtype=torch.bfloat16, device=device, generator=generator)
+    repaired_v = torch.randn_like(repaired_k)
+    if repair_rows:
+        prepared.write_repaired(repaired_k, repaired_v)
+    torch.cuda.synchronize(device)
+    maps = prepared.maps
+    mask = np.zeros(maps.token_count, dtype=np.uint8)
+    mask[prepared.repair_offsets] = 1
+    expected_k, expected_v = ko.link_pool(
+        before_k, before_v, maps.source_slots.cpu().numpy(), maps.destination_slots.cpu().numpy(),
+        maps.local_positions, maps.global_positions, rotary.cos_sin_cache.cpu().numpy(),
+        key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=dim, neox=True,
+        prefix=maps.prefix_token_count, repair_mask=mask if repair_rows else None,
+    )
+    if repair_rows:
+        expected_k, expected_v = ko.scatter_rows(expected_k, expected_v,
+                                                 prepared.repair_destination_slots.cpu().numpy(),
+                                                 bits(repaired_k), bits(repaired_v))
+    for layer in range(layers):
+        assert np.array_equal(bits(pool.k_buffer[layer]), expected_k[layer]), f"K layer {layer}"
+        assert np.array_equal(bits(pool.v_buffer[layer]), expected_v[layer]), f"V layer {layer}"
+    return prepared, [bits(k) for k in pool.k_buffer], plan
+
+
+def test_plan_link_repair_flow_matches_oracle(gpu_device):
+    prepared, _, plan = _flow(gpu_device, boundary_repair_aware=True, compact=True)
+    # imp_indices inside blocks: 16 per block after the first (4 seams).
+    assert prepared.repair_offsets.size == 4 * 16
+    assert prepared.maps.block_specs[3]["needs_rope_remap"]
+    assert prepared.linked_token_count == prepared.maps.token_count - 64
+
+
+def test_compacted_and_masked_links_agree(gpu_device):
+    _, compacted, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=9)
+    _, masked, _ = _flow(gpu_device, boundary_repair_aware=True, compact=False, seed=9)
+    for a, b in zip(compacted, masked):
+        assert np.array_equal(a, b)
+
+
+def test_link_without_repair_awareness_copies_every_token(gpu_device):
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=False, compact=True, seed=5)
+    assert prepared.repair_offsets.size == 0
+    assert prepared.linked_token_count == prepared.maps.token_count
+
+
+def test_executor_matches_the_per_layer_drop_in_operator(gpu_device):
+    layers, slots = 4, 4096
+    rng = np.random.default_rng(12)
+    registry = LegoLinkBlockRegistry()
+    generator = torch.Generator(device=gpu_device).manual_seed(12)
+    keys = [torch.randn(slots, 4, 128, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)]
+    values = [torch.randn(slots, 4, 128, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)]
+    keys_b, values_b = [k.clone() for k in keys], [v.clone() for v in values]
+    perm = rng.permutation(slots)
+    registry.register_legolink_block("x", list(range(700)), torch.from_numpy(perm[:700]).to(gpu_device))
+    registry.register_legolink_block("y", list(range(300)), torch.from_numpy(perm[700:1000]).to(gpu_device))
+    plan = {"cache_keys": ["y", "x"], "block_ranges": [{"start_token": 0, "end_token": 300},
+                                                     {"start_token": 300, "end_token": 1000}]}
+    destination = torch.from_numpy(perm[1000:2000]).to(gpu_device)
+    rotary = RotarySpec(build_cos_sin_cache(2048, 128), rotary_dim=128)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers)
+    executor.copy_linked_kv(KVPool(keys, values), destination, plan)
+    maps = executor.build_link_maps(destination, plan)
+    local = torch.from_numpy(maps.local_positions).to(gpu_device)
+    glob = torch.from_numpy(maps.global_positions).to(gpu_device)
+    for key, value in zip(keys_b, values_b):
+        kv_link.fused_kv_link_inplace(
+            key_buffer=key, value_buffer=value, source_slots=maps.source_slots,
+            destination_slots=maps.destination_slots, local_positions=local, global_positions=glob,
+            cos_sin_cache=rotary.cos_sin_cache, prefix_token_count=maps.prefix_token_count,
+            rotary_dim=128, is_neox_style=True,
+        )
+    torch.cuda.synchronize(gpu_device)
+    assert maps.prefix_token_count == 300  # block "y" sits at its compile positions
+    for a, b in zip(keys + values, keys_b + values_b):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_prepared_link_replays_in_a_hip_graph(gpu_device):
+    """The link and the repair write allocate nothing and sync nothing, so they
+    can be captured; every replay must equal the eager result."""
+
+    layers, slots, heads, dim = 3, 2048, 4, 128
+    rng = np.random.default_rng(4)
+    registry = LegoLinkBlockRegistry()
+    generator = torch.Generator(device=gpu_device).manual_seed(4)
+    pool = KVPool([torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)],
+                  [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)])
+    perm = rng.permutation(slots)
+    registry.register_legolink_block("a", list(range(400)), torch.from_numpy(perm[:400]).to(gpu_device))
+    registry.register_legolink_block("b", list(range(250)), torch.from_numpy(perm[400:650]).to(gpu_device))
+    plan = {"cache_keys": ["a", "b"], "recompute_initial_tokens": 8}
+    resolve_link_plan(registry.get_legolink_block_tokens, [1, 2, 3], plan)
+    destination = torch.from_numpy(perm[650:1400]).to(gpu_device)
+    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(1024, dim), rotary_dim=dim), end_layer=layers)
+    prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=True)
+    repaired_k = torch.randn(layers, int(prepared.repair_offsets.size), heads, dim, dtype=torch.bfloat16,
+                             device=gpu_device, generator=generator)
+    repaired_v = torch.randn_like(repaired_k)
+    write = prepared.prepare_write_repaired(repaired_k, repaired_v)
+    touched = prepared.maps.destination_slots
+    prepared.launch()
+    write()
+    torch.cuda.synchronize(gpu_device)
+    expected = [bits(k) for k in pool.k_buffer] + [bits(v) for v in pool.v_buffer]
+
+    stream = torch.cuda.Stream(device=gpu_device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            prepared.launch()
+            write()
+    torch.cuda.synchronize(gpu_device)
+    for replay in range(3):
+        for buffer in pool.k_buffer + pool.v_buffer:
+            buffer.index_fill_(0, touched, 0)  # eager work between replays
+        torch.cuda.synchronize(gpu_device)
+        graph.replay()
+        torch.cuda.synchronize(gpu_device)
+        actual = [bits(k) for k in pool.k_buffer] + [bits(v) for v in pool.v_buffer]
+        for a, b in zip(actual, expected):
+            assert np.array_equal(a, b), f"replay {replay}"

@@ -1,0 +1,182 @@
+"""Plan derivation, registry and executor map building against the reference's
+known answers (no GPU)."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from legolink_amd.errors import LinkRuntimeError
+from legolink_amd.link_plan import ResolvedLinkPlan, contiguous_ranges, resolve_link_plan
+from legolink_amd.link_runtime import KVLinkExecutor, KVPool
+from legolink_amd.registry import LegoLinkBlockRegistry
+from legolink_amd.rope import RotarySpec, build_cos_sin_cache
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+
+
+def test_contiguous_ranges_known_answer():
+    case = GOLDEN["contiguous_ranges"]
+    assert contiguous_ranges(case["input"]) == [tuple(r) for r in case["expected"]]
+    for rejected in case["rejected"]:
+        with pytest.raises(LinkRuntimeError, match="strictly increasing"):
+            contiguous_ranges(rejected)
+    assert contiguous_ranges([]) == []
+
+
+@pytest.mark.parametrize("case", GOLDEN["plan_derivation"]["cases"], ids=lambda c: c["name"])
+def test_plan_derivation_known_answers(case):
+    plan = {"cache_keys": list(case["cache_keys"]), **{k: v for k, v in case["link_plan"].items() if k != "normalized_layout"}}
+    if "block_ids" in case:
+        plan["block_ids"] = list(case["block_ids"])
+    linked = resolve_link_plan(case["blocks"], case["mutable_input_ids"], plan)
+    assert plan["imp_indices"] == case["expected_imp_indices"]
+    assert plan["kvlink"] == plan["imp_indices"]
+    if "expected_linked" in case:
+        assert linked == case["expected_linked"]
+    if "expected_mutable_start_token" in case:
+        assert plan["mutable_start_token"] == case["expected_mutable_start_token"]
+    if "expected_block_ranges" in case:
+        assert plan["block_ranges"] == case["expected_block_ranges"]
+    if "expected_block_starts" in case:
+        assert [r["start_token"] for r in plan["block_ranges"]] == case["expected_block_starts"]
+    assert plan["total_token_count"] == len(linked)
+
+
+def test_plan_is_deterministic_and_frozen():
+    blocks = {"a": [1, 2, 3], "b": [4, 5]}
+    plan_one = {"cache_keys": ["a", "b"], "recompute_initial_tokens": 1}
+    plan_two = dict(plan_one)
+    resolve_link_plan(blocks, [9], plan_one)
+    resolve_link_plan(lambda key: blocks.get(key), [9], plan_two)
+    assert plan_one == plan_two
+    frozen = ResolvedLinkPlan.freeze_ranges(plan_one["block_ranges"])
+    assert hash(frozen) == hash(ResolvedLinkPlan.freeze_ranges(plan_two["block_ranges"]))
+
+
+def test_plan_errors_follow_the_reference_messages():
+    with pytest.raises(LinkRuntimeError, match="cache_keys must be non-empty"):
+        resolve_link_plan({}, [1], {"cache_keys": []})
+    with pytest.raises(LinkRuntimeError, match="not compiled in this scheduler: x"):
+        resolve_link_plan({}, [1], {"cache_keys": ["x"]})
+    with pytest.raises(LinkRuntimeError, match="non-empty mutable query"):
+        resolve_link_plan({"a": [1]}, [], {"cache_keys": ["a"]})
+    with pytest.raises(LinkRuntimeError, match="one value per cache key"):
+        resolve_link_plan({"a": [1]}, [2], {"cache_keys": ["a"], "recompute_tokens_per_block": [1, 2]})
+    with pytest.raises(LinkRuntimeError, match="require the normalized physical token layout"):
+        resolve_link_plan({"a": [1], "b": [2]}, [3], {"cache_keys": ["a", "b"],
+                                                     "physical_interblock_fresh_token_counts": [1]})
+
+
+def test_interblock_gaps_are_recomputed_and_shift_later_blocks():
+    blocks = {"a": [10, 11], "b": [20, 21]}
+    plan = {"cache_keys": ["a", "b"], "recompute_initial_tokens": 1, "physical_prefix_token_count": 1,
+            "physical_interblock_fresh_token_counts": [2]}
+    linked = resolve_link_plan(blocks, [100, 50, 51, 30], plan)
+    assert linked == [100, 10, 11, 50, 51, 20, 21, 30]
+    assert [r["start_token"] for r in plan["block_ranges"]] == [1, 5]
+    assert plan["imp_indices"] == [0, 3, 4, 5, 7]
+
+
+def test_registry_lookup_pin_and_evict():
+    registry = LegoLinkBlockRegistry()
+    handle = registry.register_legolink_block("a", [1, 2, 3], torch.tensor([7, 8, 9]))
+    assert handle.compile_local_positions == (0, 1, 2)
+    with pytest.raises(ValueError, match="exact logical token length"):
+        registry.register_legolink_block("b", [1, 2], torch.tensor([1]))
+    with pytest.raises(ValueError, match="already registered"):
+        registry.register_legolink_block("a", [1], torch.tensor([1]))
+    result = registry.lookup_legolink_blocks(["a", "zz"])
+    assert result.missing_blocks == ["zz"] and list(result.matched_blocks) == ["a"]
+    registry.acquire_legolink_blocks(result.matched_handles)
+    assert not registry.evict_legolink_block("a")  # pinned
+    registry.release_legolink_blocks(result.matched_handles)
+    assert registry.evict_legolink_block("a")
+    assert registry.lookup_legolink_blocks(["a"]).stale_blocks == ["a"]
+    assert registry.get_legolink_block_tokens("a") is None
+    with pytest.raises(ValueError, match="not pinned"):
+        registry.release_legolink_blocks(result.matched_handles)
+
+
+def _executor(blocks, *, layers=1, compile_positions=None):
+    registry = LegoLinkBlockRegistry()
+    slot = 100
+    for key, count in blocks.items():
+        positions = None if compile_positions is None else compile_positions.get(key)
+        registry.register_legolink_block(key, list(range(count)), torch.arange(slot, slot + count),
+                                         compile_local_positions=positions)
+        slot += count
+    rotary = RotarySpec(build_cos_sin_cache(64, 8, theta=1e4), rotary_dim=8)
+    return KVLinkExecutor(registry, rotary, start_layer=0, end_layer=layers)
+
+
+@pytest.mark.parametrize("case", GOLDEN["first_block_remap"]["cases"], ids=lambda c: str(c["blocks"]))
+def test_remap_decision_follows_the_offset(case):
+    """tests/pic/test_first_block_rope_remap.py: a block is remapped iff its
+    request offset differs from its compile positions, never by its ordinal."""
+
+    blocks = {f"block-{i}": count for i, (_, count) in enumerate(case["blocks"])}
+    executor = _executor(blocks)
+    total = max(start + count for start, count in case["blocks"])
+    plan = {"cache_keys": list(blocks),
+            "block_ranges": [{"start_token": s, "end_token": s + c} for s, c in case["blocks"]]}
+    maps = executor.build_link_maps(torch.arange(total), plan)
+    assert [spec["needs_rope_remap"] for spec in maps.block_specs] == case["expected_remapped"]
+    first_count = case["blocks"][0][1]
+    assert maps.prefix_token_count == (0 if case["expected_remapped"][0] else first_count)
+
+
+def test_link_maps_follow_plan_order():
+    executor = _executor({"a": 3, "b": 2}, compile_positions={"b": [40, 41]})
+    destination = torch.arange(500, 510)
+    plan = {"cache_keys": ["b", "a"], "block_ranges": [{"start_token": 1, "end_token": 3},
+                                                       {"start_token": 3, "end_token": 6}],
+            "imp_indices": [0, 3, 4, 9]}
+    maps = executor.build_link_maps(destination, plan)
+    assert maps.source_slots.tolist() == [103, 104, 100, 101, 102]
+    assert maps.destination_slots.tolist() == [501, 502, 503, 504, 505]
+    assert maps.local_positions.tolist() == [40, 41, 0, 1, 2]
+    assert maps.global_positions.tolist() == [1, 2, 3, 4, 5]
+    assert maps.repair_offsets.tolist() == [2, 3]  # positions 3 and 4 fall inside block "a"
+    assert maps.prefix_token_count == 0
+
+
+def test_executor_errors():
+    executor = _executor({"a": 3})
+    plan = {"cache_keys": ["a", "missing"],
+            "block_ranges": [{"start_token": 0, "end_token": 3}, {"start_token": 3, "end_token": 4}]}
+    with pytest.raises(LinkRuntimeError, match="cannot safely link block\\(s\\): missing"):
+        executor.build_link_maps(torch.arange(8), plan)
+    with pytest.raises(LinkRuntimeError, match="token count mismatch for block a: plan=2, snapshot=3"):
+        executor.build_link_maps(torch.arange(8), {"cache_keys": ["a"],
+                                                   "block_ranges": [{"start_token": 0, "end_token": 2}]})
+    with pytest.raises(LinkRuntimeError, match="counts differ"):
+        executor.build_link_maps(torch.arange(8), {"cache_keys": ["a"], "block_ranges": [
+            {"start_token": 0, "end_token": 3}, {"start_token": 3, "end_token": 4}]})
+    with pytest.raises(LinkRuntimeError, match="missing block ranges"):
+        executor.build_link_maps(torch.arange(8), {"cache_keys": ["a"], "block_ranges": []})
+
+    class QuantizedPool:
+        dtype = torch.bfloat16
+        store_dtype = torch.uint8
+        def get_key_buffer(self, layer): ...
+        def get_value_buffer(self, layer): ...
+
+    with pytest.raises(LinkRuntimeError, match="quantized KV cache"):
+        executor.prepare_link(QuantizedPool(), torch.arange(8), {"cache_keys": ["a"]})
+    with pytest.raises(LinkRuntimeError, match="MHA-style KV pool"):
+        executor.prepare_link(object(), torch.arange(8), {"cache_keys": ["a"]})
+
+
+def test_cpu_pool_is_rejected_loudly():
+    executor = _executor({"a": 3})
+    pool = KVPool.allocate(num_slots=200, num_layers=1, num_heads=2, head_dim=8, device="cpu")
+    plan = {"cache_keys": ["a"], "block_ranges": [{"start_token": 2, "end_token": 5}]}
+    with pytest.raises(RuntimeError, match="cuda_tensors_required"):
+        executor.copy_linked_kv(pool, torch.arange(10), plan)
+    # the pin taken for the link is released on failure
+    assert executor.registry.lookup_legolink_blocks(["a"]).matched_handles[0].pin_count == 0
