@@ -52,6 +52,8 @@ def parse_args() -> argparse.Namespace:
                         help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
                         help="time a plain device copy of this many MiB instead of the link")
+    parser.add_argument("--ceiling", action="store_true",
+                        help="measure memory ceilings next to the link instead of the step")
     return parser.parse_args()
 
 
@@ -149,6 +151,94 @@ def cpu_baseline(workload, args) -> dict:
     }
 
 
+def _median_ms(torch, run, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    for start, end in events:
+        start.record()
+        run()
+        end.record()
+    torch.cuda.synchronize()
+    return sorted(s.elapsed_time(e) for s, e in events)[steps // 2]
+
+
+def ceiling(args: argparse.Namespace) -> None:
+    """The link next to pure-copy probes over the same rows: how close the
+    kernel is to what the memory system delivers for this access pattern."""
+
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from legolink_amd import _native, kv_link
+    from legolink_amd.build import PROBE_OUTPUT
+    from legolink_amd.rope import build_cos_sin_cache
+    from legolink_amd.workloads import make_workload
+
+    device = torch.device("cuda", 0)
+    _native.load_library()  # binds the HIP runtime torch loaded
+    probe = ctypes.CDLL(str(PROBE_OUTPUT))
+    probe.llp_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    probe.llp_row_copy.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_void_p]
+    workload = make_workload(args.workload)
+    shape = workload.shape
+    generator = torch.Generator(device=device).manual_seed(20260824)
+    keys = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                        device=device, generator=generator) for _ in range(shape.layers)]
+    values = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                          device=device, generator=generator) for _ in range(shape.layers)]
+    table = build_cos_sin_cache(workload.max_position + 1, workload.rotary_dim, theta=workload.theta).to(device)
+    maps = torch.from_numpy(np.stack([workload.source_slots, workload.destination_slots,
+                                      workload.local_positions, workload.global_positions])).to(device)
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)  # noqa: E731
+
+    def link_with_prefix(prefix: int) -> kv_link.PreparedKVLink:
+        return kv_link.PreparedKVLink(
+            key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+            local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table,
+            prefix_token_count=prefix, rotary_dim=workload.rotary_dim, is_neox_style=True,
+            layers_per_wave=args.layers_per_wave,
+        )
+
+    buffers = (ctypes.c_void_p * (2 * shape.layers))(*[b.data_ptr() for b in keys + values])
+
+    def row_copy() -> None:
+        rc = probe.llp_row_copy(buffers, 2 * shape.layers, maps[0].data_ptr(), maps[1].data_ptr(),
+                                workload.tokens, workload.num_slots, shape.row_bytes, stream())
+        if rc != 0:
+            raise RuntimeError(f"llp_row_copy failed ({rc})")
+
+    link_bytes = workload.tokens * shape.bytes_per_token
+    results = {}
+    for name, run in (("link", link_with_prefix(workload.prefix_token_count)),
+                      ("link_without_rotation", link_with_prefix(workload.tokens)),
+                      ("row_copy_probe", row_copy)):
+        ms = _median_ms(torch, run, args.steps, args.warmup)
+        results[name] = {"ms": round(ms, 5), "GBps": round(link_bytes / ms / 1e6, 1)}
+        log(f"{name}: {ms:.4f} ms, {link_bytes / ms / 1e6:.1f} GB/s")
+    del keys, values
+    torch.cuda.empty_cache()
+    nbytes = 4 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+
+    def stream_copy() -> None:
+        if probe.llp_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, stream()) != 0:
+            raise RuntimeError("llp_stream_copy failed")
+
+    ms = _median_ms(torch, stream_copy, args.steps, args.warmup)
+    results["stream_copy_4GiB"] = {"ms": round(ms, 5), "GBps": round(2 * nbytes / ms / 1e6, 1)}
+    ms = _median_ms(torch, lambda: dst.copy_(src), args.steps, args.warmup)
+    results["torch_copy_4GiB"] = {"ms": round(ms, 5), "GBps": round(2 * nbytes / ms / 1e6, 1)}
+    print(json.dumps({"ceiling": results, "workload": workload.name,
+                      "bytes_per_row_pass": link_bytes, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
+
+
 def load_traffic(link_launch_bytes: int) -> float | None:
     """HBM bytes per link launch from the committed rocprofv3 counter summary."""
 
@@ -170,6 +260,9 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         copy_calibration(args)
+        return 0
+    if args.ceiling:
+        ceiling(args)
         return 0
 
     import numpy as np

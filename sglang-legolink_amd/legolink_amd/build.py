@@ -20,6 +20,9 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 SOURCE = PACKAGE_DIR.parent / "csrc" / "legolink_kv.hip"
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
+# Memory-ceiling probes used by bench.py --ceiling (not part of the link ABI).
+PROBE_SOURCE = PACKAGE_DIR.parent / "csrc" / "row_copy_probe.hip"
+PROBE_OUTPUT = PACKAGE_DIR / "lib" / "librow_copy_probe.so"
 OFFLOAD_ARCH = "gfx950"
 
 
@@ -30,7 +33,7 @@ def hipcc_path() -> str:
     return candidate
 
 
-def compile_command(output: Path) -> list[str]:
+def compile_command(output: Path, source: Path = SOURCE) -> list[str]:
     return [
         hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
@@ -47,19 +50,25 @@ def compile_command(output: Path) -> list[str]:
         f"-I{INCLUDE_DIR}",
         "-o",
         str(output),
-        str(SOURCE),
+        str(source),
     ]
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile the library; the output is replaced atomically."""
+    """Compile the link library and the probe library; outputs are replaced atomically."""
 
-    OUTPUT.parent.mkdir(parents=True, exist_ok=True)
+    _compile(SOURCE, OUTPUT, verbose)
+    _compile(PROBE_SOURCE, PROBE_OUTPUT, verbose)
+    return OUTPUT
+
+
+def _compile(source: Path, output: Path, verbose: bool) -> None:
+    output.parent.mkdir(parents=True, exist_ok=True)
     with tempfile.NamedTemporaryFile(
-        dir=OUTPUT.parent, prefix=".liblegolink_kv.", suffix=".so.tmp", delete=False
+        dir=output.parent, prefix=f".{output.stem}.", suffix=".so.tmp", delete=False
     ) as handle:
         temporary = Path(handle.name)
-    command = compile_command(temporary)
+    command = compile_command(temporary, source)
     try:
         result = subprocess.run(command, capture_output=True, text=True)
         # hipcc's host pass does not know the packed-fp32 target feature; that
@@ -75,11 +84,10 @@ def build_library(verbose: bool = False) -> Path:
             )
         if verbose and messages:
             print("\n".join(messages), file=sys.stderr)
-        os.replace(temporary, OUTPUT)
+        os.replace(temporary, output)
     finally:
         if temporary.exists():
             temporary.unlink()
-    return OUTPUT
 
 
 if __name__ == "__main__":
