@@ -48,6 +48,7 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--cpu-reps", type=int, default=25)
     parser.add_argument("--layers-per-wave", type=int, default=0)
     parser.add_argument("--waves-per-block", type=int, default=4)
+    parser.add_argument("--layer-groups-per-block", type=int, default=0)
     parser.add_argument("--repair-rows", choices=["compact", "mask"], default="compact",
                         help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
@@ -202,7 +203,8 @@ def ceiling(args: argparse.Namespace) -> None:
             key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
             local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table,
             prefix_token_count=prefix, rotary_dim=workload.rotary_dim, is_neox_style=True,
-            layers_per_wave=args.layers_per_wave,
+            num_warps=args.waves_per_block, layers_per_wave=args.layers_per_wave,
+            layer_groups_per_block=args.layer_groups_per_block,
         )
 
     buffers = (ctypes.c_void_p * (2 * shape.layers))(*[b.data_ptr() for b in keys + values])
@@ -313,7 +315,7 @@ def main() -> int:
         local_positions=local, global_positions=glob, cos_sin_cache=table,
         prefix_token_count=prefix, rotary_dim=workload.rotary_dim,
         is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
-        layers_per_wave=args.layers_per_wave,
+        layers_per_wave=args.layers_per_wave, layer_groups_per_block=args.layer_groups_per_block,
     )
     scatter = kv_link.PreparedKVScatter(
         key_buffers=keys, value_buffers=values, destination_slots=repair_slots,

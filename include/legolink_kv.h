@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 1
+#define LL_ABI_VERSION 2
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -153,6 +153,8 @@ typedef struct ll_kv_link_args {
   int64_t kernel;                  /* LL_KERNEL_* */
   int64_t waves_per_block;         /* 0 = default; else 1, 2, 4 or 8 */
   int64_t layers_per_wave;         /* 0 = auto; else >= 1 */
+  int64_t layer_groups_per_block;  /* 0 = auto; else divides waves_per_block: waves of one
+                                      workgroup that take the same tokens' different layers */
 } ll_kv_link_args;
 
 /*
@@ -195,6 +197,7 @@ typedef struct ll_launch_info {
   int64_t grid_y;
   int64_t block_threads;
   int64_t layers_per_wave;
+  int64_t layer_groups_per_block;
 } ll_launch_info;
 
 int ll_kv_link(const ll_kv_link_args *args, ll_stream_t stream);

@@ -83,6 +83,7 @@ struct LinkParams {
   long long chunks_per_row;  // vector kernel: 16-byte chunks per K row (== per V row)
   int num_layers;            // layers in this launch
   int layers_per_wave;
+  int layer_groups_per_block;  // vector kernel: waves of a block that share a token
   int num_heads;
   int kdim;
   int vdim;
@@ -225,8 +226,12 @@ __device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const flo
 
 // ---------------------------------------------------------------------------
 // Vectorised link kernel.
-//   grid.x * (blockDim.x / 64) waves cover num_tokens * chunks_per_row chunks,
-//   grid.y splits the launch's layers into runs of layers_per_wave.
+//   Waves cover num_tokens * chunks_per_row chunks, 64 per wave; the launch's
+//   layers are split into groups of layers_per_wave.  A block of W waves holds
+//   W / G chunk-waves x G layer groups (G = layer_groups_per_block): its G waves
+//   of one chunk-wave read the same cos/sin rows, which then come from the
+//   CU's L1 instead of being fetched once per layer group.
+//   grid.x = chunk-waves / (W / G), grid.y = layer groups / G.
 // Requirements (checked on the host): key_head_dim == value_head_dim ==
 // rotary_dim == kD, fp32 cos/sin cache with unit column stride and 16-byte
 // aligned rows, 16-byte aligned layer buffers.
@@ -238,8 +243,11 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   constexpr int kHalf = kD / 2;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const long long wave =
-      static_cast<long long>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const int wave_in_block = threadIdx.x / kWave;
+  const int groups = p.layer_groups_per_block;
+  const long long wave = static_cast<long long>(blockIdx.x) * (blockDim.x / kWave / groups) +
+                         wave_in_block / groups;
+  const int layer_group = blockIdx.y * groups + wave_in_block % groups;
   const long long g = wave * kWave + lane;
   const long long C = p.chunks_per_row;
   const bool in_range = g < p.num_tokens * C;
@@ -292,7 +300,7 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     for (int e = 0; e < kPairs; ++e) dsn[e] = second_half ? ds[e] : -ds[e];
   }
 
-  const int l0 = blockIdx.y * p.layers_per_wave;
+  const int l0 = layer_group * p.layers_per_wave;
   const int l1 = min(l0 + p.layers_per_wave, p.num_layers);
   const long long k_src = src * p.k_row_bytes + c * 16;
   const long long k_dst = dst * p.k_row_bytes + c * 16;
@@ -533,6 +541,10 @@ int validate_link(const ll_kv_link_args *a) {
       a->waves_per_block != 4 && a->waves_per_block != 8)
     return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0, 1, 2, 4 or 8");
   if (a->layers_per_wave < 0) return fail(LL_ERR_LAUNCH_CONFIG, "layers_per_wave is negative");
+  if (a->layer_groups_per_block < 0 ||
+      (a->layer_groups_per_block > 0 &&
+       ((a->waves_per_block ? a->waves_per_block : 4) % a->layer_groups_per_block) != 0))
+    return fail(LL_ERR_LAUNCH_CONFIG, "layer_groups_per_block must divide waves_per_block");
   return LL_OK;
 }
 
@@ -552,17 +564,19 @@ struct LinkPlan {
   int block_threads;
   long long grid_x;
   int layers_per_wave;  // vector kernel
+  int layer_groups_per_block;  // vector kernel
   int launches;
 };
 
 // Launch shape of the vector kernel.  Short runs of layers per wave keep the
-// GPU's in-flight rows within few layer buffers at a time; measured on gfx950
-// (random 1 KB rows, 28 layers): 2 layers per wave beats one wave walking all
-// layers by 2-3 %, and by 20 % when blocks are shared between tokens.  Links
-// too small to fill the GPU with 2-layer waves are split to about
-// kTargetWaves waves instead.
+// GPU's in-flight rows within few layer buffers at a time.  Measured on gfx950
+// (random 1 KB rows, interleaved A/B in one process): 4 layers per wave beats
+// one wave walking all 28 layers by 2-8 % and 2 layers per wave by 1-3 %, and
+// by 12 % when links share source blocks; on one of the boxes measured, 2 was
+// 1.8 % ahead of 4 on the 32k-token link.  Links too small to fill the GPU
+// with such waves are split to about kTargetWaves waves instead.
 constexpr long long kTargetWaves = 16384;  // 64 waves per CU on 256 CUs
-constexpr int kDefaultLayersPerWave = 2;
+constexpr int kDefaultLayersPerWave = 4;
 
 int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   const bool fits = vector_kernel_fits(a);
@@ -579,7 +593,11 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   if (plan->kernel == LL_KERNEL_VECTOR) {
     const long long chunks = a->num_heads * a->key_head_dim / 8;
     const long long waves_x = (a->num_tokens * chunks + kWave - 1) / kWave;
-    plan->grid_x = (waves_x + waves_per_block - 1) / waves_per_block;
+    const int groups_per_block =
+        a->layer_groups_per_block ? static_cast<int>(a->layer_groups_per_block) : 1;
+    plan->layer_groups_per_block = groups_per_block;
+    const int chunk_waves_per_block = waves_per_block / groups_per_block;
+    plan->grid_x = (waves_x + chunk_waves_per_block - 1) / chunk_waves_per_block;
     int lpw = static_cast<int>(a->layers_per_wave);
     if (lpw == 0) {
       if (waves_x * ((layers_first + kDefaultLayersPerWave - 1) / kDefaultLayersPerWave) >=
@@ -596,6 +614,7 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   } else {
     plan->grid_x = a->num_tokens < 65536 ? a->num_tokens : 65536;
     plan->layers_per_wave = 1;
+    plan->layer_groups_per_block = 1;
   }
   if (plan->grid_x > 0x7fffffffLL) return fail(LL_ERR_LAUNCH_CONFIG, "link too large for one grid");
   return LL_OK;
@@ -674,11 +693,13 @@ int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info) {
   info->kernel = plan.kernel;
   info->launches = plan.launches;
   info->grid_x = plan.grid_x;
+  const int layer_groups = (layers_first + plan.layers_per_wave - 1) / plan.layers_per_wave;
   info->grid_y = plan.kernel == LL_KERNEL_VECTOR
-                     ? (layers_first + plan.layers_per_wave - 1) / plan.layers_per_wave
+                     ? (layer_groups + plan.layer_groups_per_block - 1) / plan.layer_groups_per_block
                      : layers_first;
   info->block_threads = plan.block_threads;
   info->layers_per_wave = plan.layers_per_wave;
+  info->layer_groups_per_block = plan.layer_groups_per_block;
   return LL_OK;
 }
 
@@ -731,11 +752,16 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
     if (plan.kernel == LL_KERNEL_VECTOR) {
       const int lpw = plan.layers_per_wave < n ? plan.layers_per_wave : n;
       p.layers_per_wave = lpw;
-      const dim3 grid(static_cast<unsigned>(plan.grid_x), static_cast<unsigned>((n + lpw - 1) / lpw));
+      p.layer_groups_per_block = plan.layer_groups_per_block;
+      const int layer_groups = (n + lpw - 1) / lpw;
+      const dim3 grid(static_cast<unsigned>(plan.grid_x),
+                      static_cast<unsigned>((layer_groups + plan.layer_groups_per_block - 1) /
+                                            plan.layer_groups_per_block));
       if (bf16) launch_vec<true>(p.kdim, grid, block, s, p, p.neox != 0);
       else launch_vec<false>(p.kdim, grid, block, s, p, p.neox != 0);
     } else {
       p.layers_per_wave = 1;
+      p.layer_groups_per_block = 1;
       const dim3 grid(static_cast<unsigned>(plan.grid_x), static_cast<unsigned>(n));
       if (bf16) launch_generic<2>(static_cast<int>(a->cos_sin_dtype), grid, block, s, p);
       else launch_generic<1>(static_cast<int>(a->cos_sin_dtype), grid, block, s, p);

@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -91,6 +91,7 @@ class LinkArgs(ctypes.Structure):
         ("kernel", _i64),
         ("waves_per_block", _i64),
         ("layers_per_wave", _i64),
+        ("layer_groups_per_block", _i64),
     ]
 
 
@@ -128,6 +129,7 @@ class LaunchInfo(ctypes.Structure):
         ("grid_y", _i64),
         ("block_threads", _i64),
         ("layers_per_wave", _i64),
+        ("layer_groups_per_block", _i64),
     ]
 
 

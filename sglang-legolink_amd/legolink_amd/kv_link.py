@@ -321,6 +321,7 @@ def _link_args(
     waves_per_block: int,
     layers_per_wave: int,
     kernel: int,
+    layer_groups_per_block: int = 0,
 ) -> tuple[_native.LinkArgs, tuple[Any, ...]]:
     key_table = _native.pointer_table([buffer.data_ptr() for buffer in key_buffers])
     value_table = _native.pointer_table([buffer.data_ptr() for buffer in value_buffers])
@@ -357,6 +358,7 @@ def _link_args(
     args.kernel = int(kernel)
     args.waves_per_block = int(waves_per_block)
     args.layers_per_wave = int(layers_per_wave)
+    args.layer_groups_per_block = int(layer_groups_per_block)
     # The pointer tables must outlive the call.
     return args, (key_table, value_table)
 
@@ -399,6 +401,7 @@ class PreparedKVLink:
         layers_per_wave: int = 0,
         kernel: int = _native.KERNEL_AUTO,
         validate_indices: bool = False,
+        layer_groups_per_block: int = 0,
     ) -> None:
         key_buffers = list(key_buffers)
         value_buffers = list(value_buffers)
@@ -460,6 +463,7 @@ class PreparedKVLink:
             self.launch_config.num_warps,
             layers_per_wave,
             kernel,
+            layer_groups_per_block,
         )
         self._args.struct_size = ctypes.sizeof(_native.LinkArgs)
         # Keep every tensor the argument block points at alive.
@@ -479,6 +483,7 @@ class PreparedKVLink:
             "grid_y": int(info.grid_y),
             "block_threads": int(info.block_threads),
             "layers_per_wave": int(info.layers_per_wave),
+            "layer_groups_per_block": int(info.layer_groups_per_block),
         }
         self._lib = _native.load_library()
         self._args_ref = ctypes.byref(self._args)
@@ -526,6 +531,7 @@ def fused_kv_link_layers_inplace(
     layers_per_wave: int = 0,
     kernel: int = _native.KERNEL_AUTO,
     validate_indices: bool = False,
+    layer_groups_per_block: int = 0,
 ) -> None:
     """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
     64 layers, on the current stream.  Per layer the result equals
@@ -549,6 +555,7 @@ def fused_kv_link_layers_inplace(
         layers_per_wave=layers_per_wave,
         kernel=kernel,
         validate_indices=validate_indices,
+        layer_groups_per_block=layer_groups_per_block,
     )
     prepared()
 
@@ -613,6 +620,7 @@ def describe_link_launch(
     num_warps: int = 4,
     layers_per_wave: int = 0,
     kernel: int = _native.KERNEL_AUTO,
+    layer_groups_per_block: int = 0,
 ) -> dict[str, int]:
     """Kernel and launch shape the link would use (no GPU work, no device needed)."""
 
@@ -633,6 +641,7 @@ def describe_link_launch(
         num_warps,
         layers_per_wave,
         kernel,
+        layer_groups_per_block,
     )
     info = _native.kv_link_describe(args)
     del keepalive
@@ -643,6 +652,7 @@ def describe_link_launch(
         "grid_y": int(info.grid_y),
         "block_threads": int(info.block_threads),
         "layers_per_wave": int(info.layers_per_wave),
+        "layer_groups_per_block": int(info.layer_groups_per_block),
     }
 
 

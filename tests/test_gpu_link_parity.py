@@ -319,3 +319,37 @@ def test_full_size_workload(gpu_device, name, sample):
 def test_full_size_workload_generic_kernel(gpu_device):
     result = check_workload(make_workload("c1"), gpu_device, kernel=GENERIC)
     assert result["mismatches"] == 0
+
+
+@pytest.mark.parametrize("waves,groups,layers_per_wave", [(4, 2, 2), (4, 4, 1), (4, 4, 3), (8, 8, 1), (2, 2, 4)])
+def test_layer_groups_per_block_shapes_match_oracle(gpu_device, waves, groups, layers_per_wave):
+    """Blocks whose waves share tokens across layer groups (7 layers, so the last
+    group is partial and some waves have no layer) give the same pool."""
+
+    layers, slots, tokens = 7, 900, 300
+    rng = np.random.default_rng(17)
+    perm = rng.permutation(slots)
+    src_np, dst_np = perm[:tokens], perm[tokens : 2 * tokens]
+    local_np = rng.integers(0, 4096, size=tokens)
+    global_np = rng.integers(0, 4096, size=tokens)
+    mask_np = (rng.random(tokens) < 0.1).astype(np.uint8)
+    keys, values = make_pool(layers, slots, 4, 128, 128, torch.bfloat16, gpu_device, 17)
+    table = build_cos_sin_cache(4096, 128)
+    expected_k, expected_v = ko.link_pool(
+        [bits(k) for k in keys], [bits(v) for v in values], src_np, dst_np, local_np, global_np,
+        table.numpy(), key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=128, neox=True, prefix=9,
+        repair_mask=mask_np,
+    )
+    maps = [torch.from_numpy(a).to(gpu_device) for a in (src_np, dst_np, local_np, global_np, mask_np)]
+    link = kv_link.PreparedKVLink(
+        key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+        local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table.to(gpu_device),
+        prefix_token_count=9, rotary_dim=128, is_neox_style=True, repair_mask=maps[4],
+        num_warps=waves, layers_per_wave=layers_per_wave, layer_groups_per_block=groups,
+    )
+    assert link.launch["layer_groups_per_block"] == groups
+    link()
+    torch.cuda.synchronize(gpu_device)
+    for layer in range(layers):
+        assert np.array_equal(bits(keys[layer]), expected_k[layer]), f"K layer {layer}"
+        assert np.array_equal(bits(values[layer]), expected_v[layer]), f"V layer {layer}"

@@ -106,7 +106,7 @@ def test_kernel_choice_and_launch_shape():
     info = _native.kv_link_describe(args)
     assert info.kernel == _native.KERNEL_VECTOR
     assert info.block_threads == 256 and info.grid_x == 32768 // 4
-    assert info.layers_per_wave == 2 and info.grid_y == 1  # two layers in the CPU pool
+    assert info.layers_per_wave == 2 and info.grid_y == 1  # capped by the two layers of the CPU pool
     del keepalive
     # Partial rotary falls back to the generic kernel; forcing the vector kernel fails.
     args, keepalive = _cpu_args(rotary_dim=64)
