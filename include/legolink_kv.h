@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 2
+#define LL_ABI_VERSION 3
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -95,11 +95,13 @@ enum {
 };
 
 /*
- * Link: for every token t in [0, num_tokens) and every layer l:
+ * Link: for every token t in [0, num_tokens) and every layer l, with S_l the
+ * source buffers (source_key_layers / source_value_layers, or the destination
+ * pool's own buffers when those tables are NULL):
  *     if repair_mask != NULL and repair_mask[t] != 0: nothing is written;
- *     V_l[destination_slots[t]] = V_l[source_slots[t]]                    (bit copy)
- *     K_l[destination_slots[t]] = K_l[source_slots[t]]   if t <  prefix_token_count (bit copy)
- *     K_l[destination_slots[t]] = rerotate(K_l[source_slots[t]],
+ *     V_l[destination_slots[t]] = SV_l[source_slots[t]]                    (bit copy)
+ *     K_l[destination_slots[t]] = SK_l[source_slots[t]]  if t <  prefix_token_count (bit copy)
+ *     K_l[destination_slots[t]] = rerotate(SK_l[source_slots[t]],
  *                                          local_positions[t] -> global_positions[t])
  *                                                        if t >= prefix_token_count
  * rerotate applies, per rotary pair i of every head, the delta rotation
@@ -118,7 +120,11 @@ enum {
  * (patched_sglang_files/python/sglang/srt/legolink_triton.py:550-645), and with
  * num_layers == L the per-layer loop that calls it
  * (patched_sglang_files/python/sglang/srt/pic_runtime.py:5168-5208): one launch
- * covers up to 64 layers.
+ * covers up to 64 layers.  With a separate source pool it also replaces the
+ * clone-mode snapshot copy (pic_runtime.py:3519-3527, prefix = all tokens), the
+ * link from clone snapshots (pic_runtime.py:5553-5567) and, with the position
+ * vectors swapped, the global -> local copy of group promotion
+ * (pic_runtime.py:5901-5922).
  */
 typedef struct ll_kv_link_args {
   int64_t struct_size;             /* sizeof(ll_kv_link_args) */
@@ -155,6 +161,10 @@ typedef struct ll_kv_link_args {
   int64_t layers_per_wave;         /* 0 = auto; else >= 1 */
   int64_t layer_groups_per_block;  /* 0 = auto; else divides waves_per_block: waves of one
                                       workgroup that take the same tokens' different layers */
+  void *const *source_key_layers;  /* host array [num_layers] of device pointers, or NULL:
+                                      read sources from key_layers */
+  void *const *source_value_layers;/* host array [num_layers], or NULL (with source_key_layers) */
+  int64_t source_num_slots;        /* rows of every source buffer (when the tables are set) */
 } ll_kv_link_args;
 
 /*

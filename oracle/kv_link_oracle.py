@@ -277,18 +277,25 @@ def link_pool(
     prefix: int,
     repair_mask: np.ndarray | None = None,
     rerotate=rerotate_rows_c,
+    source_key_layers: list[np.ndarray] | None = None,
+    source_value_layers: list[np.ndarray] | None = None,
 ) -> tuple[list[np.ndarray], list[np.ndarray]]:
-    """Expected pool after the link; the inputs are not modified."""
+    """Expected pool after the link; the inputs are not modified.  Source rows
+    come from ``source_*_layers`` when given, else from the pool itself."""
 
     src = np.asarray(src, dtype=np.int64)
     dst = np.asarray(dst, dtype=np.int64)
     keep = np.ones(src.shape[0], dtype=bool)
     if repair_mask is not None:
         keep = np.asarray(repair_mask) == 0
+    source_key_layers = key_layers if source_key_layers is None else source_key_layers
+    source_value_layers = value_layers if source_value_layers is None else source_value_layers
     out_k, out_v = [], []
-    for key, value in zip(key_layers, value_layers):
+    for key, value, source_key, source_value in zip(
+        key_layers, value_layers, source_key_layers, source_value_layers
+    ):
         rows = rerotate(
-            key[src],
+            source_key[src],
             local,
             global_,
             cache,
@@ -301,7 +308,7 @@ def link_pool(
         new_k = key.copy()
         new_v = value.copy()
         new_k[dst[keep]] = rows[keep]
-        new_v[dst[keep]] = value[src[keep]]
+        new_v[dst[keep]] = source_value[src[keep]]
         out_k.append(new_k)
         out_v.append(new_v)
     return out_k, out_v

@@ -64,8 +64,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // without a device-side table allocation).
 // ---------------------------------------------------------------------------
 struct LinkParams {
-  char *k_layers[kMaxLayersPerLaunch];
+  char *k_layers[kMaxLayersPerLaunch];   // destination rows
   char *v_layers[kMaxLayersPerLaunch];
+  const char *sk_layers[kMaxLayersPerLaunch];  // source rows (the same buffers, or another pool)
+  const char *sv_layers[kMaxLayersPerLaunch];
   const void *src;
   const void *dst;
   const void *lpos;
@@ -73,7 +75,8 @@ struct LinkParams {
   const unsigned char *mask;
   const void *cs;
   long long num_tokens;
-  long long num_slots;
+  long long num_slots;       // destination rows per layer
+  long long src_num_slots;   // source rows per layer
   long long cs_rows;
   long long cs_stride_row;
   long long cs_stride_col;
@@ -259,7 +262,7 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
 
   const long long src = load_index(p.src, p.idx64 & 1, t);
   const long long dst = load_index(p.dst, p.idx64 & 2, t);
-  bool ok = in_range && src >= 0 && src < p.num_slots && dst >= 0 && dst < p.num_slots;
+  bool ok = in_range && src >= 0 && src < p.src_num_slots && dst >= 0 && dst < p.num_slots;
   if (p.mask != nullptr) ok = ok && (p.mask[t] == 0);
   const bool remap = t >= p.prefix;
 
@@ -315,8 +318,8 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
       kin[u] = u32x4{0u, 0u, 0u, 0u};
       vin[u] = u32x4{0u, 0u, 0u, 0u};
       if (ok && l + u < l1) {
-        kin[u] = *reinterpret_cast<const u32x4 *>(p.k_layers[l + u] + k_src);
-        vin[u] = *reinterpret_cast<const u32x4 *>(p.v_layers[l + u] + v_src);
+        kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[l + u] + k_src);
+        vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[l + u] + v_src);
       }
     }
 #pragma unroll
@@ -365,9 +368,9 @@ __device__ __forceinline__ uint16_t f32_to_key(float f) {
 template <int kKey, int kCache>
 __global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p) {
   const int layer = blockIdx.y;
-  const uint16_t *kbase = reinterpret_cast<const uint16_t *>(p.k_layers[layer]);
+  const uint16_t *kbase = reinterpret_cast<const uint16_t *>(p.sk_layers[layer]);
   uint16_t *kout = reinterpret_cast<uint16_t *>(p.k_layers[layer]);
-  const uint16_t *vbase = reinterpret_cast<const uint16_t *>(p.v_layers[layer]);
+  const uint16_t *vbase = reinterpret_cast<const uint16_t *>(p.sv_layers[layer]);
   uint16_t *vout = reinterpret_cast<uint16_t *>(p.v_layers[layer]);
   const int half = p.rotary_dim / 2;
   const int rot_items = p.num_heads * half;
@@ -381,7 +384,7 @@ __global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p
   for (long long t = blockIdx.x; t < p.num_tokens; t += gridDim.x) {
     const long long src = load_index(p.src, p.idx64 & 1, t);
     const long long dst = load_index(p.dst, p.idx64 & 2, t);
-    if (src < 0 || src >= p.num_slots || dst < 0 || dst >= p.num_slots) continue;
+    if (src < 0 || src >= p.src_num_slots || dst < 0 || dst >= p.num_slots) continue;
     if (p.mask != nullptr && p.mask[t] != 0) continue;
     const bool remap = t >= p.prefix;
     long long lp = 0, gp = 0;
@@ -505,6 +508,16 @@ int validate_link(const ll_kv_link_args *a) {
   for (int64_t l = 0; l < a->num_layers; ++l)
     if (a->key_layers[l] == nullptr || a->value_layers[l] == nullptr)
       return fail(LL_ERR_INVALID_ARGUMENT, "layer %lld buffer is NULL", static_cast<long long>(l));
+  if ((a->source_key_layers == nullptr) != (a->source_value_layers == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "source key and value layer tables must both be set or both NULL");
+  if (a->source_key_layers != nullptr) {
+    for (int64_t l = 0; l < a->num_layers; ++l)
+      if (a->source_key_layers[l] == nullptr || a->source_value_layers[l] == nullptr)
+        return fail(LL_ERR_INVALID_ARGUMENT, "source layer %lld buffer is NULL",
+                    static_cast<long long>(l));
+    if (a->source_num_slots < 0)
+      return fail(LL_ERR_INVALID_ARGUMENT, "source_num_slots is negative");
+  }
   if (a->num_slots < 0) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots is negative");
   if (a->num_heads < 1)
     return fail(LL_ERR_MHA_3D_KV_BUFFERS_REQUIRED, "num_heads must be >= 1");
@@ -556,6 +569,9 @@ bool vector_kernel_fits(const ll_kv_link_args *a) {
   if ((a->cos_sin_stride_row % 4) != 0 || !aligned16(a->cos_sin_cache)) return false;
   for (int64_t l = 0; l < a->num_layers; ++l)
     if (!aligned16(a->key_layers[l]) || !aligned16(a->value_layers[l])) return false;
+  if (a->source_key_layers != nullptr)
+    for (int64_t l = 0; l < a->num_layers; ++l)
+      if (!aligned16(a->source_key_layers[l]) || !aligned16(a->source_value_layers[l])) return false;
   return true;
 }
 
@@ -721,6 +737,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.cs = a->cos_sin_cache;
   p.num_tokens = a->num_tokens;
   p.num_slots = a->num_slots;
+  p.src_num_slots = a->source_key_layers != nullptr ? a->source_num_slots : a->num_slots;
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;
@@ -747,6 +764,11 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
     for (int l = 0; l < n; ++l) {
       p.k_layers[l] = static_cast<char *>(a->key_layers[base + l]);
       p.v_layers[l] = static_cast<char *>(a->value_layers[base + l]);
+      const bool own = a->source_key_layers == nullptr;
+      p.sk_layers[l] = static_cast<const char *>(own ? a->key_layers[base + l]
+                                                      : a->source_key_layers[base + l]);
+      p.sv_layers[l] = static_cast<const char *>(own ? a->value_layers[base + l]
+                                                      : a->source_value_layers[base + l]);
     }
     p.num_layers = n;
     if (plan.kernel == LL_KERNEL_VECTOR) {

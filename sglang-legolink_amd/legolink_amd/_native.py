@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -92,6 +92,9 @@ class LinkArgs(ctypes.Structure):
         ("waves_per_block", _i64),
         ("layers_per_wave", _i64),
         ("layer_groups_per_block", _i64),
+        ("source_key_layers", _ptr),
+        ("source_value_layers", _ptr),
+        ("source_num_slots", _i64),
     ]
 
 

@@ -177,16 +177,26 @@ def _eligibility(
     cos_sin_cache: torch.Tensor,
     rotary_dim: int,
     repair_mask: torch.Tensor | None,
+    source_key_buffers: Sequence[torch.Tensor] = (),
+    source_value_buffers: Sequence[torch.Tensor] = (),
 ) -> LegoLinkFusionEligibility:
     """The reference's checks in the reference's order (legolink_triton.py:159-247),
-    applied to every layer, followed by the checks the raw-pointer kernels need."""
+    applied to every layer (and to a separate source pool, which must have the
+    destination pool's row layout), followed by the checks the raw-pointer
+    kernels need."""
 
     if not _native.library_available():
         return LegoLinkFusionEligibility(False, NATIVE_UNAVAILABLE_REASON)
     key_buffer, value_buffer = key_buffers[0], value_buffers[0]
+    if len(source_key_buffers) != len(source_value_buffers) or (
+        source_key_buffers and len(source_key_buffers) != len(key_buffers)
+    ):
+        return LegoLinkFusionEligibility(False, "kv_head_layout_mismatch")
     tensors = (
         *key_buffers,
         *value_buffers,
+        *source_key_buffers,
+        *source_value_buffers,
         source_slots,
         destination_slots,
         local_positions,
@@ -204,9 +214,23 @@ def _eligibility(
             return LegoLinkFusionEligibility(False, "kv_head_layout_mismatch")
         if key.dtype != value.dtype or key.dtype != key_buffer.dtype:
             return LegoLinkFusionEligibility(False, "kv_dtype_mismatch")
+    if source_key_buffers:
+        source_rows = int(source_key_buffers[0].shape[0]) if source_key_buffers[0].ndim == 3 else -1
+        for key, value in zip(source_key_buffers, source_value_buffers, strict=True):
+            if key.ndim != 3 or value.ndim != 3:
+                return LegoLinkFusionEligibility(False, "mha_3d_kv_buffers_required")
+            if key.shape[1:] != key_buffer.shape[1:] or value.shape[1:] != value_buffer.shape[1:] or (
+                int(key.shape[0]) != source_rows or int(value.shape[0]) != source_rows
+            ):
+                return LegoLinkFusionEligibility(False, "kv_head_layout_mismatch")
+            if key.dtype != key_buffer.dtype or value.dtype != key_buffer.dtype:
+                return LegoLinkFusionEligibility(False, "kv_dtype_mismatch")
     if key_buffer.dtype not in (torch.float16, torch.bfloat16):
         return LegoLinkFusionEligibility(False, "fp16_or_bf16_required")
-    if not all(buffer.is_contiguous() for buffer in (*key_buffers, *value_buffers)):
+    if not all(
+        buffer.is_contiguous()
+        for buffer in (*key_buffers, *value_buffers, *source_key_buffers, *source_value_buffers)
+    ):
         return LegoLinkFusionEligibility(False, "contiguous_kv_buffers_required")
     key_head_dim = int(key_buffer.shape[-1])
     value_head_dim = int(value_buffer.shape[-1])
@@ -293,11 +317,12 @@ def _validate_index_ranges(
     global_positions: torch.Tensor,
     cache_rows: int,
     prefix_token_count: int,
+    source_num_slots: int | None = None,
 ) -> None:
     """Optional host check (synchronises): the kernels skip out-of-range rows."""
 
     for name, tensor, limit in (
-        ("source_slots", source_slots, num_slots),
+        ("source_slots", source_slots, num_slots if source_num_slots is None else source_num_slots),
         ("destination_slots", destination_slots, num_slots),
         ("local_positions", local_positions[prefix_token_count:], cache_rows),
         ("global_positions", global_positions[prefix_token_count:], cache_rows),
@@ -322,9 +347,17 @@ def _link_args(
     layers_per_wave: int,
     kernel: int,
     layer_groups_per_block: int = 0,
+    source_key_buffers: Sequence[torch.Tensor] = (),
+    source_value_buffers: Sequence[torch.Tensor] = (),
 ) -> tuple[_native.LinkArgs, tuple[Any, ...]]:
     key_table = _native.pointer_table([buffer.data_ptr() for buffer in key_buffers])
     value_table = _native.pointer_table([buffer.data_ptr() for buffer in value_buffers])
+    source_tables: tuple[Any, ...] = ()
+    if source_key_buffers:
+        source_tables = (
+            _native.pointer_table([buffer.data_ptr() for buffer in source_key_buffers]),
+            _native.pointer_table([buffer.data_ptr() for buffer in source_value_buffers]),
+        )
     key_buffer, value_buffer = key_buffers[0], value_buffers[0]
     args = _native.LinkArgs()
     args.num_layers = len(key_buffers)
@@ -359,8 +392,12 @@ def _link_args(
     args.waves_per_block = int(waves_per_block)
     args.layers_per_wave = int(layers_per_wave)
     args.layer_groups_per_block = int(layer_groups_per_block)
+    if source_tables:
+        args.source_key_layers = ctypes_address(source_tables[0])
+        args.source_value_layers = ctypes_address(source_tables[1])
+        args.source_num_slots = int(source_key_buffers[0].shape[0])
     # The pointer tables must outlive the call.
-    return args, (key_table, value_table)
+    return args, (key_table, value_table, *source_tables)
 
 
 def ctypes_address(array: Any) -> int:
@@ -402,9 +439,13 @@ class PreparedKVLink:
         kernel: int = _native.KERNEL_AUTO,
         validate_indices: bool = False,
         layer_groups_per_block: int = 0,
+        source_key_buffers: Sequence[torch.Tensor] | None = None,
+        source_value_buffers: Sequence[torch.Tensor] | None = None,
     ) -> None:
         key_buffers = list(key_buffers)
         value_buffers = list(value_buffers)
+        source_key_buffers = list(source_key_buffers or ())
+        source_value_buffers = list(source_value_buffers or ())
         if not key_buffers or len(key_buffers) != len(value_buffers):
             raise ValueError("key_buffers and value_buffers must be equal-length, non-empty")
         eligibility = _eligibility(
@@ -417,6 +458,8 @@ class PreparedKVLink:
             cos_sin_cache,
             rotary_dim,
             repair_mask,
+            source_key_buffers,
+            source_value_buffers,
         )
         if not eligibility.supported:
             _raise_unavailable(eligibility.reason)
@@ -445,6 +488,7 @@ class PreparedKVLink:
                 global_positions,
                 int(cos_sin_cache.shape[0]),
                 int(prefix_token_count),
+                int(source_key_buffers[0].shape[0]) if source_key_buffers else None,
             )
         if repair_mask is not None and repair_mask.dtype == torch.bool:
             repair_mask = repair_mask.view(torch.uint8)
@@ -464,12 +508,15 @@ class PreparedKVLink:
             layers_per_wave,
             kernel,
             layer_groups_per_block,
+            source_key_buffers,
+            source_value_buffers,
         )
         self._args.struct_size = ctypes.sizeof(_native.LinkArgs)
         # Keep every tensor the argument block points at alive.
         self._tensors = (
             key_buffers, value_buffers, source_slots, destination_slots,
             local_positions, global_positions, cos_sin_cache, repair_mask,
+            source_key_buffers, source_value_buffers,
         )
         self.device = key_buffer.device
         try:
@@ -532,10 +579,14 @@ def fused_kv_link_layers_inplace(
     kernel: int = _native.KERNEL_AUTO,
     validate_indices: bool = False,
     layer_groups_per_block: int = 0,
+    source_key_buffers: Sequence[torch.Tensor] | None = None,
+    source_value_buffers: Sequence[torch.Tensor] | None = None,
 ) -> None:
     """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
     64 layers, on the current stream.  Per layer the result equals
-    ``fused_kv_link_inplace``."""
+    ``fused_kv_link_inplace``.  With ``source_key_buffers``/``source_value_buffers``
+    (one per layer, same row layout) the source rows are read from that pool
+    instead of the destination pool."""
 
     prepared = PreparedKVLink(
         key_buffers=key_buffers,
@@ -556,6 +607,8 @@ def fused_kv_link_layers_inplace(
         kernel=kernel,
         validate_indices=validate_indices,
         layer_groups_per_block=layer_groups_per_block,
+        source_key_buffers=source_key_buffers,
+        source_value_buffers=source_value_buffers,
     )
     prepared()
 

@@ -24,9 +24,12 @@ import torch
 class LegoLinkBlockHandle:
     cache_key: str
     token_ids: tuple[int, ...]
-    kv_slots: torch.Tensor                 # int64 [token_count], pool slots holding the block's K/V
+    kv_slots: torch.Tensor                 # int64 [token_count], slots holding the block's K/V
     compile_local_positions: tuple[int, ...]  # RoPE positions the cached K carries
     block_id: str = ""
+    # "reference": kv_slots index the KV pool; "clone": they index the snapshot
+    # arena the block was copied into (pic_runtime.py:1985-1991, :3519-3527).
+    storage_mode: str = "reference"
     pin_count: int = 0
     generation: int = 0
     valid: bool = True
@@ -62,6 +65,7 @@ class LegoLinkBlockRegistry:
         *,
         compile_local_positions: Optional[Sequence[int]] = None,
         block_id: Optional[str] = None,
+        storage_mode: str = "reference",
     ) -> LegoLinkBlockHandle:
         token_ids = tuple(int(token) for token in token_ids)
         slots = torch.as_tensor(kv_slots).long().reshape(-1).clone()
@@ -74,6 +78,8 @@ class LegoLinkBlockRegistry:
         )
         if len(positions) != len(token_ids):
             raise ValueError("compile_local_positions must hold one position per token.")
+        if storage_mode not in ("reference", "clone"):
+            raise ValueError(f"Unsupported PIC storage mode: {storage_mode}")
         with self._lock:
             resident = self._blocks.get(str(cache_key))
             if resident is not None and resident.valid:
@@ -86,6 +92,7 @@ class LegoLinkBlockRegistry:
                 compile_local_positions=positions,
                 block_id=str(block_id or cache_key),
                 generation=self._generation,
+                storage_mode=storage_mode,
             )
             self._blocks[str(cache_key)] = handle
             return handle
@@ -123,13 +130,14 @@ class LegoLinkBlockRegistry:
                     raise ValueError(f"LegoLink block {handle.cache_key} is not pinned.")
                 handle.pin_count -= 1
 
-    def evict_legolink_block(self, cache_key: str) -> bool:
-        """Invalidate an unpinned block; pinned blocks stay resident."""
+    def evict_legolink_block(self, cache_key: str) -> Optional[LegoLinkBlockHandle]:
+        """Invalidate an unpinned block and return its handle (so the caller can
+        free its slots); pinned blocks stay resident and None is returned."""
 
         with self._lock:
             handle = self._blocks.get(str(cache_key))
-            if handle is None or handle.pin_count > 0:
-                return False
+            if handle is None or handle.pin_count > 0 or not handle.valid:
+                return None
             handle.valid = False
             handle.stale_reason = "evicted"
-            return True
+            return handle

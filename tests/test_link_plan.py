@@ -93,9 +93,9 @@ def test_registry_lookup_pin_and_evict():
     result = registry.lookup_legolink_blocks(["a", "zz"])
     assert result.missing_blocks == ["zz"] and list(result.matched_blocks) == ["a"]
     registry.acquire_legolink_blocks(result.matched_handles)
-    assert not registry.evict_legolink_block("a")  # pinned
+    assert registry.evict_legolink_block("a") is None  # pinned
     registry.release_legolink_blocks(result.matched_handles)
-    assert registry.evict_legolink_block("a")
+    assert registry.evict_legolink_block("a") is not None
     assert registry.lookup_legolink_blocks(["a"]).stale_blocks == ["a"]
     assert registry.get_legolink_block_tokens("a") is None
     with pytest.raises(ValueError, match="not pinned"):
@@ -180,3 +180,41 @@ def test_cpu_pool_is_rejected_loudly():
         executor.copy_linked_kv(pool, torch.arange(10), plan)
     # the pin taken for the link is released on failure
     assert executor.registry.lookup_legolink_blocks(["a"]).matched_handles[0].pin_count == 0
+
+
+def test_snapshot_arena_allocates_and_merges_ranges():
+    from legolink_amd.link_runtime import SnapshotArena
+
+    arena = SnapshotArena([torch.zeros(10, 1, 8)], [torch.zeros(10, 1, 8)])
+    a = arena.alloc(4)
+    b = arena.alloc(3)
+    assert a.tolist() == [0, 1, 2, 3] and b.tolist() == [4, 5, 6]
+    assert arena.alloc(4) is None and arena.free_slots == 3
+    arena.free(a)
+    c = arena.alloc(2)
+    assert c.tolist() == [0, 1]
+    arena.free(b)
+    arena.free(c)
+    assert arena.free_slots == 10 and arena._free == [(0, 10)]
+    with pytest.raises(ValueError, match="already free"):
+        arena.free(torch.arange(2, 4))
+    with pytest.raises(ValueError, match="range alloc returned"):
+        arena.free(torch.tensor([1, 3]))
+
+
+def test_storage_modes_in_registry_and_maps():
+    registry = LegoLinkBlockRegistry()
+    with pytest.raises(ValueError, match="Unsupported PIC storage mode"):
+        registry.register_legolink_block("x", [1], torch.tensor([0]), storage_mode="paged")
+    registry.register_legolink_block("r", [1, 2], torch.tensor([10, 11]))
+    registry.register_legolink_block("c", [3, 4, 5], torch.tensor([0, 1, 2]), storage_mode="clone")
+    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(16, 8, theta=1e4), rotary_dim=8),
+                              end_layer=1)
+    plan = {"cache_keys": ["c", "r"], "block_ranges": [{"start_token": 0, "end_token": 3},
+                                                       {"start_token": 3, "end_token": 5}]}
+    maps = executor.build_link_maps(torch.arange(20, 25), plan)
+    assert maps.clone_tokens.tolist() == [True, True, True, False, False]
+    assert [spec["storage_mode"] for spec in maps.block_specs] == ["clone", "reference"]
+    pool = KVPool.allocate(num_slots=32, num_layers=1, num_heads=1, head_dim=8, device="cpu")
+    with pytest.raises(LinkRuntimeError, match="needs the snapshot arena"):
+        executor.prepare_link(pool, torch.arange(20, 25), plan)
