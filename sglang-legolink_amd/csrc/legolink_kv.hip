@@ -239,18 +239,24 @@ __device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const flo
 // rotary_dim == kD, fp32 cos/sin cache with unit column stride and 16-byte
 // aligned rows, 16-byte aligned layer buffers.
 // ---------------------------------------------------------------------------
-template <bool kBF16, int kD, bool kNeox>
+template <bool kBF16, int kD, bool kNeox, typename Index>
 __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   constexpr int kChunksPerHead = kD / 8;
   constexpr int kPairs = kNeox ? 8 : 4;  // rotary pairs touched by one lane
   constexpr int kHalf = kD / 2;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave_in_block = threadIdx.x / kWave;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the
+  // layer range in scalar registers, so the per-layer row pointers are read
+  // from the kernel arguments with scalar loads.
+  const int wave_in_block = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int groups = p.layer_groups_per_block;
-  const long long wave = static_cast<long long>(blockIdx.x) * (blockDim.x / kWave / groups) +
-                         wave_in_block / groups;
+  const long long wave =
+      static_cast<long long>(blockIdx.x) * (blockDim.x / kWave / groups) + wave_in_block / groups;
   const int layer_group = blockIdx.y * groups + wave_in_block % groups;
+  const int l0 = layer_group * p.layers_per_wave;
+  const int l1 = min(l0 + p.layers_per_wave, p.num_layers);
+  if (l0 >= l1) return;  // whole wave: a layer group past the last layer
   const long long g = wave * kWave + lane;
   const long long C = p.chunks_per_row;
   const bool in_range = g < p.num_tokens * C;
@@ -260,12 +266,47 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   // kChunksPerHead and kChunksPerHead divides 64, so this is lane-aligned.
   const int q = lane % kChunksPerHead;
 
-  const long long src = load_index(p.src, p.idx64 & 1, t);
-  const long long dst = load_index(p.dst, p.idx64 & 2, t);
-  bool ok = in_range && src >= 0 && src < p.src_num_slots && dst >= 0 && dst < p.num_slots;
-  if (p.mask != nullptr) ok = ok && (p.mask[t] == 0);
+  // The token's maps: five independent loads with no branch between them, so
+  // they are in flight together (t < num_tokens always holds).  Without a
+  // mask the mask byte is read from the source map and ignored.
+  const Index *maps_src = static_cast<const Index *>(p.src);
+  const long long src = static_cast<long long>(maps_src[t]);
+  const long long dst = static_cast<long long>(static_cast<const Index *>(p.dst)[t]);
+  const long long lp = static_cast<long long>(static_cast<const Index *>(p.lpos)[t]);
+  const long long gp = static_cast<long long>(static_cast<const Index *>(p.gpos)[t]);
+  const unsigned char *mask_bytes =
+      p.mask != nullptr ? p.mask : reinterpret_cast<const unsigned char *>(maps_src);
+  const unsigned char mask_byte = mask_bytes[t];
   const bool remap = t >= p.prefix;
+  const bool positions_ok = lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows;
+  const bool ok = in_range && !(p.mask != nullptr && mask_byte != 0) && src >= 0 &&
+                  src < p.src_num_slots && dst >= 0 && dst < p.num_slots &&
+                  (!remap || positions_ok);
 
+  // Row loads are unconditional so that no wait separates one layer's loads
+  // from the next: a lane without a valid source reads row 0 (the host
+  // launches only when the source pool has rows) and stores nothing.
+  const long long src_row = (src >= 0 && src < p.src_num_slots) ? src : 0;
+  const long long k_src = src_row * p.k_row_bytes + c * 16;
+  const long long k_dst = dst * p.k_row_bytes + c * 16;
+  const long long v_src = src_row * p.v_row_bytes + c * 16;
+  const long long v_dst = dst * p.v_row_bytes + c * 16;
+
+  // Rows of the first layers are requested before the cos/sin reads, so both
+  // are in flight while the delta is computed.  Past l1 the last layer is
+  // read again (uniform clamp) and not stored.
+  u32x4 kin[kLayerUnroll];
+  u32x4 vin[kLayerUnroll];
+#pragma unroll
+  for (int u = 0; u < kLayerUnroll; ++u) {
+    const int lu = min(l0 + u, l1 - 1);
+    kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[lu] + k_src);
+    vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[lu] + v_src);
+  }
+
+  // fp32 delta of this lane's rotary pairs.  Rows are clamped to 0 where the
+  // delta is not used (prefix tokens, invalid positions), so the reads stay in
+  // bounds without a branch; a table without rows is never read.
   float dc[kPairs];
   float ds[kPairs];
 #pragma unroll
@@ -273,26 +314,23 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     dc[e] = 1.0f;
     ds[e] = 0.0f;
   }
-  if (remap && in_range) {
-    const long long lp = load_index(p.lpos, p.idx64 & 4, t);
-    const long long gp = load_index(p.gpos, p.idx64 & 8, t);
-    if (lp < 0 || lp >= p.cs_rows || gp < 0 || gp >= p.cs_rows) {
-      ok = false;
-    } else {
-      const int pb = kNeox ? (q % (kChunksPerHead / 2)) * 8 : q * 4;
-      const float *lrow = static_cast<const float *>(p.cs) + lp * p.cs_stride_row + pb;
-      const float *grow = static_cast<const float *>(p.cs) + gp * p.cs_stride_row + pb;
+  if (p.cs_rows > 0) {
+    const bool use = remap && positions_ok;
+    const long long lrow_index = use ? lp : 0;
+    const long long grow_index = use ? gp : 0;
+    const int pb = kNeox ? (q % (kChunksPerHead / 2)) * 8 : q * 4;
+    const float *lrow = static_cast<const float *>(p.cs) + lrow_index * p.cs_stride_row + pb;
+    const float *grow = static_cast<const float *>(p.cs) + grow_index * p.cs_stride_row + pb;
 #pragma unroll
-      for (int e = 0; e < kPairs; e += 4) {
-        const f32x4 lc = *reinterpret_cast<const f32x4 *>(lrow + e);
-        const f32x4 ls = *reinterpret_cast<const f32x4 *>(lrow + kHalf + e);
-        const f32x4 gc = *reinterpret_cast<const f32x4 *>(grow + e);
-        const f32x4 gs = *reinterpret_cast<const f32x4 *>(grow + kHalf + e);
+    for (int e = 0; e < kPairs; e += 4) {
+      const f32x4 lc = *reinterpret_cast<const f32x4 *>(lrow + e);
+      const f32x4 ls = *reinterpret_cast<const f32x4 *>(lrow + kHalf + e);
+      const f32x4 gc = *reinterpret_cast<const f32x4 *>(grow + e);
+      const f32x4 gs = *reinterpret_cast<const f32x4 *>(grow + kHalf + e);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          dc[e + k] = gc[k] * lc[k] + gs[k] * ls[k];
-          ds[e + k] = gs[k] * lc[k] - gc[k] * ls[k];
-        }
+      for (int k = 0; k < 4; ++k) {
+        dc[e + k] = gc[k] * lc[k] + gs[k] * ls[k];
+        ds[e + k] = gs[k] * lc[k] - gc[k] * ls[k];
       }
     }
   }
@@ -303,23 +341,13 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     for (int e = 0; e < kPairs; ++e) dsn[e] = second_half ? ds[e] : -ds[e];
   }
 
-  const int l0 = layer_group * p.layers_per_wave;
-  const int l1 = min(l0 + p.layers_per_wave, p.num_layers);
-  const long long k_src = src * p.k_row_bytes + c * 16;
-  const long long k_dst = dst * p.k_row_bytes + c * 16;
-  const long long v_src = src * p.v_row_bytes + c * 16;
-  const long long v_dst = dst * p.v_row_bytes + c * 16;
-
   for (int l = l0; l < l1; l += kLayerUnroll) {
-    u32x4 kin[kLayerUnroll];
-    u32x4 vin[kLayerUnroll];
+    if (l != l0) {
 #pragma unroll
-    for (int u = 0; u < kLayerUnroll; ++u) {
-      kin[u] = u32x4{0u, 0u, 0u, 0u};
-      vin[u] = u32x4{0u, 0u, 0u, 0u};
-      if (ok && l + u < l1) {
-        kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[l + u] + k_src);
-        vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[l + u] + v_src);
+      for (int u = 0; u < kLayerUnroll; ++u) {
+        const int lu = min(l + u, l1 - 1);
+        kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[lu] + k_src);
+        vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[lu] + v_src);
       }
     }
 #pragma unroll
@@ -563,6 +591,11 @@ int validate_link(const ll_kv_link_args *a) {
 
 bool vector_kernel_fits(const ll_kv_link_args *a) {
   const int64_t d = a->key_head_dim;
+  // One index type for all four token maps.
+  if (a->destination_slots_dtype != a->source_slots_dtype ||
+      a->local_positions_dtype != a->source_slots_dtype ||
+      a->global_positions_dtype != a->source_slots_dtype)
+    return false;
   if (!(d == 32 || d == 64 || d == 128 || d == 256)) return false;
   if (a->value_head_dim != d || a->rotary_dim != d) return false;
   if (a->cos_sin_dtype != LL_DTYPE_FLOAT32 || a->cos_sin_stride_col != 1) return false;
@@ -599,7 +632,8 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   if (a->kernel == LL_KERNEL_VECTOR && !fits)
     return fail(LL_ERR_UNSUPPORTED_KERNEL,
                 "vector kernel needs key_head_dim == value_head_dim == rotary_dim in "
-                "{32,64,128,256}, an fp32 unit-stride cache and 16-byte aligned buffers");
+                "{32,64,128,256}, one index type for the four token maps, an fp32 "
+                "unit-stride cache and 16-byte aligned buffers");
   plan->kernel = (a->kernel == LL_KERNEL_GENERIC || !fits) ? LL_KERNEL_GENERIC : LL_KERNEL_VECTOR;
   const int waves_per_block = a->waves_per_block ? static_cast<int>(a->waves_per_block) : 4;
   plan->block_threads = waves_per_block * kWave;
@@ -638,8 +672,14 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
 
 template <bool kBF16, int kD>
 void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
-  if (neox) kv_link_vec_kernel<kBF16, kD, true><<<grid, block, 0, s>>>(p);
-  else kv_link_vec_kernel<kBF16, kD, false><<<grid, block, 0, s>>>(p);
+  const bool index64 = (p.idx64 & 15) == 15;  // the vector kernel needs one index type
+  if (neox) {
+    if (index64) kv_link_vec_kernel<kBF16, kD, true, long long><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, true, int><<<grid, block, 0, s>>>(p);
+  } else {
+    if (index64) kv_link_vec_kernel<kBF16, kD, false, long long><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, false, int><<<grid, block, 0, s>>>(p);
+  }
 }
 
 template <bool kBF16>
@@ -756,6 +796,10 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.neox = a->is_neox_style ? 1 : 0;
   const bool bf16 = a->kv_dtype == LL_DTYPE_BFLOAT16;
   const dim3 block(plan.block_threads);
+  // Every slot index is out of range for an empty pool: every token is
+  // skipped, and no kernel runs (the vector kernel reads row 0 of the source
+  // pool unconditionally).
+  if (p.src_num_slots == 0 || p.num_slots == 0) return LL_OK;
 
   for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
     const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch

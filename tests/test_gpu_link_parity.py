@@ -52,6 +52,10 @@ CASES = [
     ("all_masked", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 1.0, 2, 150, "vector"),
     ("single_token", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 0.0, 2, 1, "vector"),
     ("seventy_layers", torch.bfloat16, torch.float32, 2, 128, 128, 128, True, AUTO, torch.int64, 3, 0.1, 70, 64, "vector"),
+    # The vector kernel reads all four maps with one index type; a mix goes to the generic kernel.
+    ("mixed_index_dtypes", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO,
+     (torch.int32, torch.int64, torch.int64, torch.int32), 6, 0.1, 3, 200, "generic"),
+    ("five_layers_odd_tail", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int32, 2, 0.1, 5, 129, "vector"),
 ]
 
 
@@ -77,7 +81,9 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         assert table_dev.stride(1) == 2
     else:
         table_dev = table.to(device)
-    maps = [torch.from_numpy(a).to(index_dtype).to(device) for a in (src_np, dst_np, local_np, global_np)]
+    index_dtypes = index_dtype if isinstance(index_dtype, tuple) else (index_dtype,) * 4
+    maps = [torch.from_numpy(a).to(d).to(device)
+            for a, d in zip((src_np, dst_np, local_np, global_np), index_dtypes)]
     mask = torch.from_numpy(mask_np).to(device).to(mask_dtype) if mask_fraction > 0 else None
     key_np = [bits(k) for k in keys]
     value_np = [bits(v) for v in values]

@@ -118,6 +118,20 @@ def test_kernel_choice_and_launch_shape():
     del keepalive
 
 
+def test_mixed_index_dtypes_use_the_generic_kernel():
+    args, keepalive = _cpu_args(source_slots=torch.arange(8, dtype=torch.int32))
+    assert _native.kv_link_describe(args).kernel == _native.KERNEL_GENERIC
+    args.kernel = _native.KERNEL_VECTOR
+    with pytest.raises(_native.NativeCallError) as error:
+        _native.kv_link_describe(args)
+    assert error.value.reason == "unsupported_kernel_for_shape"
+    del keepalive
+    args, keepalive = _cpu_args(**{name: torch.arange(8, dtype=torch.int32) for name in (
+        "source_slots", "destination_slots", "local_positions", "global_positions")})
+    assert _native.kv_link_describe(args).kernel == _native.KERNEL_VECTOR
+    del keepalive
+
+
 def test_small_links_split_layers_across_waves():
     keys = [torch.zeros(8, 4, 128, dtype=torch.bfloat16) for _ in range(28)]
     info = kv_link.describe_link_launch(
