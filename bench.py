@@ -29,7 +29,7 @@ sys.path.insert(0, str(REPO_ROOT / "sglang-legolink_amd"))
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "linked KV GB/s (rd+wr) and % of 8 TB/s HBM; tokens linked/s, Qwen2.5-7B"
-TRAFFIC_FILE = REPO_ROOT / "profiles" / "traffic_kv_link_c2.json"
+PROFILES = REPO_ROOT / "profiles"
 
 
 def log(message: str) -> None:
@@ -241,13 +241,18 @@ def ceiling(args: argparse.Namespace) -> None:
                       "bytes_per_row_pass": link_bytes, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 
-def load_traffic(link_launch_bytes: int) -> float | None:
-    """HBM bytes per link launch from the committed rocprofv3 counter summary."""
+def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
+    """HBM bytes per link launch from the committed rocprofv3 counter summary of
+    this workload; None when there is none, or when it was taken on a launch
+    that moved a different number of algorithmic bytes (another repair-row mode)."""
 
-    if not TRAFFIC_FILE.is_file():
+    path = PROFILES / f"traffic_kv_link_{workload_name}.json"
+    if not path.is_file():
         return None
-    data = json.loads(TRAFFIC_FILE.read_text())
+    data = json.loads(path.read_text())
     try:
+        if int(data["algorithmic_bytes_per_launch"]) != int(link_launch_bytes):
+            return None
         return float(data["hbm_bytes_per_launch"])
     except (KeyError, TypeError, ValueError):
         return None
@@ -357,7 +362,7 @@ def main() -> int:
     value = total_bytes / (ms_per_step / 1e3) / 1e9
     link_avg_ms = float(np.mean(link_ms))
     achieved = bytes_info["link_bytes"] / (link_avg_ms / 1e3) / 1e9
-    traffic = load_traffic(bytes_info["link_bytes"])
+    traffic = load_traffic(workload.name, bytes_info["link_bytes"])
     result = {
         "metric": METRIC,
         "value": round(value, 2),
