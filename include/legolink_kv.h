@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 3
+#define LL_ABI_VERSION 4
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -199,6 +199,73 @@ typedef struct ll_kv_scatter_args {
   int64_t waves_per_block;         /* 0 = default; else 1, 2, 4 or 8 */
 } ll_kv_scatter_args;
 
+/*
+ * Token maps of a link, built on the device from a plan's runs.
+ *
+ * A run is a stretch of consecutive request positions taken from one block:
+ * token i of the run (0 <= i < token_count) sits at request position
+ * p = start_token + i, is written to destination_slots[destination_start + i],
+ * reads its rows from source slot source_slots[i] and carries compile-time
+ * position local_positions[i] (or local_start + i when local_positions is
+ * NULL).  For one request destination_start == start_token; runs of several
+ * requests can share one call with their destination slots concatenated.
+ * Tokens [repair_begin, repair_end) of the run are repair rows (imp_indices
+ * inside the block).  For every token:
+ *     d = destination_slots[destination_start + i]
+ *     if it is a repair row and repair_offset >= 0:
+ *         repair_destination_slots[repair_offset + i - repair_begin] = d
+ *     unless it is a repair row of a set without a mask (compacted set):
+ *         o = map_offset + i, minus (repair_end - repair_begin) past the
+ *             repair rows of a compacted set
+ *         maps[s][0][o] = source slot, maps[s][1][o] = d,
+ *         maps[s][2][o] = local position, maps[s][3][o] = p  (s = map_set)
+ *         repair_mask[s][o] = 1 for a repair row, else 0 (when the set has a mask)
+ * maps[s] is an int64 [4, map_capacity[s]] array (row stride map_capacity[s]);
+ * its rows are the source_slots, destination_slots, local_positions and
+ * global_positions of an ll_kv_link call.  Two sets let a link whose blocks
+ * live in two places (pool slots and a snapshot arena) build both launches'
+ * maps in one call.
+ *
+ * Every run is validated on the host before any launch: destination indices
+ * inside [0, num_destination_slots), map and repair indices inside their
+ * capacities, map_set 0 or 1 with a map array.  The source and local
+ * position arrays must hold token_count entries (not checkable).
+ *
+ * Replaces the per-block map construction of _copy_linked_kv_batched_blocks
+ * (patched_sglang_files/python/sglang/srt/pic_runtime.py:4905-5003: slot
+ * slices, arange positions, torch.cat of every map, the boundary repair mask
+ * built on the host and copied over).
+ */
+typedef struct ll_link_segment {
+  const int64_t *source_slots;     /* device [token_count] */
+  const int64_t *local_positions;  /* device [token_count], or NULL: local_start + i */
+  int64_t token_count;             /* >= 0 */
+  int64_t start_token;             /* request position (global position) of token 0 */
+  int64_t destination_start;       /* index of token 0's slot in destination_slots */
+  int64_t local_start;
+  int64_t repair_begin;            /* 0 <= repair_begin <= repair_end <= token_count */
+  int64_t repair_end;
+  int64_t map_set;                 /* 0 or 1 */
+  int64_t map_offset;              /* map index of the run's first map entry */
+  int64_t repair_offset;           /* index of the run's first repair row, or -1: not recorded */
+} ll_link_segment;
+
+typedef struct ll_link_maps_args {
+  int64_t struct_size;             /* sizeof(ll_link_maps_args) */
+  int64_t num_segments;            /* >= 0 */
+  const ll_link_segment *segments; /* host array [num_segments] */
+  const void *destination_slots;   /* device [num_destination_slots], int32 or int64:
+                                      the request's slots by request position (or
+                                      several requests' slots, concatenated) */
+  int64_t destination_slots_dtype;
+  int64_t num_destination_slots;
+  int64_t *maps[2];                /* device int64 [4, map_capacity[s]], or NULL for an unused set */
+  int64_t map_capacity[2];
+  uint8_t *repair_mask[2];         /* device uint8 [map_capacity[s]], or NULL: compacted set */
+  int64_t *repair_destination_slots; /* device int64 [repair_capacity], or NULL */
+  int64_t repair_capacity;
+} ll_link_maps_args;
+
 /* Which kernel and launch shape ll_kv_link would use (no GPU work). */
 typedef struct ll_launch_info {
   int64_t kernel;                  /* LL_KERNEL_VECTOR or LL_KERNEL_GENERIC */
@@ -213,6 +280,7 @@ typedef struct ll_launch_info {
 int ll_kv_link(const ll_kv_link_args *args, ll_stream_t stream);
 int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info);
 int ll_kv_scatter_rows(const ll_kv_scatter_args *args, ll_stream_t stream);
+int ll_kv_build_link_maps(const ll_link_maps_args *args, ll_stream_t stream);
 
 /* Reason string of a status code ("supported" for LL_OK). */
 const char *ll_status_reason(int status);
@@ -221,6 +289,7 @@ const char *ll_last_error(void);
 int ll_abi_version(void);
 int64_t ll_kv_link_args_size(void);
 int64_t ll_kv_scatter_args_size(void);
+int64_t ll_link_maps_args_size(void);
 
 #ifdef __cplusplus
 }

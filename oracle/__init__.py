@@ -8,6 +8,8 @@ never imports it.
 Modules:
   ll_oracle.c / kv_link_oracle.py   the fused link arithmetic (R2) in C and numpy
   r1_torch.py                       the reference's eager torch path (R1)
+  link_maps_oracle.py               a link's token maps (plan order, repair rows, prefix)
 
-Parity status of each function (how it is pinned) is listed in DESIGN.md.
+Each module's docstring names the reference lines it restates; the tests that
+pin it are tests/test_oracle_pins.py and tests/test_link_maps.py.
 """

@@ -508,6 +508,66 @@ __global__ void __launch_bounds__(512) kv_scatter_kernel(const ScatterParams p) 
 }
 
 // ---------------------------------------------------------------------------
+// Map builder: writes a link's token maps from a plan's runs.  Workgroup
+// (x, y) takes tokens [y * kMapTokensPerBlock, (y + 1) * kMapTokensPerBlock)
+// of run x; the runs of one launch travel in the kernel arguments (validated
+// on the host, so every index below is in range).  The work is a few int64
+// reads and writes per token: a latency-bound pass far below HBM bandwidth.
+// ---------------------------------------------------------------------------
+// 56 runs x 64 B keep the kernel arguments under 4 KB (hidden arguments included).
+constexpr int kMaxSegmentsPerLaunch = 56;
+constexpr int kMapTokensPerBlock = 1024;
+
+struct MapSegment {
+  const long long *src;
+  const long long *local;  // nullptr: local_start + i
+  long long start;         // global position of token 0
+  long long dst_start;     // index of token 0's slot in the destination slots
+  long long local_start;
+  int count;
+  int map_offset;
+  int repair_begin;
+  int repair_end;
+  int repair_offset;  // < 0: repair rows not recorded
+  int set;
+};
+
+struct MapParams {
+  MapSegment seg[kMaxSegmentsPerLaunch];
+  const void *dst;
+  long long *maps[2];
+  long long cap[2];
+  unsigned char *mask[2];
+  long long *repair_dst;
+  int dst64;
+};
+
+__global__ void __launch_bounds__(256) build_link_maps_kernel(const MapParams p) {
+  const MapSegment &sg = p.seg[blockIdx.x];
+  const int first = static_cast<int>(blockIdx.y) * kMapTokensPerBlock;
+  const int end = min(sg.count, first + kMapTokensPerBlock);
+  unsigned char *mask = p.mask[sg.set];
+  long long *m = p.maps[sg.set];
+  const long long cap = p.cap[sg.set];
+  const int repair_rows = sg.repair_end - sg.repair_begin;
+  for (int i = first + static_cast<int>(threadIdx.x); i < end; i += blockDim.x) {
+    const long long pos = sg.start + i;
+    const long long di = sg.dst_start + i;
+    const long long d = p.dst64 ? static_cast<const long long *>(p.dst)[di]
+                                : static_cast<long long>(static_cast<const int *>(p.dst)[di]);
+    const bool repair = i >= sg.repair_begin && i < sg.repair_end;
+    if (repair && sg.repair_offset >= 0) p.repair_dst[sg.repair_offset + (i - sg.repair_begin)] = d;
+    if (repair && mask == nullptr) continue;  // compacted set: repair rows take no entry
+    const int o = sg.map_offset + ((mask == nullptr && i >= sg.repair_end) ? i - repair_rows : i);
+    m[o] = sg.src[i];
+    m[cap + o] = d;
+    m[2 * cap + o] = sg.local != nullptr ? sg.local[i] : sg.local_start + i;
+    m[3 * cap + o] = pos;
+    if (mask != nullptr) mask[o] = repair ? 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
@@ -708,6 +768,7 @@ extern "C" {
 int ll_abi_version(void) { return LL_ABI_VERSION; }
 int64_t ll_kv_link_args_size(void) { return static_cast<int64_t>(sizeof(ll_kv_link_args)); }
 int64_t ll_kv_scatter_args_size(void) { return static_cast<int64_t>(sizeof(ll_kv_scatter_args)); }
+int64_t ll_link_maps_args_size(void) { return static_cast<int64_t>(sizeof(ll_link_maps_args)); }
 const char *ll_last_error(void) { return g_last_error.c_str(); }
 
 const char *ll_status_reason(int status) {
@@ -916,6 +977,124 @@ int ll_kv_scatter_rows(const ll_kv_scatter_args *a, ll_stream_t stream) {
       return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   }
   return LL_OK;
+}
+
+int ll_kv_build_link_maps(const ll_link_maps_args *a, ll_stream_t stream) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_link_maps_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_link_maps_args));
+  if (a->num_segments < 0) return fail(LL_ERR_INVALID_ARGUMENT, "num_segments is negative");
+  if (a->num_segments == 0) return LL_OK;
+  if (a->segments == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "segments is NULL");
+  if (!is_index_dtype(a->destination_slots_dtype))
+    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "destination slots must be int32 or int64");
+  if (a->num_destination_slots < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "num_destination_slots is negative");
+  constexpr int64_t kIntMax = 0x7fffffff;
+  for (int s = 0; s < 2; ++s)
+    if (a->map_capacity[s] < 0 || a->map_capacity[s] > kIntMax)
+      return fail(LL_ERR_INVALID_ARGUMENT, "map_capacity[%d] must be in [0, 2^31)", s);
+  if (a->repair_capacity < 0) return fail(LL_ERR_INVALID_ARGUMENT, "repair_capacity is negative");
+
+  // Validate every run before the first launch.
+  for (int64_t k = 0; k < a->num_segments; ++k) {
+    const ll_link_segment &g = a->segments[k];
+    const long long kk = static_cast<long long>(k);
+    if (g.token_count < 0 || g.token_count > kIntMax)
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: token_count out of range", kk);
+    if (g.token_count == 0) continue;
+    if (g.source_slots == nullptr)
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: source_slots is NULL", kk);
+    if (a->destination_slots == nullptr)
+      return fail(LL_ERR_INVALID_ARGUMENT, "destination_slots is NULL");
+    if (g.destination_start < 0 || g.destination_start > a->num_destination_slots - g.token_count)
+      return fail(LL_ERR_INVALID_ARGUMENT,
+                  "segment %lld: destination indices [%lld, %lld) outside the %lld destination slots",
+                  kk, static_cast<long long>(g.destination_start),
+                  static_cast<long long>(g.destination_start + g.token_count),
+                  static_cast<long long>(a->num_destination_slots));
+    if (g.start_token < 0 || g.start_token > (static_cast<int64_t>(1) << 62))
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: start_token out of range", kk);
+    if (g.repair_begin < 0 || g.repair_begin > g.repair_end || g.repair_end > g.token_count)
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: repair rows outside the run", kk);
+    if (g.map_set != 0 && g.map_set != 1)
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: map_set must be 0 or 1", kk);
+    const int set = static_cast<int>(g.map_set);
+    const int64_t repair_rows = g.repair_end - g.repair_begin;
+    const int64_t entries = g.token_count - (a->repair_mask[set] == nullptr ? repair_rows : 0);
+    if (entries > 0) {
+      if (a->maps[set] == nullptr)
+        return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: maps[%d] is NULL", kk, set);
+      if (g.map_offset < 0 || g.map_offset > a->map_capacity[set] - entries)
+        return fail(LL_ERR_INVALID_ARGUMENT,
+                    "segment %lld: map entries [%lld, %lld) outside capacity %lld", kk,
+                    static_cast<long long>(g.map_offset),
+                    static_cast<long long>(g.map_offset + entries),
+                    static_cast<long long>(a->map_capacity[set]));
+    }
+    if (g.repair_offset < -1)
+      return fail(LL_ERR_INVALID_ARGUMENT, "segment %lld: repair_offset must be >= -1", kk);
+    if (repair_rows > 0 && g.repair_offset >= 0) {
+      if (a->repair_destination_slots == nullptr)
+        return fail(LL_ERR_INVALID_ARGUMENT, "repair_destination_slots is NULL");
+      if (g.repair_offset > a->repair_capacity - repair_rows)
+        return fail(LL_ERR_INVALID_ARGUMENT,
+                    "segment %lld: repair rows [%lld, %lld) outside capacity %lld", kk,
+                    static_cast<long long>(g.repair_offset),
+                    static_cast<long long>(g.repair_offset + repair_rows),
+                    static_cast<long long>(a->repair_capacity));
+    }
+  }
+
+  MapParams p;
+  memset(&p, 0, sizeof(p));
+  p.dst = a->destination_slots;
+  p.dst64 = a->destination_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
+  for (int s = 0; s < 2; ++s) {
+    p.maps[s] = reinterpret_cast<long long *>(a->maps[s]);
+    p.cap[s] = a->map_capacity[s];
+    p.mask[s] = a->repair_mask[s];
+  }
+  p.repair_dst = reinterpret_cast<long long *>(a->repair_destination_slots);
+  hipStream_t stream_h = reinterpret_cast<hipStream_t>(stream);
+  int n = 0;
+  int64_t longest = 0;
+  auto launch = [&]() -> int {
+    if (n == 0) return LL_OK;
+    const dim3 grid(static_cast<unsigned>(n),
+                    static_cast<unsigned>((longest + kMapTokensPerBlock - 1) / kMapTokensPerBlock));
+    build_link_maps_kernel<<<grid, dim3(256), 0, stream_h>>>(p);
+    n = 0;
+    longest = 0;
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+      return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return LL_OK;
+  };
+  for (int64_t k = 0; k < a->num_segments; ++k) {
+    const ll_link_segment &g = a->segments[k];
+    if (g.token_count == 0) continue;
+    MapSegment &m = p.seg[n++];
+    m.src = reinterpret_cast<const long long *>(g.source_slots);
+    m.local = reinterpret_cast<const long long *>(g.local_positions);
+    m.start = g.start_token;
+    m.dst_start = g.destination_start;
+    m.local_start = g.local_start;
+    m.count = static_cast<int>(g.token_count);
+    m.map_offset = static_cast<int>(g.map_offset);
+    m.repair_begin = static_cast<int>(g.repair_begin);
+    m.repair_end = static_cast<int>(g.repair_end);
+    m.repair_offset = g.repair_offset >= 0 && g.repair_end > g.repair_begin
+                          ? static_cast<int>(g.repair_offset) : -1;
+    m.set = static_cast<int>(g.map_set);
+    if (g.token_count > longest) longest = g.token_count;
+    if (n == kMaxSegmentsPerLaunch) {
+      const int rc = launch();
+      if (rc != LL_OK) return rc;
+    }
+  }
+  return launch();
 }
 
 }  // extern "C"

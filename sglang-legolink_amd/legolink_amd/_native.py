@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -49,6 +49,8 @@ EXPORTED_SYMBOLS = (
     "ll_abi_version",
     "ll_kv_link_args_size",
     "ll_kv_scatter_args_size",
+    "ll_kv_build_link_maps",
+    "ll_link_maps_args_size",
 )
 
 _i64 = ctypes.c_int64
@@ -122,6 +124,46 @@ class ScatterArgs(ctypes.Structure):
     ]
 
 
+class LinkSegment(ctypes.Structure):
+    """Mirror of ``ll_link_segment`` (eleven 8-byte fields: an int64 ``[n, 11]``
+    array has the same memory layout as ``n`` of these)."""
+
+    _fields_ = [
+        ("source_slots", _ptr),
+        ("local_positions", _ptr),
+        ("token_count", _i64),
+        ("start_token", _i64),
+        ("destination_start", _i64),
+        ("local_start", _i64),
+        ("repair_begin", _i64),
+        ("repair_end", _i64),
+        ("map_set", _i64),
+        ("map_offset", _i64),
+        ("repair_offset", _i64),
+    ]
+
+
+SEGMENT_FIELDS = tuple(name for name, _ in LinkSegment._fields_)
+
+
+class LinkMapsArgs(ctypes.Structure):
+    """Mirror of ``ll_link_maps_args``."""
+
+    _fields_ = [
+        ("struct_size", _i64),
+        ("num_segments", _i64),
+        ("segments", _ptr),
+        ("destination_slots", _ptr),
+        ("destination_slots_dtype", _i64),
+        ("num_destination_slots", _i64),
+        ("maps", _ptr * 2),
+        ("map_capacity", _i64 * 2),
+        ("repair_mask", _ptr * 2),
+        ("repair_destination_slots", _ptr),
+        ("repair_capacity", _i64),
+    ]
+
+
 class LaunchInfo(ctypes.Structure):
     """Mirror of ``ll_launch_info``."""
 
@@ -190,13 +232,17 @@ def load_library() -> ctypes.CDLL:
         lib.ll_kv_link_args_size.restype = _i64
         lib.ll_kv_scatter_args_size.argtypes = []
         lib.ll_kv_scatter_args_size.restype = _i64
+        lib.ll_kv_build_link_maps.argtypes = [ctypes.POINTER(LinkMapsArgs), _ptr]
+        lib.ll_kv_build_link_maps.restype = ctypes.c_int
+        lib.ll_link_maps_args_size.argtypes = []
+        lib.ll_link_maps_args_size.restype = _i64
         if lib.ll_abi_version() != ABI_VERSION:
             raise NativeLibraryUnavailable(
                 f"{LIB_PATH} has ABI {lib.ll_abi_version()}, expected {ABI_VERSION}; rebuild it"
             )
-        if lib.ll_kv_link_args_size() != ctypes.sizeof(LinkArgs) or (
-            lib.ll_kv_scatter_args_size() != ctypes.sizeof(ScatterArgs)
-        ):
+        if (lib.ll_kv_link_args_size() != ctypes.sizeof(LinkArgs)
+                or lib.ll_kv_scatter_args_size() != ctypes.sizeof(ScatterArgs)
+                or lib.ll_link_maps_args_size() != ctypes.sizeof(LinkMapsArgs)):
             raise NativeLibraryUnavailable(f"{LIB_PATH} struct layout differs; rebuild it")
         _lib = lib
         return lib
@@ -246,3 +292,8 @@ def kv_link_describe(args: LinkArgs) -> LaunchInfo:
 def kv_scatter_rows(args: ScatterArgs, stream: int) -> None:
     args.struct_size = ctypes.sizeof(ScatterArgs)
     _check(load_library().ll_kv_scatter_rows(ctypes.byref(args), _ptr(int(stream))))
+
+
+def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
+    args.struct_size = ctypes.sizeof(LinkMapsArgs)
+    _check(load_library().ll_kv_build_link_maps(ctypes.byref(args), _ptr(int(stream))))

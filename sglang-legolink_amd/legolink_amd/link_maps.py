@@ -1,0 +1,283 @@
+"""Token maps of a link, built on the device from the plan's runs.
+
+The reference materialises a link's maps on the host, block by block
+(patched_sglang_files/python/sglang/srt/pic_runtime.py:4905-5003): the
+request's destination slots ``[start, end)`` of each block, its compile-time
+positions ``arange(n)``, its global positions ``start + arange(n)``, then a
+``torch.cat`` of every map and, with boundary-repair awareness, a uint8 mask
+of the ``imp_indices`` rows built on the host and copied over.
+
+Here the host only cuts the plan into runs, vectorised over blocks: a run is
+a stretch of one block holding at most one contiguous run of repair rows.
+One call of ``ll_kv_build_link_maps`` then writes every map of the link, in
+plan order, per source set (0: pool slots, 1: snapshot arena), with repair
+rows either left out (compacted) or flagged in a mask, and the destination
+slots of the repair rows for the write-back.  The output equals the
+reference's concatenation restricted to each set, in the same order.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+
+_FIELD = {name: index for index, name in enumerate(_native.SEGMENT_FIELDS)}
+
+
+@dataclass
+class BlockTable:
+    """A link's blocks in plan order (one entry per block)."""
+
+    starts: np.ndarray        # int64 [B] request position of the block's first token
+    counts: np.ndarray        # int64 [B] tokens
+    source_ptrs: np.ndarray   # int64 [B] device address of the block's int64 source slots
+    local_ptrs: np.ndarray    # int64 [B] device address of int64 local positions, 0: affine
+    local_starts: np.ndarray  # int64 [B] local position of token 0 (affine blocks)
+    sets: np.ndarray          # int64 [B] 0: pool slots, 1: snapshot arena
+    destination_bases: Optional[np.ndarray] = None  # int64 [B] offset of the block's request
+                                                     # in the destination slots (None: 0)
+
+    @property
+    def destination_starts(self) -> np.ndarray:
+        """Index of every block's first destination slot."""
+
+        return self.starts if self.destination_bases is None else self.starts + self.destination_bases
+
+    @property
+    def offsets(self) -> np.ndarray:
+        """Concatenation offset of every block's first token."""
+
+        return np.concatenate(([0], np.cumsum(self.counts)[:-1])).astype(np.int64)
+
+    @property
+    def token_count(self) -> int:
+        return int(self.counts.sum())
+
+
+@dataclass
+class SegmentPlan:
+    table: np.ndarray           # int64 [S, 11]: ll_link_segment records
+    map_counts: tuple[int, int]  # map entries of set 0 and set 1
+    set_repair_rows: tuple[int, int]  # repair rows whose tokens belong to each set
+    repair_count: int           # repair rows recorded (write-back order = plan order)
+    repair_offsets: np.ndarray  # int64 [R] concatenation offsets of the repair rows
+    block_entries: np.ndarray   # int64 [B] map entries each block contributes
+    set_prefix: tuple[int, int]  # identity tokens at the head of each set's maps
+
+
+def _exclusive_cumsum(values: np.ndarray) -> np.ndarray:
+    out = np.zeros(values.shape[0], dtype=np.int64)
+    if values.shape[0] > 1:
+        np.cumsum(values[:-1], out=out[1:])
+    return out
+
+
+def repair_rows_in_blocks(blocks: BlockTable, repair_positions: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(block index, offset in block) of every repair position inside a block,
+    sorted in plan order; positions outside every block are dropped
+    (pic_runtime.py:4981-5003 keeps ``start <= position < end`` only).
+
+    Positions are destination indices: the request position plus the
+    request's offset in the destination slots (0 for a single request)."""
+
+    positions = _sorted_unique(np.asarray(repair_positions, dtype=np.int64).reshape(-1))
+    if positions.size == 0 or blocks.counts.size == 0:
+        empty = np.zeros(0, dtype=np.int64)
+        return empty, empty
+    starts = blocks.destination_starts
+    in_position_order = blocks.counts.size == 1 or bool(np.all(starts[1:] > starts[:-1]))
+    order = None if in_position_order else np.argsort(starts, kind="stable")
+    sorted_starts = starts if order is None else starts[order]
+    slot = np.searchsorted(sorted_starts, positions, side="right") - 1
+    inside = slot >= 0
+    slot_c = np.where(inside, slot, 0)
+    block = slot_c if order is None else order[slot_c]
+    inside &= positions < starts[block] + blocks.counts[block]
+    block = block[inside]
+    offset = positions[inside] - starts[block]
+    if order is None:
+        # Blocks in position order: position order is plan order already.
+        return block, offset
+    concat = blocks.offsets[block] + offset
+    ordering = np.argsort(concat, kind="stable")
+    return block[ordering], offset[ordering]
+
+
+def _sorted_unique(values: np.ndarray) -> np.ndarray:
+    if values.size > 1 and not bool(np.all(values[1:] > values[:-1])):
+        return np.unique(values)
+    return values
+
+
+def plan_segments(blocks: BlockTable, repair_positions: np.ndarray, *, compact: bool,
+                  leading_blocks: Optional[np.ndarray] = None) -> SegmentPlan:
+    """Cut the blocks into runs with at most one contiguous repair run each.
+
+    ``repair_positions`` are destination indices (request positions for one
+    request; sorted or not, duplicates allowed); only those inside blocks
+    count.  With ``compact`` the repair rows take no map entry; otherwise
+    they are flagged in the set's mask.  Runs of ``leading_blocks`` (the
+    identity blocks: no token needs a remap) take the first map entries of
+    their set, in plan order, so they form the set's identity prefix; the
+    other runs follow in plan order.  The runs themselves, and so the order
+    of the repair rows, stay in plan order.
+    """
+
+    count_blocks = int(blocks.counts.size)
+    block, offset = repair_rows_in_blocks(blocks, repair_positions)
+    # Runs: consecutive offsets of one block.
+    if block.size:
+        new_run = np.ones(block.size, dtype=bool)
+        new_run[1:] = (block[1:] != block[:-1]) | (offset[1:] != offset[:-1] + 1)
+        run_start = np.flatnonzero(new_run)
+        run_stop = np.concatenate((run_start[1:], [block.size]))
+        run_block = block[run_start]
+        run_begin = offset[run_start]
+        run_end = offset[run_stop - 1] + 1
+    else:
+        run_block = run_begin = run_end = np.zeros(0, dtype=np.int64)
+    # Runs of a block, in order: segment j spans [first ? 0 : begin_j, last ? count : begin_{j+1}).
+    first = np.ones(run_block.size, dtype=bool)
+    first[1:] = run_block[1:] != run_block[:-1]
+    last = np.ones(run_block.size, dtype=bool)
+    last[:-1] = run_block[:-1] != run_block[1:]
+    next_begin = np.concatenate((run_begin[1:], [0])) if run_block.size else run_begin
+    seg_a = np.where(first, 0, run_begin)
+    seg_b = np.where(last, blocks.counts[run_block], next_begin)
+    seg_block = run_block
+    seg_rb = run_begin - seg_a
+    seg_re = run_end - seg_a
+    # Blocks without repair rows are one run each.
+    plain = np.ones(count_blocks, dtype=bool)
+    plain[run_block] = False
+    plain_blocks = np.flatnonzero(plain)
+    seg_block = np.concatenate((seg_block, plain_blocks)).astype(np.int64)
+    seg_a = np.concatenate((seg_a, np.zeros(plain_blocks.size, dtype=np.int64)))
+    seg_b = np.concatenate((seg_b, blocks.counts[plain_blocks]))
+    seg_rb = np.concatenate((seg_rb, np.zeros(plain_blocks.size, dtype=np.int64)))
+    seg_re = np.concatenate((seg_re, np.zeros(plain_blocks.size, dtype=np.int64)))
+    ordering = np.argsort(blocks.offsets[seg_block] + seg_a, kind="stable")
+    seg_block, seg_a, seg_b = seg_block[ordering], seg_a[ordering], seg_b[ordering]
+    seg_rb, seg_re = seg_rb[ordering], seg_re[ordering]
+
+    count = seg_b - seg_a
+    repair_rows = seg_re - seg_rb
+    entries = count - repair_rows if compact else count
+    sets = blocks.sets[seg_block]
+    lead = (np.zeros(count.size, dtype=bool) if leading_blocks is None
+            else np.asarray(leading_blocks, dtype=bool)[seg_block])
+    map_offset = np.zeros(count.size, dtype=np.int64)
+    map_counts = []
+    set_repairs = []
+    set_prefix = []
+    for s in (0, 1):
+        head = np.flatnonzero((sets == s) & lead)
+        tail = np.flatnonzero((sets == s) & ~lead)
+        ordered = np.concatenate((head, tail))
+        map_offset[ordered] = _exclusive_cumsum(entries[ordered])
+        map_counts.append(int(entries[ordered].sum()))
+        set_repairs.append(int(repair_rows[ordered].sum()))
+        set_prefix.append(int(entries[head].sum()))
+    table = np.empty((count.size, len(_FIELD)), dtype=np.int64)
+    local_ptr = blocks.local_ptrs[seg_block]
+    table[:, _FIELD["source_slots"]] = blocks.source_ptrs[seg_block] + 8 * seg_a
+    table[:, _FIELD["local_positions"]] = np.where(local_ptr != 0, local_ptr + 8 * seg_a, 0)
+    table[:, _FIELD["token_count"]] = count
+    table[:, _FIELD["start_token"]] = blocks.starts[seg_block] + seg_a
+    table[:, _FIELD["destination_start"]] = blocks.destination_starts[seg_block] + seg_a
+    table[:, _FIELD["local_start"]] = blocks.local_starts[seg_block] + seg_a
+    table[:, _FIELD["repair_begin"]] = seg_rb
+    table[:, _FIELD["repair_end"]] = seg_re
+    table[:, _FIELD["map_set"]] = sets
+    table[:, _FIELD["map_offset"]] = map_offset
+    table[:, _FIELD["repair_offset"]] = _exclusive_cumsum(repair_rows)
+    block_entries = np.bincount(seg_block, weights=entries, minlength=count_blocks).astype(np.int64)
+    return SegmentPlan(
+        table=table,
+        map_counts=(map_counts[0], map_counts[1]),
+        set_repair_rows=(set_repairs[0], set_repairs[1]),
+        repair_count=int(repair_rows.sum()),
+        repair_offsets=(blocks.offsets[block] + offset).astype(np.int64),
+        block_entries=block_entries,
+        set_prefix=(set_prefix[0], set_prefix[1]),
+    )
+
+
+@dataclass
+class DeviceMaps:
+    """Output of the map builder: per set an int64 ``[4, n]`` map tensor (rows:
+    source slots, destination slots, local positions, global positions) and
+    an optional uint8 mask; the destination slots of the repair rows."""
+
+    maps: list[Optional[torch.Tensor]]
+    masks: list[Optional[torch.Tensor]]
+    repair_destination_slots: torch.Tensor
+
+
+def build_device_maps(plan: SegmentPlan, destination_slots: torch.Tensor, *, compact: bool,
+                      stream: torch.cuda.Stream | None = None) -> DeviceMaps:
+    """Enqueue the map builder on ``stream`` (default: the current stream)."""
+
+    device = destination_slots.device
+    if not destination_slots.is_cuda:
+        # The reason string of the operator's eligibility check for host tensors.
+        raise RuntimeError("HIP LegoLink fusion is unavailable: cuda_tensors_required")
+    if destination_slots.dtype not in (torch.int32, torch.int64) or not destination_slots.is_contiguous():
+        raise ValueError("destination slots must be a contiguous int32 or int64 tensor")
+    maps: list[Optional[torch.Tensor]] = []
+    masks: list[Optional[torch.Tensor]] = []
+    for s in (0, 1):
+        n = plan.map_counts[s]
+        maps.append(torch.empty((4, n), dtype=torch.int64, device=device) if n else None)
+        masks.append(torch.empty(n, dtype=torch.uint8, device=device) if n and not compact else None)
+    repair = torch.empty(plan.repair_count, dtype=torch.int64, device=device)
+    args = _native.LinkMapsArgs()
+    table = np.ascontiguousarray(plan.table)
+    args.num_segments = int(table.shape[0])
+    args.segments = table.ctypes.data if table.size else None
+    args.destination_slots = destination_slots.data_ptr()
+    args.destination_slots_dtype = (_native.DTYPE_INT64 if destination_slots.dtype == torch.int64
+                                    else _native.DTYPE_INT32)
+    args.num_destination_slots = int(destination_slots.numel())
+    for s in (0, 1):
+        args.maps[s] = maps[s].data_ptr() if maps[s] is not None else None
+        args.map_capacity[s] = plan.map_counts[s]
+        args.repair_mask[s] = masks[s].data_ptr() if masks[s] is not None else None
+    args.repair_destination_slots = repair.data_ptr() if plan.repair_count else None
+    args.repair_capacity = plan.repair_count
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    _native.kv_build_link_maps(args, stream.cuda_stream)
+    return DeviceMaps(maps=maps, masks=masks, repair_destination_slots=repair)
+
+
+def block_table(starts: Sequence[int], counts: Sequence[int], source_ptrs: Sequence[int],
+                local_ptrs: Sequence[int], local_starts: Sequence[int], sets: Sequence[int],
+                destination_bases: Optional[Sequence[int]] = None) -> BlockTable:
+    as64 = lambda values: np.asarray(values, dtype=np.int64).reshape(-1)
+    return BlockTable(starts=as64(starts), counts=as64(counts), source_ptrs=as64(source_ptrs),
+                      local_ptrs=as64(local_ptrs), local_starts=as64(local_starts), sets=as64(sets),
+                      destination_bases=None if destination_bases is None else as64(destination_bases))
+
+
+def concatenate_tables(tables: Sequence[BlockTable], bases: Sequence[int]) -> BlockTable:
+    """Blocks of several requests, request after request; request r's
+    destination slots start at ``bases[r]`` in the concatenated slots."""
+
+    counts = [t.counts.size for t in tables]
+    own = [t.destination_bases if t.destination_bases is not None else np.zeros(n, dtype=np.int64)
+           for t, n in zip(tables, counts)]
+    return BlockTable(
+        starts=np.concatenate([t.starts for t in tables]),
+        counts=np.concatenate([t.counts for t in tables]),
+        source_ptrs=np.concatenate([t.source_ptrs for t in tables]),
+        local_ptrs=np.concatenate([t.local_ptrs for t in tables]),
+        local_starts=np.concatenate([t.local_starts for t in tables]),
+        sets=np.concatenate([t.sets for t in tables]),
+        destination_bases=np.concatenate([o + int(b) for o, b in zip(own, bases)]).astype(np.int64),
+    )

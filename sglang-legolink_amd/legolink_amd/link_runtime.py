@@ -39,7 +39,7 @@ from typing import Any, Mapping, Optional, Sequence
 import numpy as np
 import torch
 
-from . import kv_link
+from . import kv_link, link_maps
 from .errors import LinkRuntimeError
 from .registry import LegoLinkBlockHandle, LegoLinkBlockRegistry
 from .rope import RotarySpec
@@ -141,20 +141,103 @@ class SnapshotArena(KVPool):
 
 @dataclass
 class LinkMaps:
-    """Token maps of one link in plan order (before compaction)."""
+    """A link's blocks in plan order (pic_runtime.py:4905-5013): everything the
+    map builder needs, with no per-token host arrays.  The per-token views
+    below (concatenated in plan order) are for inspection and accounting.
 
-    source_slots: torch.Tensor        # int64 [T] on the pool device
-    destination_slots: torch.Tensor   # int64 [T] on the pool device
-    local_positions: np.ndarray       # int64 [T]
-    global_positions: np.ndarray      # int64 [T]
-    repair_offsets: np.ndarray        # int64 [R] token offsets of repair rows (sorted)
-    prefix_token_count: int
-    block_specs: list[dict[str, Any]] = field(default_factory=list)
-    clone_tokens: Optional[np.ndarray] = None  # bool [T]: token's block is clone-mode
+    A batch of requests is their blocks request after request, with the
+    requests' slots concatenated (``blocks.destination_bases``); repair
+    positions are then destination indices."""
+
+    request_slots: torch.Tensor       # the request's slots by request position (on the pool device)
+    blocks: link_maps.BlockTable
+    handles: list[LegoLinkBlockHandle]
+    repair_positions: np.ndarray      # int64, sorted unique imp_indices (destination indices)
+    prefix_token_count: int           # identity tokens (block 0 of each request when it needs no remap)
+    max_position: int                 # largest local or global position of the link
+    leading_blocks: Optional[np.ndarray] = None  # bool [B]: identity blocks
+    request_count: int = 1
+
+    @classmethod
+    def batch(cls, maps: Sequence["LinkMaps"]) -> "LinkMaps":
+        """Several requests' links as one."""
+
+        if len(maps) == 1:
+            return maps[0]
+        sizes = [int(m.request_slots.numel()) for m in maps]
+        bases = np.concatenate(([0], np.cumsum(sizes)[:-1])).astype(np.int64)
+        request_slots = torch.cat([m.request_slots.to(torch.int64) for m in maps])
+        blocks = link_maps.concatenate_tables([m.blocks for m in maps], bases)
+        leading = np.concatenate([m.leading_blocks if m.leading_blocks is not None
+                                  else np.zeros(m.blocks.counts.size, dtype=bool) for m in maps])
+        repair = np.concatenate([m.repair_positions + base for m, base in zip(maps, bases)])
+        return cls(request_slots=request_slots, blocks=blocks,
+                   handles=[h for m in maps for h in m.handles], repair_positions=repair.astype(np.int64),
+                   prefix_token_count=sum(m.prefix_token_count for m in maps),
+                   max_position=max(m.max_position for m in maps), leading_blocks=leading,
+                   request_count=sum(m.request_count for m in maps))
 
     @property
     def token_count(self) -> int:
-        return int(self.local_positions.shape[0])
+        return self.blocks.token_count
+
+    @property
+    def local_positions(self) -> np.ndarray:
+        return np.concatenate([np.asarray(h.compile_local_positions, dtype=np.int64) for h in self.handles])
+
+    @property
+    def global_positions(self) -> np.ndarray:
+        return np.concatenate([np.arange(s, s + n, dtype=np.int64)
+                               for s, n in zip(self.blocks.starts.tolist(), self.blocks.counts.tolist())])
+
+    @property
+    def source_slots(self) -> torch.Tensor:
+        return torch.cat([h.slots_on(self.request_slots.device) for h in self.handles])
+
+    @property
+    def destination_slots(self) -> torch.Tensor:
+        return torch.cat([self.request_slots[s : s + n] for s, n in
+                          zip(self.blocks.destination_starts.tolist(), self.blocks.counts.tolist())]).long()
+
+    @property
+    def repair_offsets(self) -> np.ndarray:
+        """Concatenation offsets of the repair rows inside blocks, in plan order."""
+
+        block, offset = link_maps.repair_rows_in_blocks(self.blocks, self.repair_positions)
+        return (self.blocks.offsets[block] + offset).astype(np.int64)
+
+    @property
+    def clone_tokens(self) -> np.ndarray:
+        return np.repeat(self.blocks.sets == 1, self.blocks.counts)
+
+    @property
+    def block_specs(self) -> list[dict[str, Any]]:
+        block, _ = link_maps.repair_rows_in_blocks(self.blocks, self.repair_positions)
+        repairs = np.bincount(block, minlength=len(self.handles)) if block.size else np.zeros(len(self.handles), int)
+        specs = []
+        for index, handle in enumerate(self.handles):
+            start, count = int(self.blocks.starts[index]), int(self.blocks.counts[index])
+            specs.append({
+                "block_index": index,
+                "cache_key": handle.cache_key,
+                "start": start,
+                "end": start + count,
+                "token_count": count,
+                "storage_mode": handle.storage_mode,
+                "needs_rope_remap": _needs_rope_remap(handle, start),
+                "repair_token_count": int(repairs[index]),
+            })
+        return specs
+
+
+def _needs_rope_remap(handle: LegoLinkBlockHandle, start: int) -> bool:
+    """True unless every compile-time position equals the token's global one
+    (pic_runtime.py:4951-4955 decides by ``start != 0`` for positions 0..n-1)."""
+
+    if handle.local_start is not None:
+        return handle.local_start != start
+    return not np.array_equal(np.asarray(handle.compile_local_positions, dtype=np.int64),
+                              np.arange(start, start + handle.token_count, dtype=np.int64))
 
 
 def _validate_pool(pool: Any) -> None:
@@ -169,7 +252,10 @@ def _validate_pool(pool: Any) -> None:
 class PreparedLink:
     """One link, validated and with its device maps built; ``launch()`` enqueues
     the link kernel(s) on the current stream, ``write_repaired()`` the
-    repaired-row write-back of the rows the link skipped."""
+    repaired-row write-back of the rows the link skipped.
+
+    The maps are written by the map builder on the current stream at
+    construction; launch on the same stream (or synchronise first)."""
 
     def __init__(self, *, pool: Any, layers: list[int], maps: LinkMaps,
                  groups: list[tuple[list[int], RotarySpec]], boundary_repair_aware: bool,
@@ -180,63 +266,45 @@ class PreparedLink:
         self.maps = maps
         self.host_prepare_s = 0.0
         self.boundary_repair_aware = boundary_repair_aware
-        device = maps.destination_slots.device
         key_buffers = [pool.get_key_buffer(layer) for layer in layers]
         value_buffers = [pool.get_value_buffer(layer) for layer in layers]
         self.key_buffers, self.value_buffers = key_buffers, value_buffers
         token_count = maps.token_count
-        repair = maps.repair_offsets if boundary_repair_aware else np.zeros(0, dtype=np.int64)
-        self.repair_offsets = repair
-        self.repair_destination_slots = maps.destination_slots.index_select(
-            0, torch.from_numpy(repair).to(device)
-        ) if repair.size else maps.destination_slots[:0]
-        clone = maps.clone_tokens if maps.clone_tokens is not None else np.zeros(token_count, dtype=bool)
-        if clone.any() and arena is None:
+        if bool((maps.blocks.sets == 1).any()) and arena is None:
             raise LinkRuntimeError("PIC link of clone-mode blocks needs the snapshot arena.")
-        is_repair = np.zeros(token_count, dtype=bool)
-        is_repair[repair] = True
-        # One launch per source: the pool (reference blocks), the arena (clone blocks).
-        sources: list[tuple[np.ndarray, Optional[SnapshotArena]]] = []
-        for from_arena in (False, True):
-            members = clone if from_arena else ~clone
-            if members.any():
-                sources.append((members, arena if from_arena else None))
+        repair_positions = maps.repair_positions if boundary_repair_aware else np.zeros(0, dtype=np.int64)
+        plan = link_maps.plan_segments(maps.blocks, repair_positions, compact=compact_repair_rows,
+                                       leading_blocks=maps.leading_blocks)
+        self.segment_plan = plan
+        self.repair_offsets = plan.repair_offsets
+        built = link_maps.build_device_maps(plan, maps.request_slots, compact=compact_repair_rows)
+        self.device_maps = built
+        self.repair_destination_slots = built.repair_destination_slots
+        self.linked_token_count = token_count - plan.repair_count
         self._links: list[kv_link.PreparedKVLink] = []
-        self._keepalive: list[Any] = []
-        self.linked_token_count = 0
         index_of = {layer: i for i, layer in enumerate(layers)}
-        for members, source_arena in sources:
-            if compact_repair_rows:
-                selected = np.flatnonzero(members & ~is_repair)
-                mask_tensor = None
-            else:
-                selected = np.flatnonzero(members)
-                mask_tensor = (torch.from_numpy(is_repair[selected].astype(np.uint8)).to(device)
-                               if is_repair[selected].any() else None)
-            if selected.size == 0:
+        # One launch per source: set 0 reads the pool, set 1 the snapshot arena.
+        for source_set in (0, 1):
+            device_maps = built.maps[source_set]
+            if device_maps is None:
                 continue
-            prefix = int(np.count_nonzero(selected < maps.prefix_token_count))
-            selected_device = torch.from_numpy(selected).to(device)
-            source = maps.source_slots.index_select(0, selected_device)
-            destination = maps.destination_slots.index_select(0, selected_device)
-            positions = torch.from_numpy(np.stack((maps.local_positions[selected],
-                                                   maps.global_positions[selected]))).to(device)
-            self._keepalive.append((source, destination, positions, mask_tensor))
-            self.linked_token_count += int(np.count_nonzero(~is_repair[selected]))
+            source_arena = arena if source_set == 1 else None
+            prefix = plan.set_prefix[source_set]
+            mask = built.masks[source_set] if plan.set_repair_rows[source_set] else None
             for group_layers, rotary in groups:
                 indices = [index_of[layer] for layer in group_layers]
                 self._links.append(kv_link.PreparedKVLink(
                     key_buffers=[key_buffers[i] for i in indices],
                     value_buffers=[value_buffers[i] for i in indices],
-                    source_slots=source,
-                    destination_slots=destination,
-                    local_positions=positions[0],
-                    global_positions=positions[1],
+                    source_slots=device_maps[0],
+                    destination_slots=device_maps[1],
+                    local_positions=device_maps[2],
+                    global_positions=device_maps[3],
                     cos_sin_cache=rotary.cos_sin_cache,
                     prefix_token_count=prefix,
                     rotary_dim=rotary.rotary_dim,
                     is_neox_style=rotary.is_neox_style,
-                    repair_mask=mask_tensor,
+                    repair_mask=mask,
                     num_warps=num_warps,
                     layers_per_wave=layers_per_wave,
                     validate_indices=validate_indices,
@@ -252,7 +320,7 @@ class PreparedLink:
             key_row_bytes=key_row,
             value_row_bytes=value_row,
             remapped_token_count=token_count - maps.prefix_token_count,
-            repair_token_count=int(repair.size),
+            repair_token_count=plan.repair_count,
         )
         self.algorithmic_link_bytes = self.linked_token_count * (key_row + value_row) * 2 * len(layers)
 
@@ -282,10 +350,11 @@ class PreparedLink:
         )
 
     def record(self) -> dict[str, Any]:
+        blocks = self.maps.blocks
         return {
             "token_count": self.maps.token_count,
             "linked_token_count": self.linked_token_count,
-            "block_count": len(self.maps.block_specs),
+            "block_count": len(self.maps.handles),
             "prefix_token_count": self.maps.prefix_token_count,
             "remapped_token_count": self.maps.token_count - self.maps.prefix_token_count,
             "repair_token_count": int(self.repair_offsets.size),
@@ -293,8 +362,10 @@ class PreparedLink:
             "layers_written": len(self.layers),
             "kernel_launches": sum(info["launches"] for info in self.launch_info),
             "launch": self.launch_info,
-            "rope_remapped": [spec["needs_rope_remap"] for spec in self.maps.block_specs],
-            "storage_modes": [spec["storage_mode"] for spec in self.maps.block_specs],
+            "rope_remapped": [_needs_rope_remap(handle, start)
+                              for handle, start in zip(self.maps.handles, blocks.starts.tolist())],
+            "storage_modes": [handle.storage_mode for handle in self.maps.handles],
+            "map_runs": int(self.segment_plan.table.shape[0]),
             **self.traffic,
         }
 
@@ -323,7 +394,8 @@ class KVLinkExecutor:
     # -- maps ---------------------------------------------------------------
     def build_link_maps(self, destination_slots: torch.Tensor, link_plan: Mapping[str, Any],
                         *, device: Optional[torch.device] = None) -> LinkMaps:
-        """Concatenated maps in plan order (pic_runtime.py:4911-5013)."""
+        """The plan's blocks in plan order (pic_runtime.py:4905-5013): lookups and
+        checks per block, then block-level arrays for the map builder."""
 
         ranges = link_plan.get("block_ranges") or link_plan.get("attention_ranges")
         cache_keys = link_plan.get("cache_keys")
@@ -340,54 +412,47 @@ class KVLinkExecutor:
                 f"PIC RadixCache lookup cannot safely link block(s): {', '.join(unavailable)}"
             )
         device = destination_slots.device if device is None else device
-        repair_positions = sorted({int(p) for p in (link_plan.get("imp_indices") or [])})
-        repair_array = np.asarray(repair_positions, dtype=np.int64)
-        sources, destinations, locals_, globals_, repair_offsets, clones, specs = [], [], [], [], [], [], []
-        offset = 0
-        for block_index, (block_range, raw_key) in enumerate(zip(ranges, cache_keys)):
-            cache_key = str(raw_key)
-            handle = lookup.matched_blocks[cache_key]
-            start, end = int(block_range["start_token"]), int(block_range["end_token"])
-            count = end - start
-            if count != handle.token_count:
-                raise LinkRuntimeError(
-                    f"PIC token count mismatch for block {cache_key}: plan={count}, "
-                    f"snapshot={handle.token_count}"
-                )
-            if end > int(destination_slots.numel()) or start < 0:
-                raise LinkRuntimeError(f"PIC block {cache_key} range exceeds the request's slots.")
-            local = np.asarray(handle.compile_local_positions, dtype=np.int64)
-            global_ = np.arange(start, end, dtype=np.int64)
-            sources.append(handle.kv_slots.to(device, non_blocking=True))
-            destinations.append(destination_slots[start:end])
-            locals_.append(local)
-            globals_.append(global_)
-            clones.append(np.full(count, handle.storage_mode == "clone"))
-            inside = repair_array[(repair_array >= start) & (repair_array < end)]
-            repair_offsets.append(offset + inside - start)
-            specs.append({
-                "block_index": block_index,
-                "cache_key": cache_key,
-                "start": start,
-                "end": end,
-                "token_count": count,
-                "storage_mode": handle.storage_mode,
-                "needs_rope_remap": bool(np.any(local != global_)),
-                "repair_token_count": int(inside.size),
-            })
-            offset += count
-        first = specs[0]
-        prefix = 0 if first["needs_rope_remap"] else int(first["token_count"])
-        return LinkMaps(
-            source_slots=torch.cat(sources).long(),
-            destination_slots=torch.cat(destinations).to(device).long(),
-            local_positions=np.concatenate(locals_),
-            global_positions=np.concatenate(globals_),
-            repair_offsets=np.concatenate(repair_offsets).astype(np.int64),
-            prefix_token_count=prefix,
-            block_specs=specs,
-            clone_tokens=np.concatenate(clones),
-        )
+        request_slots = destination_slots
+        if request_slots.device != device or request_slots.dtype not in (torch.int32, torch.int64):
+            request_slots = request_slots.to(device=device, dtype=torch.int64)
+        request_slots = request_slots.contiguous()
+        total = int(request_slots.numel())
+        matched = lookup.matched_blocks
+        handles = [matched[str(key)] for key in cache_keys]
+        # Per block: the handle's cached record (count, slot and position
+        # addresses, local start, set, max local position) and the plan range.
+        records = np.array([handle.link_record(device) for handle in handles], dtype=np.int64)
+        bounds = np.array([(int(r["start_token"]), int(r["end_token"])) for r in ranges], dtype=np.int64)
+        starts, ends = bounds[:, 0].copy(), bounds[:, 1]
+        counts = records[:, 0].copy()
+        mismatch = np.flatnonzero(ends - starts != counts)
+        if mismatch.size:
+            index = int(mismatch[0])
+            raise LinkRuntimeError(
+                f"PIC token count mismatch for block {handles[index].cache_key}: "
+                f"plan={int(ends[index] - starts[index])}, snapshot={int(counts[index])}"
+            )
+        outside = np.flatnonzero((ends > total) | (starts < 0))
+        if outside.size:
+            raise LinkRuntimeError(
+                f"PIC block {handles[int(outside[0])].cache_key} range exceeds the request's slots.")
+        source_ptrs = records[:, 1].copy()
+        local_ptrs = records[:, 2].copy()
+        local_starts = records[:, 3].copy()
+        sets = records[:, 4].copy()
+        max_position = int(max(int(ends.max()) - 1, int(records[:, 5].max())))
+        blocks = link_maps.BlockTable(starts=starts, counts=counts, source_ptrs=source_ptrs,
+                                      local_ptrs=local_ptrs, local_starts=local_starts, sets=sets)
+        imp = link_plan.get("imp_indices")
+        repair = np.asarray(imp if imp is not None else [], dtype=np.int64).reshape(-1)
+        if repair.size > 1 and not bool(np.all(repair[1:] > repair[:-1])):
+            repair = np.unique(repair)
+        identity = not _needs_rope_remap(handles[0], int(starts[0]))
+        leading = np.zeros(len(handles), dtype=bool)
+        leading[0] = identity
+        return LinkMaps(request_slots=request_slots, blocks=blocks, handles=handles,
+                        repair_positions=repair, prefix_token_count=int(counts[0]) if identity else 0,
+                        max_position=int(max_position), leading_blocks=leading)
 
     # -- link ---------------------------------------------------------------
     def _layer_groups(self, layers: list[int], max_position: int,
@@ -417,8 +482,36 @@ class KVLinkExecutor:
             boundary_repair_aware = _env_flag("SGLANG_PIC_TRITON_BOUNDARY_REPAIR_AWARE", "0")
         device = pool.get_key_buffer(self.start_layer).device
         maps = self.build_link_maps(destination_slots, link_plan, device=device)
-        max_position = int(max(maps.local_positions.max(), maps.global_positions.max()))
-        groups = self._layer_groups(self.layers, max_position, device)
+        groups = self._layer_groups(self.layers, maps.max_position, device)
+        prepared = PreparedLink(
+            pool=pool, layers=self.layers, maps=maps, groups=groups,
+            boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,
+            num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
+            validate_indices=validate_indices, arena=self.arena,
+        )
+        prepared.host_prepare_s = time.perf_counter() - started
+        return prepared
+
+    def prepare_links(self, pool: Any, requests: Sequence[tuple[torch.Tensor, Mapping[str, Any]]], *,
+                      boundary_repair_aware: Optional[bool] = None, compact_repair_rows: bool = True,
+                      validate_indices: bool = False) -> PreparedLink:
+        """Several requests' links as one prepared link: one map-builder call and
+        one link launch per source for the whole batch.  ``requests`` holds
+        (destination_slots, link_plan) pairs; the result equals linking them one
+        by one (destinations of different requests must be distinct).  Every
+        request's identity block heads its set's maps, so it is copied
+        unrotated as in a single link; the repair rows of the write-back are
+        request after request, each in plan order."""
+
+        started = time.perf_counter()
+        if not requests:
+            raise LinkRuntimeError("PIC batched link has no requests.")
+        _validate_pool(pool)
+        if boundary_repair_aware is None:
+            boundary_repair_aware = _env_flag("SGLANG_PIC_TRITON_BOUNDARY_REPAIR_AWARE", "0")
+        device = pool.get_key_buffer(self.start_layer).device
+        maps = LinkMaps.batch([self.build_link_maps(slots, plan, device=device) for slots, plan in requests])
+        groups = self._layer_groups(self.layers, maps.max_position, device)
         prepared = PreparedLink(
             pool=pool, layers=self.layers, maps=maps, groups=groups,
             boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,

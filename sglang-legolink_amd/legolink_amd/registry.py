@@ -17,6 +17,7 @@ import threading
 from dataclasses import dataclass, field
 from typing import Iterable, Optional, Sequence
 
+import numpy as np
 import torch
 
 
@@ -34,10 +35,56 @@ class LegoLinkBlockHandle:
     generation: int = 0
     valid: bool = True
     stale_reason: Optional[str] = None
+    # Derived at registration: local position of token 0 when the positions
+    # are consecutive (None otherwise), and their maximum (-1 when empty).
+    local_start: Optional[int] = 0
+    max_local_position: int = -1
+    # Per-device copies the link reads (int64 slots; non-consecutive positions).
+    _device_tensors: dict = field(default_factory=dict, repr=False, compare=False)
 
     @property
     def token_count(self) -> int:
         return len(self.token_ids)
+
+    def link_record(self, device: torch.device) -> tuple[int, int, int, int, int, int]:
+        """(token count, address of the int64 slots on ``device``, address of the
+        int64 compile-time positions or 0 when consecutive, local position of
+        token 0, source set (1: snapshot arena), largest local position) --
+        what a link reads per block, cached per device."""
+
+        key = ("record", device.type, device.index)
+        record = self._device_tensors.get(key)
+        if record is None:
+            local = self.local_positions_on(device)
+            record = (self.token_count, self.slots_on(device).data_ptr(),
+                      0 if local is None else local.data_ptr(),
+                      0 if self.local_start is None else self.local_start,
+                      1 if self.storage_mode == "clone" else 0, self.max_local_position)
+            self._device_tensors[key] = record
+        return record
+
+    def slots_on(self, device: torch.device) -> torch.Tensor:
+        """``kv_slots`` as a contiguous int64 tensor on ``device`` (cached)."""
+
+        key = ("slots", str(device))
+        cached = self._device_tensors.get(key)
+        if cached is None:
+            cached = self.kv_slots.to(device=device, dtype=torch.int64).contiguous()
+            self._device_tensors[key] = cached
+        return cached
+
+    def local_positions_on(self, device: torch.device) -> Optional[torch.Tensor]:
+        """The compile-time positions as an int64 tensor on ``device``, or None
+        when they are consecutive (``local_start + i``)."""
+
+        if self.local_start is not None:
+            return None
+        key = ("local", str(device))
+        cached = self._device_tensors.get(key)
+        if cached is None:
+            cached = torch.tensor(self.compile_local_positions, dtype=torch.int64, device=device)
+            self._device_tensors[key] = cached
+        return cached
 
 
 @dataclass
@@ -80,6 +127,14 @@ class LegoLinkBlockRegistry:
             raise ValueError("compile_local_positions must hold one position per token.")
         if storage_mode not in ("reference", "clone"):
             raise ValueError(f"Unsupported PIC storage mode: {storage_mode}")
+        position_array = np.asarray(positions, dtype=np.int64)
+        if position_array.size == 0:
+            local_start, max_local = 0, -1
+        else:
+            consecutive = bool(np.array_equal(
+                position_array, position_array[0] + np.arange(position_array.size, dtype=np.int64)))
+            local_start = int(position_array[0]) if consecutive else None
+            max_local = int(position_array.max())
         with self._lock:
             resident = self._blocks.get(str(cache_key))
             if resident is not None and resident.valid:
@@ -93,6 +148,8 @@ class LegoLinkBlockRegistry:
                 block_id=str(block_id or cache_key),
                 generation=self._generation,
                 storage_mode=storage_mode,
+                local_start=local_start,
+                max_local_position=max_local,
             )
             self._blocks[str(cache_key)] = handle
             return handle

@@ -231,3 +231,77 @@ def test_prepared_link_replays_in_a_hip_graph(gpu_device):
         actual = [bits(k) for k in pool.k_buffer] + [bits(v) for v in pool.v_buffer]
         for a, b in zip(actual, expected):
             assert np.array_equal(a, b), f"replay {replay}"
+
+
+def test_batched_link_equals_request_by_request_links(gpu_device):
+    """prepare_links over several requests -- identity first blocks, a request
+    behind a chat prefix, a block compiled behind a prefix, clone blocks in
+    the snapshot arena, shared blocks, repair rows -- leaves the pool
+    bit-identical to linking and repairing each request alone."""
+
+    from legolink_amd.link_runtime import SnapshotArena
+
+    layers, slots, heads, dim = 3, 8192, 4, 128
+    rng = np.random.default_rng(31)
+    generator = torch.Generator(device=gpu_device).manual_seed(31)
+    keys = [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
+            for _ in range(layers)]
+    values = [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
+              for _ in range(layers)]
+    pool_a = KVPool(keys, values)
+    pool_b = KVPool([k.clone() for k in keys], [v.clone() for v in values])
+    arena = SnapshotArena.allocate(num_slots=2048, num_layers=layers, num_heads=heads, head_dim=dim,
+                                   device=gpu_device)
+    registry = LegoLinkBlockRegistry()
+    rotary = RotarySpec(build_cos_sin_cache(8192, dim), rotary_dim=dim)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers, arena=arena)
+    perm = rng.permutation(slots)
+    cursor = 0
+    lengths = [120, 64, 300, 45, 200, 90]
+    for index, length in enumerate(lengths):
+        block_slots = torch.from_numpy(perm[cursor : cursor + length]).to(gpu_device)
+        cursor += length
+        positions = (np.arange(length) + 700).tolist() if index == 3 else None
+        executor.capture_block(pool_a, f"b{index}", list(range(length)), block_slots,
+                               storage_mode="clone" if index in (1, 4) else "reference",
+                               compile_local_positions=positions)
+    torch.cuda.synchronize(gpu_device)
+
+    def plan_of(names, start=0):
+        ranges, cursor_ = [], start
+        for name in names:
+            count = lengths[int(name[1:])]
+            ranges.append({"start_token": cursor_, "end_token": cursor_ + count})
+            cursor_ += count
+        imp = [r["start_token"] + k for r in ranges[1:] for k in range(8)]
+        return {"cache_keys": list(names), "block_ranges": ranges, "imp_indices": imp}, cursor_
+
+    requests = []
+    for names, start in ((["b0", "b1", "b2"], 0), (["b4", "b3"], 5), (["b1", "b5", "b0"], 0),
+                         (["b2", "b4"], 0)):
+        plan, total = plan_of(names, start)
+        destination = torch.from_numpy(perm[cursor : cursor + total]).to(gpu_device)
+        cursor += total
+        requests.append((destination, plan))
+    report(f"batched link: {len(requests)} requests, {cursor} slots used")
+
+    batched = executor.prepare_links(pool_a, requests, boundary_repair_aware=True)
+    batched.launch()
+    rows = int(batched.repair_offsets.size)
+    repaired_k = torch.randn(layers, rows, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
+    repaired_v = torch.randn_like(repaired_k)
+    batched.write_repaired(repaired_k, repaired_v)
+    assert len(batched.launch_info) == 2  # one launch per source: pool, arena
+
+    row = 0
+    for destination, plan in requests:
+        single = executor.prepare_link(pool_b, destination, plan, boundary_repair_aware=True)
+        single.launch()
+        count = int(single.repair_offsets.size)
+        single.write_repaired(repaired_k[:, row : row + count].contiguous(),
+                              repaired_v[:, row : row + count].contiguous())
+        row += count
+    assert row == rows
+    torch.cuda.synchronize(gpu_device)
+    for a, b in zip(pool_a.k_buffer + pool_a.v_buffer, pool_b.k_buffer + pool_b.v_buffer):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
