@@ -2,9 +2,11 @@
 
 One step = one link of the workload: the fused gather -> RoPE re-rotation ->
 scatter over every layer (repair rows left out) plus the repaired-row
-write-back, with every input already resident in HBM.  The link and the
-write-back are prepared once (validation, argument blocks) and launched per
-step; preparation is reported separately.  Prints one JSON line.
+write-back, with every input already resident in HBM.  The link runs through
+the product's executor: the workload's blocks are registered, each request's
+plan is prepared once (registry lookup, token maps built on the device,
+launch arguments) and the prepared link and write-back are launched per step;
+preparation is timed separately (``host_prepare_ms``).  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload c2]
 
@@ -223,7 +225,7 @@ def ceiling(args: argparse.Namespace) -> None:
         ms = _median_ms(torch, run, args.steps, args.warmup)
         results[name] = {"ms": round(ms, 5), "GBps": round(link_bytes / ms / 1e6, 1)}
         log(f"{name}: {ms:.4f} ms, {link_bytes / ms / 1e6:.1f} GB/s")
-    del keys, values
+    del keys, values, pool, prepared, link, scatter
     torch.cuda.empty_cache()
     nbytes = 4 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
@@ -275,8 +277,9 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from legolink_amd import kv_link
-    from legolink_amd.rope import build_cos_sin_cache
+    from legolink_amd.link_runtime import KVLinkExecutor, KVPool
+    from legolink_amd.registry import LegoLinkBlockRegistry
+    from legolink_amd.rope import RotarySpec, build_cos_sin_cache
     from legolink_amd.workloads import make_workload
 
     device = torch.device("cuda", 0)
@@ -298,37 +301,41 @@ def main() -> int:
     torch.cuda.synchronize(device)
     setup_s = time.perf_counter() - host_start
 
-    # Host preparation of one link: token maps to the device, argument blocks
-    # validated and built.  Timed separately; not part of the step.
-    prepare_start = time.perf_counter()
-    if args.repair_rows == "compact":
-        keep = workload.repair_mask == 0
-        maps = [workload.source_slots[keep], workload.destination_slots[keep],
-                workload.local_positions[keep], workload.global_positions[keep]]
-        prefix = int(np.count_nonzero(keep[: workload.prefix_token_count]))
-        mask = None
-    else:
-        maps = [workload.source_slots, workload.destination_slots, workload.local_positions,
-                workload.global_positions]
-        prefix = workload.prefix_token_count
-        mask = torch.from_numpy(workload.repair_mask).to(device)
-    packed = torch.from_numpy(np.stack(maps)).to(device)
-    src, dst, local, glob = packed[0], packed[1], packed[2], packed[3]
-    repair_slots = torch.from_numpy(workload.repair_destination_slots).to(device)
-    link = kv_link.PreparedKVLink(
-        key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
-        local_positions=local, global_positions=glob, cos_sin_cache=table,
-        prefix_token_count=prefix, rotary_dim=workload.rotary_dim,
-        is_neox_style=True, repair_mask=mask, num_warps=args.waves_per_block,
-        layers_per_wave=args.layers_per_wave, layer_groups_per_block=args.layer_groups_per_block,
-    )
-    scatter = kv_link.PreparedKVScatter(
-        key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
-        repaired_keys=repaired_k, repaired_values=repaired_v,
-    )
+    # Host preparation of one link through the executor, as a serving loop runs
+    # it: registry lookup -> plan -> token maps built on the device -> launch
+    # arguments validated and built.  Timed separately (median of 5); not part
+    # of the step.  Batched workloads (several requests) prepare one link.
+    registry = LegoLinkBlockRegistry()
+    blocks, requests = workload.link_requests()
+    for key, (source, local) in blocks.items():
+        registry.register_legolink_block(key, range(source.size), torch.from_numpy(source).to(device),
+                                         compile_local_positions=local.tolist())
+    requests = [(torch.from_numpy(slots).to(device), plan) for slots, plan in requests]
+    executor = KVLinkExecutor(registry, RotarySpec(table, rotary_dim=workload.rotary_dim),
+                              end_layer=shape.layers, num_warps=args.waves_per_block,
+                              layers_per_wave=args.layers_per_wave,
+                              layer_groups_per_block=args.layer_groups_per_block)
+    pool = KVPool(keys, values)
+    compact = args.repair_rows == "compact"
+    prepare_ms = []
+    for _ in range(5):
+        torch.cuda.synchronize(device)
+        prepare_start = time.perf_counter()
+        if len(requests) == 1:
+            prepared = executor.prepare_link(pool, requests[0][0], requests[0][1], boundary_repair_aware=True,
+                                             compact_repair_rows=compact)
+        else:
+            prepared = executor.prepare_links(pool, requests, boundary_repair_aware=True,
+                                              compact_repair_rows=compact)
+        prepare_ms.append((time.perf_counter() - prepare_start) * 1e3)
     torch.cuda.synchronize(device)
-    host_prepare_ms = (time.perf_counter() - prepare_start) * 1e3
-    launch = link.launch
+    host_prepare_ms = float(np.median(prepare_ms))
+    if (prepared.linked_token_count != workload.tokens - workload.repair_rows
+            or int(prepared.repair_offsets.size) != workload.repair_rows):
+        raise RuntimeError("prepared link does not match the workload's token and repair-row counts")
+    link = prepared.launch
+    scatter = prepared.prepare_write_repaired(repaired_k, repaired_v)
+    launch = prepared.launch_info[0]
     log(f"setup {setup_s:.1f}s; host prepare {host_prepare_ms:.2f} ms; link launch {launch}")
 
     for _ in range(args.warmup):
@@ -409,7 +416,7 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
-    del keys, values
+    del keys, values, pool, prepared, link, scatter
     torch.cuda.empty_cache()
     if args.cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(workload, args)

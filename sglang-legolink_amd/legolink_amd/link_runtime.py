@@ -260,7 +260,8 @@ class PreparedLink:
     def __init__(self, *, pool: Any, layers: list[int], maps: LinkMaps,
                  groups: list[tuple[list[int], RotarySpec]], boundary_repair_aware: bool,
                  compact_repair_rows: bool, num_warps: Optional[int], layers_per_wave: int,
-                 validate_indices: bool, arena: Optional[SnapshotArena] = None) -> None:
+                 validate_indices: bool, arena: Optional[SnapshotArena] = None,
+                 layer_groups_per_block: int = 0) -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -307,6 +308,7 @@ class PreparedLink:
                     repair_mask=mask,
                     num_warps=num_warps,
                     layers_per_wave=layers_per_wave,
+                    layer_groups_per_block=layer_groups_per_block,
                     validate_indices=validate_indices,
                     source_key_buffers=(None if source_arena is None else
                                         [source_arena.get_key_buffer(layer) for layer in group_layers]),
@@ -375,7 +377,8 @@ class KVLinkExecutor:
 
     def __init__(self, registry: LegoLinkBlockRegistry, rotary: RotarySpec | Mapping[int, RotarySpec], *,
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
-                 layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None) -> None:
+                 layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
+                 layer_groups_per_block: int = 0) -> None:
         self.registry = registry
         self.start_layer = int(start_layer)
         self.end_layer = int(end_layer)
@@ -385,6 +388,7 @@ class KVLinkExecutor:
             self.rotary_by_layer = dict(rotary)
         self.num_warps = num_warps
         self.layers_per_wave = layers_per_wave
+        self.layer_groups_per_block = layer_groups_per_block
         self.arena = arena
 
     @property
@@ -488,6 +492,7 @@ class KVLinkExecutor:
             boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
+            layer_groups_per_block=self.layer_groups_per_block,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -517,6 +522,7 @@ class KVLinkExecutor:
             boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
+            layer_groups_per_block=self.layer_groups_per_block,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared

@@ -90,6 +90,41 @@ class LinkWorkload:
     def max_position(self) -> int:
         return int(max(self.local_positions.max(), self.global_positions.max()))
 
+    def link_requests(self) -> tuple[dict[str, tuple[np.ndarray, np.ndarray]],
+                                     list[tuple[np.ndarray, dict]]]:
+        """The workload as the link executor's inputs.
+
+        Returns the blocks to register (cache key -> (source slots, compile-time
+        positions); a catalogue block shared by several requests is one entry)
+        and, per request, its destination slots indexed by request position
+        (positions before its first block hold 0 and are never read) and its
+        link plan (``cache_keys``, ``block_ranges``, ``imp_indices``)."""
+
+        blocks: dict[str, tuple[np.ndarray, np.ndarray]] = {}
+        requests: list[tuple[np.ndarray, dict]] = []
+        lengths = self.block_lengths
+        per_request = len(lengths) // self.requests
+        cursor = 0
+        for request in range(self.requests):
+            own = lengths[request * per_request : (request + 1) * per_request]
+            span = slice(cursor, cursor + int(sum(own)))
+            positions = self.global_positions[span]
+            destination = np.zeros(int(positions.max()) + 1, dtype=np.int64)
+            destination[positions] = self.destination_slots[span]
+            keys, ranges = [], []
+            for n in own:
+                source = self.source_slots[cursor : cursor + n]
+                local = self.local_positions[cursor : cursor + n]
+                key = f"blk-{int(source[0])}-{n}-{int(local[0])}"
+                blocks.setdefault(key, (source, local))
+                start = int(self.global_positions[cursor])
+                keys.append(key)
+                ranges.append({"start_token": start, "end_token": start + int(n)})
+                cursor += n
+            imp = positions[self.repair_mask[span] == 1].tolist()
+            requests.append((destination, {"cache_keys": keys, "block_ranges": ranges, "imp_indices": imp}))
+        return blocks, requests
+
     def algorithmic_bytes(self) -> dict[str, int]:
         """Bytes the link step must move: copied tokens plus repaired rows,
         K and V of every layer, read once and written once."""
