@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 4
+#define LL_ABI_VERSION 5
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -266,6 +266,82 @@ typedef struct ll_link_maps_args {
   int64_t repair_capacity;
 } ll_link_maps_args;
 
+/*
+ * Sparse repair attention: the attention of the repair pass over the linked KV.
+ *
+ * A repair row is a contiguous span of query positions [query_start,
+ * query_start + query_count) of one request.  Its keys and values are the
+ * request's tokens at logical positions 0 .. query_start + query_count - 1,
+ * found through the request's slot list: the slot of logical position j is
+ * kv_slots[kv_offset + j].  Query i of the row (position p = query_start + i)
+ * sees exactly the positions j <= p (the explicit causal rule of the
+ * reference's physical-slot pattern); with G = num_q_heads / num_kv_heads,
+ * query head h reads KV head h / G:
+ *     out[query_index + i][h] = sum_j softmax_j(scale * q . K[slot_j][h / G]) V[slot_j][h / G]
+ * The softmax is computed online in fp32 with exp2; scores and probabilities
+ * come from bf16 MFMA products accumulated in fp32 (probabilities are rounded
+ * to bf16 for the value product), and the output is rounded once to bf16.
+ * Slots outside [0, num_slots) are invisible (never read).
+ *
+ * Two phases, like the reference's plan/run wrapper:
+ *   ll_repair_attention_plan (host only) cuts the rows into work items of at
+ *   most 16 queries, splitting long KV ranges for parallelism, and writes the
+ *   item and combine tables; the caller copies them to the device once and
+ *   reuses them for every layer.  Call it with NULL tables to size them.
+ *   ll_repair_attention runs one layer.
+ *
+ * Replaces the FlashInfer block-sparse repair attention of
+ * patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py
+ * (build_explicit_causal_masked_pattern :1241-1263, the plan/run of
+ * _try_flashinfer_sparse_attention_single :2009-2272, and the row batching of
+ * build_grouped_explicit_causal_masked_pattern :1266-1318), whose semantics the
+ * reference restates as gqa_attention + logical_causal_mask in
+ * tests/pic/reference/attention_reference.py.
+ */
+typedef struct ll_repair_row {
+  int64_t query_index;             /* index of the row's first query in query / output */
+  int64_t query_start;             /* logical position of the row's first query */
+  int64_t query_count;             /* >= 1 */
+  int64_t kv_offset;               /* index in kv_slots of logical position 0's slot */
+} ll_repair_row;
+
+typedef struct ll_repair_attention_plan_info {
+  int64_t num_items;               /* int32 [num_items, 8] work items */
+  int64_t num_combine;             /* int32 [num_combine, 4] combine items */
+  int64_t workspace_items;         /* partial results (see ll_repair_attention_args.workspace) */
+  int64_t split_tokens;            /* KV tokens per work item (the plan's choice when 0 was asked) */
+} ll_repair_attention_plan_info;
+
+typedef struct ll_repair_attention_args {
+  int64_t struct_size;             /* sizeof(ll_repair_attention_args) */
+  const void *query;               /* device bf16 [num_queries, num_q_heads, head_dim], dense */
+  void *output;                    /* device bf16 [num_queries, num_q_heads, head_dim], dense */
+  int64_t num_queries;
+  const void *key_buffer;          /* device bf16 [num_slots, num_kv_heads, head_dim]: one layer */
+  const void *value_buffer;        /* device bf16 [num_slots, num_kv_heads, head_dim] */
+  int64_t num_slots;
+  int64_t num_q_heads;
+  int64_t num_kv_heads;            /* divides num_q_heads, at most 8 query heads per KV head */
+  int64_t head_dim;                /* 64 or 128 */
+  int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 */
+  double softmax_scale;
+  const void *kv_slots;            /* device int32/int64 [kv_slots_len]: the requests' slot lists */
+  int64_t kv_slots_dtype;
+  int64_t kv_slots_len;
+  const int32_t *items;            /* device copy of the plan's work items */
+  int64_t num_items;
+  const int32_t *combine;          /* device copy of the plan's combine items, or NULL */
+  int64_t num_combine;
+  float *workspace;                /* device fp32 [workspace_items, num_q_heads, 16, head_dim + 2] */
+  int64_t workspace_items;
+} ll_repair_attention_args;
+
+int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_kv_heads,
+                             int64_t split_tokens, int32_t *items, int64_t items_capacity,
+                             int32_t *combine, int64_t combine_capacity,
+                             ll_repair_attention_plan_info *info);
+int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream);
+
 /* Which kernel and launch shape ll_kv_link would use (no GPU work). */
 typedef struct ll_launch_info {
   int64_t kernel;                  /* LL_KERNEL_VECTOR or LL_KERNEL_GENERIC */
@@ -290,6 +366,7 @@ int ll_abi_version(void);
 int64_t ll_kv_link_args_size(void);
 int64_t ll_kv_scatter_args_size(void);
 int64_t ll_link_maps_args_size(void);
+int64_t ll_repair_attention_args_size(void);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,7 @@
 #include <string>
 
 #include "legolink_kv.h"
+#include "ll_internal.h"
 
 #pragma clang fp contract(off)
 
@@ -573,13 +574,11 @@ __global__ void __launch_bounds__(256) build_link_maps_kernel(const MapParams p)
 thread_local std::string g_last_error;
 
 int fail(int code, const char *fmt, ...) {
-  char buf[512];
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
+  const int rc = ll_record_error(code, fmt, ap);
   va_end(ap);
-  g_last_error = buf;
-  return code;
+  return rc;
 }
 
 bool is_index_dtype(int64_t dt) { return dt == LL_DTYPE_INT32 || dt == LL_DTYPE_INT64; }
@@ -762,6 +761,13 @@ void launch_generic(int cache_dtype, dim3 grid, dim3 block, hipStream_t s, const
 }
 
 }  // namespace
+
+int ll_record_error(int code, const char *fmt, va_list ap) {
+  char buf[512];
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  g_last_error = buf;
+  return code;
+}
 
 extern "C" {
 

@@ -1,0 +1,463 @@
+// Sparse repair attention on gfx950 (MI355X): the repair pass's attention of
+// repair rows over the linked KV, read through each request's slot list.
+//
+// Work decomposition (planned on the host by ll_repair_attention_plan):
+//   item = up to 16 consecutive queries of one repair row and a KV range
+//   [kv_begin, kv_end) of logical positions; long ranges are split and the
+//   partial results merged by a combine pass.
+//   workgroup = (item, KV head); wave w = query head hk * G + w (G query heads
+//   share one KV head, G <= 8), so the K/V tiles staged in LDS serve G heads.
+//
+// Per 64-token KV tile:
+//   1. gather the tile's K rows (token-major, [token][dim]) and V rows
+//      (transposed, [dim][token]) of this KV head into LDS by slot;
+//   2. S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 K rows from LDS,
+//      B = the wave's 16 queries (kept in registers).  The accumulator layout
+//      gives each lane 4 consecutive tokens of one query;
+//   3. masking (causal by logical position, split range, invalid slots),
+//      online softmax in fp32 with exp2 (row statistics reduced across the
+//      four lanes of a query with xor shuffles 16 and 32);
+//   4. O^T += V^T P^T with v_mfma_f32_16x16x16_bf16: B = the probabilities
+//      straight from the S^T accumulators (4 consecutive tokens of one query
+//      per lane is exactly the B operand layout), A = 4 tokens of one dim row
+//      of the transposed V tile.
+// Lane layouts (checked on the device): 16x16x32 A/B lane l element e ->
+// row/column l % 16, k = 8 (l / 16) + e; 16x16x16 k = 4 (l / 16) + e;
+// accumulator register r -> row 4 (l / 16) + r, column l % 16.
+//
+// Roofline: MFMA-bound.  Algorithmic work per (query, visible key) pair and
+// query head: 4 * head_dim flops (QK and PV); KV bytes are read once per
+// 16-query item and KV head.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "legolink_kv.h"
+#include "ll_internal.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kQueries = 16;  // queries per item: one MFMA column tile
+constexpr int kTile = 64;     // KV tokens per LDS tile
+constexpr int kItemInts = 8;
+constexpr int kCombineInts = 4;
+constexpr int kMaxGroup = 8;  // query heads per KV head = waves per workgroup
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  const int rc = ll_record_error(code, fmt, ap);
+  va_end(ap);
+  return rc;
+}
+
+struct AttnParams {
+  const uint16_t *q;
+  uint16_t *out;
+  const uint16_t *k;
+  const uint16_t *v;
+  const void *slots;
+  const int *items;
+  const int *combine;
+  float *ws;
+  long long num_queries;
+  long long num_slots;
+  long long slots_len;
+  long long ws_items;
+  int hq;
+  int hkv;
+  int group;
+  int slots64;
+  float scale_log2;
+};
+
+__device__ inline uint16_t bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ inline long long slot_at(const AttnParams &p, long long i) {
+  return p.slots64 ? static_cast<const long long *>(p.slots)[i]
+                   : static_cast<long long>(static_cast<const int *>(p.slots)[i]);
+}
+
+// Partial results of item `partial`, query head h: O [16][D] then (m, l) [16][2].
+template <int D>
+__device__ inline float *partial_block(const AttnParams &p, int partial, int h) {
+  return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
+}
+
+template <int D>
+__global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(const AttnParams p) {
+  constexpr int kSteps = D / 32;     // k-steps of S^T = K Q^T
+  constexpr int kDimTiles = D / 16;  // 16-row tiles of O^T
+  constexpr int kKRow = D + 8;       // LDS row stride of K (elements), spreads banks
+  constexpr int kVRow = kTile + 8;   // LDS row stride of transposed V
+  constexpr int kParts = D / 8;      // 16-byte chunks per head row
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTile * kKRow];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * kVRow];
+  __shared__ unsigned char token_ok[kTile];
+
+  const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
+  const int q_index = it[0], q_pos = it[1], q_count = it[2], kv_off = it[3];
+  const int kv_begin = it[4], kv_end = it[5], partial = it[6];
+  const int hk = blockIdx.y;
+  // Items come from the planner; a malformed one is skipped whole (uniform).
+  if (q_count < 1 || q_count > kQueries || q_index < 0 ||
+      static_cast<long long>(q_index) + q_count > p.num_queries || q_pos < 0 || kv_off < 0 ||
+      kv_begin < 0 || kv_begin > kv_end || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
+      partial >= p.ws_items || (partial < 0 && partial != -1) || hk >= p.hkv)
+    return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int g = lane / 16;   // lane group: k (or row) block of the MFMA operands
+  const int c = lane % 16;   // query of this lane in the S^T / O^T accumulators
+  const int hq = hk * p.group + wave;
+  const bool q_ok = c < q_count;
+  const int my_pos = q_pos + c;
+  const int kv_stop = min(kv_end, q_pos + q_count);  // last query sees [0, q_pos + q_count)
+
+  // The wave's queries as the B operand of S^T = K Q^T: query c, dims 32 ks + 8 g + e.
+  bf16x8 qf[kSteps];
+  {
+    const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      u32x4 bits = {0u, 0u, 0u, 0u};
+      if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
+      qf[ks] = __builtin_bit_cast(bf16x8, bits);
+    }
+  }
+
+  float m = -INFINITY;
+  float l = 0.f;
+  f32x4 o[kDimTiles];
+#pragma unroll
+  for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const long long row_stride = static_cast<long long>(p.hkv) * D;  // elements per slot
+  for (int t0 = kv_begin; t0 < kv_stop; t0 += kTile) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    // K: token-major (16 lanes cover one 256-byte row: coalesced), V: token-minor
+    // (consecutive lanes write consecutive tokens of a transposed row).
+    for (int ci = tid; ci < kTile * kParts; ci += blockDim.x) {
+      {
+        const int tok = ci / kParts, part = ci % kParts;
+        const int j = t0 + tok;
+        u32x4 kc = {0u, 0u, 0u, 0u};
+        if (j < kv_stop) {
+          const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
+          if (slot >= 0 && slot < p.num_slots)
+            kc = *reinterpret_cast<const u32x4 *>(p.k + slot * row_stride + hk * D + part * 8);
+        }
+        *reinterpret_cast<u32x4 *>(&k_lds[tok * kKRow + part * 8]) = kc;
+      }
+      {
+        const int tok = ci % kTile, part = ci / kTile;
+        const int j = t0 + tok;
+        u32x4 vc = {0u, 0u, 0u, 0u};
+        bool ok = false;
+        if (j < kv_stop) {
+          const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
+          ok = slot >= 0 && slot < p.num_slots;
+          if (ok) vc = *reinterpret_cast<const u32x4 *>(p.v + slot * row_stride + hk * D + part * 8);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v_lds[(part * 8 + 2 * e) * kVRow + tok] = static_cast<uint16_t>(vc[e] & 0xffffu);
+          v_lds[(part * 8 + 2 * e + 1) * kVRow + tok] = static_cast<uint16_t>(vc[e] >> 16);
+        }
+        if (part == 0) token_ok[tok] = ok ? 1 : 0;
+      }
+    }
+    __syncthreads();
+
+    // S^T tile: lane holds tokens 16 n + 4 g + r for query c.
+    f32x4 s[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(&k_lds[(16 * n + c) * kKRow + 32 * ks + 8 * g]);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
+      }
+    }
+    float tile_max = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 16 * n + 4 * g + r;
+        const int j = t0 + tok;
+        const bool visible = q_ok && j < kv_stop && j <= my_pos && token_ok[tok];
+        const float val = visible ? s[n][r] * p.scale_log2 : -INFINITY;
+        s[n][r] = val;
+        tile_max = fmaxf(tile_max, val);
+      }
+    }
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+    const float m_new = fmaxf(m, tile_max);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - m_use);
+    float row_sum = 0.f;
+    i16x4 pb[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = exp2f(s[n][r] - m_use);
+        row_sum += pv;
+        pb[n][r] = static_cast<short>(bf16_rne(pv));
+      }
+    }
+    row_sum += __shfl_xor(row_sum, 16);
+    row_sum += __shfl_xor(row_sum, 32);
+    l = l * alpha + row_sum;
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      o[dt] *= alpha;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const i16x4 a = *reinterpret_cast<const i16x4 *>(&v_lds[(16 * dt + c) * kVRow + 16 * n + 4 * g]);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[n], o[dt], 0, 0, 0);
+      }
+    }
+  }
+  // o[dt][r] = O^T[dim 16 dt + 4 g + r][query c].
+  if (partial < 0) {
+    if (!q_ok) return;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      u32x2 packed;
+      packed[0] = bf16_rne(o[dt][0] * inv) | (static_cast<uint32_t>(bf16_rne(o[dt][1] * inv)) << 16);
+      packed[1] = bf16_rne(o[dt][2] * inv) | (static_cast<uint32_t>(bf16_rne(o[dt][3] * inv)) << 16);
+      *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
+    }
+  } else {
+    float *block = partial_block<D>(p, partial, hq);
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt)
+      *reinterpret_cast<f32x4 *>(block + c * D + 16 * dt + 4 * g) = o[dt];
+    if (g == 0) {
+      block[kQueries * D + 2 * c] = m;
+      block[kQueries * D + 2 * c + 1] = l;
+    }
+  }
+}
+
+// Merges the split partial results of one 16-query tile: workgroup (combine
+// item, query head); thread = (query, 1/16 of the dims).
+template <int D>
+__global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p) {
+  constexpr int kPer = D / 16;
+  const int *ci = p.combine + static_cast<long long>(blockIdx.x) * kCombineInts;
+  const int q_index = ci[0], q_count = ci[1], first = ci[2], count = ci[3];
+  if (q_count < 1 || q_count > kQueries || q_index < 0 ||
+      static_cast<long long>(q_index) + q_count > p.num_queries || first < 0 || count < 1 ||
+      static_cast<long long>(first) + count > p.ws_items)
+    return;
+  const int h = blockIdx.y;
+  const int c = threadIdx.x / 16;
+  const int part = threadIdx.x % 16;
+  if (c >= q_count) return;
+  float big = -INFINITY;
+  for (int s = 0; s < count; ++s) big = fmaxf(big, partial_block<D>(p, first + s, h)[kQueries * D + 2 * c]);
+  float total = 0.f;
+  float acc[kPer];
+#pragma unroll
+  for (int d = 0; d < kPer; ++d) acc[d] = 0.f;
+  for (int s = 0; s < count; ++s) {
+    const float *block = partial_block<D>(p, first + s, h);
+    const float ms = block[kQueries * D + 2 * c];
+    const float w = ms == -INFINITY ? 0.f : exp2f(ms - big);
+    total += block[kQueries * D + 2 * c + 1] * w;
+#pragma unroll
+    for (int d = 0; d < kPer; ++d) acc[d] += w * block[c * D + part * kPer + d];
+  }
+  const float inv = total > 0.f ? 1.f / total : 0.f;
+  uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + h) * D + part * kPer;
+#pragma unroll
+  for (int d = 0; d < kPer; ++d) dst[d] = bf16_rne(acc[d] * inv);
+}
+
+bool aligned(const void *ptr, uintptr_t bytes) {
+  return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t ll_repair_attention_args_size(void) {
+  return static_cast<int64_t>(sizeof(ll_repair_attention_args));
+}
+
+int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_kv_heads,
+                             int64_t split_tokens, int32_t *items, int64_t items_capacity,
+                             int32_t *combine, int64_t combine_capacity,
+                             ll_repair_attention_plan_info *info) {
+  if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
+  if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
+  if (num_kv_heads < 1) return fail(LL_ERR_INVALID_ARGUMENT, "num_kv_heads must be >= 1");
+  if (split_tokens < 0 || split_tokens % kTile != 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d", kTile);
+  constexpr int64_t kIntMax = 0x7fffffff;
+  int64_t work = 0;  // sum over 16-query tiles of the KV tokens they read
+  for (int64_t r = 0; r < num_rows; ++r) {
+    const ll_repair_row &row = rows[r];
+    if (row.query_count < 1 || row.query_start < 0 || row.query_index < 0 || row.kv_offset < 0 ||
+        row.query_start + row.query_count > kIntMax || row.query_index + row.query_count > kIntMax ||
+        row.kv_offset + row.query_start + row.query_count > kIntMax)
+      return fail(LL_ERR_INVALID_ARGUMENT, "row %lld: counts, positions and offsets must be >= 0 "
+                  "(query_count >= 1) and fit in int32", static_cast<long long>(r));
+    for (int64_t t = 0; t < row.query_count; t += kQueries)
+      work += row.query_start + t + (row.query_count - t < kQueries ? row.query_count - t : kQueries);
+  }
+  int64_t split = split_tokens;
+  if (split == 0) {
+    // Aim at ~2048 workgroups (8 per CU): split = work * kv_heads / 2048, in [512, 8192].
+    split = (work * num_kv_heads / 2048 + kTile - 1) / kTile * kTile;
+    if (split < 512) split = 512;
+    if (split > 8192) split = 8192;
+  }
+  int64_t n_items = 0, n_combine = 0, n_partial = 0;
+  for (int64_t r = 0; r < num_rows; ++r) {
+    const ll_repair_row &row = rows[r];
+    for (int64_t t = 0; t < row.query_count; t += kQueries) {
+      const int64_t count = row.query_count - t < kQueries ? row.query_count - t : kQueries;
+      const int64_t pos = row.query_start + t;
+      const int64_t needed = pos + count;
+      const int64_t splits = (needed + split - 1) / split;
+      for (int64_t s = 0; s < splits; ++s) {
+        if (items != nullptr) {
+          if (n_items >= items_capacity)
+            return fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
+                        static_cast<long long>(items_capacity));
+          int32_t *it = items + n_items * kItemInts;
+          it[0] = static_cast<int32_t>(row.query_index + t);
+          it[1] = static_cast<int32_t>(pos);
+          it[2] = static_cast<int32_t>(count);
+          it[3] = static_cast<int32_t>(row.kv_offset);
+          it[4] = static_cast<int32_t>(s * split);
+          it[5] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
+          it[6] = splits == 1 ? -1 : static_cast<int32_t>(n_partial + s);
+          it[7] = 0;
+        }
+        ++n_items;
+      }
+      if (splits > 1) {
+        if (combine != nullptr) {
+          if (n_combine >= combine_capacity)
+            return fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
+                        static_cast<long long>(combine_capacity));
+          int32_t *ci = combine + n_combine * kCombineInts;
+          ci[0] = static_cast<int32_t>(row.query_index + t);
+          ci[1] = static_cast<int32_t>(count);
+          ci[2] = static_cast<int32_t>(n_partial);
+          ci[3] = static_cast<int32_t>(splits);
+        }
+        ++n_combine;
+        n_partial += splits;
+      }
+    }
+  }
+  if (n_items > kIntMax || n_partial > kIntMax)
+    return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
+  info->num_items = n_items;
+  info->num_combine = n_combine;
+  info->workspace_items = n_partial;
+  info->split_tokens = split;
+  return LL_OK;
+}
+
+int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_repair_attention_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_repair_attention_args));
+  if (a->kv_dtype != LL_DTYPE_BFLOAT16)
+    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes bf16 queries and KV");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64 or 128");
+  if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
+      a->num_q_heads / a->num_kv_heads > kMaxGroup || a->num_kv_heads > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
+                "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
+                kMaxGroup);
+  if (a->num_queries < 0 || a->num_slots < 0 || a->kv_slots_len < 0 || a->num_items < 0 ||
+      a->num_combine < 0 || a->workspace_items < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "counts must be >= 0");
+  if (!(a->softmax_scale > 0.0) || !isfinite(a->softmax_scale))
+    return fail(LL_ERR_INVALID_ARGUMENT, "softmax_scale must be finite and > 0");
+  if (a->num_items == 0) return LL_OK;
+  if (a->num_items > 0x7fffffff || a->num_combine > 0x7fffffff)
+    return fail(LL_ERR_INVALID_ARGUMENT, "too many items");
+  if (a->query == nullptr || a->output == nullptr || a->key_buffer == nullptr ||
+      a->value_buffer == nullptr || a->kv_slots == nullptr || a->items == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "query/output/key/value/kv_slots/items pointer is NULL");
+  if (a->kv_slots_dtype != LL_DTYPE_INT32 && a->kv_slots_dtype != LL_DTYPE_INT64)
+    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "kv_slots must be int32 or int64");
+  if (a->num_combine > 0 && (a->combine == nullptr || a->workspace == nullptr || a->workspace_items < 1))
+    return fail(LL_ERR_INVALID_ARGUMENT, "split items need the combine table and a workspace");
+  if (!aligned(a->query, 16) || !aligned(a->key_buffer, 16) || !aligned(a->value_buffer, 16) ||
+      !aligned(a->output, 8) || !aligned(a->workspace, 16))
+    return fail(LL_ERR_INVALID_ARGUMENT, "query/key/value (16-byte), output (8-byte) and workspace "
+                "(16-byte) must be aligned");
+
+  AttnParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t *>(a->query);
+  p.out = static_cast<uint16_t *>(a->output);
+  p.k = static_cast<const uint16_t *>(a->key_buffer);
+  p.v = static_cast<const uint16_t *>(a->value_buffer);
+  p.slots = a->kv_slots;
+  p.items = a->items;
+  p.combine = a->combine;
+  p.ws = a->workspace;
+  p.num_queries = a->num_queries;
+  p.num_slots = a->num_slots;
+  p.slots_len = a->kv_slots_len;
+  p.ws_items = a->workspace != nullptr ? a->workspace_items : 0;
+  p.hq = static_cast<int>(a->num_q_heads);
+  p.hkv = static_cast<int>(a->num_kv_heads);
+  p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
+  p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
+  p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads));
+  const dim3 block(static_cast<unsigned>(kWave * p.group));
+  if (a->head_dim == 128) repair_attention_kernel<128><<<grid, block, 0, s>>>(p);
+  else repair_attention_kernel<64><<<grid, block, 0, s>>>(p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  if (a->num_combine > 0) {
+    const dim3 cgrid(static_cast<unsigned>(a->num_combine), static_cast<unsigned>(a->num_q_heads));
+    if (a->head_dim == 128) repair_combine_kernel<128><<<cgrid, dim3(256), 0, s>>>(p);
+    else repair_combine_kernel<64><<<cgrid, dim3(256), 0, s>>>(p);
+    err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return LL_OK;
+}
+
+}  // extern "C"

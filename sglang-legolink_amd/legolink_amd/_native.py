@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -51,6 +51,9 @@ EXPORTED_SYMBOLS = (
     "ll_kv_scatter_args_size",
     "ll_kv_build_link_maps",
     "ll_link_maps_args_size",
+    "ll_repair_attention_plan",
+    "ll_repair_attention",
+    "ll_repair_attention_args_size",
 )
 
 _i64 = ctypes.c_int64
@@ -164,6 +167,61 @@ class LinkMapsArgs(ctypes.Structure):
     ]
 
 
+class RepairRow(ctypes.Structure):
+    """Mirror of ``ll_repair_row`` (four int64: an int64 ``[n, 4]`` array has the
+    same memory layout as ``n`` of these)."""
+
+    _fields_ = [
+        ("query_index", _i64),
+        ("query_start", _i64),
+        ("query_count", _i64),
+        ("kv_offset", _i64),
+    ]
+
+
+class RepairPlanInfo(ctypes.Structure):
+    """Mirror of ``ll_repair_attention_plan_info``."""
+
+    _fields_ = [
+        ("num_items", _i64),
+        ("num_combine", _i64),
+        ("workspace_items", _i64),
+        ("split_tokens", _i64),
+    ]
+
+
+class RepairAttentionArgs(ctypes.Structure):
+    """Mirror of ``ll_repair_attention_args``."""
+
+    _fields_ = [
+        ("struct_size", _i64),
+        ("query", _ptr),
+        ("output", _ptr),
+        ("num_queries", _i64),
+        ("key_buffer", _ptr),
+        ("value_buffer", _ptr),
+        ("num_slots", _i64),
+        ("num_q_heads", _i64),
+        ("num_kv_heads", _i64),
+        ("head_dim", _i64),
+        ("kv_dtype", _i64),
+        ("softmax_scale", ctypes.c_double),
+        ("kv_slots", _ptr),
+        ("kv_slots_dtype", _i64),
+        ("kv_slots_len", _i64),
+        ("items", _ptr),
+        ("num_items", _i64),
+        ("combine", _ptr),
+        ("num_combine", _i64),
+        ("workspace", _ptr),
+        ("workspace_items", _i64),
+    ]
+
+
+REPAIR_ITEM_INTS = 8
+REPAIR_COMBINE_INTS = 4
+
+
 class LaunchInfo(ctypes.Structure):
     """Mirror of ``ll_launch_info``."""
 
@@ -236,13 +294,21 @@ def load_library() -> ctypes.CDLL:
         lib.ll_kv_build_link_maps.restype = ctypes.c_int
         lib.ll_link_maps_args_size.argtypes = []
         lib.ll_link_maps_args_size.restype = _i64
+        lib.ll_repair_attention_plan.argtypes = [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64,
+                                                 ctypes.POINTER(RepairPlanInfo)]
+        lib.ll_repair_attention_plan.restype = ctypes.c_int
+        lib.ll_repair_attention.argtypes = [ctypes.POINTER(RepairAttentionArgs), _ptr]
+        lib.ll_repair_attention.restype = ctypes.c_int
+        lib.ll_repair_attention_args_size.argtypes = []
+        lib.ll_repair_attention_args_size.restype = _i64
         if lib.ll_abi_version() != ABI_VERSION:
             raise NativeLibraryUnavailable(
                 f"{LIB_PATH} has ABI {lib.ll_abi_version()}, expected {ABI_VERSION}; rebuild it"
             )
         if (lib.ll_kv_link_args_size() != ctypes.sizeof(LinkArgs)
                 or lib.ll_kv_scatter_args_size() != ctypes.sizeof(ScatterArgs)
-                or lib.ll_link_maps_args_size() != ctypes.sizeof(LinkMapsArgs)):
+                or lib.ll_link_maps_args_size() != ctypes.sizeof(LinkMapsArgs)
+                or lib.ll_repair_attention_args_size() != ctypes.sizeof(RepairAttentionArgs)):
             raise NativeLibraryUnavailable(f"{LIB_PATH} struct layout differs; rebuild it")
         _lib = lib
         return lib
@@ -297,3 +363,28 @@ def kv_scatter_rows(args: ScatterArgs, stream: int) -> None:
 def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
     args.struct_size = ctypes.sizeof(LinkMapsArgs)
     _check(load_library().ll_kv_build_link_maps(ctypes.byref(args), _ptr(int(stream))))
+
+
+def repair_attention_plan(rows, num_kv_heads: int, split_tokens: int = 0):
+    """Host planning: returns (items int32 [n, 8], combine int32 [m, 4], info)."""
+
+    import numpy as np
+
+    rows = np.ascontiguousarray(np.asarray(rows, dtype=np.int64).reshape(-1, 4))
+    lib = load_library()
+    info = RepairPlanInfo()
+    rows_ptr = rows.ctypes.data if rows.size else None
+    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_kv_heads), int(split_tokens),
+                                        None, 0, None, 0, ctypes.byref(info)))
+    items = np.zeros((info.num_items, REPAIR_ITEM_INTS), dtype=np.int32)
+    combine = np.zeros((info.num_combine, REPAIR_COMBINE_INTS), dtype=np.int32)
+    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_kv_heads), int(split_tokens),
+                                        items.ctypes.data if items.size else None, info.num_items,
+                                        combine.ctypes.data if combine.size else None, info.num_combine,
+                                        ctypes.byref(info)))
+    return items, combine, info
+
+
+def repair_attention(args: RepairAttentionArgs, stream: int) -> None:
+    args.struct_size = ctypes.sizeof(RepairAttentionArgs)
+    _check(load_library().ll_repair_attention(ctypes.byref(args), _ptr(int(stream))))

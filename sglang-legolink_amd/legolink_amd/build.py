@@ -18,6 +18,8 @@ from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 SOURCE = PACKAGE_DIR.parent / "csrc" / "legolink_kv.hip"
+# Translation units of liblegolink_kv.so: the link kernels and the repair attention.
+SOURCES = (SOURCE, PACKAGE_DIR.parent / "csrc" / "repair_attention.hip")
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
 # Memory-ceiling probes used by bench.py --ceiling (not part of the link ABI).
@@ -33,7 +35,8 @@ def hipcc_path() -> str:
     return candidate
 
 
-def compile_command(output: Path, source: Path = SOURCE) -> list[str]:
+def compile_command(output: Path, sources=SOURCES) -> list[str]:
+    sources = [sources] if isinstance(sources, Path) else list(sources)
     return [
         hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
@@ -50,25 +53,25 @@ def compile_command(output: Path, source: Path = SOURCE) -> list[str]:
         f"-I{INCLUDE_DIR}",
         "-o",
         str(output),
-        str(source),
+        *[str(source) for source in sources],
     ]
 
 
 def build_library(verbose: bool = False) -> Path:
     """Compile the link library and the probe library; outputs are replaced atomically."""
 
-    _compile(SOURCE, OUTPUT, verbose)
-    _compile(PROBE_SOURCE, PROBE_OUTPUT, verbose)
+    _compile(SOURCES, OUTPUT, verbose)
+    _compile((PROBE_SOURCE,), PROBE_OUTPUT, verbose)
     return OUTPUT
 
 
-def _compile(source: Path, output: Path, verbose: bool) -> None:
+def _compile(sources, output: Path, verbose: bool) -> None:
     output.parent.mkdir(parents=True, exist_ok=True)
     with tempfile.NamedTemporaryFile(
         dir=output.parent, prefix=f".{output.stem}.", suffix=".so.tmp", delete=False
     ) as handle:
         temporary = Path(handle.name)
-    command = compile_command(temporary, source)
+    command = compile_command(temporary, sources)
     try:
         result = subprocess.run(command, capture_output=True, text=True)
         # hipcc's host pass does not know the packed-fp32 target feature; that

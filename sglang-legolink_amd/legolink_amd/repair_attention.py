@@ -1,0 +1,186 @@
+"""Sparse repair attention: the repair pass's attention over the linked KV.
+
+After a link, the repair pass recomputes the ``imp_indices`` rows. Each
+contiguous repair span [repair_start, repair_end) of a request attends over the
+request's tokens at logical positions 0 .. repair_end - 1, which live in
+physical pool slots, under the explicit logical causal rule: query position p
+sees exactly the positions j <= p.  The reference runs this as a FlashInfer
+block-sparse attention over physical slot ids with that rule carried in a
+mask (patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py:
+``build_explicit_causal_masked_pattern`` :1241-1263, the plan/run of
+``_try_flashinfer_sparse_attention_single`` :2009-2272, the row batching of
+``build_grouped_explicit_causal_masked_pattern`` :1266-1318), and restates its
+semantics as ``gqa_attention`` over ``logical_causal_mask``
+(tests/pic/reference/attention_reference.py:8-48).
+
+Here it is one hand-written gfx950 kernel (MFMA bf16, online softmax in fp32)
+behind ``ll_repair_attention``, with the same two phases as the reference's
+wrapper: a host plan built once per request batch (shared by every layer:
+the slots and spans do not depend on the layer) and a run per layer.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+
+
+class SparseRepairAttentionError(RuntimeError):
+    """A repair attention request that must not run (flashinfer_sparse_repair.py:65-66)."""
+
+
+def _check_span(slot_ids: torch.Tensor, repair_start: int, repair_end: int) -> None:
+    # The checks and messages of build_explicit_causal_pattern (:1217-1238).
+    if slot_ids.ndim != 1:
+        raise SparseRepairAttentionError("slot_ids must be rank 1")
+    if repair_start < 0 or repair_end <= repair_start:
+        raise SparseRepairAttentionError("invalid repair range")
+    if slot_ids.numel() < repair_end:
+        raise SparseRepairAttentionError("slot_ids is shorter than repair_end")
+
+
+class RepairAttentionPlan:
+    """The work of one repair batch: ``spans`` is a list of
+    ``(slot_ids, repair_start, repair_end)`` in query order -- the queries of
+    span i are the next ``repair_end - repair_start`` rows of the query tensor.
+    ``slot_ids[j]`` is the pool slot of logical position j of that span's
+    request; spans of one request share its slot tensor.
+
+    With ``validate`` (the reference always checks, :1235-1236) every slot of
+    every span is checked against ``pool_size`` once, here (one device sync);
+    without it, slots outside the pool are treated as invisible keys.
+    """
+
+    def __init__(self, spans: Sequence[tuple[torch.Tensor, int, int]], *, num_q_heads: int,
+                 num_kv_heads: int, head_dim: int, pool_size: Optional[int] = None,
+                 split_tokens: int = 0, validate: bool = True) -> None:
+        if not spans:
+            raise SparseRepairAttentionError("no repair spans")
+        self.num_q_heads = int(num_q_heads)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = int(head_dim)
+        device = spans[0][0].device
+        tables: list[torch.Tensor] = []
+        offset_of: dict[int, int] = {}
+        rows = np.empty((len(spans), 4), dtype=np.int64)
+        cursor = 0
+        table_len = 0
+        dtype = None
+        for index, (slot_ids, start, end) in enumerate(spans):
+            start, end = int(start), int(end)
+            _check_span(slot_ids, start, end)
+            if slot_ids.device != device:
+                raise SparseRepairAttentionError("repair spans must share one device")
+            if slot_ids.dtype not in (torch.int32, torch.int64):
+                raise SparseRepairAttentionError("slot_ids must be int32 or int64")
+            key = id(slot_ids)
+            if key not in offset_of:
+                offset_of[key] = table_len
+                tables.append(slot_ids.contiguous())
+                table_len += int(slot_ids.numel())
+                dtype = slot_ids.dtype if dtype in (None, slot_ids.dtype) else torch.int64
+            rows[index] = (cursor, start, end - start, offset_of[key])
+            cursor += end - start
+        self.num_queries = cursor
+        self.spans = [(int(s), int(e)) for _, s, e in spans]
+        table = tables[0] if len(tables) == 1 else torch.cat([t.to(dtype) for t in tables])
+        if validate and pool_size is not None:
+            needed = torch.cat([slot_ids[:end] for slot_ids, _, end in spans])
+            if bool(((needed < 0) | (needed >= int(pool_size))).any()):
+                raise SparseRepairAttentionError("slot_ids contains invalid KV slots")
+        self.kv_slots = table
+        self.rows = rows
+        items, combine, info = _native.repair_attention_plan(rows, self.num_kv_heads, split_tokens)
+        self.info = {"num_items": int(info.num_items), "num_combine": int(info.num_combine),
+                     "workspace_items": int(info.workspace_items), "split_tokens": int(info.split_tokens)}
+        packed = np.concatenate((items.reshape(-1), combine.reshape(-1))).astype(np.int32)
+        self._tables = torch.from_numpy(packed).to(device)
+        self.items = self._tables[: items.size]
+        self.combine = self._tables[items.size :]
+        per_item = self.num_q_heads * (16 * self.head_dim + 32)
+        self.workspace = (torch.empty(info.workspace_items * per_item, dtype=torch.float32, device=device)
+                          if info.workspace_items else None)
+
+    @property
+    def algorithmic_flops(self) -> int:
+        """4 * head_dim flops per (query, visible key) pair and query head."""
+
+        pairs = sum((end - start) * (start + end + 1) // 2 for start, end in self.spans)
+        return 4 * self.head_dim * self.num_q_heads * pairs
+
+    @property
+    def kv_bytes_read(self) -> int:
+        """Bytes of K and V the kernel gathers: each 16-query item reads its KV
+        range once per KV head (bf16)."""
+
+        items = self.items.view(-1, _native.REPAIR_ITEM_INTS).cpu().numpy()
+        tokens = int(np.minimum(items[:, 5], items[:, 1] + items[:, 2]).astype(np.int64).sum()
+                     - items[:, 4].astype(np.int64).sum())
+        return tokens * self.num_kv_heads * self.head_dim * 2 * 2
+
+    def run(self, query: torch.Tensor, key_buffer: torch.Tensor, value_buffer: torch.Tensor, *,
+            scale: Optional[float] = None, output: Optional[torch.Tensor] = None,
+            stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """One layer: ``query`` [num_queries, num_q_heads, head_dim] bf16 (or its
+        [num_queries, num_q_heads * head_dim] view), ``key_buffer`` /
+        ``value_buffer`` the layer's [slots, num_kv_heads, head_dim] pool buffers.
+        Returns (or fills) the [num_queries, num_q_heads, head_dim] output."""
+
+        shape = (self.num_queries, self.num_q_heads, self.head_dim)
+        query = query.view(shape)
+        for name, tensor in (("query", query), ("key_buffer", key_buffer), ("value_buffer", value_buffer)):
+            if not tensor.is_cuda:
+                raise SparseRepairAttentionError(f"{name} must be a device tensor")
+            if tensor.dtype != torch.bfloat16:
+                raise SparseRepairAttentionError(f"{name} must be bf16")
+            if not tensor.is_contiguous():
+                raise SparseRepairAttentionError(f"{name} must be contiguous")
+        if key_buffer.ndim != 3 or key_buffer.shape[1:] != (self.num_kv_heads, self.head_dim) or (
+                value_buffer.shape != key_buffer.shape):
+            raise SparseRepairAttentionError("KV buffers must be [slots, num_kv_heads, head_dim]")
+        if output is None:
+            output = torch.empty(shape, dtype=torch.bfloat16, device=query.device)
+        elif output.shape != shape or output.dtype != torch.bfloat16 or not output.is_contiguous():
+            raise SparseRepairAttentionError("output must be a contiguous bf16 tensor of the query's shape")
+        args = _native.RepairAttentionArgs()
+        args.query = query.data_ptr()
+        args.output = output.data_ptr()
+        args.num_queries = self.num_queries
+        args.key_buffer = key_buffer.data_ptr()
+        args.value_buffer = value_buffer.data_ptr()
+        args.num_slots = int(key_buffer.shape[0])
+        args.num_q_heads = self.num_q_heads
+        args.num_kv_heads = self.num_kv_heads
+        args.head_dim = self.head_dim
+        args.kv_dtype = _native.DTYPE_BFLOAT16
+        args.softmax_scale = float(scale) if scale is not None else 1.0 / math.sqrt(self.head_dim)
+        args.kv_slots = self.kv_slots.data_ptr()
+        args.kv_slots_dtype = _native.DTYPE_INT64 if self.kv_slots.dtype == torch.int64 else _native.DTYPE_INT32
+        args.kv_slots_len = int(self.kv_slots.numel())
+        args.items = self.items.data_ptr()
+        args.num_items = self.info["num_items"]
+        args.combine = self.combine.data_ptr() if self.info["num_combine"] else None
+        args.num_combine = self.info["num_combine"]
+        args.workspace = self.workspace.data_ptr() if self.workspace is not None else None
+        args.workspace_items = self.info["workspace_items"]
+        if stream is None:
+            stream = torch.cuda.current_stream(query.device)
+        _native.repair_attention(args, stream.cuda_stream)
+        return output
+
+
+def sparse_repair_attention(query: torch.Tensor, key_buffer: torch.Tensor, value_buffer: torch.Tensor,
+                            slot_ids: torch.Tensor, *, repair_start: int, repair_end: int,
+                            scale: Optional[float] = None) -> torch.Tensor:
+    """One repair span of one layer (the reference's single-row path):
+    ``query`` [repair_end - repair_start, num_q_heads, head_dim]."""
+
+    plan = RepairAttentionPlan([(slot_ids, repair_start, repair_end)], num_q_heads=int(query.shape[1]),
+                               num_kv_heads=int(key_buffer.shape[1]), head_dim=int(key_buffer.shape[2]),
+                               pool_size=int(key_buffer.shape[0]))
+    return plan.run(query, key_buffer, value_buffer, scale=scale)

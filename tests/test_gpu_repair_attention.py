@@ -1,0 +1,182 @@
+"""GPU parity of the sparse repair attention kernel against the fp64 oracle of
+the reference's gqa_attention over logical_causal_mask, and against a plain
+torch fp32 restatement.
+
+Tolerance, elementwise: |got - ref| <= 2^-7 * (sum_j w_j |v_j| + |ref|) + 1e-5,
+where w are the softmax weights.  The kernel rounds each probability to bf16
+for the value product (relative error <= 2^-8, so the output moves by at most
+2^-8 * sum_j w_j |v_j|) and the output to bf16 (<= 2^-8 * |ref|); the bound
+takes twice that.  The reference's own FlashInfer check is atol = rtol = 3e-2
+(tests/pic/test_sparse_attention_reference.py:103).  Short KVs, a sharp
+softmax (scale 1) and zero queries make an off-by-one mask or a dropped key
+(an output change of w_j |v_j - ref|, >= 2.5e-2 there) visible above it.
+"""
+
+from __future__ import annotations
+
+import math
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from legolink_amd.repair_attention import RepairAttentionPlan, SparseRepairAttentionError, sparse_repair_attention
+from oracle import attention_oracle as ao
+from tests.gpu_helpers import report
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(shape, generator, device, scale=1.0):
+    return (torch.randn(shape, generator=generator, device=device) * scale).to(torch.bfloat16)
+
+
+def _torch_fp32(query, key_rows, value_rows, visible, scale):
+    """Plain fp32 torch attention on the CPU (GQA by head // group)."""
+
+    q = query.float().cpu()
+    k = key_rows.float().cpu()
+    v = value_rows.float().cpu()
+    group = q.shape[1] // k.shape[1]
+    k = k.repeat_interleave(group, dim=1)
+    v = v.repeat_interleave(group, dim=1)
+    scores = torch.einsum("qhd,khd->hqk", q, k) * scale
+    scores = scores.masked_fill(~torch.from_numpy(visible)[None], float("-inf"))
+    return torch.einsum("hqk,khd->qhd", torch.softmax(scores, dim=-1), v).numpy()
+
+
+def _check(plan_spans, query, key_pool, value_pool, got, scale):
+    q_np = query.float().cpu().numpy()
+    k_np = key_pool.float().cpu().numpy()
+    v_np = value_pool.float().cpu().numpy()
+    got_np = got.float().cpu().numpy()
+    cursor = 0
+    worst = 0.0
+    for slots, start, end in plan_spans:
+        n = end - start
+        slots_np = slots.cpu().numpy()
+        q_part = q_np[cursor : cursor + n]
+        want = ao.repair_attention(q_part, k_np, v_np, slots_np, start, end, scale=scale)
+        magnitude = ao.repair_attention(q_part, k_np, np.abs(v_np), slots_np, start, end, scale=scale)
+        bound = 2.0 ** -7 * (magnitude + np.abs(want)) + 1e-5
+        valid = (slots_np[:end] >= 0) & (slots_np[:end] < k_np.shape[0])
+        safe = torch.from_numpy(np.where(valid, slots_np[:end], 0))
+        visible = ao.logical_causal_mask(np.arange(start, end), np.arange(end)) & valid[None]
+        fp32 = _torch_fp32(query[cursor : cursor + n], key_pool.cpu()[safe], value_pool.cpu()[safe], visible, scale)
+        part = got_np[cursor : cursor + n]
+        err = np.abs(part - want)
+        worst = max(worst, float((err / bound).max()))
+        bad = err > bound
+        assert not bad.any(), f"span [{start}, {end}): {int(bad.sum())} elements off, max err {err.max():.3g}"
+        assert (np.abs(part - fp32) <= bound + 2.0 ** -8 * np.abs(fp32)).all()
+        cursor += n
+    report(f"largest error / bound vs fp64: {worst:.3f}")
+
+
+CASES = [
+    # name, q heads, kv heads, head dim, spans (start, end), pool slots, split tokens, scale
+    ("qwen7b_one_span", 28, 4, 128, [(100, 116)], 4096, 0, None),
+    ("partial_tiles", 28, 4, 128, [(0, 1), (5, 22), (40, 73)], 4096, 0, None),
+    ("long_kv_forced_splits", 28, 4, 128, [(9000, 9020)], 16384, 512, None),
+    ("seams_auto_split", 28, 4, 128, [(s, s + 16) for s in range(1024, 16384, 1024)], 32768, 0, None),
+    ("group8_head_dim64", 16, 2, 64, [(30, 50), (200, 201)], 2048, 0, None),
+    ("group1", 8, 8, 128, [(10, 26)], 2048, 0, None),
+    ("sharp_softmax", 28, 4, 128, [(3, 40), (300, 333)], 4096, 128, 1.0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_repair_attention_matches_oracle(gpu_device, case):
+    name, hq, hkv, dim, spans, pool, split, scale = case
+    report(f"case {name}: hq={hq} hkv={hkv} d={dim} spans={spans[:3]}... pool={pool} split={split}")
+    generator = torch.Generator(device=gpu_device).manual_seed(zlib.crc32(name.encode()) % 1000)
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    length = max(end for _, end in spans)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:length]
+    plan_spans = [(slots, start, end) for start, end in spans]
+    plan = RepairAttentionPlan(plan_spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim,
+                               pool_size=pool, split_tokens=split)
+    report(f"plan {plan.info}")
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device)
+    use_scale = scale if scale is not None else 1.0 / math.sqrt(dim)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    _check(plan_spans, query, key_pool, value_pool, got, use_scale)
+
+
+def test_two_requests_in_one_plan_with_int32_slots(gpu_device):
+    generator = torch.Generator(device=gpu_device).manual_seed(2)
+    hq, hkv, dim, pool = 28, 4, 128, 8192
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    order = torch.randperm(pool, generator=generator, device=gpu_device)
+    first = order[:700]
+    second = order[700:1100].to(torch.int32)
+    spans = [(first, 500, 516), (second, 20, 45), (first, 680, 700), (second, 399, 400)]
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, pool_size=pool)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device)
+    got = plan.run(query, key_pool, value_pool)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
+
+
+def test_invalid_slots_are_invisible_keys(gpu_device):
+    generator = torch.Generator(device=gpu_device).manual_seed(3)
+    hq, hkv, dim, pool = 28, 4, 128, 1024
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:200].clone()
+    slots[[3, 77, 150]] = torch.tensor([-1, pool, pool + 50], device=gpu_device)
+    spans = [(slots, 140, 180)]
+    with pytest.raises(SparseRepairAttentionError, match="invalid KV slots"):
+        RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, pool_size=pool)
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, validate=False)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device)
+    got = plan.run(query, key_pool, value_pool)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
+
+
+def test_zero_queries_average_the_visible_values(gpu_device):
+    """q = 0 gives equal weights: output row i is the mean of the values at
+    positions 0..start + i -- exact up to the final bf16 rounding."""
+
+    generator = torch.Generator(device=gpu_device).manual_seed(4)
+    hq, hkv, dim, pool = 28, 4, 128, 2048
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:300]
+    start, end = 250, 290
+    query = torch.zeros((end - start, hq, dim), dtype=torch.bfloat16, device=gpu_device)
+    got = sparse_repair_attention(query, key_pool, value_pool, slots, repair_start=start, repair_end=end)
+    torch.cuda.synchronize(gpu_device)
+    values = value_pool.float().cpu().numpy()[slots.cpu().numpy()]
+    for i in range(end - start):
+        mean = values[: start + i + 1].mean(axis=0)                      # [hkv, dim]
+        want = np.repeat(mean, hq // hkv, axis=0)
+        assert np.allclose(got[i].float().cpu().numpy(), want, rtol=2 ** -8, atol=1e-6), i
+
+
+def test_one_plan_serves_every_layer(gpu_device):
+    generator = torch.Generator(device=gpu_device).manual_seed(6)
+    hq, hkv, dim, pool = 28, 4, 128, 4096
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:2500]
+    spans = [(slots, 1000, 1016), (slots, 2000, 2016), (slots, 2400, 2450)]
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, pool_size=pool)
+    for layer in range(3):
+        key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+        value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
+        query = _bf16((plan.num_queries, hq, dim), generator, gpu_device)
+        got = plan.run(query, key_pool, value_pool)
+        torch.cuda.synchronize(gpu_device)
+        _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
+
+
+def test_span_checks_follow_the_reference(gpu_device):
+    slots = torch.arange(10, device=gpu_device)
+    for bad, message in [((slots.view(2, 5), 1, 3), "rank 1"), ((slots, 3, 3), "invalid repair range"),
+                         ((slots, 5, 12), "shorter than repair_end")]:
+        with pytest.raises(SparseRepairAttentionError, match=message):
+            RepairAttentionPlan([bad], num_q_heads=4, num_kv_heads=2, head_dim=64)

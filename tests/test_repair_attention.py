@@ -1,0 +1,195 @@
+"""Sparse repair attention without a GPU: the oracle pinned to the reference's
+cases and closed forms, the host planner's coverage, and the C entry's
+argument validation."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from legolink_amd import _native
+from oracle import attention_oracle as ao
+
+
+def _visible_slots(slots, start, end):
+    mask = ao.logical_causal_mask(np.arange(start, end), np.arange(end))
+    slots = np.asarray(slots)[:end]
+    return [slots[row].tolist() for row in mask]
+
+
+def test_gqa_head_mapping_is_query_head_divided_by_group_size():
+    # tests/pic/test_sparse_attention_reference.py:46-52
+    query = np.zeros((1, 4, 2))
+    key = np.zeros((1, 2, 2))
+    value = np.array([[[10.0, 11.0], [20.0, 21.0]]])
+    out = ao.gqa_attention(query, key, value, np.ones((1, 1), dtype=bool))
+    assert out[0, :, 0].tolist() == [10.0, 10.0, 20.0, 20.0]
+
+
+def test_physical_slots_never_define_logical_causal_order():
+    # tests/pic/test_sparse_attention_mask.py:21-33 with the scrambled-slot fixture
+    # (tests/pic/reference/fixtures.py:6-9).
+    assert _visible_slots([100, 5, 80, 12], 2, 4) == [[100, 5, 80], [100, 5, 80, 12]]
+
+
+def test_visibility_keeps_order_and_multiplicity():
+    # tests/pic/test_sparse_attention_mask.py:36-43
+    assert _visible_slots([9, 3, 9, 17, 2], 3, 5) == [[9, 3, 9, 17], [9, 3, 9, 17, 2]]
+
+
+def test_physical_slot_gather_reconstructs_logical_attention():
+    # tests/pic/test_sparse_attention_reference.py:12-43
+    rng = np.random.default_rng(20260824)
+    query = rng.standard_normal((2, 4, 8))
+    logical_key = rng.standard_normal((4, 2, 8))
+    logical_value = rng.standard_normal((4, 2, 8))
+    slots = np.array([11, 2, 19, 7])
+    key_pool = np.zeros((24, 2, 8))
+    value_pool = np.zeros((24, 2, 8))
+    key_pool[slots] = logical_key
+    value_pool[slots] = logical_value
+    expected = ao.gqa_attention(query, logical_key, logical_value,
+                                ao.logical_causal_mask(np.array([2, 3]), np.arange(4)))
+    actual = ao.repair_attention(query, key_pool, value_pool, slots, 2, 4)
+    assert np.allclose(actual, expected, rtol=0, atol=1e-15)
+
+
+def _loop_attention(query, key, value, visible, scale):
+    """Independent pair-by-pair restatement with math.exp (tiny cases only)."""
+
+    q_tokens, q_heads, dim = query.shape
+    group = q_heads // key.shape[1]
+    out = np.zeros((q_tokens, q_heads, value.shape[2]))
+    for i in range(q_tokens):
+        for h in range(q_heads):
+            kv = h // group
+            scores = [sum(query[i, h, d] * key[j, kv, d] for d in range(dim)) * scale
+                      for j in range(key.shape[0])]
+            top = max(s for s, v in zip(scores, visible[i]) if v)
+            weights = [math.exp(s - top) if v else 0.0 for s, v in zip(scores, visible[i])]
+            total = sum(weights)
+            for d in range(value.shape[2]):
+                out[i, h, d] = sum(w * value[j, kv, d] for j, w in enumerate(weights)) / total
+    return out
+
+
+def test_oracle_matches_pairwise_loops_and_closed_forms():
+    rng = np.random.default_rng(5)
+    query = rng.standard_normal((3, 6, 4))
+    key = rng.standard_normal((5, 2, 4))
+    value = rng.standard_normal((5, 2, 4))
+    visible = ao.logical_causal_mask(np.array([2, 3, 4]), np.arange(5))
+    scale = 0.37
+    assert np.allclose(ao.gqa_attention(query, key, value, visible, scale=scale),
+                       _loop_attention(query, key, value, visible, scale), rtol=0, atol=1e-12)
+    # One visible key: the output is that key's value row.
+    only = np.zeros((3, 5), dtype=bool)
+    only[:, 1] = True
+    out = ao.gqa_attention(query, key, value, only)
+    assert np.allclose(out[:, :3], value[1, 0][None, None, :]) and np.allclose(out[:, 3:], value[1, 1])
+    # Zero queries: the mean of the visible values.
+    out = ao.gqa_attention(np.zeros_like(query), key, value, visible)
+    for i, p in enumerate([2, 3, 4]):
+        assert np.allclose(out[i, 0], value[: p + 1, 0].mean(axis=0))
+    # Invalid slots are invisible keys.
+    pool_k, pool_v = rng.standard_normal((8, 2, 4)), rng.standard_normal((8, 2, 4))
+    with_bad = ao.repair_attention(query[:2], pool_k, pool_v, [3, 9, 1, 0], 2, 4)
+    visible = ao.logical_causal_mask(np.array([2, 3]), np.arange(4))
+    visible[:, 1] = False
+    safe = np.array([3, 0, 1, 0])
+    assert np.allclose(with_bad, ao.gqa_attention(query[:2], pool_k[safe], pool_v[safe], visible))
+
+
+def test_a_planted_head_mapping_mistake_fails_the_reference_case():
+    query = np.zeros((1, 4, 2))
+    key = np.zeros((1, 2, 2))
+    value = np.array([[[10.0, 11.0], [20.0, 21.0]]])
+    # h % num_kv_heads instead of h // group interleaves the heads.
+    wrong = [value[0, h % 2, 0] for h in range(4)]
+    assert wrong != ao.gqa_attention(query, key, value, np.ones((1, 1), dtype=bool))[0, :, 0].tolist()
+
+
+def _plan(rows, kv_heads=4, split=0):
+    return _native.repair_attention_plan(np.asarray(rows, dtype=np.int64), kv_heads, split)
+
+
+@pytest.mark.parametrize("split", [0, 64, 512])
+def test_plan_covers_every_query_tile_and_key_range_once(split):
+    rng = np.random.default_rng(split + 1)
+    rows, cursor = [], 0
+    for _ in range(20):
+        count = int(rng.integers(1, 70))
+        start = int(rng.integers(0, 3000))
+        rows.append((cursor, start, count, int(rng.integers(0, 500))))
+        cursor += count
+    items, combine, info = _plan(rows, split=split)
+    assert info.split_tokens % 64 == 0 and (split == 0 or info.split_tokens == split)
+    covered = {}
+    for q_index, q_pos, q_count, kv_off, kv_begin, kv_end, partial, _ in items.tolist():
+        assert 1 <= q_count <= 16 and kv_begin < kv_end <= q_pos + q_count
+        assert kv_begin % 64 == 0
+        covered.setdefault((q_index, q_pos, q_count, kv_off), []).append((kv_begin, kv_end, partial))
+    tiles = set()
+    for q_index, start, count, kv_off in rows:
+        for t in range(0, count, 16):
+            tiles.add((q_index + t, start + t, min(16, count - t), kv_off))
+    assert set(covered) == tiles
+    partials = set()
+    for tile, ranges in covered.items():
+        ranges.sort()
+        assert ranges[0][0] == 0 and ranges[-1][1] == tile[1] + tile[2]
+        assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+        if len(ranges) == 1:
+            assert ranges[0][2] == -1
+        else:
+            ids = [r[2] for r in ranges]
+            assert ids == list(range(ids[0], ids[0] + len(ids)))
+            partials.update(ids)
+            assert [tile[0], tile[2], ids[0], len(ids)] in combine.tolist()
+    assert len(partials) == info.workspace_items == combine[:, 3].sum()
+
+
+def test_plan_rejects_bad_rows():
+    with pytest.raises(_native.NativeCallError, match="row 0"):
+        _plan([(0, 5, 0, 0)])
+    with pytest.raises(_native.NativeCallError, match="row 1"):
+        _plan([(0, 5, 3, 0), (3, -1, 3, 0)])
+    with pytest.raises(_native.NativeCallError, match="multiple of 64"):
+        _plan([(0, 5, 3, 0)], split=100)
+
+
+def test_attention_entry_validates_before_any_launch():
+    lib = _native.load_library()
+    assert lib.ll_repair_attention_args_size() == ctypes.sizeof(_native.RepairAttentionArgs)
+    assert lib.ll_repair_attention(None, None) == _native.LL_ERR_INVALID_ARGUMENT
+
+    def args(**overrides):
+        a = _native.RepairAttentionArgs()
+        a.query, a.output, a.key_buffer, a.value_buffer = 0x1000, 0x2000, 0x3000, 0x4000
+        a.num_queries, a.num_slots, a.num_q_heads, a.num_kv_heads, a.head_dim = 16, 64, 28, 4, 128
+        a.kv_dtype = _native.DTYPE_BFLOAT16
+        a.softmax_scale = 0.088
+        a.kv_slots, a.kv_slots_dtype, a.kv_slots_len = 0x5000, _native.DTYPE_INT64, 64
+        a.items, a.num_items = 0x6000, 1
+        for name, value in overrides.items():
+            setattr(a, name, value)
+        return a
+
+    for overrides, reason in [
+        (dict(head_dim=96), "head_dimension_out_of_range"),
+        (dict(num_q_heads=36), "kv_head_layout_mismatch"),   # 9 query heads per KV head
+        (dict(num_q_heads=30), "kv_head_layout_mismatch"),
+        (dict(kv_dtype=_native.DTYPE_FLOAT16), "fp16_or_bf16_required"),
+        (dict(kv_slots_dtype=_native.DTYPE_FLOAT32), "integer_token_maps_required"),
+        (dict(query=None), "invalid_argument"),
+        (dict(softmax_scale=float("nan")), "invalid_argument"),
+        (dict(num_combine=1), "invalid_argument"),             # split items without a workspace
+        (dict(query=0x1008), "invalid_argument"),              # misaligned
+    ]:
+        with pytest.raises(_native.NativeCallError) as error:
+            _native.repair_attention(args(**overrides), 0)
+        assert error.value.reason == reason, overrides
+    _native.repair_attention(args(num_items=0), 0)  # nothing to do, no GPU touched
