@@ -57,6 +57,11 @@ def parse_args() -> argparse.Namespace:
                         help="time a plain device copy of this many MiB instead of the link")
     parser.add_argument("--ceiling", action="store_true",
                         help="measure memory ceilings next to the link instead of the step")
+    parser.add_argument("--repair-attention", action="store_true",
+                        help="time the sparse repair attention of the workload's repair spans "
+                             "(one layer) instead of the link")
+    parser.add_argument("--split-tokens", type=int, default=0,
+                        help="repair attention: KV tokens per work item (0: the planner's choice)")
     return parser.parse_args()
 
 
@@ -260,6 +265,81 @@ def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
         return None
 
 
+def repair_attention_bench(args: argparse.Namespace) -> None:
+    """The repair pass's attention for the workload's repair spans, one layer
+    of the Qwen2.5-7B shape (28 query heads over 4 KV heads, head dim 128):
+    each contiguous run of imp_indices attends over its request's tokens
+    0..end-1 through the request's slots.  Prints one JSON line."""
+
+    import math
+
+    import numpy as np
+    import torch
+
+    from legolink_amd.link_plan import contiguous_ranges
+    from legolink_amd.repair_attention import RepairAttentionPlan
+    from legolink_amd.workloads import make_workload
+
+    device = torch.device("cuda", 0)
+    workload = make_workload(args.workload)
+    shape = workload.shape
+    q_heads = 28 if shape.kv_heads == 4 else 64  # Qwen2.5-7B: 28 / 4; Qwen3-32B: 64 / 8
+    generator = torch.Generator(device=device).manual_seed(20260824)
+    key = torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, generator=generator,
+                      device=device).to(torch.bfloat16)
+    value = torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, generator=generator,
+                        device=device).to(torch.bfloat16)
+    spans = []
+    for destination, plan in workload.link_requests()[1]:
+        slots = torch.from_numpy(destination).to(device)
+        for start, end in contiguous_ranges(plan["imp_indices"]):
+            spans.append((slots, int(start), int(end)))
+    plan_start = time.perf_counter()
+    plan = RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads,
+                               head_dim=shape.head_dim, pool_size=workload.num_slots,
+                               split_tokens=args.split_tokens)
+    torch.cuda.synchronize(device)
+    plan_ms = (time.perf_counter() - plan_start) * 1e3
+    query = torch.randn(plan.num_queries, q_heads, shape.head_dim, generator=generator,
+                        device=device).to(torch.bfloat16)
+    output = torch.empty_like(query)
+    for _ in range(args.warmup):
+        plan.run(query, key, value, output=output)
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.current_stream(device)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    for start_event, end_event in events:
+        start_event.record(stream)
+        plan.run(query, key, value, output=output)
+        end_event.record(stream)
+    torch.cuda.synchronize(device)
+    ms = float(np.mean([s.elapsed_time(e) for s, e in events]))
+    flops = plan.algorithmic_flops
+    achieved = flops / (ms / 1e3) / 1e12
+    kv_bytes = plan.kv_bytes_read
+    log(f"repair attention {workload.name}: {len(spans)} spans, {plan.num_queries} queries, "
+        f"plan {plan.info}, {ms:.4f} ms per layer")
+    print(json.dumps({
+        "metric": "sparse repair attention TFLOP/s (bf16 MFMA, one layer)",
+        "value": round(achieved, 2),
+        "unit": "TFLOP/s",
+        "ms_per_layer": round(ms, 5),
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 queries and KV pool",
+        "config": {"workload": f"{workload.name}: repair spans of {workload.description}",
+                   "spans": len(spans), "queries": plan.num_queries, "q_heads": q_heads,
+                   "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
+                   "algorithmic_flops": flops, "plan": plan.info, "host_plan_ms": round(plan_ms, 3)},
+        "roofline": {"bound": "mfma", "kernel": "repair_attention_kernel", "achieved": round(achieved, 2),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(achieved / 2500.0, 4),
+                     "kv_bytes_gathered": kv_bytes,
+                     "kv_gather_GBps": round(kv_bytes / (ms / 1e3) / 1e9, 1)},
+    }), flush=True)
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -272,6 +352,9 @@ def main() -> int:
         return 0
     if args.ceiling:
         ceiling(args)
+        return 0
+    if args.repair_attention:
+        repair_attention_bench(args)
         return 0
 
     import numpy as np

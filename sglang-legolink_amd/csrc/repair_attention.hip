@@ -44,6 +44,8 @@ typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 
 constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
@@ -87,6 +89,11 @@ __device__ inline uint16_t bf16_rne(float x) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two floats to two bf16 with one v_cvt_pk_bf16_f32 (round to nearest even).
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
 __device__ inline long long slot_at(const AttnParams &p, long long i) {
   return p.slots64 ? static_cast<const long long *>(p.slots)[i]
                    : static_cast<long long>(static_cast<const int *>(p.slots)[i]);
@@ -108,6 +115,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTile * kKRow];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * kVRow];
   __shared__ unsigned char token_ok[kTile];
+  __shared__ int tile_invalid;  // tokens of the current tile that are out of range or invalid
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int q_index = it[0], q_pos = it[1], q_count = it[2], kv_off = it[3];
@@ -149,8 +157,11 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
   for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const long long row_stride = static_cast<long long>(p.hkv) * D;  // elements per slot
+  const float scale_log2 = p.scale_log2;
   for (int t0 = kv_begin; t0 < kv_stop; t0 += kTile) {
     __syncthreads();  // the previous tile's LDS reads are done
+    if (tid == 0) tile_invalid = 0;
+    __syncthreads();
     // K: token-major (16 lanes cover one 256-byte row: coalesced), V: token-minor
     // (consecutive lanes write consecutive tokens of a transposed row).
     for (int ci = tid; ci < kTile * kParts; ci += blockDim.x) {
@@ -180,7 +191,10 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
           v_lds[(part * 8 + 2 * e) * kVRow + tok] = static_cast<uint16_t>(vc[e] & 0xffffu);
           v_lds[(part * 8 + 2 * e + 1) * kVRow + tok] = static_cast<uint16_t>(vc[e] >> 16);
         }
-        if (part == 0) token_ok[tok] = ok ? 1 : 0;
+        if (part == 0) {
+          token_ok[tok] = ok ? 1 : 0;
+          if (!ok) atomicAdd(&tile_invalid, 1);
+        }
       }
     }
     __syncthreads();
@@ -196,49 +210,83 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
       }
     }
+    // Raw scores are kept unscaled: the max commutes with the positive scale,
+    // which is folded into the exponent (one FMA and one v_exp_f32 per score).
+    // A tile that every query sees whole, with every slot valid, needs no mask.
+    const bool whole = tile_invalid == 0 && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
     float tile_max = -INFINITY;
+    if (whole) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * n + 4 * g + r;
-        const int j = t0 + tok;
-        const bool visible = q_ok && j < kv_stop && j <= my_pos && token_ok[tok];
-        const float val = visible ? s[n][r] * p.scale_log2 : -INFINITY;
-        s[n][r] = val;
-        tile_max = fmaxf(tile_max, val);
+        for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[n][r]);
+      if (!q_ok) tile_max = -INFINITY;
+    } else {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * n + 4 * g + r;
+          const int j = t0 + tok;
+          const bool visible = q_ok && j < kv_stop && j <= my_pos && token_ok[tok];
+          s[n][r] = visible ? s[n][r] : -INFINITY;
+          tile_max = fmaxf(tile_max, s[n][r]);
+        }
       }
     }
     tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
     tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
     const float m_new = fmaxf(m, tile_max);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m - m_use);
+    const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
+    const float bias = -m_use * scale_log2;
     float row_sum = 0.f;
-    i16x4 pb[4];
+    float pv[4][4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = exp2f(s[n][r] - m_use);
-        row_sum += pv;
-        pb[n][r] = static_cast<short>(bf16_rne(pv));
+        pv[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
+        row_sum += pv[n][r];
       }
     }
+    if (!q_ok) row_sum = 0.f;
     row_sum += __shfl_xor(row_sum, 16);
     row_sum += __shfl_xor(row_sum, 32);
     l = l * alpha + row_sum;
     m = m_new;
+    // P^T as the B operand of 16x16x32 MFMAs over 32 tokens: k-step h takes the
+    // accumulators of token tiles 2h and 2h + 1, so lane group g holds tokens
+    // 32 h + 4 g + {0..3} and 32 h + 16 + 4 g + {0..3}; the A operand (V^T)
+    // reads the same tokens for its dim row.
+    bf16x8 pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 bits;
+      bits[0] = pack_bf16x2(pv[2 * h][0], pv[2 * h][1]);
+      bits[1] = pack_bf16x2(pv[2 * h][2], pv[2 * h][3]);
+      bits[2] = pack_bf16x2(pv[2 * h + 1][0], pv[2 * h + 1][1]);
+      bits[3] = pack_bf16x2(pv[2 * h + 1][2], pv[2 * h + 1][3]);
+      pb[h] = __builtin_bit_cast(bf16x8, bits);
+    }
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
       o[dt] *= alpha;
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const i16x4 a = *reinterpret_cast<const i16x4 *>(&v_lds[(16 * dt + c) * kVRow + 16 * n + 4 * g]);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[n], o[dt], 0, 0, 0);
+      for (int h = 0; h < 2; ++h) {
+        const uint16_t *row = &v_lds[(16 * dt + c) * kVRow + 32 * h + 4 * g];
+        u32x4 bits;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(row);
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(row + 16);
+        bits[0] = lo[0];
+        bits[1] = lo[1];
+        bits[2] = hi[0];
+        bits[3] = hi[1];
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bits), pb[h], o[dt], 0, 0, 0);
       }
     }
   }
+
   // o[dt][r] = O^T[dim 16 dt + 4 g + r][query c].
   if (partial < 0) {
     if (!q_ok) return;
@@ -256,8 +304,8 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt)
       *reinterpret_cast<f32x4 *>(block + c * D + 16 * dt + 4 * g) = o[dt];
-    if (g == 0) {
-      block[kQueries * D + 2 * c] = m;
+    if (g == 0) {  // the running max in the combine's units: log2-scaled scores
+      block[kQueries * D + 2 * c] = m * scale_log2;
       block[kQueries * D + 2 * c + 1] = l;
     }
   }
