@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 5
+#define LL_ABI_VERSION 6
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -284,11 +284,13 @@ typedef struct ll_link_maps_args {
  * Slots outside [0, num_slots) are invisible (never read).
  *
  * Two phases, like the reference's plan/run wrapper:
- *   ll_repair_attention_plan (host only) cuts the rows into work items of at
- *   most 16 queries, splitting long KV ranges for parallelism, and writes the
- *   item and combine tables; the caller copies them to the device once and
- *   reuses them for every layer.  Call it with NULL tables to size them.
- *   ll_repair_attention runs one layer.
+ *   ll_repair_attention_plan (host only) cuts the rows into 16-query tiles,
+ *   groups consecutive tiles of one request (same kv_offset) into work items
+ *   that share every staged K/V tile (as many tiles as 16 waves hold: 2 for 7
+ *   or 8 query heads per KV head), splits long KV ranges for parallelism, and
+ *   writes the item and combine tables; the caller copies them to the device
+ *   once and reuses them for every layer.  Call it with NULL tables to size
+ *   them.  ll_repair_attention runs one layer.
  *
  * Replaces the FlashInfer block-sparse repair attention of
  * patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py
@@ -306,7 +308,7 @@ typedef struct ll_repair_row {
 } ll_repair_row;
 
 typedef struct ll_repair_attention_plan_info {
-  int64_t num_items;               /* int32 [num_items, 8] work items */
+  int64_t num_items;               /* int32 [num_items, 24] work items */
   int64_t num_combine;             /* int32 [num_combine, 4] combine items */
   int64_t workspace_items;         /* partial results (see ll_repair_attention_args.workspace) */
   int64_t split_tokens;            /* KV tokens per work item (the plan's choice when 0 was asked) */
@@ -336,9 +338,9 @@ typedef struct ll_repair_attention_args {
   int64_t workspace_items;
 } ll_repair_attention_args;
 
-int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_kv_heads,
-                             int64_t split_tokens, int32_t *items, int64_t items_capacity,
-                             int32_t *combine, int64_t combine_capacity,
+int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
+                             int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
+                             int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
                              ll_repair_attention_plan_info *info);
 int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream);
 

@@ -50,9 +50,11 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
 constexpr int kTile = 64;     // KV tokens per LDS tile
-constexpr int kItemInts = 8;
+constexpr int kMaxTiles = 4;    // 16-query tiles per work item
+constexpr int kItemInts = 24;   // kv_offset, kv_begin, kv_end, tiles, 4 x (q_index, q_pos, q_count, partial), pad
 constexpr int kCombineInts = 4;
-constexpr int kMaxGroup = 8;  // query heads per KV head = waves per workgroup
+constexpr int kMaxGroup = 8;  // query heads per KV head
+constexpr int kMaxWaves = 16;  // waves per workgroup: (query tile, query head) pairs = waves per workgroup
 
 int fail(int code, const char *fmt, ...) {
   va_list ap;
@@ -94,6 +96,12 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
+// Query tiles per work item for a GQA group: as many as 16 waves hold.
+__host__ __device__ inline int tiles_per_item(int group) {
+  const int tiles = kMaxWaves / group;
+  return tiles < 1 ? 1 : (tiles > kMaxTiles ? kMaxTiles : tiles);
+}
+
 __device__ inline long long slot_at(const AttnParams &p, long long i) {
   return p.slots64 ? static_cast<const long long *>(p.slots)[i]
                    : static_cast<long long>(static_cast<const int *>(p.slots)[i]);
@@ -106,7 +114,7 @@ __device__ inline float *partial_block(const AttnParams &p, int partial, int h) 
 }
 
 template <int D>
-__global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(const AttnParams p) {
   constexpr int kSteps = D / 32;     // k-steps of S^T = K Q^T
   constexpr int kDimTiles = D / 16;  // 16-row tiles of O^T
   constexpr int kKRow = D + 8;       // LDS row stride of K (elements), spreads banks
@@ -118,14 +126,11 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
   __shared__ int tile_invalid;  // tokens of the current tile that are out of range or invalid
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
-  const int q_index = it[0], q_pos = it[1], q_count = it[2], kv_off = it[3];
-  const int kv_begin = it[4], kv_end = it[5], partial = it[6];
+  const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
   const int hk = blockIdx.y;
   // Items come from the planner; a malformed one is skipped whole (uniform).
-  if (q_count < 1 || q_count > kQueries || q_index < 0 ||
-      static_cast<long long>(q_index) + q_count > p.num_queries || q_pos < 0 || kv_off < 0 ||
-      kv_begin < 0 || kv_begin > kv_end || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
-      partial >= p.ws_items || (partial < 0 && partial != -1) || hk >= p.hkv)
+  if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
+      static_cast<long long>(kv_off) + kv_end > p.slots_len || hk >= p.hkv)
     return;
 
   const int tid = threadIdx.x;
@@ -133,10 +138,24 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
   const int lane = tid % kWave;
   const int g = lane / 16;   // lane group: k (or row) block of the MFMA operands
   const int c = lane % 16;   // query of this lane in the S^T / O^T accumulators
-  const int hq = hk * p.group + wave;
-  const bool q_ok = c < q_count;
+  // Wave w computes query head hk * G + w % G for the item's query tile w / G.
+  const int tile = wave / p.group;
+  const int hq = hk * p.group + wave % p.group;
+  const int *entry = it + 4 + 4 * (tile < kMaxTiles ? tile : 0);
+  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3];
+  const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
+                        static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
+                        (partial == -1 || (partial >= 0 && partial < p.ws_items));
+  const bool q_ok = computes && c < q_count;
   const int my_pos = q_pos + c;
-  const int kv_stop = min(kv_end, q_pos + q_count);  // last query sees [0, q_pos + q_count)
+  // The wave's keys end where its last query's do; the workgroup loads up to the
+  // furthest of its tiles.
+  const int kv_stop = computes ? min(kv_end, q_pos + q_count) : kv_begin;
+  int load_stop = kv_begin;
+  for (int t = 0; t < n_tiles; ++t) {
+    const int *e = it + 4 + 4 * t;
+    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[1] + e[2]));
+  }
 
   // The wave's queries as the B operand of S^T = K Q^T: query c, dims 32 ks + 8 g + e.
   bf16x8 qf[kSteps];
@@ -158,7 +177,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
 
   const long long row_stride = static_cast<long long>(p.hkv) * D;  // elements per slot
   const float scale_log2 = p.scale_log2;
-  for (int t0 = kv_begin; t0 < kv_stop; t0 += kTile) {
+  for (int t0 = kv_begin; t0 < load_stop; t0 += kTile) {
     __syncthreads();  // the previous tile's LDS reads are done
     if (tid == 0) tile_invalid = 0;
     __syncthreads();
@@ -169,7 +188,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
         const int tok = ci / kParts, part = ci % kParts;
         const int j = t0 + tok;
         u32x4 kc = {0u, 0u, 0u, 0u};
-        if (j < kv_stop) {
+        if (j < load_stop) {
           const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
           if (slot >= 0 && slot < p.num_slots)
             kc = *reinterpret_cast<const u32x4 *>(p.k + slot * row_stride + hk * D + part * 8);
@@ -181,7 +200,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
         const int j = t0 + tok;
         u32x4 vc = {0u, 0u, 0u, 0u};
         bool ok = false;
-        if (j < kv_stop) {
+        if (j < load_stop) {
           const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
           ok = slot >= 0 && slot < p.num_slots;
           if (ok) vc = *reinterpret_cast<const u32x4 *>(p.v + slot * row_stride + hk * D + part * 8);
@@ -198,6 +217,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
       }
     }
     __syncthreads();
+    if (!computes || t0 >= kv_stop) continue;  // this wave's tile has no keys here
 
     // S^T tile: lane holds tokens 16 n + 4 g + r for query c.
     f32x4 s[4];
@@ -287,6 +307,7 @@ __global__ void __launch_bounds__(kWave * kMaxGroup) repair_attention_kernel(con
     }
   }
 
+  if (!computes) return;
   // o[dt][r] = O^T[dim 16 dt + 4 g + r][query c].
   if (partial < 0) {
     if (!q_ok) return;
@@ -358,18 +379,27 @@ int64_t ll_repair_attention_args_size(void) {
   return static_cast<int64_t>(sizeof(ll_repair_attention_args));
 }
 
-int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_kv_heads,
-                             int64_t split_tokens, int32_t *items, int64_t items_capacity,
-                             int32_t *combine, int64_t combine_capacity,
+int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
+                             int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
+                             int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
                              ll_repair_attention_plan_info *info) {
   if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
   if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
     return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
-  if (num_kv_heads < 1) return fail(LL_ERR_INVALID_ARGUMENT, "num_kv_heads must be >= 1");
+  if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0 ||
+      num_q_heads / num_kv_heads > kMaxGroup)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
+                "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
+                kMaxGroup);
   if (split_tokens < 0 || split_tokens % kTile != 0)
     return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d", kTile);
   constexpr int64_t kIntMax = 0x7fffffff;
-  int64_t work = 0;  // sum over 16-query tiles of the KV tokens they read
+  const int per_item = tiles_per_item(static_cast<int>(num_q_heads / num_kv_heads));
+  // 16-query tiles in row order; consecutive tiles of one request (same kv_offset)
+  // share work items, up to per_item at a time.
+  struct Tile { int64_t q_index, pos, count, kv_offset, needed; };
+  int64_t work = 0;
+  int64_t n_tiles = 0;
   for (int64_t r = 0; r < num_rows; ++r) {
     const ll_repair_row &row = rows[r];
     if (row.query_count < 1 || row.query_start < 0 || row.query_index < 0 || row.kv_offset < 0 ||
@@ -377,57 +407,94 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
         row.kv_offset + row.query_start + row.query_count > kIntMax)
       return fail(LL_ERR_INVALID_ARGUMENT, "row %lld: counts, positions and offsets must be >= 0 "
                   "(query_count >= 1) and fit in int32", static_cast<long long>(r));
-    for (int64_t t = 0; t < row.query_count; t += kQueries)
-      work += row.query_start + t + (row.query_count - t < kQueries ? row.query_count - t : kQueries);
+    n_tiles += (row.query_count + kQueries - 1) / kQueries;
   }
-  int64_t split = split_tokens;
-  if (split == 0) {
-    // Aim at ~2048 workgroups (8 per CU): split = work * kv_heads / 2048, in [512, 8192].
-    split = (work * num_kv_heads / 2048 + kTile - 1) / kTile * kTile;
-    if (split < 512) split = 512;
-    if (split > 8192) split = 8192;
-  }
-  int64_t n_items = 0, n_combine = 0, n_partial = 0;
+  Tile *tiles = n_tiles ? new Tile[n_tiles] : nullptr;
+  int64_t k = 0;
   for (int64_t r = 0; r < num_rows; ++r) {
     const ll_repair_row &row = rows[r];
     for (int64_t t = 0; t < row.query_count; t += kQueries) {
       const int64_t count = row.query_count - t < kQueries ? row.query_count - t : kQueries;
-      const int64_t pos = row.query_start + t;
-      const int64_t needed = pos + count;
-      const int64_t splits = (needed + split - 1) / split;
-      for (int64_t s = 0; s < splits; ++s) {
-        if (items != nullptr) {
-          if (n_items >= items_capacity)
-            return fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
-                        static_cast<long long>(items_capacity));
-          int32_t *it = items + n_items * kItemInts;
-          it[0] = static_cast<int32_t>(row.query_index + t);
-          it[1] = static_cast<int32_t>(pos);
-          it[2] = static_cast<int32_t>(count);
-          it[3] = static_cast<int32_t>(row.kv_offset);
-          it[4] = static_cast<int32_t>(s * split);
-          it[5] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
-          it[6] = splits == 1 ? -1 : static_cast<int32_t>(n_partial + s);
-          it[7] = 0;
-        }
-        ++n_items;
-      }
-      if (splits > 1) {
-        if (combine != nullptr) {
-          if (n_combine >= combine_capacity)
-            return fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
-                        static_cast<long long>(combine_capacity));
-          int32_t *ci = combine + n_combine * kCombineInts;
-          ci[0] = static_cast<int32_t>(row.query_index + t);
-          ci[1] = static_cast<int32_t>(count);
-          ci[2] = static_cast<int32_t>(n_partial);
-          ci[3] = static_cast<int32_t>(splits);
-        }
-        ++n_combine;
-        n_partial += splits;
-      }
+      tiles[k++] = Tile{row.query_index + t, row.query_start + t, count, row.kv_offset,
+                        row.query_start + t + count};
     }
   }
+  // Groups of up to per_item consecutive tiles of one request.
+  auto group_end = [&](int64_t first) {
+    int64_t last = first + 1;
+    while (last < n_tiles && last - first < per_item && tiles[last].kv_offset == tiles[first].kv_offset) ++last;
+    return last;
+  };
+  for (int64_t first = 0; first < n_tiles; first = group_end(first)) {
+    int64_t needed = 0;
+    for (int64_t t = first; t < group_end(first); ++t) needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+    work += needed;
+  }
+  int64_t split = split_tokens;
+  if (split == 0) {
+    // Aim at ~1024 workgroups (16 waves each, 4 per CU): split = work * kv_heads / 1024, in [512, 8192].
+    split = (work * num_kv_heads / 1024 + kTile - 1) / kTile * kTile;
+    if (split < 512) split = 512;
+    if (split > 8192) split = 8192;
+  }
+  int64_t n_items = 0, n_combine = 0, n_partial = 0;
+  int rc = LL_OK;
+  for (int64_t first = 0; first < n_tiles && rc == LL_OK; first = group_end(first)) {
+    const int64_t last = group_end(first);
+    int64_t needed = 0;
+    int64_t base[kMaxTiles];
+    int64_t chunks[kMaxTiles];
+    for (int64_t t = first; t < last; ++t) {
+      needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+      chunks[t - first] = (tiles[t].needed + split - 1) / split;
+      base[t - first] = -1;
+      if (chunks[t - first] > 1) {
+        if (combine != nullptr) {
+          if (n_combine >= combine_capacity) {
+            rc = fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
+                      static_cast<long long>(combine_capacity));
+            break;
+          }
+          int32_t *ci = combine + n_combine * kCombineInts;
+          ci[0] = static_cast<int32_t>(tiles[t].q_index);
+          ci[1] = static_cast<int32_t>(tiles[t].count);
+          ci[2] = static_cast<int32_t>(n_partial);
+          ci[3] = static_cast<int32_t>(chunks[t - first]);
+        }
+        base[t - first] = n_partial;
+        n_partial += chunks[t - first];
+        ++n_combine;
+      }
+    }
+    if (rc != LL_OK) break;
+    const int64_t group_chunks = (needed + split - 1) / split;
+    for (int64_t s = 0; s < group_chunks; ++s) {
+      if (items != nullptr) {
+        if (n_items >= items_capacity) {
+          rc = fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
+                    static_cast<long long>(items_capacity));
+          break;
+        }
+        int32_t *it = items + n_items * kItemInts;
+        for (int i = 0; i < kItemInts; ++i) it[i] = 0;
+        it[0] = static_cast<int32_t>(tiles[first].kv_offset);
+        it[1] = static_cast<int32_t>(s * split);
+        it[2] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
+        it[3] = static_cast<int32_t>(last - first);
+        for (int64_t t = first; t < last; ++t) {
+          int32_t *e = it + 4 + 4 * (t - first);
+          e[0] = static_cast<int32_t>(tiles[t].q_index);
+          e[1] = static_cast<int32_t>(tiles[t].pos);
+          const bool present = s < chunks[t - first];  // this chunk holds keys the tile sees
+          e[2] = present ? static_cast<int32_t>(tiles[t].count) : 0;
+          e[3] = !present || chunks[t - first] == 1 ? -1 : static_cast<int32_t>(base[t - first] + s);
+        }
+      }
+      ++n_items;
+    }
+  }
+  delete[] tiles;
+  if (rc != LL_OK) return rc;
   if (n_items > kIntMax || n_partial > kIntMax)
     return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
   info->num_items = n_items;
@@ -493,7 +560,7 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads));
-  const dim3 block(static_cast<unsigned>(kWave * p.group));
+  const dim3 block(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group)));
   if (a->head_dim == 128) repair_attention_kernel<128><<<grid, block, 0, s>>>(p);
   else repair_attention_kernel<64><<<grid, block, 0, s>>>(p);
   hipError_t err = hipGetLastError();

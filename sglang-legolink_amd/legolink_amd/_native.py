@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -218,7 +218,7 @@ class RepairAttentionArgs(ctypes.Structure):
     ]
 
 
-REPAIR_ITEM_INTS = 8
+REPAIR_ITEM_INTS = 24
 REPAIR_COMBINE_INTS = 4
 
 
@@ -294,7 +294,7 @@ def load_library() -> ctypes.CDLL:
         lib.ll_kv_build_link_maps.restype = ctypes.c_int
         lib.ll_link_maps_args_size.argtypes = []
         lib.ll_link_maps_args_size.restype = _i64
-        lib.ll_repair_attention_plan.argtypes = [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64,
+        lib.ll_repair_attention_plan.argtypes = [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64,
                                                  ctypes.POINTER(RepairPlanInfo)]
         lib.ll_repair_attention_plan.restype = ctypes.c_int
         lib.ll_repair_attention.argtypes = [ctypes.POINTER(RepairAttentionArgs), _ptr]
@@ -365,8 +365,8 @@ def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
     _check(load_library().ll_kv_build_link_maps(ctypes.byref(args), _ptr(int(stream))))
 
 
-def repair_attention_plan(rows, num_kv_heads: int, split_tokens: int = 0):
-    """Host planning: returns (items int32 [n, 8], combine int32 [m, 4], info)."""
+def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_tokens: int = 0):
+    """Host planning: returns (items int32 [n, 24], combine int32 [m, 4], info)."""
 
     import numpy as np
 
@@ -374,12 +374,13 @@ def repair_attention_plan(rows, num_kv_heads: int, split_tokens: int = 0):
     lib = load_library()
     info = RepairPlanInfo()
     rows_ptr = rows.ctypes.data if rows.size else None
-    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_kv_heads), int(split_tokens),
-                                        None, 0, None, 0, ctypes.byref(info)))
+    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
+                                        int(split_tokens), None, 0, None, 0, ctypes.byref(info)))
     items = np.zeros((info.num_items, REPAIR_ITEM_INTS), dtype=np.int32)
     combine = np.zeros((info.num_combine, REPAIR_COMBINE_INTS), dtype=np.int32)
-    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_kv_heads), int(split_tokens),
-                                        items.ctypes.data if items.size else None, info.num_items,
+    _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
+                                        int(split_tokens), items.ctypes.data if items.size else None,
+                                        info.num_items,
                                         combine.ctypes.data if combine.size else None, info.num_combine,
                                         ctypes.byref(info)))
     return items, combine, info

@@ -95,7 +95,8 @@ class RepairAttentionPlan:
                 raise SparseRepairAttentionError("slot_ids contains invalid KV slots")
         self.kv_slots = table
         self.rows = rows
-        items, combine, info = _native.repair_attention_plan(rows, self.num_kv_heads, split_tokens)
+        items, combine, info = _native.repair_attention_plan(rows, self.num_q_heads, self.num_kv_heads,
+                                                             split_tokens)
         self.info = {"num_items": int(info.num_items), "num_combine": int(info.num_combine),
                      "workspace_items": int(info.workspace_items), "split_tokens": int(info.split_tokens)}
         packed = np.concatenate((items.reshape(-1), combine.reshape(-1))).astype(np.int32)
@@ -115,12 +116,11 @@ class RepairAttentionPlan:
 
     @property
     def kv_bytes_read(self) -> int:
-        """Bytes of K and V the kernel gathers: each 16-query item reads its KV
-        range once per KV head (bf16)."""
+        """Bytes of K and V the kernel gathers: each work item reads its KV range
+        [kv_begin, kv_end) once per KV head (bf16)."""
 
-        items = self.items.view(-1, _native.REPAIR_ITEM_INTS).cpu().numpy()
-        tokens = int(np.minimum(items[:, 5], items[:, 1] + items[:, 2]).astype(np.int64).sum()
-                     - items[:, 4].astype(np.int64).sum())
+        items = self.items.view(-1, _native.REPAIR_ITEM_INTS).cpu().numpy().astype(np.int64)
+        tokens = int((items[:, 2] - items[:, 1]).sum())
         return tokens * self.num_kv_heads * self.head_dim * 2 * 2
 
     def run(self, query: torch.Tensor, key_buffer: torch.Tensor, value_buffer: torch.Tensor, *,

@@ -112,35 +112,48 @@ def test_a_planted_head_mapping_mistake_fails_the_reference_case():
     assert wrong != ao.gqa_attention(query, key, value, np.ones((1, 1), dtype=bool))[0, :, 0].tolist()
 
 
-def _plan(rows, kv_heads=4, split=0):
-    return _native.repair_attention_plan(np.asarray(rows, dtype=np.int64), kv_heads, split)
+def _plan(rows, q_heads=28, kv_heads=4, split=0):
+    return _native.repair_attention_plan(np.asarray(rows, dtype=np.int64), q_heads, kv_heads, split)
 
 
-@pytest.mark.parametrize("split", [0, 64, 512])
-def test_plan_covers_every_query_tile_and_key_range_once(split):
-    rng = np.random.default_rng(split + 1)
+@pytest.mark.parametrize("split,q_heads,kv_heads", [(0, 28, 4), (64, 28, 4), (512, 28, 4), (128, 8, 8),
+                                                     (256, 8, 2)])
+def test_plan_covers_every_query_tile_and_key_range_once(split, q_heads, kv_heads):
+    rng = np.random.default_rng(split + q_heads)
     rows, cursor = [], 0
     for _ in range(20):
         count = int(rng.integers(1, 70))
         start = int(rng.integers(0, 3000))
-        rows.append((cursor, start, count, int(rng.integers(0, 500))))
+        rows.append((cursor, start, count, int(rng.integers(0, 3)) * 5000))  # three requests
         cursor += count
-    items, combine, info = _plan(rows, split=split)
+    items, combine, info = _plan(rows, q_heads, kv_heads, split)
+    per_item = max(1, min(4, 16 // (q_heads // kv_heads)))
     assert info.split_tokens % 64 == 0 and (split == 0 or info.split_tokens == split)
     covered = {}
-    for q_index, q_pos, q_count, kv_off, kv_begin, kv_end, partial, _ in items.tolist():
-        assert 1 <= q_count <= 16 and kv_begin < kv_end <= q_pos + q_count
-        assert kv_begin % 64 == 0
-        covered.setdefault((q_index, q_pos, q_count, kv_off), []).append((kv_begin, kv_end, partial))
-    tiles = set()
+    for item in items.tolist():
+        kv_off, kv_begin, kv_end, n_tiles = item[:4]
+        assert 1 <= n_tiles <= per_item and kv_begin % 64 == 0 and kv_begin < kv_end
+        furthest = 0
+        for t in range(n_tiles):
+            q_index, q_pos, q_count, partial = item[4 + 4 * t : 8 + 4 * t]
+            key = (q_index, q_pos, kv_off)
+            if q_count == 0:
+                assert partial == -1
+                continue
+            assert 1 <= q_count <= 16
+            furthest = max(furthest, q_pos + q_count)
+            covered.setdefault(key, []).append((kv_begin, min(kv_end, q_pos + q_count), partial, q_count))
+        assert kv_end <= furthest  # an item never loads keys past its last present tile's
+    tiles = {}
     for q_index, start, count, kv_off in rows:
         for t in range(0, count, 16):
-            tiles.add((q_index + t, start + t, min(16, count - t), kv_off))
-    assert set(covered) == tiles
+            tiles[(q_index + t, start + t, kv_off)] = min(16, count - t)
+    assert set(covered) == set(tiles)
     partials = set()
-    for tile, ranges in covered.items():
+    combine_rows = [tuple(r) for r in combine.tolist()]
+    for key, ranges in covered.items():
         ranges.sort()
-        assert ranges[0][0] == 0 and ranges[-1][1] == tile[1] + tile[2]
+        assert ranges[0][0] == 0 and ranges[-1][1] == key[1] + tiles[key]
         assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
         if len(ranges) == 1:
             assert ranges[0][2] == -1
@@ -148,7 +161,7 @@ def test_plan_covers_every_query_tile_and_key_range_once(split):
             ids = [r[2] for r in ranges]
             assert ids == list(range(ids[0], ids[0] + len(ids)))
             partials.update(ids)
-            assert [tile[0], tile[2], ids[0], len(ids)] in combine.tolist()
+            assert (key[0], tiles[key], ids[0], len(ids)) in combine_rows
     assert len(partials) == info.workspace_items == combine[:, 3].sum()
 
 
@@ -159,6 +172,9 @@ def test_plan_rejects_bad_rows():
         _plan([(0, 5, 3, 0), (3, -1, 3, 0)])
     with pytest.raises(_native.NativeCallError, match="multiple of 64"):
         _plan([(0, 5, 3, 0)], split=100)
+    with pytest.raises(_native.NativeCallError) as error:
+        _plan([(0, 5, 3, 0)], q_heads=36, kv_heads=4)  # 9 query heads per KV head
+    assert error.value.reason == "kv_head_layout_mismatch"
 
 
 def test_attention_entry_validates_before_any_launch():
