@@ -294,12 +294,15 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
         slots = torch.from_numpy(destination).to(device)
         for start, end in contiguous_ranges(plan["imp_indices"]):
             spans.append((slots, int(start), int(end)))
-    plan_start = time.perf_counter()
-    plan = RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads,
-                               head_dim=shape.head_dim, pool_size=workload.num_slots,
-                               split_tokens=args.split_tokens)
-    torch.cuda.synchronize(device)
-    plan_ms = (time.perf_counter() - plan_start) * 1e3
+    plan_times = []
+    for _ in range(3):  # the first plan also pays torch's first-use costs; report the median
+        plan_start = time.perf_counter()
+        plan = RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads,
+                                   head_dim=shape.head_dim, pool_size=workload.num_slots,
+                                   split_tokens=args.split_tokens)
+        torch.cuda.synchronize(device)
+        plan_times.append((time.perf_counter() - plan_start) * 1e3)
+    plan_ms = float(np.median(plan_times))
     query = torch.randn(plan.num_queries, q_heads, shape.head_dim, generator=generator,
                         device=device).to(torch.bfloat16)
     output = torch.empty_like(query)
@@ -333,7 +336,8 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
                    "spans": len(spans), "queries": plan.num_queries, "q_heads": q_heads,
                    "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
                    "algorithmic_flops": flops, "plan": plan.info, "host_plan_ms": round(plan_ms, 3)},
-        "roofline": {"bound": "mfma", "kernel": "repair_attention_kernel", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": ("repair_attention_dma_kernel" if shape.head_dim == 128
+                                                        else "repair_attention_kernel<64>"), "achieved": round(achieved, 2),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(achieved / 2500.0, 4),
                      "kv_bytes_gathered": kv_bytes,
                      "kv_gather_GBps": round(kv_bytes / (ms / 1e3) / 1e9, 1)},

@@ -67,5 +67,9 @@ def repair_attention(query: np.ndarray, key_pool: np.ndarray, value_pool: np.nda
     valid = (slots >= 0) & (slots < key_pool.shape[0])
     safe = np.where(valid, slots, 0)
     visible = logical_causal_mask(np.arange(repair_start, repair_end), np.arange(repair_end)) & valid[None, :]
-    return gqa_attention(query, np.asarray(key_pool)[safe], np.asarray(value_pool)[safe], visible,
-                         scale=scale)
+    # An invalid slot contributes nothing, whatever the pool holds at the row it
+    # would alias: its K and V rows are zeros (an invisible key with a NaN value
+    # would otherwise leak through 0 * NaN).
+    keys = np.where(valid[:, None, None], np.asarray(key_pool)[safe], 0.0)
+    values = np.where(valid[:, None, None], np.asarray(value_pool)[safe], 0.0)
+    return gqa_attention(query, keys, values, visible, scale=scale)

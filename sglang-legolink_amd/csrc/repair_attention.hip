@@ -2,32 +2,36 @@
 // repair rows over the linked KV, read through each request's slot list.
 //
 // Work decomposition (planned on the host by ll_repair_attention_plan):
-//   item = up to 16 consecutive queries of one repair row and a KV range
-//   [kv_begin, kv_end) of logical positions; long ranges are split and the
-//   partial results merged by a combine pass.
-//   workgroup = (item, KV head); wave w = query head hk * G + w (G query heads
-//   share one KV head, G <= 8), so the K/V tiles staged in LDS serve G heads.
+//   item = up to four 16-query tiles of one request (consecutive repair
+//   rows) and a KV range [kv_begin, kv_end) of logical positions; long ranges
+//   are split and the partial results merged by a combine pass.
+//   workgroup = (item, KV head); wave w computes query tile w / G for query
+//   head hk * G + w % G (G query heads share one KV head, G <= 8), so each
+//   K/V tile staged in LDS serves every query tile and head of the item.
 //
 // Per 64-token KV tile:
-//   1. gather the tile's K rows (token-major, [token][dim]) and V rows
-//      (transposed, [dim][token]) of this KV head into LDS by slot;
+//   1. gather the tile's K and V rows of this KV head into LDS by slot;
 //   2. S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 K rows from LDS,
 //      B = the wave's 16 queries (kept in registers).  The accumulator layout
 //      gives each lane 4 consecutive tokens of one query;
 //   3. masking (causal by logical position, split range, invalid slots),
 //      online softmax in fp32 with exp2 (row statistics reduced across the
 //      four lanes of a query with xor shuffles 16 and 32);
-//   4. O^T += V^T P^T with v_mfma_f32_16x16x16_bf16: B = the probabilities
-//      straight from the S^T accumulators (4 consecutive tokens of one query
-//      per lane is exactly the B operand layout), A = 4 tokens of one dim row
-//      of the transposed V tile.
+//   4. O^T += V^T P^T with v_mfma_f32_16x16x32_bf16: B = the probabilities
+//      straight from the S^T accumulators of two 16-token groups (the token
+//      order inside the K step is free, as long as A uses the same one),
+//      A = 8 tokens of one dim row of V^T.
 // Lane layouts (checked on the device): 16x16x32 A/B lane l element e ->
-// row/column l % 16, k = 8 (l / 16) + e; 16x16x16 k = 4 (l / 16) + e;
-// accumulator register r -> row 4 (l / 16) + r, column l % 16.
+// row/column l % 16, k = 8 (l / 16) + e; accumulator register r -> row
+// 4 (l / 16) + r, column l % 16.
 //
-// Roofline: MFMA-bound.  Algorithmic work per (query, visible key) pair and
-// query head: 4 * head_dim flops (QK and PV); KV bytes are read once per
-// 16-query item and KV head.
+// Head dim 128 runs repair_attention_dma_kernel (LDS ring filled by
+// global_load_lds two tiles ahead); head dim 64 runs repair_attention_kernel,
+// which stages each tile through registers.
+//
+// Roofline: MFMA-bound in principle.  Algorithmic work per (query, visible
+// key) pair and query head: 4 * head_dim flops (QK and PV); KV bytes are read
+// once per item and KV head.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
@@ -332,6 +336,315 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
   }
 }
 
+// The same work on a pipelined schedule (head dim 128): K and V rows are
+// gathered straight into a three-stage LDS ring with global_load_lds, two
+// tiles ahead of the MFMAs, so no registers stage them and no wave waits on a
+// gather it could overlap.  Rows are stored token-major with their sixteen
+// 16-byte chunks XOR-swizzled by token (chunk c of token t at c ^ (t % 16)),
+// which keeps both the K fragment reads and the transposed V reads free of
+// bank conflicts.  V^T fragments come from ds_read_b64_tr_b16: within a group
+// of 16 lanes it returns to lane i, element e, element i % 4 of the 8 bytes
+// that lane 4 e + i / 4 addressed (checked on the device), so lanes addressing
+// 4 dims of 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.
+// The item's slots are read once into LDS (at most kDmaMaxRange of them).
+constexpr int kDmaThreads = 1024;    // 16 waves: two gather instructions each per tile
+constexpr int kDmaStages = 3;
+constexpr int kDmaMaxRange = 4096;   // KV tokens per work item on this path
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Two 16-byte-per-lane gathers into LDS (global_load_lds_dwordx4: lane l's
+// bytes land at the LDS base in M0 + 16 l).  They are issued from inline
+// assembly so that the compiler, which cannot tell the ring's stages apart,
+// does not add waits for every outstanding gather before each LDS access:
+// the loop below orders the stages itself with explicit vmcnt waits and
+// barriers.  M0 is saved and restored around them.
+__device__ inline void dma_pair(const void *src0, void *lds0, const void *src1, void *lds1) {
+  const unsigned base0 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds0)));
+  const unsigned base1 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds1)));
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %4\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src0), "v"(src1), "s"(base0), "s"(base1)
+      : "memory");
+}
+
+// s_barrier without __syncthreads()'s wait for all outstanding memory
+// operations (which would drain the gathers in flight); the empty asm keeps
+// the compiler from moving LDS accesses across it.
+__device__ inline void workgroup_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int kSteps = D / 32;
+  constexpr int kDimTiles = D / 16;
+  constexpr int kChunksPerRow = D / 8;                   // 16-byte chunks per row: 16
+  constexpr int kStageBytes = kTile * D * 2;             // one K or V tile: 16 KB
+  constexpr int kRangeTiles = kDmaMaxRange / kTile;  // 64-token KV tiles per item
+  __shared__ __attribute__((aligned(16))) unsigned char k_ring[kDmaStages * kStageBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char v_ring[kDmaStages * kStageBytes];
+  __shared__ int slot_lds[kDmaMaxRange];
+  __shared__ int tile_invalid[kRangeTiles];
+
+  const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
+  const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
+  const int hk = blockIdx.y;
+  if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
+      kv_end - kv_begin > kDmaMaxRange || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
+      hk >= p.hkv)
+    return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int g = lane / 16;
+  const int c = lane % 16;
+  const int tile = wave / p.group;
+  const int hq = hk * p.group + wave % p.group;
+  const int *entry = it + 4 + 4 * (tile < kMaxTiles ? tile : 0);
+  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3];
+  const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
+                        static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
+                        (partial == -1 || (partial >= 0 && partial < p.ws_items));
+  const bool q_ok = computes && c < q_count;
+  const int my_pos = q_pos + c;
+  const int kv_stop = computes ? min(kv_end, q_pos + q_count) : kv_begin;
+  int load_stop = kv_begin;
+  for (int t = 0; t < n_tiles; ++t) {
+    const int *e = it + 4 + 4 * t;
+    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[1] + e[2]));
+  }
+  const int range = load_stop - kv_begin;
+  const int tiles = (range + kTile - 1) / kTile;
+
+  // Slots of the item's range (-1: out of range or invalid), and per tile the
+  // number of such tokens.
+  for (int i = tid; i < kRangeTiles; i += kDmaThreads) tile_invalid[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < tiles * kTile; i += kDmaThreads) {
+    int slot = -1;
+    if (i < range) {
+      const long long s = slot_at(p, static_cast<long long>(kv_off) + kv_begin + i);
+      if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
+    }
+    slot_lds[i] = slot;
+    if (slot < 0) atomicAdd(&tile_invalid[i / kTile], 1);
+  }
+
+  bf16x8 qf[kSteps];
+  {
+    const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      u32x4 bits = {0u, 0u, 0u, 0u};
+      if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
+      qf[ks] = __builtin_bit_cast(bf16x8, bits);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): queries and slots are in
+  __syncthreads();
+
+  // Gather of tile t: 32 instructions of 64 lanes (16 for K, 16 for V), two per
+  // wave.  Instruction k covers ring chunks 64 k .. 64 k + 63 of its stage;
+  // chunk P holds token P / 16, row chunk (P % 16) ^ (token % 16).
+  const long long row_stride = static_cast<long long>(p.hkv) * D;
+  // Wave w issues instruction w of the K tile and instruction w of the V tile.
+  const int chunk_index = wave * kWave + lane;
+  const int gather_token = chunk_index / kChunksPerRow;
+  const int gather_chunk = (chunk_index % kChunksPerRow) ^ (gather_token % 16);
+  // Every wave issues exactly two loads per tile (the waits below count
+  // them): a token without a valid slot loads slot 0's row instead (gather
+  // leaves it out when the pool is empty), which the masking hides for K and
+  // the V clean-up below replaces by zeros.
+  const bool have_slots = p.num_slots > 0;  // else every token is invalid and nothing is loaded
+  auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
+    if (!have_slots) return;
+    const int slot = max(slot_lds[t * kTile + gather_token], 0);
+    const long long offset = slot * row_stride + hk * D + gather_chunk * 8;
+    dma_pair(p.k + offset, k_dst + wave * kWave * 16, p.v + offset, v_dst + wave * kWave * 16);
+  };
+
+  float m = -INFINITY;
+  float l = 0.f;
+  f32x4 o[kDimTiles];
+#pragma unroll
+  for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float scale_log2 = p.scale_log2;
+
+  // Lane offsets of the transposed V reads (see below): the tokens a lane
+  // group reads share the swizzle key x = 4 g + c / 4.
+  const int x = 4 * g + c / 4;
+  const int lane_base = x * (kChunksPerRow * 16) + (((c % 4) / 2) ^ (x & 1)) * 16 + (c % 2) * 8;
+  const int xh = x >> 1;
+
+  if (tiles > 0) gather(0, k_ring, v_ring);
+  if (tiles > 1) gather(1, k_ring + kStageBytes, v_ring + kStageBytes);
+  // Inside the loop the barriers are plain s_barrier: __syncthreads() would
+  // also wait for every outstanding gather and serialise the pipeline.  What
+  // the loop needs is ordering: a wave's LDS reads of a stage are consumed by
+  // its MFMAs before it reaches the next barrier, and each wave waits for its
+  // own gathers (vmcnt) before the barrier that releases a stage to compute.
+  for (int t = 0, stage = 0; t < tiles; ++t) {
+    const int next = stage == 0 ? kDmaStages - 1 : stage - 1;  // the stage of tile t + 2
+    const unsigned char *k_stage = k_ring + stage * kStageBytes;
+    unsigned char *v_stage = v_ring + stage * kStageBytes;
+    stage = stage == kDmaStages - 1 ? 0 : stage + 1;
+    workgroup_barrier();          // every wave is done with the stage tile t + 2 reuses
+    unsigned char *k_next = k_ring + next * kStageBytes;
+    unsigned char *v_next = v_ring + next * kStageBytes;
+    if (t + 2 < tiles) gather(t + 2, k_next, v_next);
+    // This wave's gathers of tile t are complete when at most those of the
+    // tiles after it (two instructions each) are outstanding.
+    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF74);
+    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF72);
+    else __builtin_amdgcn_s_waitcnt(0xF70);
+    workgroup_barrier();          // and so are every other wave's
+    if (tile_invalid[t] != 0) {
+      // Zero the V rows of tokens without a valid slot: their probability is
+      // 0, and 0 * V must not turn an Inf or NaN of slot 0's row into a NaN.
+      // Thread i owns bytes 16 i .. 16 i + 15 of the stage (token i / 16).
+      if (slot_lds[t * kTile + tid / kChunksPerRow] < 0)
+        *reinterpret_cast<u32x4 *>(v_stage + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      workgroup_barrier();
+    }
+    const int t0 = kv_begin + t * kTile;
+    if (!computes || t0 >= kv_stop) continue;
+    // Keep the per-lane LDS offsets below from being precomputed for every
+    // (dim tile, token half) and held across tiles: 16 addresses would not fit
+    // in the register budget of a 16-wave workgroup.
+    int k_lane = c * kChunksPerRow * 16;
+    int v_lane = lane_base;
+    asm volatile("" : "+v"(k_lane), "+v"(v_lane));
+
+    f32x4 s[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) {
+        // Token 16 n + c: its swizzle key is c, so row chunk 4 ks + g sits at (4 ks + g) ^ c.
+        const int chunk = (4 * ks + g) ^ c;
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(k_stage + k_lane + n * 16 * kChunksPerRow * 16 + chunk * 16);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
+      }
+    }
+    const bool all_valid = tile_invalid[t] == 0;
+    const bool whole = all_valid && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
+    float tile_max = -INFINITY;
+    if (whole) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[n][r]);
+      if (!q_ok) tile_max = -INFINITY;
+    } else {
+      // Token 16 n + 4 g + r is visible iff 16 n + r <= limit (positions below
+      // the split end and not after the query), and its slot is valid.
+      const int limit = q_ok ? min(kv_stop - 1, my_pos) - t0 - 4 * g : -1;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          bool visible = 16 * n + r <= limit;
+          if (!all_valid) visible = visible && slot_lds[t * kTile + 16 * n + 4 * g + r] >= 0;
+          s[n][r] = visible ? s[n][r] : -INFINITY;
+          tile_max = fmaxf(tile_max, s[n][r]);
+        }
+      }
+    }
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+    const float m_new = fmaxf(m, tile_max);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
+    const float bias = -m_use * scale_log2;
+    float row_sum = 0.f;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
+        row_sum += s[n][r];
+      }
+    }
+    if (!q_ok) row_sum = 0.f;
+    row_sum += __shfl_xor(row_sum, 16);
+    row_sum += __shfl_xor(row_sum, 32);
+    l = l * alpha + row_sum;
+    m = m_new;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 bits;
+      bits[0] = pack_bf16x2(s[2 * h][0], s[2 * h][1]);
+      bits[1] = pack_bf16x2(s[2 * h][2], s[2 * h][3]);
+      bits[2] = pack_bf16x2(s[2 * h + 1][0], s[2 * h + 1][1]);
+      bits[3] = pack_bf16x2(s[2 * h + 1][2], s[2 * h + 1][3]);
+      pb[h] = __builtin_bit_cast(bf16x8, bits);
+    }
+    // V^T fragment of dim tile dt and token half h: two transposed reads; lane
+    // j of a 16-lane group addresses dims 16 dt + 4 (j % 4) .. +3 of token
+    // 32 h + 4 g + j / 4 (first read) or that + 16 (second read).  All those
+    // tokens share the swizzle key x = 4 g + j / 4, so the byte offset is
+    // row(token) + ((2 dt + (j % 4) / 2) ^ x) * 16 + 8 (j % 2)
+    //   = lane_base + 8192 h (+ 4096) + ((dt ^ (x >> 1)) << 5).
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      o[dt] *= alpha;
+      const int dim_offset = v_lane + ((dt ^ xh) << 5);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const unsigned char *lo = v_stage + dim_offset + h * 32 * kChunksPerRow * 16;
+        const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)lo);
+        const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lo + 16 * kChunksPerRow * 16));
+        u32x4 bits;
+        bits[0] = __builtin_bit_cast(u32x2, a_lo)[0];
+        bits[1] = __builtin_bit_cast(u32x2, a_lo)[1];
+        bits[2] = __builtin_bit_cast(u32x2, a_hi)[0];
+        bits[3] = __builtin_bit_cast(u32x2, a_hi)[1];
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bits), pb[h], o[dt], 0, 0, 0);
+      }
+    }
+  }
+  if (!computes) return;
+  if (partial < 0) {
+    if (!q_ok) return;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      u32x2 packed;
+      packed[0] = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+      packed[1] = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+      *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
+    }
+  } else {
+    float *block = partial_block<D>(p, partial, hq);
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt)
+      *reinterpret_cast<f32x4 *>(block + c * D + 16 * dt + 4 * g) = o[dt];
+    if (g == 0) {
+      block[kQueries * D + 2 * c] = m * scale_log2;
+      block[kQueries * D + 2 * c + 1] = l;
+    }
+  }
+}
+
 // Merges the split partial results of one 16-query tile: workgroup (combine
 // item, query head); thread = (query, 1/16 of the dims).
 template <int D>
@@ -391,8 +704,9 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
                 "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
                 kMaxGroup);
-  if (split_tokens < 0 || split_tokens % kTile != 0)
-    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d", kTile);
+  if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > kDmaMaxRange)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
+                kTile, kDmaMaxRange);
   constexpr int64_t kIntMax = 0x7fffffff;
   const int per_item = tiles_per_item(static_cast<int>(num_q_heads / num_kv_heads));
   // 16-query tiles in row order; consecutive tiles of one request (same kv_offset)
@@ -432,10 +746,11 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   }
   int64_t split = split_tokens;
   if (split == 0) {
-    // Aim at ~1024 workgroups (16 waves each, 4 per CU): split = work * kv_heads / 1024, in [512, 8192].
+    // Aim at ~1024 workgroups (four rounds of the 256 CUs): split = work * kv_heads / 1024,
+    // in [512, kDmaMaxRange].
     split = (work * num_kv_heads / 1024 + kTile - 1) / kTile * kTile;
     if (split < 512) split = 512;
-    if (split > 8192) split = 8192;
+    if (split > kDmaMaxRange) split = kDmaMaxRange;
   }
   int64_t n_items = 0, n_combine = 0, n_partial = 0;
   int rc = LL_OK;
@@ -521,6 +836,7 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->num_queries < 0 || a->num_slots < 0 || a->kv_slots_len < 0 || a->num_items < 0 ||
       a->num_combine < 0 || a->workspace_items < 0)
     return fail(LL_ERR_INVALID_ARGUMENT, "counts must be >= 0");
+  if (a->num_slots > 0x7fffffff) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots must be below 2^31");
   if (!(a->softmax_scale > 0.0) || !isfinite(a->softmax_scale))
     return fail(LL_ERR_INVALID_ARGUMENT, "softmax_scale must be finite and > 0");
   if (a->num_items == 0) return LL_OK;
@@ -560,9 +876,11 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads));
-  const dim3 block(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group)));
-  if (a->head_dim == 128) repair_attention_kernel<128><<<grid, block, 0, s>>>(p);
-  else repair_attention_kernel<64><<<grid, block, 0, s>>>(p);
+  if (a->head_dim == 128)
+    repair_attention_dma_kernel<<<grid, dim3(kDmaThreads), 0, s>>>(p);
+  else
+    repair_attention_kernel<64><<<grid, dim3(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group))),
+                                 0, s>>>(p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   if (a->num_combine > 0) {

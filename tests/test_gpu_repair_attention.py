@@ -63,7 +63,9 @@ def _check(plan_spans, query, key_pool, value_pool, got, scale):
         valid = (slots_np[:end] >= 0) & (slots_np[:end] < k_np.shape[0])
         safe = torch.from_numpy(np.where(valid, slots_np[:end], 0))
         visible = ao.logical_causal_mask(np.arange(start, end), np.arange(end)) & valid[None]
-        fp32 = _torch_fp32(query[cursor : cursor + n], key_pool.cpu()[safe], value_pool.cpu()[safe], visible, scale)
+        keep = torch.from_numpy(valid)[:, None, None]
+        fp32 = _torch_fp32(query[cursor : cursor + n], torch.where(keep, key_pool.cpu()[safe], 0),
+                           torch.where(keep, value_pool.cpu()[safe], 0), visible, scale)
         part = got_np[cursor : cursor + n]
         err = np.abs(part - want)
         worst = max(worst, float((err / bound).max()))
@@ -127,8 +129,12 @@ def test_invalid_slots_are_invisible_keys(gpu_device):
     hq, hkv, dim, pool = 28, 4, 128, 1024
     key_pool = _bf16((pool, hkv, dim), generator, gpu_device)
     value_pool = _bf16((pool, hkv, dim), generator, gpu_device)
-    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:200].clone()
+    # Slot 0 is never visible and holds Inf and NaN: tokens without a valid slot
+    # (and the padding of the last key tile) must not reach the output.
+    slots = (torch.randperm(pool - 1, generator=generator, device=gpu_device)[:200] + 1).clone()
     slots[[3, 77, 150]] = torch.tensor([-1, pool, pool + 50], device=gpu_device)
+    key_pool[0] = float("inf")
+    value_pool[0] = float("nan")
     spans = [(slots, 140, 180)]
     with pytest.raises(SparseRepairAttentionError, match="invalid KV slots"):
         RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, pool_size=pool)

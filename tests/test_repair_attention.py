@@ -101,6 +101,11 @@ def test_oracle_matches_pairwise_loops_and_closed_forms():
     visible[:, 1] = False
     safe = np.array([3, 0, 1, 0])
     assert np.allclose(with_bad, ao.gqa_attention(query[:2], pool_k[safe], pool_v[safe], visible))
+    # ... whatever the row they alias holds.
+    pool_k[0], pool_v[0] = np.inf, np.nan
+    poisoned = ao.repair_attention(query[:2], pool_k, pool_v, [3, 9, 1, 11], 2, 4)
+    assert np.isfinite(poisoned).all()
+    assert np.allclose(poisoned, ao.repair_attention(query[:2], pool_k, pool_v, [3, -1, 1, 12], 2, 4))
 
 
 def test_a_planted_head_mapping_mistake_fails_the_reference_case():
@@ -172,6 +177,8 @@ def test_plan_rejects_bad_rows():
         _plan([(0, 5, 3, 0), (3, -1, 3, 0)])
     with pytest.raises(_native.NativeCallError, match="multiple of 64"):
         _plan([(0, 5, 3, 0)], split=100)
+    with pytest.raises(_native.NativeCallError, match="at most 4096"):
+        _plan([(0, 5, 3, 0)], split=4160)
     with pytest.raises(_native.NativeCallError) as error:
         _plan([(0, 5, 3, 0)], q_heads=36, kv_heads=4)  # 9 query heads per KV head
     assert error.value.reason == "kv_head_layout_mismatch"
