@@ -388,6 +388,44 @@ __device__ inline void workgroup_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Max and sum over the four lanes of one query column (l % 16 fixed).
+// v_permlane16_swap a, b exchanges the odd 16-lane rows of a with the even
+// rows of b, v_permlane32_swap the upper half of a with the lower half of b;
+// from two copies of x they leave (x[l], x[l ^ 16]) and then
+// (y[l], y[l ^ 32]) in the lane, up to order -- the operands of xor shuffles
+// 16 and 32.  (Inline assembly: the compiler builtins lose the second result
+// when both operands hold the same value.)  The s_nop covers the wait states
+// between a VALU write of an operand and the permute.
+__device__ inline void permlane16_swap(unsigned &a, unsigned &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+__device__ inline void permlane32_swap(unsigned &a, unsigned &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+__device__ inline float quad_max(float x) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  permlane16_swap(a, b);
+  x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  a = __builtin_bit_cast(unsigned, x);
+  b = a;
+  permlane32_swap(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+__device__ inline float quad_sum(float x) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  permlane16_swap(a, b);
+  x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  a = __builtin_bit_cast(unsigned, x);
+  b = a;
+  permlane32_swap(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
+
 __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int kSteps = D / 32;
@@ -398,7 +436,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   __shared__ __attribute__((aligned(16))) unsigned char k_ring[kDmaStages * kStageBytes];
   __shared__ __attribute__((aligned(16))) unsigned char v_ring[kDmaStages * kStageBytes];
   __shared__ int slot_lds[kDmaMaxRange];
-  __shared__ int tile_invalid[kRangeTiles];
+  __shared__ unsigned long long tile_valid[kRangeTiles];  // bit j: token j of the tile has a valid slot
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
@@ -433,7 +471,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
 
   // Slots of the item's range (-1: out of range or invalid), and per tile the
   // number of such tokens.
-  for (int i = tid; i < kRangeTiles; i += kDmaThreads) tile_invalid[i] = 0;
+  for (int i = tid; i < kRangeTiles; i += kDmaThreads) tile_valid[i] = 0ull;
   __syncthreads();
   for (int i = tid; i < tiles * kTile; i += kDmaThreads) {
     int slot = -1;
@@ -442,7 +480,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
       if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
     }
     slot_lds[i] = slot;
-    if (slot < 0) atomicAdd(&tile_invalid[i / kTile], 1);
+    if (slot >= 0) atomicOr(&tile_valid[i / kTile], 1ull << (i % kTile));
   }
 
   bf16x8 qf[kSteps];
@@ -484,6 +522,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
 #pragma unroll
   for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float scale_log2 = p.scale_log2;
+  const float slack = kSlack / scale_log2;  // kSlack in raw score units
 
   // Lane offsets of the transposed V reads (see below): the tokens a lane
   // group reads share the swizzle key x = 4 g + c / 4.
@@ -497,23 +536,22 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   // also wait for every outstanding gather and serialise the pipeline.  What
   // the loop needs is ordering: a wave's LDS reads of a stage are consumed by
   // its MFMAs before it reaches the next barrier, and each wave waits for its
-  // own gathers (vmcnt) before the barrier that releases a stage to compute.
+  // own gathers (vmcnt) before the barrier that hands a stage to compute.
   for (int t = 0, stage = 0; t < tiles; ++t) {
     const int next = stage == 0 ? kDmaStages - 1 : stage - 1;  // the stage of tile t + 2
     const unsigned char *k_stage = k_ring + stage * kStageBytes;
     unsigned char *v_stage = v_ring + stage * kStageBytes;
     stage = stage == kDmaStages - 1 ? 0 : stage + 1;
-    workgroup_barrier();          // every wave is done with the stage tile t + 2 reuses
-    unsigned char *k_next = k_ring + next * kStageBytes;
-    unsigned char *v_next = v_ring + next * kStageBytes;
-    if (t + 2 < tiles) gather(t + 2, k_next, v_next);
-    // This wave's gathers of tile t are complete when at most those of the
-    // tiles after it (two instructions each) are outstanding.
-    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF74);
-    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF72);
+    // This wave's loads of tile t are complete when at most those of tile
+    // t + 1 (two instructions) are outstanding.  One barrier then says both
+    // that every wave's loads of tile t have landed and that every wave is
+    // done with tile t - 1, whose stage tile t + 2 takes over.
+    if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF72);
     else __builtin_amdgcn_s_waitcnt(0xF70);
-    workgroup_barrier();          // and so are every other wave's
-    if (tile_invalid[t] != 0) {
+    workgroup_barrier();
+    if (t + 2 < tiles) gather(t + 2, k_ring + next * kStageBytes, v_ring + next * kStageBytes);
+    const unsigned long long valid_bits = tile_valid[t];
+    if (valid_bits != ~0ull) {
       // Zero the V rows of tokens without a valid slot: their probability is
       // 0, and 0 * V must not turn an Inf or NaN of slot 0's row into a NaN.
       // Thread i owns bytes 16 i .. 16 i + 15 of the stage (token i / 16).
@@ -543,8 +581,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
       }
     }
-    const bool all_valid = tile_invalid[t] == 0;
-    const bool whole = all_valid && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
+    const bool whole = valid_bits == ~0ull && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
     float tile_max = -INFINITY;
     if (whole) {
 #pragma unroll
@@ -556,22 +593,25 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
       // Token 16 n + 4 g + r is visible iff 16 n + r <= limit (positions below
       // the split end and not after the query), and its slot is valid.
       const int limit = q_ok ? min(kv_stop - 1, my_pos) - t0 - 4 * g : -1;
+      const unsigned long long lane_bits = valid_bits >> (4 * g);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          bool visible = 16 * n + r <= limit;
-          if (!all_valid) visible = visible && slot_lds[t * kTile + 16 * n + 4 * g + r] >= 0;
+          const bool visible = 16 * n + r <= limit && ((lane_bits >> (16 * n + r)) & 1ull) != 0;
           s[n][r] = visible ? s[n][r] : -INFINITY;
           tile_max = fmaxf(tile_max, s[n][r]);
         }
       }
     }
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-    const float m_new = fmaxf(m, tile_max);
+    tile_max = quad_max(tile_max);
+    // The reference maximum m moves only when the tile's maximum exceeds it by
+    // more than kSlack in log2 units, so most tiles keep it and skip rescaling
+    // O.  Probabilities relative to m stay <= 2^kSlack: no overflow in the
+    // fp32 sums, and their bf16 rounding is relative, as before.
+    const bool raise = tile_max > m + slack;
+    const float m_new = raise ? tile_max : m;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
     const float bias = -m_use * scale_log2;
     float row_sum = 0.f;
 #pragma unroll
@@ -583,9 +623,14 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
       }
     }
     if (!q_ok) row_sum = 0.f;
-    row_sum += __shfl_xor(row_sum, 16);
-    row_sum += __shfl_xor(row_sum, 32);
-    l = l * alpha + row_sum;
+    row_sum = quad_sum(row_sum);
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform
+      const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
+    }
+    l += row_sum;
     m = m_new;
     bf16x8 pb[2];
 #pragma unroll
@@ -605,7 +650,6 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
     //   = lane_base + 8192 h (+ 4096) + ((dt ^ (x >> 1)) << 5).
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
-      o[dt] *= alpha;
       const int dim_offset = v_lane + ((dt ^ xh) << 5);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -661,23 +705,36 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
   const int part = threadIdx.x % 16;
   if (c >= q_count) return;
   float big = -INFINITY;
+#pragma unroll 8
   for (int s = 0; s < count; ++s) big = fmaxf(big, partial_block<D>(p, first + s, h)[kQueries * D + 2 * c]);
   float total = 0.f;
-  float acc[kPer];
+  f32x4 acc[kPer / 4];
 #pragma unroll
-  for (int d = 0; d < kPer; ++d) acc[d] = 0.f;
+  for (int d = 0; d < kPer / 4; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Unrolled so that several partials' loads are in flight at once.
+#pragma unroll 4
   for (int s = 0; s < count; ++s) {
     const float *block = partial_block<D>(p, first + s, h);
     const float ms = block[kQueries * D + 2 * c];
     const float w = ms == -INFINITY ? 0.f : exp2f(ms - big);
     total += block[kQueries * D + 2 * c + 1] * w;
+    const f32x4 *row = reinterpret_cast<const f32x4 *>(block + c * D + part * kPer);
 #pragma unroll
-    for (int d = 0; d < kPer; ++d) acc[d] += w * block[c * D + part * kPer + d];
+    for (int d = 0; d < kPer / 4; ++d) acc[d] += w * row[d];
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
   uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + h) * D + part * kPer;
+  uint32_t packed[kPer / 2];
 #pragma unroll
-  for (int d = 0; d < kPer; ++d) dst[d] = bf16_rne(acc[d] * inv);
+  for (int d = 0; d < kPer / 4; ++d) {
+    packed[2 * d] = static_cast<uint32_t>(bf16_rne(acc[d][0] * inv)) |
+                    (static_cast<uint32_t>(bf16_rne(acc[d][1] * inv)) << 16);
+    packed[2 * d + 1] = static_cast<uint32_t>(bf16_rne(acc[d][2] * inv)) |
+                        (static_cast<uint32_t>(bf16_rne(acc[d][3] * inv)) << 16);
+  }
+#pragma unroll
+  for (int d = 0; d < kPer / 4; ++d)  // the output is 8-byte aligned
+    *reinterpret_cast<u32x2 *>(dst + 4 * d) = u32x2{packed[2 * d], packed[2 * d + 1]};
 }
 
 bool aligned(const void *ptr, uintptr_t bytes) {
