@@ -337,18 +337,20 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
 }
 
 // The same work on a pipelined schedule (head dim 128): K and V rows are
-// gathered straight into a three-stage LDS ring with global_load_lds, two
+// gathered straight into a four-stage LDS ring with global_load_lds, two
 // tiles ahead of the MFMAs, so no registers stage them and no wave waits on a
-// gather it could overlap.  Rows are stored token-major with their sixteen
-// 16-byte chunks XOR-swizzled by token (chunk c of token t at c ^ (t % 16)),
-// which keeps both the K fragment reads and the transposed V reads free of
-// bank conflicts.  V^T fragments come from ds_read_b64_tr_b16: within a group
+// gather it could overlap.  The workgroup synchronises once per two tiles,
+// so its waves drift apart within a pair of tiles and one wave's softmax
+// overlaps another's MFMAs.  Rows are stored token-major with their sixteen
+// 16-byte chunks XOR-swizzled by token (K: chunk c of token t at c ^ (t % 16),
+// V: at c ^ 2 (t % 8)), which keeps the K fragment reads and the transposed V
+// reads free of bank conflicts.  V^T fragments come from ds_read_b64_tr_b16: within a group
 // of 16 lanes it returns to lane i, element e, element i % 4 of the 8 bytes
 // that lane 4 e + i / 4 addressed (checked on the device), so lanes addressing
 // 4 dims of 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.
 // The item's slots are read once into LDS (at most kDmaMaxRange of them).
 constexpr int kDmaThreads = 1024;    // 16 waves: two gather instructions each per tile
-constexpr int kDmaStages = 3;
+constexpr int kDmaStages = 4;
 constexpr int kDmaMaxRange = 4096;   // KV tokens per work item on this path
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -388,7 +390,7 @@ __device__ inline void workgroup_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Max and sum over the four lanes of one query column (l % 16 fixed).
+// Max over the four lanes of one query column (l % 16 fixed).
 // v_permlane16_swap a, b exchanges the odd 16-lane rows of a with the even
 // rows of b, v_permlane32_swap the upper half of a with the lower half of b;
 // from two copies of x they leave (x[l], x[l ^ 16]) and then
@@ -404,27 +406,27 @@ __device__ inline void permlane32_swap(unsigned &a, unsigned &b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
+// v_max_f32 straight from assembly: fmaxf would first quiet its operands
+// (which come out of inline assembly) with two more instructions.  Scores
+// reaching here are never NaN (masked ones are -inf).
+__device__ inline float max_f32(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 __device__ inline float quad_max(float x) {
   unsigned a = __builtin_bit_cast(unsigned, x), b = a;
   permlane16_swap(a, b);
-  x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  x = max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
   a = __builtin_bit_cast(unsigned, x);
   b = a;
   permlane32_swap(a, b);
-  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
-
-__device__ inline float quad_sum(float x) {
-  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-  permlane16_swap(a, b);
-  x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-  a = __builtin_bit_cast(unsigned, x);
-  b = a;
-  permlane32_swap(a, b);
-  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  return max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
 constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
+constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score units)
 
 __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
   constexpr int D = 128;
@@ -497,13 +499,16 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   __syncthreads();
 
   // Gather of tile t: 32 instructions of 64 lanes (16 for K, 16 for V), two per
-  // wave.  Instruction k covers ring chunks 64 k .. 64 k + 63 of its stage;
-  // chunk P holds token P / 16, row chunk (P % 16) ^ (token % 16).
+  // wave.  Instruction k covers stage chunks 64 k .. 64 k + 63; stage chunk P
+  // holds token P / 16 and, of its row, chunk (P % 16) ^ (token % 16) for K
+  // and chunk (P % 16) ^ (2 (token % 8)) for V (each swizzle is its own
+  // inverse, so a row chunk r sits at r ^ key).
   const long long row_stride = static_cast<long long>(p.hkv) * D;
   // Wave w issues instruction w of the K tile and instruction w of the V tile.
   const int chunk_index = wave * kWave + lane;
   const int gather_token = chunk_index / kChunksPerRow;
-  const int gather_chunk = (chunk_index % kChunksPerRow) ^ (gather_token % 16);
+  const int k_chunk = (chunk_index % kChunksPerRow) ^ (gather_token % 16);
+  const int v_chunk = (chunk_index % kChunksPerRow) ^ (2 * (gather_token % 8));
   // Every wave issues exactly two loads per tile (the waits below count
   // them): a token without a valid slot loads slot 0's row instead (gather
   // leaves it out when the pool is empty), which the masking hides for K and
@@ -512,23 +517,31 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
     const int slot = max(slot_lds[t * kTile + gather_token], 0);
-    const long long offset = slot * row_stride + hk * D + gather_chunk * 8;
-    dma_pair(p.k + offset, k_dst + wave * kWave * 16, p.v + offset, v_dst + wave * kWave * 16);
+    const long long row = slot * row_stride + hk * D;
+    dma_pair(p.k + row + k_chunk * 8, k_dst + wave * kWave * 16, p.v + row + v_chunk * 8,
+             v_dst + wave * kWave * 16);
   };
 
-  float m = -INFINITY;
-  float l = 0.f;
+  // m starts at a finite floor far below any score, so the exponent bias
+  // needs no -inf special case: a query with no visible key yet keeps it and
+  // gets probabilities exp2(-inf) = 0.
+  float m = kScoreFloor;
   f32x4 o[kDimTiles];
 #pragma unroll
   for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The softmax denominators come out of the value MFMA: a 16-row A operand of
+  // ones times P^T gives, in every accumulator register of lane (g, c), the
+  // sum of query c's probabilities as the value product sees them (bf16).
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   const float scale_log2 = p.scale_log2;
   const float slack = kSlack / scale_log2;  // kSlack in raw score units
 
   // Lane offsets of the transposed V reads (see below): the tokens a lane
-  // group reads share the swizzle key x = 4 g + c / 4.
+  // reads are congruent to x = 4 g + c / 4 modulo 16.
   const int x = 4 * g + c / 4;
-  const int lane_base = x * (kChunksPerRow * 16) + (((c % 4) / 2) ^ (x & 1)) * 16 + (c % 2) * 8;
-  const int xh = x >> 1;
+  const int lane_base = x * (kChunksPerRow * 16) + ((c % 4) / 2) * 16 + (c % 2) * 8;
+  const int x8 = x & 7;
 
   if (tiles > 0) gather(0, k_ring, v_ring);
   if (tiles > 1) gather(1, k_ring + kStageBytes, v_ring + kStageBytes);
@@ -537,19 +550,21 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   // the loop needs is ordering: a wave's LDS reads of a stage are consumed by
   // its MFMAs before it reaches the next barrier, and each wave waits for its
   // own gathers (vmcnt) before the barrier that hands a stage to compute.
-  for (int t = 0, stage = 0; t < tiles; ++t) {
-    const int next = stage == 0 ? kDmaStages - 1 : stage - 1;  // the stage of tile t + 2
-    const unsigned char *k_stage = k_ring + stage * kStageBytes;
-    unsigned char *v_stage = v_ring + stage * kStageBytes;
-    stage = stage == kDmaStages - 1 ? 0 : stage + 1;
-    // This wave's loads of tile t are complete when at most those of tile
-    // t + 1 (two instructions) are outstanding.  One barrier then says both
-    // that every wave's loads of tile t have landed and that every wave is
-    // done with tile t - 1, whose stage tile t + 2 takes over.
-    if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF72);
-    else __builtin_amdgcn_s_waitcnt(0xF70);
-    workgroup_barrier();
-    if (t + 2 < tiles) gather(t + 2, k_ring + next * kStageBytes, v_ring + next * kStageBytes);
+  for (int t = 0; t < tiles; ++t) {
+    const unsigned char *k_stage = k_ring + (t % kDmaStages) * kStageBytes;
+    unsigned char *v_stage = v_ring + (t % kDmaStages) * kStageBytes;
+    if (t % 2 == 0) {
+      // Tiles t and t + 1 were gathered two tiles ago.  Once this wave's loads
+      // are complete, one barrier says both that every wave's loads of them
+      // have landed and that every wave is done with tiles t - 2 and t - 1,
+      // whose stages tiles t + 2 and t + 3 take over.
+      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+      workgroup_barrier();
+      if (t + 2 < tiles)
+        gather(t + 2, k_ring + ((t + 2) % kDmaStages) * kStageBytes, v_ring + ((t + 2) % kDmaStages) * kStageBytes);
+      if (t + 3 < tiles)
+        gather(t + 3, k_ring + ((t + 3) % kDmaStages) * kStageBytes, v_ring + ((t + 3) % kDmaStages) * kStageBytes);
+    }
     const unsigned long long valid_bits = tile_valid[t];
     if (valid_bits != ~0ull) {
       // Zero the V rows of tokens without a valid slot: their probability is
@@ -611,26 +626,18 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
     // fp32 sums, and their bf16 rounding is relative, as before.
     const bool raise = tile_max > m + slack;
     const float m_new = raise ? tile_max : m;
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float bias = -m_use * scale_log2;
-    float row_sum = 0.f;
+    const float bias = -m_new * scale_log2;
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
-        row_sum += s[n][r];
-      }
+      for (int r = 0; r < 4; ++r) s[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
     }
-    if (!q_ok) row_sum = 0.f;
-    row_sum = quad_sum(row_sum);
     if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform
-      const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
-      l *= alpha;
+      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);
+      lsum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
     }
-    l += row_sum;
     m = m_new;
     bf16x8 pb[2];
 #pragma unroll
@@ -644,13 +651,15 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
     }
     // V^T fragment of dim tile dt and token half h: two transposed reads; lane
     // j of a 16-lane group addresses dims 16 dt + 4 (j % 4) .. +3 of token
-    // 32 h + 4 g + j / 4 (first read) or that + 16 (second read).  All those
-    // tokens share the swizzle key x = 4 g + j / 4, so the byte offset is
-    // row(token) + ((2 dt + (j % 4) / 2) ^ x) * 16 + 8 (j % 2)
-    //   = lane_base + 8192 h (+ 4096) + ((dt ^ (x >> 1)) << 5).
+    // 32 h + 4 g + j / 4 (first read) or that + 16 (second read).  Those dims
+    // are row chunk 2 dt + (j % 4) / 2, stored at (2 dt + (j % 4) / 2) ^ 2 (x % 8)
+    // = 2 (dt ^ (x % 8)) + (j % 4) / 2, so the byte offset is
+    //   lane_base + 8192 h (+ 4096) + ((dt ^ (x % 8)) << 5).
+    // Within 32 lanes (x % 8 takes all 8 values) the 16-byte slots are distinct:
+    // every bank is read once.
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
-      const int dim_offset = v_lane + ((dt ^ xh) << 5);
+      const int dim_offset = v_lane + ((dt ^ x8) << 5);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const unsigned char *lo = v_stage + dim_offset + h * 32 * kChunksPerRow * 16;
@@ -664,7 +673,10 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bits), pb[h], o[dt], 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[h], lsum, 0, 0, 0);
   }
+  const float l = lsum[0];
   if (!computes) return;
   if (partial < 0) {
     if (!q_ok) return;
