@@ -38,6 +38,10 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <functional>
+#include <queue>
+#include <vector>
+
 #include "legolink_kv.h"
 #include "ll_internal.h"
 
@@ -749,6 +753,51 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
     *reinterpret_cast<u32x2 *>(dst + 4 * d) = u32x2{packed[2 * d], packed[2 * d + 1]};
 }
 
+// Modelled run time of a plan in units of one 64-token key tile of a work
+// item (about 2.4 us for Qwen's 28/4 heads on MI355X).  `groups` calls its
+// argument with (key tokens, partial results) of every group of query tiles.
+constexpr int kComputeUnits = 256;          // MI355X
+constexpr double kItemOverheadTiles = 3.0;  // slots, queries, write-out
+constexpr double kPartialBytesPerTile = 12e6;  // partial results the combine reads in one tile's time
+constexpr double kCombineLaunchTiles = 2.0;
+template <typename Groups>
+double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_heads, Groups &&groups) {
+  std::vector<double> item_cost;
+  int64_t partials = 0;
+  groups([&](int64_t needed, int64_t group_partials) {
+    for (int64_t begin = 0; begin < needed; begin += split) {
+      const int64_t len = needed - begin < split ? needed - begin : split;
+      item_cost.push_back(static_cast<double>((len + kTile - 1) / kTile) + kItemOverheadTiles);
+    }
+    partials += group_partials;
+  });
+  double makespan = 0.0;
+  if (static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits) {
+    // Many rounds: the last one's imbalance is small against the total.
+    double total = 0.0, longest = 0.0;
+    for (const double cost : item_cost) {
+      total += cost;
+      longest = cost > longest ? cost : longest;
+    }
+    makespan = total * num_kv_heads / kComputeUnits + longest;
+  } else {
+    std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+    for (int i = 0; i < kComputeUnits; ++i) free_at.push(0.0);
+    for (int64_t h = 0; h < num_kv_heads; ++h) {
+      for (const double cost : item_cost) {
+        const double start = free_at.top();
+        free_at.pop();
+        free_at.push(start + cost);
+        makespan = start + cost > makespan ? start + cost : makespan;
+      }
+    }
+  }
+  if (partials > 0)
+    makespan += kCombineLaunchTiles +
+                static_cast<double>(partials) * num_q_heads * (kQueries * 128 + 2 * kQueries) * 4 / kPartialBytesPerTile;
+  return makespan;
+}
+
 bool aligned(const void *ptr, uintptr_t bytes) {
   return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0;
 }
@@ -815,11 +864,33 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   }
   int64_t split = split_tokens;
   if (split == 0) {
-    // Aim at ~1024 workgroups (four rounds of the 256 CUs): split = work * kv_heads / 1024,
-    // in [512, kDmaMaxRange].
-    split = (work * num_kv_heads / 1024 + kTile - 1) / kTile * kTile;
-    if (split < 512) split = 512;
-    if (split > kDmaMaxRange) split = kDmaMaxRange;
+    // Pick the chunk length whose plan finishes first on a model of the
+    // device: one workgroup per CU at a time (its LDS allows no more),
+    // workgroups dispatched in grid order to the first free CU, each costing
+    // its key tiles plus a fixed overhead, then the combine pass reading every
+    // partial result.  Few long chunks leave CUs idle in the last round; many
+    // short ones add overhead and partials.
+    static const int64_t kCandidates[] = {512, 640, 768, 1024, 1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096};
+    double best = -1.0;
+    for (const int64_t candidate : kCandidates) {
+      const double estimate = plan_cost_estimate(
+          candidate, num_kv_heads, num_q_heads, [&](auto &&visit) {
+            for (int64_t first = 0; first < n_tiles; first = group_end(first)) {
+              const int64_t last = group_end(first);
+              int64_t needed = 0, partials = 0;
+              for (int64_t t = first; t < last; ++t) {
+                needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+                const int64_t chunks = (tiles[t].needed + candidate - 1) / candidate;
+                partials += chunks > 1 ? chunks : 0;
+              }
+              visit(needed, partials);
+            }
+          });
+      if (best < 0.0 || estimate <= best) {
+        best = estimate;
+        split = candidate;
+      }
+    }
   }
   int64_t n_items = 0, n_combine = 0, n_partial = 0;
   int rc = LL_OK;
