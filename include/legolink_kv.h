@@ -287,10 +287,13 @@ typedef struct ll_link_maps_args {
  *   ll_repair_attention_plan (host only) cuts the rows into 16-query tiles,
  *   groups consecutive tiles of one request (same kv_offset) into work items
  *   that share every staged K/V tile (as many tiles as 16 waves hold: 2 for 7
- *   or 8 query heads per KV head), splits long KV ranges for parallelism, and
- *   writes the item and combine tables; the caller copies them to the device
- *   once and reuses them for every layer.  Call it with NULL tables to size
- *   them.  ll_repair_attention runs one layer.
+ *   or 8 query heads per KV head), splits long KV ranges into chunks of
+ *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
+ *   from a model of the device's workgroup rounds), and writes the item and
+ *   combine tables; the caller copies them to the device once and reuses them
+ *   for every layer.  Call it with NULL tables to size them.
+ *   ll_repair_attention runs one layer; it takes tables made by this plan
+ *   (items over more than 4096 keys are not computed) and num_slots < 2^31.
  *
  * Replaces the FlashInfer block-sparse repair attention of
  * patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py
