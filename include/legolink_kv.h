@@ -319,16 +319,16 @@ typedef struct ll_repair_attention_plan_info {
 
 typedef struct ll_repair_attention_args {
   int64_t struct_size;             /* sizeof(ll_repair_attention_args) */
-  const void *query;               /* device bf16 [num_queries, num_q_heads, head_dim], dense */
-  void *output;                    /* device bf16 [num_queries, num_q_heads, head_dim], dense */
+  const void *query;               /* device kv_dtype [num_queries, num_q_heads, head_dim], dense */
+  void *output;                    /* device kv_dtype [num_queries, num_q_heads, head_dim], dense */
   int64_t num_queries;
-  const void *key_buffer;          /* device bf16 [num_slots, num_kv_heads, head_dim]: one layer */
-  const void *value_buffer;        /* device bf16 [num_slots, num_kv_heads, head_dim] */
+  const void *key_buffer;          /* device kv_dtype [num_slots, num_kv_heads, head_dim]: one layer */
+  const void *value_buffer;        /* device kv_dtype [num_slots, num_kv_heads, head_dim] */
   int64_t num_slots;
   int64_t num_q_heads;
   int64_t num_kv_heads;            /* divides num_q_heads, at most 8 query heads per KV head */
   int64_t head_dim;                /* 64 or 128 */
-  int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 */
+  int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16: queries, K/V and output */
   double softmax_scale;
   const void *kv_slots;            /* device int32/int64 [kv_slots_len]: the requests' slot lists */
   int64_t kv_slots_dtype;

@@ -54,6 +54,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 
 constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
@@ -92,17 +94,30 @@ struct AttnParams {
   float scale_log2;
 };
 
-__device__ inline uint16_t bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
+// The 16-bit element types of queries, keys, values and outputs: the MFMA
+// that takes them (fp32 accumulation) and the rounding of fp32 results back
+// to them (two at a time, round to nearest even).
+struct Bf16 {
+  typedef bf16x8 frag;
+  static constexpr uint32_t kOnes = 0x3F803F80u;  // two 1.0s
+  __device__ static f32x4 mfma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  }
+};
 
-// Two floats to two bf16 with one v_cvt_pk_bf16_f32 (round to nearest even).
-__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
-}
+struct F16 {
+  typedef f16x8 frag;
+  static constexpr uint32_t kOnes = 0x3C003C00u;
+  __device__ static f32x4 mfma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
+};
 
 // Query tiles per work item for a GQA group: as many as 16 waves hold.
 __host__ __device__ inline int tiles_per_item(int group) {
@@ -121,8 +136,9 @@ __device__ inline float *partial_block(const AttnParams &p, int partial, int h) 
   return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
 }
 
-template <int D>
+template <int D, typename E>
 __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(const AttnParams p) {
+  typedef typename E::frag frag;
   constexpr int kSteps = D / 32;     // k-steps of S^T = K Q^T
   constexpr int kDimTiles = D / 16;  // 16-row tiles of O^T
   constexpr int kKRow = D + 8;       // LDS row stride of K (elements), spreads banks
@@ -166,14 +182,14 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
   }
 
   // The wave's queries as the B operand of S^T = K Q^T: query c, dims 32 ks + 8 g + e.
-  bf16x8 qf[kSteps];
+  frag qf[kSteps];
   {
     const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) {
       u32x4 bits = {0u, 0u, 0u, 0u};
       if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
-      qf[ks] = __builtin_bit_cast(bf16x8, bits);
+      qf[ks] = __builtin_bit_cast(frag, bits);
     }
   }
 
@@ -234,8 +250,8 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
       s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(&k_lds[(16 * n + c) * kKRow + 32 * ks + 8 * g]);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
+        const frag a = *reinterpret_cast<const frag *>(&k_lds[(16 * n + c) * kKRow + 32 * ks + 8 * g]);
+        s[n] = E::mfma(a, qf[ks], s[n]);
       }
     }
     // Raw scores are kept unscaled: the max commutes with the positive scale,
@@ -287,15 +303,15 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
     // accumulators of token tiles 2h and 2h + 1, so lane group g holds tokens
     // 32 h + 4 g + {0..3} and 32 h + 16 + 4 g + {0..3}; the A operand (V^T)
     // reads the same tokens for its dim row.
-    bf16x8 pb[2];
+    frag pb[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       u32x4 bits;
-      bits[0] = pack_bf16x2(pv[2 * h][0], pv[2 * h][1]);
-      bits[1] = pack_bf16x2(pv[2 * h][2], pv[2 * h][3]);
-      bits[2] = pack_bf16x2(pv[2 * h + 1][0], pv[2 * h + 1][1]);
-      bits[3] = pack_bf16x2(pv[2 * h + 1][2], pv[2 * h + 1][3]);
-      pb[h] = __builtin_bit_cast(bf16x8, bits);
+      bits[0] = E::pack(pv[2 * h][0], pv[2 * h][1]);
+      bits[1] = E::pack(pv[2 * h][2], pv[2 * h][3]);
+      bits[2] = E::pack(pv[2 * h + 1][0], pv[2 * h + 1][1]);
+      bits[3] = E::pack(pv[2 * h + 1][2], pv[2 * h + 1][3]);
+      pb[h] = __builtin_bit_cast(frag, bits);
     }
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
@@ -310,7 +326,7 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
         bits[1] = lo[1];
         bits[2] = hi[0];
         bits[3] = hi[1];
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bits), pb[h], o[dt], 0, 0, 0);
+        o[dt] = E::mfma(__builtin_bit_cast(frag, bits), pb[h], o[dt]);
       }
     }
   }
@@ -324,8 +340,8 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
       u32x2 packed;
-      packed[0] = bf16_rne(o[dt][0] * inv) | (static_cast<uint32_t>(bf16_rne(o[dt][1] * inv)) << 16);
-      packed[1] = bf16_rne(o[dt][2] * inv) | (static_cast<uint32_t>(bf16_rne(o[dt][3] * inv)) << 16);
+      packed[0] = E::pack(o[dt][0] * inv, o[dt][1] * inv);
+      packed[1] = E::pack(o[dt][2] * inv, o[dt][3] * inv);
       *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
     }
   } else {
@@ -432,7 +448,9 @@ __device__ inline float quad_max(float x) {
 constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
 constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score units)
 
+template <typename E>
 __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
+  typedef typename E::frag frag;
   constexpr int D = 128;
   constexpr int kSteps = D / 32;
   constexpr int kDimTiles = D / 16;
@@ -489,14 +507,14 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
     if (slot >= 0) atomicOr(&tile_valid[i / kTile], 1ull << (i % kTile));
   }
 
-  bf16x8 qf[kSteps];
+  frag qf[kSteps];
   {
     const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) {
       u32x4 bits = {0u, 0u, 0u, 0u};
       if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
-      qf[ks] = __builtin_bit_cast(bf16x8, bits);
+      qf[ks] = __builtin_bit_cast(frag, bits);
     }
   }
   __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): queries and slots are in
@@ -537,7 +555,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   // ones times P^T gives, in every accumulator register of lane (g, c), the
   // sum of query c's probabilities as the value product sees them (bf16).
   f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const frag ones = __builtin_bit_cast(frag, u32x4{E::kOnes, E::kOnes, E::kOnes, E::kOnes});
   const float scale_log2 = p.scale_log2;
   const float slack = kSlack / scale_log2;  // kSlack in raw score units
 
@@ -596,8 +614,8 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
       for (int ks = 0; ks < kSteps; ++ks) {
         // Token 16 n + c: its swizzle key is c, so row chunk 4 ks + g sits at (4 ks + g) ^ c.
         const int chunk = (4 * ks + g) ^ c;
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(k_stage + k_lane + n * 16 * kChunksPerRow * 16 + chunk * 16);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[n], 0, 0, 0);
+        const frag a = *reinterpret_cast<const frag *>(k_stage + k_lane + n * 16 * kChunksPerRow * 16 + chunk * 16);
+        s[n] = E::mfma(a, qf[ks], s[n]);
       }
     }
     const bool whole = valid_bits == ~0ull && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
@@ -643,15 +661,15 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
       for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
     }
     m = m_new;
-    bf16x8 pb[2];
+    frag pb[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       u32x4 bits;
-      bits[0] = pack_bf16x2(s[2 * h][0], s[2 * h][1]);
-      bits[1] = pack_bf16x2(s[2 * h][2], s[2 * h][3]);
-      bits[2] = pack_bf16x2(s[2 * h + 1][0], s[2 * h + 1][1]);
-      bits[3] = pack_bf16x2(s[2 * h + 1][2], s[2 * h + 1][3]);
-      pb[h] = __builtin_bit_cast(bf16x8, bits);
+      bits[0] = E::pack(s[2 * h][0], s[2 * h][1]);
+      bits[1] = E::pack(s[2 * h][2], s[2 * h][3]);
+      bits[2] = E::pack(s[2 * h + 1][0], s[2 * h + 1][1]);
+      bits[3] = E::pack(s[2 * h + 1][2], s[2 * h + 1][3]);
+      pb[h] = __builtin_bit_cast(frag, bits);
     }
     // V^T fragment of dim tile dt and token half h: two transposed reads; lane
     // j of a 16-lane group addresses dims 16 dt + 4 (j % 4) .. +3 of token
@@ -674,11 +692,11 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
         bits[1] = __builtin_bit_cast(u32x2, a_lo)[1];
         bits[2] = __builtin_bit_cast(u32x2, a_hi)[0];
         bits[3] = __builtin_bit_cast(u32x2, a_hi)[1];
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bits), pb[h], o[dt], 0, 0, 0);
+        o[dt] = E::mfma(__builtin_bit_cast(frag, bits), pb[h], o[dt]);
       }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[h], lsum, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) lsum = E::mfma(ones, pb[h], lsum);
   }
   const float l = lsum[0];
   if (!computes) return;
@@ -689,8 +707,8 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
       u32x2 packed;
-      packed[0] = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-      packed[1] = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+      packed[0] = E::pack(o[dt][0] * inv, o[dt][1] * inv);
+      packed[1] = E::pack(o[dt][2] * inv, o[dt][3] * inv);
       *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
     }
   } else {
@@ -707,7 +725,7 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
 
 // Merges the split partial results of one 16-query tile: workgroup (combine
 // item, query head); thread = (query, 1/16 of the dims).
-template <int D>
+template <int D, typename E>
 __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p) {
   constexpr int kPer = D / 16;
   const int *ci = p.combine + static_cast<long long>(blockIdx.x) * kCombineInts;
@@ -743,10 +761,8 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
   uint32_t packed[kPer / 2];
 #pragma unroll
   for (int d = 0; d < kPer / 4; ++d) {
-    packed[2 * d] = static_cast<uint32_t>(bf16_rne(acc[d][0] * inv)) |
-                    (static_cast<uint32_t>(bf16_rne(acc[d][1] * inv)) << 16);
-    packed[2 * d + 1] = static_cast<uint32_t>(bf16_rne(acc[d][2] * inv)) |
-                        (static_cast<uint32_t>(bf16_rne(acc[d][3] * inv)) << 16);
+    packed[2 * d] = E::pack(acc[d][0] * inv, acc[d][1] * inv);
+    packed[2 * d + 1] = E::pack(acc[d][2] * inv, acc[d][3] * inv);
   }
 #pragma unroll
   for (int d = 0; d < kPer / 4; ++d)  // the output is 8-byte aligned
@@ -964,8 +980,8 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->struct_size != static_cast<int64_t>(sizeof(ll_repair_attention_args)))
     return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
                 static_cast<long long>(a->struct_size), sizeof(ll_repair_attention_args));
-  if (a->kv_dtype != LL_DTYPE_BFLOAT16)
-    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes bf16 queries and KV");
+  if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
+    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes fp16 or bf16 queries and KV");
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64 or 128");
   if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
@@ -1016,17 +1032,26 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads));
-  if (a->head_dim == 128)
-    repair_attention_dma_kernel<<<grid, dim3(kDmaThreads), 0, s>>>(p);
-  else
-    repair_attention_kernel<64><<<grid, dim3(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group))),
-                                 0, s>>>(p);
+  const dim3 block64(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group)));
+  const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
+  if (a->head_dim == 128) {
+    if (f16) repair_attention_dma_kernel<F16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
+    else repair_attention_dma_kernel<Bf16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
+  } else {
+    if (f16) repair_attention_kernel<64, F16><<<grid, block64, 0, s>>>(p);
+    else repair_attention_kernel<64, Bf16><<<grid, block64, 0, s>>>(p);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   if (a->num_combine > 0) {
     const dim3 cgrid(static_cast<unsigned>(a->num_combine), static_cast<unsigned>(a->num_q_heads));
-    if (a->head_dim == 128) repair_combine_kernel<128><<<cgrid, dim3(256), 0, s>>>(p);
-    else repair_combine_kernel<64><<<cgrid, dim3(256), 0, s>>>(p);
+    if (a->head_dim == 128) {
+      if (f16) repair_combine_kernel<128, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<128, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    } else {
+      if (f16) repair_combine_kernel<64, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<64, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    }
     err = hipGetLastError();
     if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   }

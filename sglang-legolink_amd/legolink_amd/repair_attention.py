@@ -13,7 +13,7 @@ mask (patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py:
 semantics as ``gqa_attention`` over ``logical_causal_mask``
 (tests/pic/reference/attention_reference.py:8-48).
 
-Here it is one hand-written gfx950 kernel (MFMA bf16, online softmax in fp32)
+Here it is one hand-written gfx950 kernel (fp16 or bf16 MFMA, online softmax in fp32)
 behind ``ll_repair_attention``, with the same two phases as the reference's
 wrapper: a host plan built once per request batch (shared by every layer:
 the slots and spans do not depend on the layer) and a run per layer.
@@ -117,7 +117,7 @@ class RepairAttentionPlan:
     @property
     def kv_bytes_read(self) -> int:
         """Bytes of K and V the kernel gathers: each work item reads its KV range
-        [kv_begin, kv_end) once per KV head (bf16)."""
+        [kv_begin, kv_end) once per KV head (2-byte elements)."""
 
         items = self.items.view(-1, _native.REPAIR_ITEM_INTS).cpu().numpy().astype(np.int64)
         tokens = int((items[:, 2] - items[:, 1]).sum())
@@ -126,27 +126,32 @@ class RepairAttentionPlan:
     def run(self, query: torch.Tensor, key_buffer: torch.Tensor, value_buffer: torch.Tensor, *,
             scale: Optional[float] = None, output: Optional[torch.Tensor] = None,
             stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        """One layer: ``query`` [num_queries, num_q_heads, head_dim] bf16 (or its
-        [num_queries, num_q_heads * head_dim] view), ``key_buffer`` /
-        ``value_buffer`` the layer's [slots, num_kv_heads, head_dim] pool buffers.
-        Returns (or fills) the [num_queries, num_q_heads, head_dim] output."""
+        """One layer: ``query`` [num_queries, num_q_heads, head_dim] fp16 or bf16
+        (or its [num_queries, num_q_heads * head_dim] view), ``key_buffer`` /
+        ``value_buffer`` the layer's [slots, num_kv_heads, head_dim] pool buffers
+        of the same dtype.  Returns (or fills) the [num_queries, num_q_heads,
+        head_dim] output, in that dtype."""
 
         shape = (self.num_queries, self.num_q_heads, self.head_dim)
         query = query.view(shape)
+        # The checks of the reference's _compatibility_error
+        # (flashinfer_sparse_repair.py:973-980).
+        if query.dtype not in (torch.float16, torch.bfloat16):
+            raise SparseRepairAttentionError(f"unsupported Q dtype: {query.dtype}")
+        if key_buffer.dtype != query.dtype or value_buffer.dtype != query.dtype:
+            raise SparseRepairAttentionError("Q/K/V dtypes must match")
         for name, tensor in (("query", query), ("key_buffer", key_buffer), ("value_buffer", value_buffer)):
             if not tensor.is_cuda:
                 raise SparseRepairAttentionError(f"{name} must be a device tensor")
-            if tensor.dtype != torch.bfloat16:
-                raise SparseRepairAttentionError(f"{name} must be bf16")
             if not tensor.is_contiguous():
                 raise SparseRepairAttentionError(f"{name} must be contiguous")
         if key_buffer.ndim != 3 or key_buffer.shape[1:] != (self.num_kv_heads, self.head_dim) or (
                 value_buffer.shape != key_buffer.shape):
             raise SparseRepairAttentionError("KV buffers must be [slots, num_kv_heads, head_dim]")
         if output is None:
-            output = torch.empty(shape, dtype=torch.bfloat16, device=query.device)
-        elif output.shape != shape or output.dtype != torch.bfloat16 or not output.is_contiguous():
-            raise SparseRepairAttentionError("output must be a contiguous bf16 tensor of the query's shape")
+            output = torch.empty(shape, dtype=query.dtype, device=query.device)
+        elif output.shape != shape or output.dtype != query.dtype or not output.is_contiguous():
+            raise SparseRepairAttentionError("output must be a contiguous tensor of the query's shape and dtype")
         args = _native.RepairAttentionArgs()
         args.query = query.data_ptr()
         args.output = output.data_ptr()
@@ -157,7 +162,7 @@ class RepairAttentionPlan:
         args.num_q_heads = self.num_q_heads
         args.num_kv_heads = self.num_kv_heads
         args.head_dim = self.head_dim
-        args.kv_dtype = _native.DTYPE_BFLOAT16
+        args.kv_dtype = _native.DTYPE_BFLOAT16 if query.dtype == torch.bfloat16 else _native.DTYPE_FLOAT16
         args.softmax_scale = float(scale) if scale is not None else 1.0 / math.sqrt(self.head_dim)
         args.kv_slots = self.kv_slots.data_ptr()
         args.kv_slots_dtype = _native.DTYPE_INT64 if self.kv_slots.dtype == torch.int64 else _native.DTYPE_INT32

@@ -6,7 +6,8 @@ Tolerance, elementwise: |got - ref| <= 2^-7 * (sum_j w_j |v_j| + |ref|) + 1e-5,
 where w are the softmax weights.  The kernel rounds each probability to bf16
 for the value product (relative error <= 2^-8, so the output moves by at most
 2^-8 * sum_j w_j |v_j|) and the output to bf16 (<= 2^-8 * |ref|); the bound
-takes twice that.  The reference's own FlashInfer check is atol = rtol = 3e-2
+takes twice that.  fp16 inputs round to fp16 instead (2^-11) and keep the same
+bound.  The reference's own FlashInfer check is atol = rtol = 3e-2
 (tests/pic/test_sparse_attention_reference.py:103).  Short KVs, a sharp
 softmax (scale 1) and zero queries make an off-by-one mask or a dropped key
 (an output change of w_j |v_j - ref|, >= 2.5e-2 there) visible above it.
@@ -28,8 +29,8 @@ from tests.gpu_helpers import report
 pytestmark = pytest.mark.gpu
 
 
-def _bf16(shape, generator, device, scale=1.0):
-    return (torch.randn(shape, generator=generator, device=device) * scale).to(torch.bfloat16)
+def _bf16(shape, generator, device, scale=1.0, dtype=torch.bfloat16):
+    return (torch.randn(shape, generator=generator, device=device) * scale).to(dtype)
 
 
 def _torch_fp32(query, key_rows, value_rows, visible, scale):
@@ -106,6 +107,42 @@ def test_repair_attention_matches_oracle(gpu_device, case):
     got = plan.run(query, key_pool, value_pool, scale=scale)
     torch.cuda.synchronize(gpu_device)
     _check(plan_spans, query, key_pool, value_pool, got, use_scale)
+
+
+FP16_CASES = [c for c in CASES if c[0] in ("qwen7b_one_span", "long_kv_forced_splits", "seams_auto_split",
+                                           "group8_head_dim64")]
+
+
+@pytest.mark.parametrize("case", FP16_CASES, ids=[c[0] for c in FP16_CASES])
+def test_fp16_matches_oracle(gpu_device, case):
+    """The reference takes fp16 or bf16 Q/K/V (flashinfer_sparse_repair.py:977-980)."""
+
+    name, hq, hkv, dim, spans, pool, split, scale = case
+    report(f"fp16 case {name}")
+    generator = torch.Generator(device=gpu_device).manual_seed(zlib.crc32(name.encode()) % 1000 + 1)
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=torch.float16)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=torch.float16)
+    length = max(end for _, end in spans)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:length]
+    plan_spans = [(slots, start, end) for start, end in spans]
+    plan = RepairAttentionPlan(plan_spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim,
+                               pool_size=pool, split_tokens=split)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device, dtype=torch.float16)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    assert got.dtype == torch.float16
+    _check(plan_spans, query, key_pool, value_pool, got, scale if scale is not None else 1.0 / math.sqrt(dim))
+
+
+def test_dtype_checks_follow_the_reference(gpu_device):
+    slots = torch.arange(64, device=gpu_device)
+    plan = RepairAttentionPlan([(slots, 10, 26)], num_q_heads=8, num_kv_heads=2, head_dim=64)
+    kv16 = torch.zeros((64, 2, 64), dtype=torch.float16, device=gpu_device)
+    q = torch.zeros((16, 8, 64), dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(SparseRepairAttentionError, match="dtypes must match"):
+        plan.run(q, kv16, kv16)
+    with pytest.raises(SparseRepairAttentionError, match="unsupported Q dtype"):
+        plan.run(q.float(), kv16.float(), kv16.float())
 
 
 def test_two_requests_in_one_plan_with_int32_slots(gpu_device):

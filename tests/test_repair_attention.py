@@ -205,7 +205,7 @@ def test_attention_entry_validates_before_any_launch():
         (dict(head_dim=96), "head_dimension_out_of_range"),
         (dict(num_q_heads=36), "kv_head_layout_mismatch"),   # 9 query heads per KV head
         (dict(num_q_heads=30), "kv_head_layout_mismatch"),
-        (dict(kv_dtype=_native.DTYPE_FLOAT16), "fp16_or_bf16_required"),
+        (dict(kv_dtype=_native.DTYPE_FLOAT32), "fp16_or_bf16_required"),
         (dict(kv_slots_dtype=_native.DTYPE_FLOAT32), "integer_token_maps_required"),
         (dict(query=None), "invalid_argument"),
         (dict(softmax_scale=float("nan")), "invalid_argument"),
