@@ -46,6 +46,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     parser.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    parser.add_argument("--cpu-attention-gflop", type=float, default=20.0,
+                        help="flop budget of the repair attention CPU baseline sample")
     parser.add_argument("--cpu-sample-tokens", type=int, default=32768)
     parser.add_argument("--cpu-reps", type=int, default=25)
     parser.add_argument("--layers-per-wave", type=int, default=0)
@@ -323,6 +325,10 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
     kv_bytes = plan.kv_bytes_read
     log(f"repair attention {workload.name}: {len(spans)} spans, {plan.num_queries} queries, "
         f"plan {plan.info}, {ms:.4f} ms per layer")
+    baseline = None
+    if args.cpu_baseline:
+        baseline = cpu_attention_baseline(spans, query, key, value, q_heads, shape.head_dim,
+                                          args.cpu_attention_gflop)
     print(json.dumps({
         "metric": "sparse repair attention TFLOP/s (bf16 MFMA, one layer)",
         "value": round(achieved, 2),
@@ -341,7 +347,57 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(achieved / 2500.0, 4),
                      "kv_bytes_gathered": kv_bytes,
                      "kv_gather_GBps": round(kv_bytes / (ms / 1e3) / 1e9, 1)},
+        "cpu_baseline": baseline,
     }), flush=True)
+
+
+def cpu_attention_baseline(spans, query, key, value, q_heads: int, head_dim: int, gflop_budget: float) -> dict:
+    """The reference's restated repair attention (gqa_attention over the logical
+    causal mask, tests/pic/reference/attention_reference.py:8-48) in fp32 torch
+    on the host cores, over the first spans of the workload up to a flop budget."""
+
+    import math
+
+    import numpy as np
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kv_heads = key.shape[1]
+    group = q_heads // kv_heads
+    scale = 1.0 / math.sqrt(head_dim)
+    jobs, flops, cursor = [], 0, 0
+    for slots, start, end in spans:
+        n = end - start
+        if flops and flops + 4 * head_dim * q_heads * n * (start + end + 1) // 2 > gflop_budget * 1e9:
+            break
+        rows = slots[:end]
+        jobs.append((query[cursor : cursor + n].float().cpu(), key[rows].float().cpu(),
+                     value[rows].float().cpu(), start, end))
+        flops += 4 * head_dim * q_heads * n * (start + end + 1) // 2
+        cursor += n
+
+    def run() -> None:
+        for q, k, v, start, end in jobs:
+            positions = torch.arange(start, end)[:, None]
+            visible = torch.arange(end)[None, :] <= positions                       # [n, end]
+            kh = k.repeat_interleave(group, dim=1).permute(1, 2, 0).contiguous()    # [hq, d, end]
+            vh = v.repeat_interleave(group, dim=1).permute(1, 0, 2).contiguous()    # [hq, end, d]
+            scores = torch.bmm(q.permute(1, 0, 2).contiguous(), kh) * scale        # [hq, n, end]
+            scores = scores.masked_fill(~visible[None], float("-inf"))
+            torch.bmm(torch.softmax(scores, dim=-1), vh)
+
+    run()
+    times = []
+    for _ in range(3):
+        start = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - start)
+    seconds = float(np.median(times))
+    return {"value": round(flops / seconds / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"first {len(jobs)} of {len(spans)} spans ({flops / 1e9:.1f} GFLOP): fp32 torch "
+                      f"gather -> masked softmax attention per span, {cores} threads, median of 3 after a "
+                      f"warm-up"}
 
 
 def main() -> int:
