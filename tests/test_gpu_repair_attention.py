@@ -134,6 +134,50 @@ def test_fp16_matches_oracle(gpu_device, case):
     _check(plan_spans, query, key_pool, value_pool, got, scale if scale is not None else 1.0 / math.sqrt(dim))
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_configurations(gpu_device, seed):
+    """Seeded random shapes: GQA group, head dim, dtype, slot dtype, several
+    requests and spans (partial tiles, seams near chunk edges), chunk length,
+    scale and a few invalid slots; checked against the fp64 oracle."""
+
+    rng = np.random.default_rng(1000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 5, 7, 8]))
+    hq = hkv * group
+    dim = int(rng.choice([64, 128]))
+    dtype = torch.float16 if rng.random() < 0.4 else torch.bfloat16
+    pool = int(rng.integers(2048, 8192))
+    split = int(rng.choice([0, 64, 128, 512, 1024]))
+    scale = float(rng.choice([1.0 / math.sqrt(dim), 0.5, 1.0]))
+    generator = torch.Generator(device=gpu_device).manual_seed(seed)
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=dtype)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=dtype)
+    order = torch.randperm(pool, generator=generator, device=gpu_device)
+    spans, cursor = [], 0
+    for _ in range(int(rng.integers(1, 4))):
+        length = min(int(rng.integers(20, 3000)), pool - cursor)
+        if length < 20:
+            break
+        slots = order[cursor : cursor + length].clone()
+        cursor += length
+        if rng.random() < 0.5:
+            slots = slots.to(torch.int32)
+        if rng.random() < 0.3:
+            slots[int(rng.integers(0, length))] = -1
+        for _ in range(int(rng.integers(1, 4))):
+            end = int(rng.integers(1, length + 1))
+            start = max(0, end - int(rng.integers(1, 40)))
+            spans.append((slots, start, end))
+    report(f"seed {seed}: hq={hq} hkv={hkv} d={dim} {dtype} split={split} scale={scale:.3f} "
+           f"spans={[(s, e) for _, s, e in spans]}")
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, split_tokens=split,
+                               validate=False)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device, dtype=dtype)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, scale)
+
+
 def test_dtype_checks_follow_the_reference(gpu_device):
     slots = torch.arange(64, device=gpu_device)
     plan = RepairAttentionPlan([(slots, 10, 26)], num_q_heads=8, num_kv_heads=2, head_dim=64)
