@@ -261,7 +261,7 @@ class PreparedLink:
                  groups: list[tuple[list[int], RotarySpec]], boundary_repair_aware: bool,
                  compact_repair_rows: bool, num_warps: Optional[int], layers_per_wave: int,
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
-                 layer_groups_per_block: int = 0) -> None:
+                 layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None) -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -283,7 +283,16 @@ class PreparedLink:
         self.repair_destination_slots = built.repair_destination_slots
         self.linked_token_count = token_count - plan.repair_count
         self._links: list[kv_link.PreparedKVLink] = []
+        self._kernel_maps: list[torch.Tensor] = []
         index_of = {layer: i for i, layer in enumerate(layers)}
+        # A batch of requests often reads the same catalogue blocks: with the
+        # rotated rows in source-slot order, repeated sources are read close
+        # together and hit in cache (c3: 6.2 -> 7.2 TB/s).  The link's result
+        # does not depend on the order (every destination is written once);
+        # the identity rows stay first, and `device_maps` keeps plan order.
+        if order_by_source is None:
+            order_by_source = maps.request_count > 1
+        self.order_by_source = bool(order_by_source)
         # One launch per source: set 0 reads the pool, set 1 the snapshot arena.
         for source_set in (0, 1):
             device_maps = built.maps[source_set]
@@ -292,6 +301,12 @@ class PreparedLink:
             source_arena = arena if source_set == 1 else None
             prefix = plan.set_prefix[source_set]
             mask = built.masks[source_set] if plan.set_repair_rows[source_set] else None
+            if self.order_by_source and device_maps.shape[1] - prefix > 1:
+                order = torch.argsort(device_maps[0, prefix:], stable=True) + prefix
+                device_maps = torch.cat([device_maps[:, :prefix], device_maps[:, order]], dim=1)
+                if mask is not None:
+                    mask = torch.cat([mask[:prefix], mask[order]])
+                self._kernel_maps.append(device_maps)
             for group_layers, rotary in groups:
                 indices = [index_of[layer] for layer in group_layers]
                 self._links.append(kv_link.PreparedKVLink(
@@ -499,14 +514,16 @@ class KVLinkExecutor:
 
     def prepare_links(self, pool: Any, requests: Sequence[tuple[torch.Tensor, Mapping[str, Any]]], *,
                       boundary_repair_aware: Optional[bool] = None, compact_repair_rows: bool = True,
-                      validate_indices: bool = False) -> PreparedLink:
+                      validate_indices: bool = False, order_by_source: Optional[bool] = None) -> PreparedLink:
         """Several requests' links as one prepared link: one map-builder call and
         one link launch per source for the whole batch.  ``requests`` holds
         (destination_slots, link_plan) pairs; the result equals linking them one
         by one (destinations of different requests must be distinct).  Every
         request's identity block heads its set's maps, so it is copied
         unrotated as in a single link; the repair rows of the write-back are
-        request after request, each in plan order."""
+        request after request, each in plan order.  ``order_by_source``
+        (default: on for more than one request) has the kernel visit the
+        rotated rows in source-slot order."""
 
         started = time.perf_counter()
         if not requests:
@@ -522,7 +539,7 @@ class KVLinkExecutor:
             boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
-            layer_groups_per_block=self.layer_groups_per_block,
+            layer_groups_per_block=self.layer_groups_per_block, order_by_source=order_by_source,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared

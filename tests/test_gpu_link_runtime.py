@@ -233,11 +233,13 @@ def test_prepared_link_replays_in_a_hip_graph(gpu_device):
             assert np.array_equal(a, b), f"replay {replay}"
 
 
-def test_batched_link_equals_request_by_request_links(gpu_device):
+@pytest.mark.parametrize("order_by_source", [True, False])
+def test_batched_link_equals_request_by_request_links(gpu_device, order_by_source):
     """prepare_links over several requests -- identity first blocks, a request
     behind a chat prefix, a block compiled behind a prefix, clone blocks in
     the snapshot arena, shared blocks, repair rows -- leaves the pool
-    bit-identical to linking and repairing each request alone."""
+    bit-identical to linking and repairing each request alone, whether the
+    kernel visits the rows in plan order or in source-slot order."""
 
     from legolink_amd.link_runtime import SnapshotArena
 
@@ -285,7 +287,8 @@ def test_batched_link_equals_request_by_request_links(gpu_device):
         requests.append((destination, plan))
     report(f"batched link: {len(requests)} requests, {cursor} slots used")
 
-    batched = executor.prepare_links(pool_a, requests, boundary_repair_aware=True)
+    batched = executor.prepare_links(pool_a, requests, boundary_repair_aware=True, order_by_source=order_by_source)
+    assert batched.order_by_source == order_by_source
     batched.launch()
     rows = int(batched.repair_offsets.size)
     repaired_k = torch.randn(layers, rows, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
