@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 6
+#define LL_ABI_VERSION 7
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -284,8 +284,11 @@ typedef struct ll_link_maps_args {
  * Slots outside [0, num_slots) are invisible (never read).
  *
  * Two phases, like the reference's plan/run wrapper:
- *   ll_repair_attention_plan (host only) cuts the rows into 16-query tiles,
- *   groups consecutive tiles of one request (same kv_offset) into work items
+ *   ll_repair_attention_plan (host only) cuts the rows into 16-query tiles
+ *   (consecutive rows of one request -- contiguous query_index, same
+ *   kv_offset -- share a tile, so short repair spans fill it; rows must not
+ *   overlap), writes every query's logical position into the positions
+ *   table, groups consecutive tiles of one request into work items
  *   that share every staged K/V tile (as many tiles as 16 waves hold: 2 for 7
  *   or 8 query heads per KV head), splits long KV ranges into chunks of
  *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
@@ -315,6 +318,7 @@ typedef struct ll_repair_attention_plan_info {
   int64_t num_combine;             /* int32 [num_combine, 4] combine items */
   int64_t workspace_items;         /* partial results (see ll_repair_attention_args.workspace) */
   int64_t split_tokens;            /* KV tokens per work item (the plan's choice when 0 was asked) */
+  int64_t num_queries;             /* entries of the positions table: max(query_index + query_count) */
 } ll_repair_attention_plan_info;
 
 typedef struct ll_repair_attention_args {
@@ -337,6 +341,7 @@ typedef struct ll_repair_attention_args {
   int64_t num_items;
   const int32_t *combine;          /* device copy of the plan's combine items, or NULL */
   int64_t num_combine;
+  const int32_t *query_positions;  /* device copy of the plan's positions table [num_queries] */
   float *workspace;                /* device fp32 [workspace_items, num_q_heads, 16, head_dim + 2] */
   int64_t workspace_items;
 } ll_repair_attention_args;
@@ -344,6 +349,7 @@ typedef struct ll_repair_attention_args {
 int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
                              int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
                              int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
+                             int32_t *positions, int64_t positions_capacity,
                              ll_repair_attention_plan_info *info);
 int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream);
 

@@ -62,7 +62,10 @@ constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
 constexpr int kTile = 64;     // KV tokens per LDS tile
 constexpr int kMaxTiles = 4;    // 16-query tiles per work item
-constexpr int kItemInts = 24;   // kv_offset, kv_begin, kv_end, tiles, 4 x (q_index, q_pos, q_count, partial), pad
+// kv_offset, kv_begin, kv_end, tiles, then per tile (first query, lowest
+// position, query count (0: absent), partial slot (-1: none), key end).
+constexpr int kItemInts = 24;
+constexpr int kTileInts = 5;
 constexpr int kCombineInts = 4;
 constexpr int kMaxGroup = 8;  // query heads per KV head
 constexpr int kMaxWaves = 16;  // waves per workgroup: (query tile, query head) pairs = waves per workgroup
@@ -83,6 +86,7 @@ struct AttnParams {
   const void *slots;
   const int *items;
   const int *combine;
+  const int *positions;  // logical position of every query
   float *ws;
   long long num_queries;
   long long num_slots;
@@ -166,20 +170,22 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
   // Wave w computes query head hk * G + w % G for the item's query tile w / G.
   const int tile = wave / p.group;
   const int hq = hk * p.group + wave % p.group;
-  const int *entry = it + 4 + 4 * (tile < kMaxTiles ? tile : 0);
-  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3];
+  const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
+  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
   const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
                         static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
-                        (partial == -1 || (partial >= 0 && partial < p.ws_items));
+                        needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
   const bool q_ok = computes && c < q_count;
-  const int my_pos = q_pos + c;
-  // The wave's keys end where its last query's do; the workgroup loads up to the
-  // furthest of its tiles.
-  const int kv_stop = computes ? min(kv_end, q_pos + q_count) : kv_begin;
+  // A tile's queries are consecutive rows of one request, not always
+  // consecutive positions (several short repair spans share a tile).
+  const int my_pos = q_ok ? p.positions[q_index + c] : 0;
+  // The wave's keys end where its furthest query's do; the workgroup loads up
+  // to the furthest of its tiles.
+  const int kv_stop = computes ? min(kv_end, needed) : kv_begin;
   int load_stop = kv_begin;
   for (int t = 0; t < n_tiles; ++t) {
-    const int *e = it + 4 + 4 * t;
-    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[1] + e[2]));
+    const int *e = it + 4 + kTileInts * t;
+    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
   }
 
   // The wave's queries as the B operand of S^T = K Q^T: query c, dims 32 ks + 8 g + e.
@@ -478,18 +484,20 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int c = lane % 16;
   const int tile = wave / p.group;
   const int hq = hk * p.group + wave % p.group;
-  const int *entry = it + 4 + 4 * (tile < kMaxTiles ? tile : 0);
-  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3];
+  const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
+  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
   const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
                         static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
-                        (partial == -1 || (partial >= 0 && partial < p.ws_items));
+                        needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
   const bool q_ok = computes && c < q_count;
-  const int my_pos = q_pos + c;
-  const int kv_stop = computes ? min(kv_end, q_pos + q_count) : kv_begin;
+  // A tile's queries are consecutive rows of one request, not always
+  // consecutive positions (several short repair spans share a tile).
+  const int my_pos = q_ok ? p.positions[q_index + c] : 0;
+  const int kv_stop = computes ? min(kv_end, needed) : kv_begin;
   int load_stop = kv_begin;
   for (int t = 0; t < n_tiles; ++t) {
-    const int *e = it + 4 + 4 * t;
-    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[1] + e[2]));
+    const int *e = it + 4 + kTileInts * t;
+    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
   }
   const int range = load_stop - kv_begin;
   const int tiles = (range + kTile - 1) / kTile;
@@ -832,6 +840,7 @@ int64_t ll_repair_attention_args_size(void) {
 int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
                              int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
                              int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
+                             int32_t *positions, int64_t positions_capacity,
                              ll_repair_attention_plan_info *info) {
   if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
   if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
@@ -846,11 +855,13 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
                 kTile, kDmaMaxRange);
   constexpr int64_t kIntMax = 0x7fffffff;
   const int per_item = tiles_per_item(static_cast<int>(num_q_heads / num_kv_heads));
-  // 16-query tiles in row order; consecutive tiles of one request (same kv_offset)
-  // share work items, up to per_item at a time.
+  // 16-query tiles in row order.  Consecutive rows of one request (the next
+  // row's queries follow the last one's, same kv_offset) share a tile, so
+  // short repair spans fill it; a tile records its lowest position and its
+  // key end (highest position + 1).  Consecutive tiles of one request share
+  // work items, up to per_item at a time.
   struct Tile { int64_t q_index, pos, count, kv_offset, needed; };
-  int64_t work = 0;
-  int64_t n_tiles = 0;
+  int64_t num_queries = 0;
   for (int64_t r = 0; r < num_rows; ++r) {
     const ll_repair_row &row = rows[r];
     if (row.query_count < 1 || row.query_start < 0 || row.query_index < 0 || row.kv_offset < 0 ||
@@ -858,18 +869,34 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
         row.kv_offset + row.query_start + row.query_count > kIntMax)
       return fail(LL_ERR_INVALID_ARGUMENT, "row %lld: counts, positions and offsets must be >= 0 "
                   "(query_count >= 1) and fit in int32", static_cast<long long>(r));
-    n_tiles += (row.query_count + kQueries - 1) / kQueries;
+    if (row.query_index + row.query_count > num_queries) num_queries = row.query_index + row.query_count;
   }
-  Tile *tiles = n_tiles ? new Tile[n_tiles] : nullptr;
-  int64_t k = 0;
+  if (positions != nullptr && positions_capacity < num_queries)
+    return fail(LL_ERR_INVALID_ARGUMENT, "positions_capacity %lld is below the %lld queries",
+                static_cast<long long>(positions_capacity), static_cast<long long>(num_queries));
+  std::vector<Tile> tiles;
+  int64_t fill = 0;  // queries in the open tile
   for (int64_t r = 0; r < num_rows; ++r) {
     const ll_repair_row &row = rows[r];
-    for (int64_t t = 0; t < row.query_count; t += kQueries) {
-      const int64_t count = row.query_count - t < kQueries ? row.query_count - t : kQueries;
-      tiles[k++] = Tile{row.query_index + t, row.query_start + t, count, row.kv_offset,
-                        row.query_start + t + count};
+    if (positions != nullptr)
+      for (int64_t i = 0; i < row.query_count; ++i)
+        positions[row.query_index + i] = static_cast<int32_t>(row.query_start + i);
+    const bool continues = fill > 0 && row.kv_offset == tiles.back().kv_offset &&
+                           row.query_index == tiles.back().q_index + tiles.back().count;
+    if (!continues) fill = 0;
+    for (int64_t i = 0; i < row.query_count;) {
+      if (fill == 0) tiles.push_back(Tile{row.query_index + i, kIntMax, 0, row.kv_offset, 0});
+      Tile &tile = tiles.back();
+      const int64_t take = row.query_count - i < kQueries - fill ? row.query_count - i : kQueries - fill;
+      if (row.query_start + i < tile.pos) tile.pos = row.query_start + i;
+      if (row.query_start + i + take > tile.needed) tile.needed = row.query_start + i + take;
+      tile.count += take;
+      fill = fill + take == kQueries ? 0 : fill + take;
+      i += take;
     }
   }
+  const int64_t n_tiles = static_cast<int64_t>(tiles.size());
+  int64_t work = 0;
   // Groups of up to per_item consecutive tiles of one request.
   auto group_end = [&](int64_t first) {
     int64_t last = first + 1;
@@ -956,18 +983,18 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
         it[2] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
         it[3] = static_cast<int32_t>(last - first);
         for (int64_t t = first; t < last; ++t) {
-          int32_t *e = it + 4 + 4 * (t - first);
+          int32_t *e = it + 4 + kTileInts * (t - first);
           e[0] = static_cast<int32_t>(tiles[t].q_index);
           e[1] = static_cast<int32_t>(tiles[t].pos);
           const bool present = s < chunks[t - first];  // this chunk holds keys the tile sees
           e[2] = present ? static_cast<int32_t>(tiles[t].count) : 0;
           e[3] = !present || chunks[t - first] == 1 ? -1 : static_cast<int32_t>(base[t - first] + s);
+          e[4] = static_cast<int32_t>(tiles[t].needed);
         }
       }
       ++n_items;
     }
   }
-  delete[] tiles;
   if (rc != LL_OK) return rc;
   if (n_items > kIntMax || n_partial > kIntMax)
     return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
@@ -993,6 +1020,7 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   info->num_combine = n_combine;
   info->workspace_items = n_partial;
   info->split_tokens = split;
+  info->num_queries = num_queries;
   return LL_OK;
 }
 
@@ -1020,8 +1048,9 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->num_items > 0x7fffffff || a->num_combine > 0x7fffffff)
     return fail(LL_ERR_INVALID_ARGUMENT, "too many items");
   if (a->query == nullptr || a->output == nullptr || a->key_buffer == nullptr ||
-      a->value_buffer == nullptr || a->kv_slots == nullptr || a->items == nullptr)
-    return fail(LL_ERR_INVALID_ARGUMENT, "query/output/key/value/kv_slots/items pointer is NULL");
+      a->value_buffer == nullptr || a->kv_slots == nullptr || a->items == nullptr ||
+      a->query_positions == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "query/output/key/value/kv_slots/items/query_positions pointer is NULL");
   if (a->kv_slots_dtype != LL_DTYPE_INT32 && a->kv_slots_dtype != LL_DTYPE_INT64)
     return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "kv_slots must be int32 or int64");
   if (a->num_combine > 0 && (a->combine == nullptr || a->workspace == nullptr || a->workspace_items < 1))
@@ -1040,6 +1069,7 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   p.slots = a->kv_slots;
   p.items = a->items;
   p.combine = a->combine;
+  p.positions = a->query_positions;
   p.ws = a->workspace;
   p.num_queries = a->num_queries;
   p.num_slots = a->num_slots;

@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -187,6 +187,7 @@ class RepairPlanInfo(ctypes.Structure):
         ("num_combine", _i64),
         ("workspace_items", _i64),
         ("split_tokens", _i64),
+        ("num_queries", _i64),
     ]
 
 
@@ -213,12 +214,14 @@ class RepairAttentionArgs(ctypes.Structure):
         ("num_items", _i64),
         ("combine", _ptr),
         ("num_combine", _i64),
+        ("query_positions", _ptr),
         ("workspace", _ptr),
         ("workspace_items", _i64),
     ]
 
 
 REPAIR_ITEM_INTS = 24
+REPAIR_TILE_INTS = 5   # per tile of an item: first query, lowest position, count, partial, key end
 REPAIR_COMBINE_INTS = 4
 
 
@@ -295,7 +298,7 @@ def load_library() -> ctypes.CDLL:
         lib.ll_link_maps_args_size.argtypes = []
         lib.ll_link_maps_args_size.restype = _i64
         lib.ll_repair_attention_plan.argtypes = [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64,
-                                                 ctypes.POINTER(RepairPlanInfo)]
+                                                 _ptr, _i64, ctypes.POINTER(RepairPlanInfo)]
         lib.ll_repair_attention_plan.restype = ctypes.c_int
         lib.ll_repair_attention.argtypes = [ctypes.POINTER(RepairAttentionArgs), _ptr]
         lib.ll_repair_attention.restype = ctypes.c_int
@@ -366,7 +369,8 @@ def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
 
 
 def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_tokens: int = 0):
-    """Host planning: returns (items int32 [n, 24], combine int32 [m, 4], info)."""
+    """Host planning: returns (items int32 [n, 24], combine int32 [m, 4],
+    positions int32 [num_queries], info)."""
 
     import numpy as np
 
@@ -375,15 +379,17 @@ def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_token
     info = RepairPlanInfo()
     rows_ptr = rows.ctypes.data if rows.size else None
     _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
-                                        int(split_tokens), None, 0, None, 0, ctypes.byref(info)))
+                                        int(split_tokens), None, 0, None, 0, None, 0, ctypes.byref(info)))
     items = np.zeros((info.num_items, REPAIR_ITEM_INTS), dtype=np.int32)
     combine = np.zeros((info.num_combine, REPAIR_COMBINE_INTS), dtype=np.int32)
+    positions = np.zeros(info.num_queries, dtype=np.int32)
     _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
                                         int(split_tokens), items.ctypes.data if items.size else None,
                                         info.num_items,
                                         combine.ctypes.data if combine.size else None, info.num_combine,
+                                        positions.ctypes.data if positions.size else None, positions.size,
                                         ctypes.byref(info)))
-    return items, combine, info
+    return items, combine, positions, info
 
 
 def repair_attention(args: RepairAttentionArgs, stream: int) -> None:

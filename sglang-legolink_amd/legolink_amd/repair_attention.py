@@ -95,14 +95,15 @@ class RepairAttentionPlan:
                 raise SparseRepairAttentionError("slot_ids contains invalid KV slots")
         self.kv_slots = table
         self.rows = rows
-        items, combine, info = _native.repair_attention_plan(rows, self.num_q_heads, self.num_kv_heads,
-                                                             split_tokens)
+        items, combine, positions, info = _native.repair_attention_plan(rows, self.num_q_heads,
+                                                                        self.num_kv_heads, split_tokens)
         self.info = {"num_items": int(info.num_items), "num_combine": int(info.num_combine),
                      "workspace_items": int(info.workspace_items), "split_tokens": int(info.split_tokens)}
-        packed = np.concatenate((items.reshape(-1), combine.reshape(-1))).astype(np.int32)
-        self._tables = torch.from_numpy(packed).to(device)
+        packed = np.concatenate((items.reshape(-1), combine.reshape(-1), positions)).astype(np.int32)
+        self._tables = torch.from_numpy(packed).to(device)  # one copy to the device
         self.items = self._tables[: items.size]
-        self.combine = self._tables[items.size :]
+        self.combine = self._tables[items.size : items.size + combine.size]
+        self.positions = self._tables[items.size + combine.size :]
         per_item = self.num_q_heads * (16 * self.head_dim + 32)
         self.workspace = (torch.empty(info.workspace_items * per_item, dtype=torch.float32, device=device)
                           if info.workspace_items else None)
@@ -171,6 +172,7 @@ class RepairAttentionPlan:
         args.num_items = self.info["num_items"]
         args.combine = self.combine.data_ptr() if self.info["num_combine"] else None
         args.num_combine = self.info["num_combine"]
+        args.query_positions = self.positions.data_ptr()
         args.workspace = self.workspace.data_ptr() if self.workspace is not None else None
         args.workspace_items = self.info["workspace_items"]
         if stream is None:

@@ -123,42 +123,60 @@ def _plan(rows, q_heads=28, kv_heads=4, split=0):
 
 @pytest.mark.parametrize("split,q_heads,kv_heads", [(0, 28, 4), (64, 28, 4), (512, 28, 4), (128, 8, 8),
                                                      (256, 8, 2)])
-def test_plan_covers_every_query_tile_and_key_range_once(split, q_heads, kv_heads):
+def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
     rng = np.random.default_rng(split + q_heads)
     rows, cursor = [], 0
-    for _ in range(20):
-        count = int(rng.integers(1, 70))
+    for _ in range(30):
+        count = int(rng.integers(1, 40))
         start = int(rng.integers(0, 3000))
         rows.append((cursor, start, count, int(rng.integers(0, 3)) * 5000))  # three requests
         cursor += count
-    items, combine, info = _plan(rows, q_heads, kv_heads, split)
+    items, combine, positions, info = _plan(rows, q_heads, kv_heads, split)
+    T = _native.REPAIR_TILE_INTS
     per_item = max(1, min(4, 16 // (q_heads // kv_heads)))
     assert info.split_tokens % 64 == 0 and (split == 0 or info.split_tokens == split)
+    # The positions table holds every query's logical position.
+    position, request = np.zeros(cursor, np.int64), np.zeros(cursor, np.int64)
+    for q_index, start, count, kv_off in rows:
+        position[q_index : q_index + count] = np.arange(start, start + count)
+        request[q_index : q_index + count] = kv_off
+    assert info.num_queries == cursor and positions.tolist() == position.tolist()
+    # Every item entry: its tile's keys, a chunk of them, and its partial slot.
     covered = {}
     for item in items.tolist():
         kv_off, kv_begin, kv_end, n_tiles = item[:4]
         assert 1 <= n_tiles <= per_item and kv_begin % 64 == 0 and kv_begin < kv_end
         furthest = 0
         for t in range(n_tiles):
-            q_index, q_pos, q_count, partial = item[4 + 4 * t : 8 + 4 * t]
-            key = (q_index, q_pos, kv_off)
+            q_index, low, q_count, partial, needed = item[4 + T * t : 4 + T * (t + 1)]
             if q_count == 0:
                 assert partial == -1
                 continue
             assert 1 <= q_count <= 16
-            furthest = max(furthest, q_pos + q_count)
-            covered.setdefault(key, []).append((kv_begin, min(kv_end, q_pos + q_count), partial, q_count))
+            queries = np.arange(q_index, q_index + q_count)
+            assert (request[queries] == kv_off).all()          # one request per tile
+            assert low == position[queries].min() and needed == position[queries].max() + 1
+            furthest = max(furthest, needed)
+            covered.setdefault((q_index, q_count), []).append((kv_begin, min(kv_end, needed), partial, needed))
         assert kv_end <= furthest  # an item never loads keys past its last present tile's
-    tiles = {}
+    # Tiles partition the queries; consecutive rows of a request share tiles.
+    seen = np.zeros(cursor, np.int64)
+    for q_index, q_count in covered:
+        seen[q_index : q_index + q_count] += 1
+    assert (seen == 1).all()
+    runs, expected_tiles = [], 0
     for q_index, start, count, kv_off in rows:
-        for t in range(0, count, 16):
-            tiles[(q_index + t, start + t, kv_off)] = min(16, count - t)
-    assert set(covered) == set(tiles)
+        if runs and runs[-1][0] == kv_off:
+            runs[-1][1] += count
+        else:
+            runs.append([kv_off, count])
+    assert len(covered) == sum((n + 15) // 16 for _, n in runs)
     partials = set()
     combine_rows = [tuple(r) for r in combine.tolist()]
-    for key, ranges in covered.items():
+    for (q_index, q_count), ranges in covered.items():
         ranges.sort()
-        assert ranges[0][0] == 0 and ranges[-1][1] == key[1] + tiles[key]
+        needed = ranges[0][3]
+        assert ranges[0][0] == 0 and ranges[-1][1] == needed
         assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
         if len(ranges) == 1:
             assert ranges[0][2] == -1
@@ -166,8 +184,21 @@ def test_plan_covers_every_query_tile_and_key_range_once(split, q_heads, kv_head
             ids = [r[2] for r in ranges]
             assert ids == list(range(ids[0], ids[0] + len(ids)))
             partials.update(ids)
-            assert (key[0], tiles[key], ids[0], len(ids)) in combine_rows
+            assert (q_index, q_count, ids[0], len(ids)) in combine_rows
     assert len(partials) == info.workspace_items == combine[:, 3].sum()
+
+
+def test_plan_packs_short_spans_of_one_request_into_tiles():
+    # Four 8-query spans of one request: two full tiles; a span of another
+    # request, or a gap in the query rows, starts a new tile.
+    rows = [(0, 100, 8, 0), (8, 300, 8, 0), (16, 500, 8, 0), (24, 700, 8, 0), (32, 40, 8, 9000),
+            (48, 60, 4, 9000)]
+    items, combine, positions, info = _plan(rows, 28, 4, 4096)
+    T = _native.REPAIR_TILE_INTS
+    tiles = sorted(tuple(item[4 + T * t : 4 + T * (t + 1)]) for item in items.tolist() for t in range(item[3])
+                   if item[4 + T * t + 2])
+    assert tiles == [(0, 100, 16, -1, 308), (16, 500, 16, -1, 708), (32, 40, 8, -1, 48), (48, 60, 4, -1, 64)]
+    assert positions[:16].tolist() == list(range(100, 108)) + list(range(300, 308))
 
 
 def test_plan_rejects_bad_rows():
@@ -197,6 +228,7 @@ def test_attention_entry_validates_before_any_launch():
         a.softmax_scale = 0.088
         a.kv_slots, a.kv_slots_dtype, a.kv_slots_len = 0x5000, _native.DTYPE_INT64, 64
         a.items, a.num_items = 0x6000, 1
+        a.query_positions = 0x7000
         for name, value in overrides.items():
             setattr(a, name, value)
         return a
@@ -208,6 +240,7 @@ def test_attention_entry_validates_before_any_launch():
         (dict(kv_dtype=_native.DTYPE_FLOAT32), "fp16_or_bf16_required"),
         (dict(kv_slots_dtype=_native.DTYPE_FLOAT32), "integer_token_maps_required"),
         (dict(query=None), "invalid_argument"),
+        (dict(query_positions=None), "invalid_argument"),
         (dict(softmax_scale=float("nan")), "invalid_argument"),
         (dict(num_combine=1), "invalid_argument"),             # split items without a workspace
         (dict(query=0x1008), "invalid_argument"),              # misaligned
