@@ -261,6 +261,55 @@ def test_one_plan_serves_every_layer(gpu_device):
         _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
 
 
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_full_size_workload_sampled(gpu_device, name):
+    """The benchmark workloads at full size (c5: 511 spans over a 32,768-token
+    request, 4,096-key chunks and their combine; c3: 448 eight-query spans of
+    64 requests sharing tiles), every output row of a random sample checked
+    against fp32 torch attention on the device, within the same bound."""
+
+    from legolink_amd.link_plan import contiguous_ranges
+    from legolink_amd.workloads import make_workload
+
+    workload = make_workload(name)
+    shape = workload.shape
+    hq = 28
+    generator = torch.Generator(device=gpu_device).manual_seed(7)
+    key_pool = _bf16((workload.num_slots, shape.kv_heads, shape.head_dim), generator, gpu_device)
+    value_pool = _bf16((workload.num_slots, shape.kv_heads, shape.head_dim), generator, gpu_device)
+    spans = []
+    for destination, plan in workload.link_requests()[1]:
+        slots = torch.from_numpy(destination).to(gpu_device)
+        spans += [(slots, int(s), int(e)) for s, e in contiguous_ranges(plan["imp_indices"])]
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=shape.kv_heads, head_dim=shape.head_dim,
+                               pool_size=workload.num_slots)
+    report(f"{name}: {len(spans)} spans, {plan.num_queries} queries, plan {plan.info}")
+    query = _bf16((plan.num_queries, hq, shape.head_dim), generator, gpu_device)
+    scale = 1.0 / math.sqrt(shape.head_dim)
+    got = plan.run(query, key_pool, value_pool, scale=scale).float()
+    torch.cuda.synchronize(gpu_device)
+    rng = np.random.default_rng(3)
+    starts = np.cumsum([0] + [e - s for _, s, e in spans])
+    group = hq // shape.kv_heads
+    worst = 0.0
+    for index in rng.choice(len(spans), size=24, replace=False):
+        slots, start, end = spans[index]
+        row = int(rng.integers(0, end - start))
+        q = query[starts[index] + row].float()                                  # [hq, d]
+        keys = key_pool[slots[: start + row + 1]].float()                       # [n, hkv, d]
+        values = value_pool[slots[: start + row + 1]].float()
+        keys = keys.repeat_interleave(group, dim=1).permute(1, 0, 2)            # [hq, n, d]
+        values = values.repeat_interleave(group, dim=1).permute(1, 0, 2)
+        weights = torch.softmax((keys @ q[:, :, None])[:, :, 0] * scale, dim=-1)  # [hq, n]
+        want = (weights[:, None, :] @ values)[:, 0, :]
+        magnitude = (weights[:, None, :] @ values.abs())[:, 0, :]
+        bound = 2.0 ** -7 * (magnitude + want.abs()) + 1e-5
+        err = (got[starts[index] + row] - want).abs()
+        worst = max(worst, float((err / bound).max()))
+        assert bool((err <= bound).all()), f"span {index} row {row}: max err {float(err.max()):.3g}"
+    report(f"largest error / bound vs fp32: {worst:.3f}")
+
+
 def test_span_checks_follow_the_reference(gpu_device):
     slots = torch.arange(10, device=gpu_device)
     for bad, message in [((slots.view(2, 5), 1, 3), "rank 1"), ((slots, 3, 3), "invalid repair range"),
