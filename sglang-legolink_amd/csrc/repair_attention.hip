@@ -1034,7 +1034,7 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64 or 128");
   if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
-      a->num_q_heads / a->num_kv_heads > kMaxGroup || a->num_kv_heads > 65535)
+      a->num_q_heads / a->num_kv_heads > kMaxGroup || a->num_q_heads > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
                 "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
                 kMaxGroup);
