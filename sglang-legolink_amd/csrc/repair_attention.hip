@@ -502,8 +502,8 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int range = load_stop - kv_begin;
   const int tiles = (range + kTile - 1) / kTile;
 
-  // Slots of the item's range (-1: out of range or invalid), and per tile the
-  // number of such tokens.
+  // Slots of the item's range (-1: out of range or invalid), and per tile a
+  // mask of its tokens with a valid slot.
   for (int i = tid; i < kRangeTiles; i += kDmaThreads) tile_valid[i] = 0ull;
   __syncthreads();
   for (int i = tid; i < tiles * kTile; i += kDmaThreads) {
@@ -540,10 +540,10 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int gather_token = chunk_index / kChunksPerRow;
   const int k_chunk = (chunk_index % kChunksPerRow) ^ (gather_token % 16);
   const int v_chunk = (chunk_index % kChunksPerRow) ^ (2 * (gather_token % 8));
-  // Every wave issues exactly two loads per tile (the waits below count
-  // them): a token without a valid slot loads slot 0's row instead (gather
-  // leaves it out when the pool is empty), which the masking hides for K and
-  // the V clean-up below replaces by zeros.
+  // Every wave issues the same two loads for every tile: a token without a
+  // valid slot loads slot 0's row instead (nothing is loaded when the pool is
+  // empty), which the masking hides for K and the V clean-up below replaces
+  // by zeros.
   const bool have_slots = p.num_slots > 0;  // else every token is invalid and nothing is loaded
   auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
