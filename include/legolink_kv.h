@@ -290,7 +290,7 @@ typedef struct ll_link_maps_args {
  *   overlap), writes every query's logical position into the positions
  *   table, groups consecutive tiles of one request into work items
  *   that share every staged K/V tile (as many tiles as 16 waves hold: 2 for 7
- *   or 8 query heads per KV head), splits long KV ranges into chunks of
+ *   or 8 query heads per KV head, 1 above 8), splits long KV ranges into chunks of
  *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
  *   from a model of the device's workgroup rounds), and writes the item and
  *   combine tables; the caller copies them to the device once and reuses them
@@ -330,7 +330,7 @@ typedef struct ll_repair_attention_args {
   const void *value_buffer;        /* device kv_dtype [num_slots, num_kv_heads, head_dim] */
   int64_t num_slots;
   int64_t num_q_heads;
-  int64_t num_kv_heads;            /* divides num_q_heads, at most 8 query heads per KV head */
+  int64_t num_kv_heads;            /* divides num_q_heads (any GQA ratio; MQA: 1); num_q_heads <= 65535 */
   int64_t head_dim;                /* 64 or 128 */
   int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16: queries, K/V and output */
   double softmax_scale;

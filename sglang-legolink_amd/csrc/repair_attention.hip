@@ -6,8 +6,10 @@
 //   rows) and a KV range [kv_begin, kv_end) of logical positions; long ranges
 //   are split and the partial results merged by a combine pass.
 //   workgroup = (item, KV head); wave w computes query tile w / G for query
-//   head hk * G + w % G (G query heads share one KV head, G <= 8), so each
-//   K/V tile staged in LDS serves every query tile and head of the item.
+//   head hk * G + w % G (G query heads share one KV head), so each K/V tile
+//   staged in LDS serves every query tile and head of the item.  With more
+//   than 16 query heads per KV head, items have one tile and each KV head
+//   gets ceil(G / 16) workgroups of 16 heads.
 //
 // Per 64-token KV tile:
 //   1. gather the tile's K and V rows of this KV head into LDS by slot;
@@ -67,7 +69,6 @@ constexpr int kMaxTiles = 4;    // 16-query tiles per work item
 constexpr int kItemInts = 24;
 constexpr int kTileInts = 5;
 constexpr int kCombineInts = 4;
-constexpr int kMaxGroup = 8;  // query heads per KV head
 constexpr int kMaxWaves = 16;  // waves per workgroup: (query tile, query head) pairs = waves per workgroup
 
 int fail(int code, const char *fmt, ...) {
@@ -95,6 +96,8 @@ struct AttnParams {
   int hq;
   int hkv;
   int group;
+  int heads_per_wg;  // query heads of a KV head that one workgroup computes: min(group, 16)
+  int head_chunks;   // workgroups per (item, KV head): group / heads_per_wg, rounded up
   int slots64;
   float scale_log2;
 };
@@ -156,7 +159,8 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
-  const int hk = blockIdx.y;
+  const int hk = blockIdx.y / p.head_chunks;
+  const int head_base = (blockIdx.y % p.head_chunks) * p.heads_per_wg;
   // Items come from the planner; a malformed one is skipped whole (uniform).
   if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
       static_cast<long long>(kv_off) + kv_end > p.slots_len || hk >= p.hkv)
@@ -167,12 +171,14 @@ __global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(con
   const int lane = tid % kWave;
   const int g = lane / 16;   // lane group: k (or row) block of the MFMA operands
   const int c = lane % 16;   // query of this lane in the S^T / O^T accumulators
-  // Wave w computes query head hk * G + w % G for the item's query tile w / G.
-  const int tile = wave / p.group;
-  const int hq = hk * p.group + wave % p.group;
+  // Wave w computes query head hk * G + head_base + w % H for the item's query
+  // tile w / H, H = heads_per_wg (G itself unless G > 16).
+  const int tile = wave / p.heads_per_wg;
+  const int head = head_base + wave % p.heads_per_wg;
+  const int hq = hk * p.group + head;
   const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
   const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
-  const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
+  const bool computes = tile < n_tiles && head < p.group && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
                         static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
                         needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
   const bool q_ok = computes && c < q_count;
@@ -471,7 +477,8 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
-  const int hk = blockIdx.y;
+  const int hk = blockIdx.y / p.head_chunks;
+  const int head_base = (blockIdx.y % p.head_chunks) * p.heads_per_wg;
   if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
       kv_end - kv_begin > kDmaMaxRange || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
       hk >= p.hkv)
@@ -482,11 +489,12 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int lane = tid % kWave;
   const int g = lane / 16;
   const int c = lane % 16;
-  const int tile = wave / p.group;
-  const int hq = hk * p.group + wave % p.group;
+  const int tile = wave / p.heads_per_wg;
+  const int head = head_base + wave % p.heads_per_wg;
+  const int hq = hk * p.group + head;
   const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
   const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
-  const bool computes = tile < n_tiles && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
+  const bool computes = tile < n_tiles && head < p.group && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
                         static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
                         needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
   const bool q_ok = computes && c < q_count;
@@ -845,11 +853,8 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
   if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
     return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
-  if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0 ||
-      num_q_heads / num_kv_heads > kMaxGroup)
-    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
-                "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
-                kMaxGroup);
+  if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be a multiple of num_kv_heads");
   if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > kDmaMaxRange)
     return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
                 kTile, kDmaMaxRange);
@@ -1034,10 +1039,9 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64 or 128");
   if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
-      a->num_q_heads / a->num_kv_heads > kMaxGroup || a->num_q_heads > 65535)
+      a->num_q_heads > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
-                "num_q_heads must be a multiple of num_kv_heads, at most %d query heads per KV head",
-                kMaxGroup);
+                "num_q_heads must be a multiple of num_kv_heads, at most 65535");
   if (a->num_queries < 0 || a->num_slots < 0 || a->kv_slots_len < 0 || a->num_items < 0 ||
       a->num_combine < 0 || a->workspace_items < 0)
     return fail(LL_ERR_INVALID_ARGUMENT, "counts must be >= 0");
@@ -1078,12 +1082,16 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   p.hq = static_cast<int>(a->num_q_heads);
   p.hkv = static_cast<int>(a->num_kv_heads);
   p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
+  p.heads_per_wg = p.group < kMaxWaves ? p.group : kMaxWaves;
+  p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
   p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
   p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads));
-  const dim3 block64(static_cast<unsigned>(kWave * p.group * tiles_per_item(p.group)));
+  if (a->num_kv_heads * p.head_chunks > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
+  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
+  const dim3 block64(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
     if (f16) repair_attention_dma_kernel<F16><<<grid, dim3(kDmaThreads), 0, s>>>(p);

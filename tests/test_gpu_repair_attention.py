@@ -86,6 +86,10 @@ CASES = [
     ("group8_head_dim64", 16, 2, 64, [(30, 50), (200, 201)], 2048, 0, None),
     ("group1", 8, 8, 128, [(10, 26)], 2048, 0, None),
     ("sharp_softmax", 28, 4, 128, [(3, 40), (300, 333)], 4096, 128, 1.0),
+    # GQA ratios above 8: one tile per item; above 16, several workgroups per KV head.
+    ("group12", 24, 2, 128, [(50, 70), (400, 416)], 2048, 0, None),
+    ("mqa_group32", 32, 1, 128, [(100, 133)], 2048, 256, None),
+    ("mqa_group71_head_dim64", 71, 1, 64, [(20, 37), (900, 905)], 2048, 0, None),
 ]
 
 
@@ -142,7 +146,7 @@ def test_random_configurations(gpu_device, seed):
 
     rng = np.random.default_rng(1000 + seed)
     hkv = int(rng.choice([1, 2, 4, 8]))
-    group = int(rng.choice([1, 2, 3, 4, 5, 7, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 20]))
     hq = hkv * group
     dim = int(rng.choice([64, 128]))
     dtype = torch.float16 if rng.random() < 0.4 else torch.bfloat16

@@ -211,8 +211,9 @@ def test_plan_rejects_bad_rows():
     with pytest.raises(_native.NativeCallError, match="at most 4096"):
         _plan([(0, 5, 3, 0)], split=4160)
     with pytest.raises(_native.NativeCallError) as error:
-        _plan([(0, 5, 3, 0)], q_heads=36, kv_heads=4)  # 9 query heads per KV head
+        _plan([(0, 5, 3, 0)], q_heads=30, kv_heads=4)  # not a multiple
     assert error.value.reason == "kv_head_layout_mismatch"
+    _plan([(0, 5, 3, 0)], q_heads=71, kv_heads=1)  # any ratio, MQA included
 
 
 def test_attention_entry_validates_before_any_launch():
@@ -235,8 +236,8 @@ def test_attention_entry_validates_before_any_launch():
 
     for overrides, reason in [
         (dict(head_dim=96), "head_dimension_out_of_range"),
-        (dict(num_q_heads=36), "kv_head_layout_mismatch"),   # 9 query heads per KV head
-        (dict(num_q_heads=30), "kv_head_layout_mismatch"),
+        (dict(num_q_heads=30), "kv_head_layout_mismatch"),   # not a multiple of the KV heads
+        (dict(num_q_heads=70000, num_kv_heads=1), "kv_head_layout_mismatch"),
         (dict(kv_dtype=_native.DTYPE_FLOAT32), "fp16_or_bf16_required"),
         (dict(kv_slots_dtype=_native.DTYPE_FLOAT32), "integer_token_maps_required"),
         (dict(query=None), "invalid_argument"),
