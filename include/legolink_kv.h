@@ -331,7 +331,7 @@ typedef struct ll_repair_attention_args {
   int64_t num_slots;
   int64_t num_q_heads;
   int64_t num_kv_heads;            /* divides num_q_heads (any GQA ratio; MQA: 1); num_q_heads <= 65535 */
-  int64_t head_dim;                /* 64 or 128 */
+  int64_t head_dim;                /* 64, 128 or 256 */
   int64_t kv_dtype;                /* LL_DTYPE_BFLOAT16 or LL_DTYPE_FLOAT16: queries, K/V and output */
   double softmax_scale;
   const void *kv_slots;            /* device int32/int64 [kv_slots_len]: the requests' slot lists */

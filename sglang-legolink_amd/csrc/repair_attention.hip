@@ -144,8 +144,12 @@ __device__ inline float *partial_block(const AttnParams &p, int partial, int h) 
   return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
 }
 
+// Waves per workgroup of the register-staged kernel: head dim 256 needs twice
+// the registers per wave (256 at 8 waves per CU).
+__host__ __device__ constexpr int staged_max_waves(int d) { return d == 256 ? kMaxWaves / 2 : kMaxWaves; }
+
 template <int D, typename E>
-__global__ void __launch_bounds__(kWave * kMaxWaves) repair_attention_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_kernel(const AttnParams p) {
   typedef typename E::frag frag;
   constexpr int kSteps = D / 32;     // k-steps of S^T = K Q^T
   constexpr int kDimTiles = D / 16;  // 16-row tiles of O^T
@@ -1036,8 +1040,8 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
                 static_cast<long long>(a->struct_size), sizeof(ll_repair_attention_args));
   if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
     return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes fp16 or bf16 queries and KV");
-  if (a->head_dim != 64 && a->head_dim != 128)
-    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64 or 128");
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64, 128 or 256");
   if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
       a->num_q_heads > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
@@ -1082,7 +1086,11 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   p.hq = static_cast<int>(a->num_q_heads);
   p.hkv = static_cast<int>(a->num_kv_heads);
   p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
-  p.heads_per_wg = p.group < kMaxWaves ? p.group : kMaxWaves;
+  // A workgroup holds every (tile, head) pair of its item when the waves
+  // allow, else the heads are split over several workgroups per KV head.
+  const int max_waves = a->head_dim == 128 ? kMaxWaves : staged_max_waves(static_cast<int>(a->head_dim));
+  const int head_room = max_waves / tiles_per_item(p.group);
+  p.heads_per_wg = p.group < head_room ? p.group : head_room;
   p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
   p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
   p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
@@ -1091,14 +1099,17 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->num_kv_heads * p.head_chunks > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
-  const dim3 block64(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
+  const dim3 staged(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
     if (f16) repair_attention_dma_kernel<F16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
     else repair_attention_dma_kernel<Bf16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
+  } else if (a->head_dim == 64) {
+    if (f16) repair_attention_kernel<64, F16><<<grid, staged, 0, s>>>(p);
+    else repair_attention_kernel<64, Bf16><<<grid, staged, 0, s>>>(p);
   } else {
-    if (f16) repair_attention_kernel<64, F16><<<grid, block64, 0, s>>>(p);
-    else repair_attention_kernel<64, Bf16><<<grid, block64, 0, s>>>(p);
+    if (f16) repair_attention_kernel<256, F16><<<grid, staged, 0, s>>>(p);
+    else repair_attention_kernel<256, Bf16><<<grid, staged, 0, s>>>(p);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
@@ -1107,9 +1118,12 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
     if (a->head_dim == 128) {
       if (f16) repair_combine_kernel<128, F16><<<cgrid, dim3(256), 0, s>>>(p);
       else repair_combine_kernel<128, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
-    } else {
+    } else if (a->head_dim == 64) {
       if (f16) repair_combine_kernel<64, F16><<<cgrid, dim3(256), 0, s>>>(p);
       else repair_combine_kernel<64, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    } else {
+      if (f16) repair_combine_kernel<256, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<256, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
     }
     err = hipGetLastError();
     if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));

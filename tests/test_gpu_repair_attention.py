@@ -90,6 +90,9 @@ CASES = [
     ("group12", 24, 2, 128, [(50, 70), (400, 416)], 2048, 0, None),
     ("mqa_group32", 32, 1, 128, [(100, 133)], 2048, 256, None),
     ("mqa_group71_head_dim64", 71, 1, 64, [(20, 37), (900, 905)], 2048, 0, None),
+    # Head dim 256: at most 8 waves per workgroup, so 7 heads x 2 tiles take two workgroups.
+    ("head_dim256_group2", 8, 4, 256, [(10, 40), (600, 616)], 2048, 0, None),
+    ("head_dim256_group7_split", 28, 4, 256, [(1500, 1520)], 4096, 512, None),
 ]
 
 
@@ -114,7 +117,7 @@ def test_repair_attention_matches_oracle(gpu_device, case):
 
 
 FP16_CASES = [c for c in CASES if c[0] in ("qwen7b_one_span", "long_kv_forced_splits", "seams_auto_split",
-                                           "group8_head_dim64")]
+                                           "group8_head_dim64", "head_dim256_group7_split")]
 
 
 @pytest.mark.parametrize("case", FP16_CASES, ids=[c[0] for c in FP16_CASES])
@@ -148,7 +151,7 @@ def test_random_configurations(gpu_device, seed):
     hkv = int(rng.choice([1, 2, 4, 8]))
     group = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 20]))
     hq = hkv * group
-    dim = int(rng.choice([64, 128]))
+    dim = int(rng.choice([64, 128, 256]))
     dtype = torch.float16 if rng.random() < 0.4 else torch.bfloat16
     pool = int(rng.integers(2048, 8192))
     split = int(rng.choice([0, 64, 128, 512, 1024]))

@@ -236,6 +236,7 @@ def test_attention_entry_validates_before_any_launch():
 
     for overrides, reason in [
         (dict(head_dim=96), "head_dimension_out_of_range"),
+        (dict(head_dim=512), "head_dimension_out_of_range"),
         (dict(num_q_heads=30), "kv_head_layout_mismatch"),   # not a multiple of the KV heads
         (dict(num_q_heads=70000, num_kv_heads=1), "kv_head_layout_mismatch"),
         (dict(kv_dtype=_native.DTYPE_FLOAT32), "fp16_or_bf16_required"),
