@@ -144,6 +144,44 @@ __device__ inline float *partial_block(const AttnParams &p, int partial, int h) 
   return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
 }
 
+// Max over the four lanes of one query column (l % 16 fixed).
+// v_permlane16_swap a, b exchanges the odd 16-lane rows of a with the even
+// rows of b, v_permlane32_swap the upper half of a with the lower half of b;
+// from two copies of x they leave (x[l], x[l ^ 16]) and then
+// (y[l], y[l ^ 32]) in the lane, up to order -- the operands of xor shuffles
+// 16 and 32.  (Inline assembly: the compiler builtins lose the second result
+// when both operands hold the same value.)  The s_nop covers the wait states
+// between a VALU write of an operand and the permute.
+__device__ inline void permlane16_swap(unsigned &a, unsigned &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+__device__ inline void permlane32_swap(unsigned &a, unsigned &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// v_max_f32 straight from assembly: fmaxf would first quiet its operands
+// (which come out of inline assembly) with two more instructions.  Scores
+// reaching here are never NaN (masked ones are -inf).
+__device__ inline float max_f32(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+__device__ inline float quad_max(float x) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  permlane16_swap(a, b);
+  x = max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  a = __builtin_bit_cast(unsigned, x);
+  b = a;
+  permlane32_swap(a, b);
+  return max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
+constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score units)
+
 // Waves per workgroup of the register-staged kernel: head dim 256 needs twice
 // the registers per wave (256 at 8 waves per CU).
 __host__ __device__ constexpr int staged_max_waves(int d) { return d == 256 ? kMaxWaves / 2 : kMaxWaves; }
@@ -210,14 +248,18 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
     }
   }
 
-  float m = -INFINITY;
-  float l = 0.f;
+  // The softmax state as in repair_attention_dma_kernel: a lazily raised
+  // maximum from a finite floor, denominators from the value MFMA.
+  float m = kScoreFloor;
   f32x4 o[kDimTiles];
 #pragma unroll
   for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+  const frag ones = __builtin_bit_cast(frag, u32x4{E::kOnes, E::kOnes, E::kOnes, E::kOnes});
 
   const long long row_stride = static_cast<long long>(p.hkv) * D;  // elements per slot
   const float scale_log2 = p.scale_log2;
+  const float slack = kSlack / scale_log2;
   for (int t0 = kv_begin; t0 < load_stop; t0 += kTile) {
     __syncthreads();  // the previous tile's LDS reads are done
     if (tid == 0) tile_invalid = 0;
@@ -295,26 +337,23 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
         }
       }
     }
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-    const float m_new = fmaxf(m, tile_max);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m - m_use) * scale_log2);
-    const float bias = -m_use * scale_log2;
-    float row_sum = 0.f;
+    tile_max = quad_max(tile_max);
+    // The maximum moves only past kSlack (log2 units) above the current one.
+    const bool raise = tile_max > m + slack;
+    const float m_new = raise ? tile_max : m;
+    const float bias = -m_new * scale_log2;
     float pv[4][4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pv[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
-        row_sum += pv[n][r];
-      }
+      for (int r = 0; r < 4; ++r) pv[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
     }
-    if (!q_ok) row_sum = 0.f;
-    row_sum += __shfl_xor(row_sum, 16);
-    row_sum += __shfl_xor(row_sum, 32);
-    l = l * alpha + row_sum;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform
+      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
+    }
     m = m_new;
     // P^T as the B operand of 16x16x32 MFMAs over 32 tokens: k-step h takes the
     // accumulators of token tiles 2h and 2h + 1, so lane group g holds tokens
@@ -332,7 +371,6 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
     }
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
-      o[dt] *= alpha;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint16_t *row = &v_lds[(16 * dt + c) * kVRow + 32 * h + 4 * g];
@@ -346,8 +384,11 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
         o[dt] = E::mfma(__builtin_bit_cast(frag, bits), pb[h], o[dt]);
       }
     }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lsum = E::mfma(ones, pb[h], lsum);
   }
 
+  const float l = lsum[0];
   if (!computes) return;
   // o[dt][r] = O^T[dim 16 dt + 4 g + r][query c].
   if (partial < 0) {
@@ -427,43 +468,6 @@ __device__ inline void workgroup_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Max over the four lanes of one query column (l % 16 fixed).
-// v_permlane16_swap a, b exchanges the odd 16-lane rows of a with the even
-// rows of b, v_permlane32_swap the upper half of a with the lower half of b;
-// from two copies of x they leave (x[l], x[l ^ 16]) and then
-// (y[l], y[l ^ 32]) in the lane, up to order -- the operands of xor shuffles
-// 16 and 32.  (Inline assembly: the compiler builtins lose the second result
-// when both operands hold the same value.)  The s_nop covers the wait states
-// between a VALU write of an operand and the permute.
-__device__ inline void permlane16_swap(unsigned &a, unsigned &b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
-__device__ inline void permlane32_swap(unsigned &a, unsigned &b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
-// v_max_f32 straight from assembly: fmaxf would first quiet its operands
-// (which come out of inline assembly) with two more instructions.  Scores
-// reaching here are never NaN (masked ones are -inf).
-__device__ inline float max_f32(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
-__device__ inline float quad_max(float x) {
-  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-  permlane16_swap(a, b);
-  x = max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-  a = __builtin_bit_cast(unsigned, x);
-  b = a;
-  permlane32_swap(a, b);
-  return max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
-
-constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
-constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score units)
 
 template <typename E>
 __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
