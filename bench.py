@@ -62,6 +62,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--repair-attention", action="store_true",
                         help="time the sparse repair attention of the workload's repair spans "
                              "(one layer) instead of the link")
+    parser.add_argument("--storage", choices=["reference", "clone"], default="reference",
+                        help="blocks read from pool slots (reference) or captured into a snapshot arena and "
+                             "linked from it (clone); clone also times the capture and a group promotion")
     parser.add_argument("--split-tokens", type=int, default=0,
                         help="repair attention: KV tokens per work item (0: the planner's choice)")
     return parser.parse_args()
@@ -450,15 +453,71 @@ def main() -> int:
     # of the step.  Batched workloads (several requests) prepare one link.
     registry = LegoLinkBlockRegistry()
     blocks, requests = workload.link_requests()
-    for key, (source, local) in blocks.items():
-        registry.register_legolink_block(key, range(source.size), torch.from_numpy(source).to(device),
-                                         compile_local_positions=local.tolist())
-    requests = [(torch.from_numpy(slots).to(device), plan) for slots, plan in requests]
+    arena = None
+    clone = args.storage == "clone"
+    if clone:
+        from legolink_amd.link_runtime import SnapshotArena
+        arena = SnapshotArena.allocate(num_slots=sum(source.size for source, _ in blocks.values()),
+                                       num_layers=shape.layers, num_heads=shape.kv_heads,
+                                       head_dim=shape.head_dim, device=device)
     executor = KVLinkExecutor(registry, RotarySpec(table, rotary_dim=workload.rotary_dim),
                               end_layer=shape.layers, num_warps=args.waves_per_block,
                               layers_per_wave=args.layers_per_wave,
-                              layer_groups_per_block=args.layer_groups_per_block)
+                              layer_groups_per_block=args.layer_groups_per_block, arena=arena)
     pool = KVPool(keys, values)
+    row_bytes = 2 * shape.kv_heads * shape.head_dim * 2  # one token's K and V row, one layer
+    storage = {"mode": args.storage}
+    if clone:
+        # Capture every block into the arena (a bit copy of all its layers,
+        # capture_compile_blocks), then link from the arena.
+        sources = {key: torch.from_numpy(source).to(device) for key, (source, _) in blocks.items()}
+
+        entries = [{"cache_key": key, "token_ids": range(source.size), "slots": sources[key],
+                    "storage_mode": "clone", "compile_local_positions": local}
+                   for key, (source, local) in blocks.items()]
+
+        def capture_all() -> float:
+            torch.cuda.synchronize(device)
+            start = time.perf_counter()
+            executor.capture_blocks(pool, entries)
+            torch.cuda.synchronize(device)
+            return time.perf_counter() - start
+
+        capture_all()  # the first pass also loads the kernels
+        for key in blocks:
+            executor.release_block(key)
+        capture_s = capture_all()
+        captured = int(arena.size)
+        capture_bytes = captured * shape.layers * row_bytes * 2
+        # The capture's device copy alone: the same one-launch row copy over
+        # the same maps (it rewrites identical rows), 10 launches back to back
+        # between two HIP events so that host work overlaps the kernels.
+        handles = registry.lookup_legolink_blocks(list(blocks)).matched_handles
+        copy_src = torch.cat([sources[handle.cache_key] for handle in handles])
+        copy_dst = torch.cat([handle.kv_slots for handle in handles])
+        zeros = torch.zeros_like(copy_src)
+
+        def copy_once() -> None:
+            executor._copy_rows(destination=arena, source=pool, source_slots=copy_src, destination_slots=copy_dst,
+                                local=zeros, global_=zeros, prefix=captured)
+
+        copy_once()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(10):
+            copy_once()
+        end.record()
+        end.synchronize()
+        copy = begin.elapsed_time(end) / 10
+        storage.update({"captured_tokens": captured, "capture_ms": round(capture_s * 1e3, 3),
+                        "capture_GBps": round(capture_bytes / capture_s / 1e9, 1),
+                        "capture_copy_ms": round(copy, 4),
+                        "capture_copy_GBps": round(capture_bytes / (copy / 1e3) / 1e9, 1)})
+    else:
+        for key, (source, local) in blocks.items():
+            registry.register_legolink_block(key, range(source.size), torch.from_numpy(source).to(device),
+                                             compile_local_positions=local.tolist())
+    requests = [(torch.from_numpy(slots).to(device), plan) for slots, plan in requests]
     compact = args.repair_rows == "compact"
     prepare_ms = []
     for _ in range(5):
@@ -506,6 +565,26 @@ def main() -> int:
     ms_per_step = wall_s * 1e3 / args.steps
     log(f"timed: {ms_per_step:.4f} ms/step wall, {gpu_ms:.4f} ms/step events, "
         f"link {np.mean(link_ms):.4f} ms, scatter {np.mean(scatter_ms):.4f} ms")
+    if clone:
+        # Group promotion (_promote_reconstructed_group): the first request's
+        # linked rows copied into free pool slots with K rotated back to local
+        # positions, then registered as a block.  Median of 5.
+        destination = requests[0][0]
+        count = int(destination.numel())
+        used = np.union1d(workload.source_slots, workload.destination_slots)
+        free = torch.from_numpy(np.setdiff1d(np.arange(workload.num_slots), used)[:count]).to(device)
+        promote_ms = []
+        for index in range(6):
+            torch.cuda.synchronize(device)
+            promote_start = time.perf_counter()
+            executor.promote_group(pool, destination, group_start=0, group_end=count, new_slots=free,
+                                   cache_key=f"promoted-{index}", token_ids=range(count))
+            torch.cuda.synchronize(device)
+            promote_ms.append((time.perf_counter() - promote_start) * 1e3)
+            registry.evict_legolink_block(f"promoted-{index}")
+        promote = float(np.median(promote_ms[1:]))
+        storage.update({"promoted_tokens": count, "promote_ms": round(promote, 3),
+                        "promote_GBps": round(count * shape.layers * row_bytes * 2 / (promote / 1e3) / 1e9, 1)})
 
     bytes_info = workload.algorithmic_bytes()
     total_bytes = bytes_info["total_bytes"]
@@ -546,6 +625,7 @@ def main() -> int:
         "event_ms_per_step": round(gpu_ms, 5),
         "host_prepare_ms": round(host_prepare_ms, 3),
         "repair_rows_mode": args.repair_rows,
+        "storage": storage,
         "launch": launch,
         "roofline": {
             "bound": "hbm",
@@ -554,7 +634,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
+            "traffic": traffic if not clone else None,
             "algorithmic_bytes_per_launch": bytes_info["link_bytes"],
         },
         "cpu_baseline": None,

@@ -643,6 +643,58 @@ class KVLinkExecutor:
             self.arena.free(arena_slots)
             raise
 
+    def capture_blocks(self, pool: Any, blocks: Sequence[Mapping[str, Any]]) -> list[LegoLinkBlockHandle]:
+        """Register several compiled blocks at once, as capture_compile_blocks does
+        for every compile request of a forward batch (pic_runtime.py:3485-3560).
+        Each entry holds ``cache_key``, ``token_ids``, ``slots`` and optionally
+        ``storage_mode`` ("reference" or "clone"), ``compile_local_positions`` and
+        ``block_id``.
+        The clone blocks' rows are copied into their arena ranges by one launch
+        over every layer; on any error no block is registered and no arena range
+        is kept."""
+
+        _validate_pool(pool)
+        device = pool.get_key_buffer(self.start_layer).device
+        entries = []
+        for block in blocks:
+            mode = block.get("storage_mode", "reference")
+            if mode not in ("reference", "clone"):
+                raise LinkRuntimeError(f"Unsupported PIC storage mode: {mode}")
+            slots = torch.as_tensor(block["slots"]).long().reshape(-1).to(device)
+            entries.append((block, mode, slots))
+        clones = [entry for entry in entries if entry[1] == "clone"]
+        if clones and self.arena is None:
+            raise LinkRuntimeError("PIC clone storage needs a snapshot arena.")
+        ranges: list[torch.Tensor] = []
+        handles: list[LegoLinkBlockHandle] = []
+        try:
+            for block, _, slots in clones:
+                arena_slots = self.arena.alloc(int(slots.numel()))
+                if arena_slots is None:
+                    raise LinkRuntimeError(f"PIC snapshot arena has no {int(slots.numel())} free slots for "
+                                           f"{block['cache_key']}.")
+                ranges.append(arena_slots)
+            if clones:
+                source = torch.cat([slots for _, _, slots in clones])
+                target = torch.cat(ranges)
+                positions = torch.zeros(int(source.numel()), dtype=torch.long, device=device)
+                self._copy_rows(destination=self.arena, source=pool, source_slots=source,
+                                destination_slots=target, local=positions, global_=positions,
+                                prefix=int(source.numel()))
+            arena_of = {id(entry[0]): arena_slots for entry, arena_slots in zip(clones, ranges)}
+            for block, mode, slots in entries:
+                handles.append(self.registry.register_legolink_block(
+                    block["cache_key"], block["token_ids"], arena_of.get(id(block), slots),
+                    compile_local_positions=block.get("compile_local_positions"),
+                    block_id=block.get("block_id"), storage_mode=mode))
+            return handles
+        except Exception:
+            for handle in handles:
+                self.registry.evict_legolink_block(handle.cache_key)
+            for arena_slots in ranges:
+                self.arena.free(arena_slots)
+            raise
+
     def release_block(self, cache_key: str) -> bool:
         """Evict an unpinned block; a clone block's arena range is freed."""
 

@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import threading
 from dataclasses import dataclass, field
-from typing import Iterable, Optional, Sequence
+from typing import Any, Iterable, Optional, Sequence
 
 import numpy as np
 import torch
@@ -96,6 +96,23 @@ class LegoLinkLookupResult:
     matched_handles: list[LegoLinkBlockHandle] = field(default_factory=list)
 
 
+def _int_array(values: Any) -> np.ndarray:
+    """A flat int64 array of ``values`` (a range, list, array or tensor)."""
+
+    if isinstance(values, range):
+        return np.arange(values.start, values.stop, values.step, dtype=np.int64)
+    if isinstance(values, torch.Tensor):
+        return values.detach().reshape(-1).to("cpu", torch.int64).numpy()
+    array = np.asarray(values)
+    if array.size and not np.issubdtype(array.dtype, np.integer):
+        array = np.asarray([int(value) for value in values], dtype=np.int64)
+    return array.astype(np.int64, copy=False).reshape(-1)
+
+
+def _int_tuple(values: Any) -> tuple[int, ...]:
+    return tuple(_int_array(values).tolist())
+
+
 class LegoLinkBlockRegistry:
     """cache_key -> handle.  Callers on several threads are serialised by a lock."""
 
@@ -114,20 +131,19 @@ class LegoLinkBlockRegistry:
         block_id: Optional[str] = None,
         storage_mode: str = "reference",
     ) -> LegoLinkBlockHandle:
-        token_ids = tuple(int(token) for token in token_ids)
+        token_ids = _int_tuple(token_ids)
         slots = torch.as_tensor(kv_slots).long().reshape(-1).clone()
         if int(slots.numel()) != len(token_ids):
             raise ValueError("LegoLink KV slot count must equal the exact logical token length.")
-        positions = (
-            tuple(range(len(token_ids)))
-            if compile_local_positions is None
-            else tuple(int(p) for p in compile_local_positions)
-        )
+        if compile_local_positions is None:
+            position_array = np.arange(len(token_ids), dtype=np.int64)
+        else:
+            position_array = _int_array(compile_local_positions)
+        positions = tuple(position_array.tolist())
         if len(positions) != len(token_ids):
             raise ValueError("compile_local_positions must hold one position per token.")
         if storage_mode not in ("reference", "clone"):
             raise ValueError(f"Unsupported PIC storage mode: {storage_mode}")
-        position_array = np.asarray(positions, dtype=np.int64)
         if position_array.size == 0:
             local_start, max_local = 0, -1
         else:

@@ -167,3 +167,74 @@ def test_group_promotion_round_trip(gpu_device):
     assert np.abs(promoted - compiled_b).max() < 0.06  # two bf16 re-rotations away from the original
     handle = registry.lookup_legolink_blocks(["b-promoted"]).matched_handles[0]
     assert handle.compile_local_positions == tuple(range(n_b))
+
+
+def test_batched_capture_matches_block_by_block_capture(gpu_device):
+    """capture_blocks copies every clone block with one launch; the arena rows,
+    the handles and a link over them match what capture_block gives."""
+
+    pool, arena, registry, executor = _setup(gpu_device, seed=53)
+    rng = np.random.default_rng(53)
+    perm = rng.permutation(pool.size)
+    lengths = {"x-clone": 260, "y-ref": 130, "z-clone": 90, "w-clone": 1}
+    blocks, cursor = [], 0
+    for key, length in lengths.items():
+        blocks.append({"cache_key": key, "token_ids": list(range(5, 5 + length)),
+                       "slots": torch.from_numpy(perm[cursor : cursor + length]).to(gpu_device),
+                       "storage_mode": "clone" if key.endswith("clone") else "reference",
+                       "compile_local_positions": list(range(3, 3 + length))})
+        cursor += length
+    report("batched capture of three clone blocks and one reference block")
+    handles = executor.capture_blocks(pool, blocks)
+    torch.cuda.synchronize(gpu_device)
+    assert [handle.cache_key for handle in handles] == list(lengths)
+    assert arena.free_slots == arena.size - (260 + 90 + 1)
+    original_k = [bits(k) for k in pool.k_buffer]
+    original_v = [bits(v) for v in pool.v_buffer]
+    for block, handle in zip(blocks, handles):
+        assert handle.storage_mode == block["storage_mode"]
+        assert handle.compile_local_positions == tuple(block["compile_local_positions"])
+        source = block["slots"].cpu().numpy()
+        if block["storage_mode"] == "reference":
+            assert np.array_equal(handle.kv_slots.cpu().numpy(), source)
+            continue
+        held = handle.kv_slots.cpu().numpy()
+        for layer in range(pool.layer_num):
+            assert np.array_equal(bits(arena.k_buffer[layer])[held], original_k[layer][source])
+            assert np.array_equal(bits(arena.v_buffer[layer])[held], original_v[layer][source])
+
+    # An arena too small for the batch leaves no block registered and no range taken.
+    free_before = arena.free_slots
+    too_big = [{"cache_key": "fits", "token_ids": [1] * 8, "slots": blocks[0]["slots"][:8], "storage_mode": "clone"},
+               {"cache_key": "overflow", "token_ids": [1] * (free_before + 1),
+                "slots": torch.arange(free_before + 1, device=gpu_device), "storage_mode": "clone"}]
+    with pytest.raises(Exception, match="free slots"):
+        executor.capture_blocks(pool, too_big)
+    assert arena.free_slots == free_before
+    assert registry.lookup_legolink_blocks(["fits"]).matched_handles == []
+
+    # Link the batch-captured blocks after their pool slots were reused.
+    clone_slots = torch.cat([block["slots"] for block in blocks if block["storage_mode"] == "clone"])
+    for buffer in pool.k_buffer + pool.v_buffer:
+        buffer.index_fill_(0, clone_slots, 0)
+    plan = {"cache_keys": ["z-clone", "y-ref", "x-clone", "w-clone"], "recompute_initial_tokens": 4}
+    resolve_link_plan(registry.get_legolink_block_tokens, [7, 8, 9], plan)
+    destination = torch.from_numpy(perm[cursor : cursor + plan["total_token_count"]]).to(gpu_device)
+    prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=True)
+    prepared.launch()
+    torch.cuda.synchronize(gpu_device)
+    maps = prepared.maps
+    by_key = {block["cache_key"]: block["slots"] for block in blocks}
+    original_src = torch.cat([by_key[key] for key in plan["cache_keys"]]).cpu().numpy()
+    mask = np.zeros(maps.token_count, dtype=np.uint8)
+    mask[prepared.repair_offsets] = 1
+    expected_k, expected_v = ko.link_pool(
+        original_k, original_v, original_src, maps.destination_slots.cpu().numpy(),
+        maps.local_positions, maps.global_positions, build_cos_sin_cache(4096, 128).numpy(),
+        key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=128, neox=True,
+        prefix=maps.prefix_token_count, repair_mask=mask,
+    )
+    written = maps.destination_slots.cpu().numpy()[mask == 0]
+    for layer in range(pool.layer_num):
+        assert np.array_equal(bits(pool.k_buffer[layer])[written], expected_k[layer][written])
+        assert np.array_equal(bits(pool.v_buffer[layer])[written], expected_v[layer][written])

@@ -218,3 +218,28 @@ def test_storage_modes_in_registry_and_maps():
     pool = KVPool.allocate(num_slots=32, num_layers=1, num_heads=1, head_dim=8, device="cpu")
     with pytest.raises(LinkRuntimeError, match="needs the snapshot arena"):
         executor.prepare_link(pool, torch.arange(20, 25), plan)
+
+
+def test_batched_capture_rejects_before_any_registration():
+    """capture_blocks checks every entry before it copies or registers one."""
+
+    registry = LegoLinkBlockRegistry()
+    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(16, 8, theta=1e4), rotary_dim=8),
+                              end_layer=1)
+    pool = KVPool.allocate(num_slots=32, num_layers=1, num_heads=1, head_dim=8, device="cpu")
+    reference = {"cache_key": "r", "token_ids": [1, 2], "slots": [3, 4]}
+    with pytest.raises(LinkRuntimeError, match="needs a snapshot arena"):
+        executor.capture_blocks(pool, [reference, {"cache_key": "c", "token_ids": [5], "slots": [6],
+                                                   "storage_mode": "clone"}])
+    with pytest.raises(LinkRuntimeError, match="Unsupported PIC storage mode"):
+        executor.capture_blocks(pool, [reference, {"cache_key": "p", "token_ids": [5], "slots": [6],
+                                                   "storage_mode": "paged"}])
+    assert registry.get_legolink_block_tokens("r") is None
+    # A reference-only batch needs no copy and registers every entry.
+    handles = executor.capture_blocks(pool, [reference, {"cache_key": "s", "token_ids": [7], "slots": [8],
+                                                         "block_id": "seg"}])
+    assert [handle.cache_key for handle in handles] == ["r", "s"]
+    assert handles[0].kv_slots.tolist() == [3, 4] and handles[1].block_id == "seg"
+    with pytest.raises(ValueError, match="slot count"):
+        executor.capture_blocks(pool, [{"cache_key": "t", "token_ids": [1, 2, 3], "slots": [0]}])
+    assert registry.get_legolink_block_tokens("t") is None
