@@ -5,31 +5,31 @@
 //   item = up to four 16-query tiles of one request (consecutive repair
 //   rows) and a KV range [kv_begin, kv_end) of logical positions; long ranges
 //   are split and the partial results merged by a combine pass.
-//   workgroup = (item, KV head); wave w computes query tile w / G for query
-//   head hk * G + w % G (G query heads share one KV head), so each K/V tile
-//   staged in LDS serves every query tile and head of the item.  With more
-//   than 16 query heads per KV head, items have one tile and each KV head
-//   gets ceil(G / 16) workgroups of 16 heads.
+//   workgroup = (item, KV head); the item's (query tile, query head) pairs
+//   -- pair n is query tile n / G, query head hk * G + n % G (G query heads
+//   share one KV head) -- are spread over its waves, so each K/V tile staged
+//   in LDS serves every query tile and head of the item.  With more than 16
+//   query heads per KV head, items have one tile and each KV head gets
+//   ceil(G / 16) workgroups of 16 heads.
 //
 // Per 64-token KV tile:
 //   1. gather the tile's K and V rows of this KV head into LDS by slot;
-//   2. S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 K rows from LDS,
-//      B = the wave's 16 queries (kept in registers).  The accumulator layout
-//      gives each lane 4 consecutive tokens of one query;
+//   2. S^T = K Q^T on MFMAs: A = K rows from LDS, B = the queries (kept in
+//      registers);
 //   3. masking (causal by logical position, split range, invalid slots),
 //      online softmax in fp32 with exp2 (row statistics reduced across the
-//      four lanes of a query with xor shuffles 16 and 32);
-//   4. O^T += V^T P^T with v_mfma_f32_16x16x32_bf16: B = the probabilities
-//      straight from the S^T accumulators of two 16-token groups (the token
-//      order inside the K step is free, as long as A uses the same one),
-//      A = 8 tokens of one dim row of V^T.
-// Lane layouts (checked on the device): 16x16x32 A/B lane l element e ->
-// row/column l % 16, k = 8 (l / 16) + e; accumulator register r -> row
-// 4 (l / 16) + r, column l % 16.
+//      lanes of a query with permlane swaps);
+//   4. O^T += V^T P^T: B = the probabilities straight from the S^T
+//      accumulators (the token order inside the K step is free, as long as
+//      A uses the same one), A = V^T from transposed LDS reads.
 //
-// Head dim 128 runs repair_attention_dma_kernel (LDS ring filled by
-// global_load_lds two tiles ahead); head dim 64 runs repair_attention_kernel,
-// which stages each tile through registers.
+// Head dim 128 runs repair_attention_m32_kernel: two pairs per wave on
+// v_mfma_f32_32x32x16, rows gathered into an LDS ring by global_load_lds.
+// Head dims 64 and 256 run repair_attention_kernel: one pair per wave on
+// v_mfma_f32_16x16x32, each tile staged through registers.  Its lane layouts
+// (checked on the device): A/B lane l element e -> row/column l % 16,
+// k = 8 (l / 16) + e; accumulator register r -> row 4 (l / 16) + r, column
+// l % 16.
 //
 // Roofline: MFMA-bound in principle.  Algorithmic work per (query, visible
 // key) pair and query head: 4 * head_dim flops (QK and PV); KV bytes are read
@@ -53,6 +53,7 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((ext_vector_type(2))) float f32x2;
@@ -114,6 +115,13 @@ struct Bf16 {
   __device__ static uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
   }
+  __device__ static f32x16 mfma32(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static float dot2_ones(uint32_t pair, float acc) {  // acc + lo + hi, one v_dot2_f32_bf16
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), __builtin_bit_cast(bf16x2, kOnes),
+                                           acc, false);
+  }
 };
 
 struct F16 {
@@ -124,6 +132,12 @@ struct F16 {
   }
   __device__ static uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
+  __device__ static f32x16 mfma32(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static float dot2_ones(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, kOnes), acc, false);
   }
 };
 
@@ -248,8 +262,9 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
     }
   }
 
-  // The softmax state as in repair_attention_dma_kernel: a lazily raised
-  // maximum from a finite floor, denominators from the value MFMA.
+  // The softmax state: a lazily raised maximum from a finite floor (as in
+  // repair_attention_m32_kernel), denominators from a value MFMA with a
+  // 16-row A operand of ones.
   float m = kScoreFloor;
   f32x4 o[kDimTiles];
 #pragma unroll
@@ -414,20 +429,15 @@ __global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_
   }
 }
 
-// The same work on a pipelined schedule (head dim 128): K and V rows are
-// gathered straight into a four-stage LDS ring with global_load_lds, two
-// tiles ahead of the MFMAs, so no registers stage them and no wave waits on a
-// gather it could overlap.  The workgroup synchronises once per two tiles,
-// so its waves drift apart within a pair of tiles and one wave's softmax
-// overlaps another's MFMAs.  Rows are stored token-major with their sixteen
-// 16-byte chunks XOR-swizzled by token (K: chunk c of token t at c ^ (t % 16),
-// V: at c ^ 2 (t % 8)), which keeps the K fragment reads and the transposed V
-// reads free of bank conflicts.  V^T fragments come from ds_read_b64_tr_b16: within a group
-// of 16 lanes it returns to lane i, element e, element i % 4 of the 8 bytes
-// that lane 4 e + i / 4 addressed (checked on the device), so lanes addressing
-// 4 dims of 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.
-// The item's slots are read once into LDS (at most kDmaMaxRange of them).
-constexpr int kDmaThreads = 1024;    // 16 waves: two gather instructions each per tile
+// Head dim 128 gathers K and V rows straight into a four-stage LDS ring with
+// global_load_lds, three tiles ahead of the MFMAs, so no registers stage them.
+// Rows are stored token-major with their sixteen 16-byte chunks XOR-swizzled
+// by token, which keeps the fragment reads free of bank conflicts.  V^T
+// fragments come from ds_read_b64_tr_b16: within a group of 16 lanes it
+// returns to lane i, element e, element i % 4 of the 8 bytes that lane
+// 4 e + i / 4 addressed (checked on the device), so lanes addressing 4 dims of
+// 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.  The item's
+// slots are read once into LDS (at most kDmaMaxRange of them).
 constexpr int kDmaStages = 4;
 constexpr int kDmaMaxRange = 4096;   // KV tokens per work item on this path
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -469,19 +479,41 @@ __device__ inline void workgroup_barrier() {
 }
 
 
+// Head dim 128 on v_mfma_f32_32x32x16 (issues at ~34 cycles for twice the work
+// of a 16x16x32 at ~20, and hides about four VALU instructions in the wave
+// that issued it, against two).  Each wave owns two (query tile, head) pairs,
+// 32 MFMA columns: column n = 16 (pair - 2 wave) + query.  Lane layouts
+// (checked on the device with integer matrices): A and B lane l element e ->
+// row / column l % 32, k = 8 (l / 32) + e; accumulator register r -> row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+//   S^T = K Q^T per 32-token block: A = K rows from LDS (token l % 32, dims
+//   16 ks + 8 (l / 32) + e: one 16-byte chunk), B = the lane's query (held).
+//   O^T += V^T P^T per 16-token step s of a block: B = accumulator registers
+//   8 s .. 8 s + 7 rounded in place, which puts token 16 s + 8 (e / 4) +
+//   4 (l / 32) + e % 4 at k = 8 (l / 32) + e; A = V^T through two transposed
+//   reads giving each lane one dim of that token order.
+// Each lane sums its bf16/fp16 probabilities with v_dot2 against ones (the
+// values the value product sees); the two lanes of a column add at the end.
+// K rows keep the chunk swizzle c ^ (t % 16); V rows use c ^ 4 (t % 4), under
+// which the 32 lanes of one transposed read (4 tokens x 64 bytes) cover the 64
+// banks once.  Each of the 8 waves issues four of a tile's 32 gathers.
+constexpr int kM32Threads = 512;
+
 template <typename E>
-__global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const AttnParams p) {
   typedef typename E::frag frag;
   constexpr int D = 128;
-  constexpr int kSteps = D / 32;
-  constexpr int kDimTiles = D / 16;
+  constexpr int kKSteps = D / 16;                        // 16-dim steps of the score MFMAs
+  constexpr int kDimBlocks = D / 32;                     // 32-dim blocks of O^T
   constexpr int kChunksPerRow = D / 8;                   // 16-byte chunks per row: 16
-  constexpr int kStageBytes = kTile * D * 2;             // one K or V tile: 16 KB
-  constexpr int kRangeTiles = kDmaMaxRange / kTile;  // 64-token KV tiles per item
+  constexpr int kRowBytes = D * 2;
+  constexpr int kStageBytes = kTile * kRowBytes;         // one K or V tile: 16 KB
+  constexpr int kRangeTiles = kDmaMaxRange / kTile;
+  static_assert(kM32Threads / kWave * 2 == kMaxWaves, "two (tile, head) pairs per wave");
   __shared__ __attribute__((aligned(16))) unsigned char k_ring[kDmaStages * kStageBytes];
   __shared__ __attribute__((aligned(16))) unsigned char v_ring[kDmaStages * kStageBytes];
   __shared__ int slot_lds[kDmaMaxRange];
-  __shared__ unsigned long long tile_valid[kRangeTiles];  // bit j: token j of the tile has a valid slot
+  __shared__ unsigned long long tile_valid[kRangeTiles];
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
@@ -495,21 +527,45 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  const int g = lane / 16;
-  const int c = lane % 16;
-  const int tile = wave / p.heads_per_wg;
-  const int head = head_base + wave % p.heads_per_wg;
-  const int hq = hk * p.group + head;
-  const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
-  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
-  const bool computes = tile < n_tiles && head < p.group && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
-                        static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
-                        needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
-  const bool q_ok = computes && c < q_count;
-  // A tile's queries are consecutive rows of one request, not always
-  // consecutive positions (several short repair spans share a tile).
-  const int my_pos = q_ok ? p.positions[q_index + c] : 0;
-  const int kv_stop = computes ? min(kv_end, needed) : kv_begin;
+  const int h = lane / 32;   // k half of the A/B operands, row group of the accumulators
+  const int col = lane % 32;  // MFMA column of this lane
+  const int qc = col % 16;    // query within the column's pair
+
+  // The wave's two pairs; a pair computes when its tile and head exist and its
+  // table entry is sane.
+  struct PairInfo {
+    bool computes;
+    int q_index, q_pos, q_count, partial, stop, hq;
+  };
+  auto pair_info = [&](int pair) {
+    PairInfo r;
+    const int tile = pair / p.heads_per_wg;
+    const int head = head_base + pair % p.heads_per_wg;
+    const int *e = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
+    r.q_index = e[0];
+    r.q_pos = e[1];
+    r.q_count = e[2];
+    r.partial = e[3];
+    const int needed = e[4];
+    r.hq = hk * p.group + head;
+    r.computes = tile < n_tiles && head < p.group && r.q_count >= 1 && r.q_count <= kQueries && r.q_index >= 0 &&
+                 static_cast<long long>(r.q_index) + r.q_count <= p.num_queries && r.q_pos >= 0 &&
+                 needed > r.q_pos && (r.partial == -1 || (r.partial >= 0 && r.partial < p.ws_items));
+    r.stop = r.computes ? min(kv_end, needed) : kv_begin;
+    return r;
+  };
+  const PairInfo pair0 = pair_info(2 * wave), pair1 = pair_info(2 * wave + 1);
+  const PairInfo &mine = col < 16 ? pair0 : pair1;
+  const bool wave_computes = pair0.computes || pair1.computes;
+  const int wave_stop = max(pair0.stop, pair1.stop);
+  // Keys below both pairs' lowest query position and stop need no causal mask.
+  int wave_unmasked = kv_end;
+  if (pair0.computes) wave_unmasked = min(wave_unmasked, min(pair0.q_pos, pair0.stop));
+  if (pair1.computes) wave_unmasked = min(wave_unmasked, min(pair1.q_pos, pair1.stop));
+  const bool q_ok = mine.computes && qc < mine.q_count;
+  const int my_pos = q_ok ? p.positions[mine.q_index + qc] : 0;
+  const int my_stop = mine.stop;
+
   int load_stop = kv_begin;
   for (int t = 0; t < n_tiles; ++t) {
     const int *e = it + 4 + kTileInts * t;
@@ -518,11 +574,9 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
   const int range = load_stop - kv_begin;
   const int tiles = (range + kTile - 1) / kTile;
 
-  // Slots of the item's range (-1: out of range or invalid), and per tile a
-  // mask of its tokens with a valid slot.
-  for (int i = tid; i < kRangeTiles; i += kDmaThreads) tile_valid[i] = 0ull;
+  for (int i = tid; i < kRangeTiles; i += kM32Threads) tile_valid[i] = 0ull;
   __syncthreads();
-  for (int i = tid; i < tiles * kTile; i += kDmaThreads) {
+  for (int i = tid; i < tiles * kTile; i += kM32Threads) {
     int slot = -1;
     if (i < range) {
       const long long s = slot_at(p, static_cast<long long>(kv_off) + kv_begin + i);
@@ -532,218 +586,246 @@ __global__ void __launch_bounds__(kDmaThreads) repair_attention_dma_kernel(const
     if (slot >= 0) atomicOr(&tile_valid[i / kTile], 1ull << (i % kTile));
   }
 
-  frag qf[kSteps];
+  // B operand of the score MFMAs: the lane's query, dims 16 ks + 8 h .. + 7.
+  frag qf[kKSteps];
   {
-    const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
+    const uint16_t *qrow = p.q + (static_cast<long long>(mine.q_index + qc) * p.hq + mine.hq) * D + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
+    for (int ks = 0; ks < kKSteps; ++ks) {
       u32x4 bits = {0u, 0u, 0u, 0u};
-      if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
+      if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 16 * ks);
       qf[ks] = __builtin_bit_cast(frag, bits);
     }
   }
   __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): queries and slots are in
   __syncthreads();
 
-  // Gather of tile t: 32 instructions of 64 lanes (16 for K, 16 for V), two per
-  // wave.  Instruction k covers stage chunks 64 k .. 64 k + 63; stage chunk P
-  // holds token P / 16 and, of its row, chunk (P % 16) ^ (token % 16) for K
-  // and chunk (P % 16) ^ (2 (token % 8)) for V (each swizzle is its own
-  // inverse, so a row chunk r sits at r ^ key).
+  // Gather of tile t: 16 K and 16 V instructions of 64 lanes; wave w issues
+  // instructions 2 w and 2 w + 1 of each.  Instruction k fills stage chunks
+  // 64 k .. 64 k + 63: chunk P holds token P / 16 and, of its row, chunk
+  // (P % 16) ^ swizzle(token) (each swizzle is its own inverse).
   const long long row_stride = static_cast<long long>(p.hkv) * D;
-  // Wave w issues instruction w of the K tile and instruction w of the V tile.
-  const int chunk_index = wave * kWave + lane;
-  const int gather_token = chunk_index / kChunksPerRow;
-  const int k_chunk = (chunk_index % kChunksPerRow) ^ (gather_token % 16);
-  const int v_chunk = (chunk_index % kChunksPerRow) ^ (2 * (gather_token % 8));
-  // Every wave issues the same two loads for every tile: a token without a
-  // valid slot loads slot 0's row instead (nothing is loaded when the pool is
-  // empty), which the masking hides for K and the V clean-up below replaces
-  // by zeros.
-  const bool have_slots = p.num_slots > 0;  // else every token is invalid and nothing is loaded
+  const bool have_slots = p.num_slots > 0;
+  int g_token[2], g_kchunk[2], g_vchunk[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int chunk_index = (2 * wave + j) * kWave + lane;
+    g_token[j] = chunk_index / kChunksPerRow;
+    g_kchunk[j] = (chunk_index % kChunksPerRow) ^ (g_token[j] % 16);
+    g_vchunk[j] = (chunk_index % kChunksPerRow) ^ (4 * (g_token[j] % 4));
+  }
   auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
-    const int slot = max(slot_lds[t * kTile + gather_token], 0);
-    const long long row = slot * row_stride + hk * D;
-    dma_pair(p.k + row + k_chunk * 8, k_dst + wave * kWave * 16, p.v + row + v_chunk * 8,
-             v_dst + wave * kWave * 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int slot = max(slot_lds[t * kTile + g_token[j]], 0);
+      const long long row = slot * row_stride + hk * D;
+      const int offset = (2 * wave + j) * kWave * 16;
+      dma_pair(p.k + row + g_kchunk[j] * 8, k_dst + offset, p.v + row + g_vchunk[j] * 8, v_dst + offset);
+    }
   };
 
-  // m starts at a finite floor far below any score, so the exponent bias
-  // needs no -inf special case: a query with no visible key yet keeps it and
-  // gets probabilities exp2(-inf) = 0.
   float m = kScoreFloor;
-  f32x4 o[kDimTiles];
+  float l = 0.f;
+  f32x16 o[kDimBlocks];
 #pragma unroll
-  for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // The softmax denominators come out of the value MFMA: a 16-row A operand of
-  // ones times P^T gives, in every accumulator register of lane (g, c), the
-  // sum of query c's probabilities as the value product sees them (bf16).
-  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
-  const frag ones = __builtin_bit_cast(frag, u32x4{E::kOnes, E::kOnes, E::kOnes, E::kOnes});
+  for (int b = 0; b < kDimBlocks; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
   const float scale_log2 = p.scale_log2;
-  const float slack = kSlack / scale_log2;  // kSlack in raw score units
+  const float slack = kSlack / scale_log2;
 
-  // Lane offsets of the transposed V reads (see below): the tokens a lane
-  // reads are congruent to x = 4 g + c / 4 modulo 16.
-  const int x = 4 * g + c / 4;
-  const int lane_base = x * (kChunksPerRow * 16) + ((c % 4) / 2) * 16 + (c % 2) * 8;
-  const int x8 = x & 7;
+  // Per-lane LDS offsets.  K: token col of a 32-token block, chunk
+  // (2 ks + h) ^ (col % 16).  V (transposed reads): lane i of 16-lane group q
+  // addresses token 4 h + i / 4 (+ the step's base) and the 8 bytes of dims
+  // 32 b + 16 (q % 2) + 4 (i % 4); that dim chunk sits at chunk position
+  // (4 b + 2 (q % 2) + (i % 4) / 2) ^ 4 (i / 4) = 4 (b ^ (i / 4)) + ...
+  const int li = lane % 16;
+  const int vu = li / 4;
+  const int v_lane = (4 * h + vu) * kRowBytes + (2 * ((lane / 16) % 2) + (li % 4) / 2) * 16 + 8 * (li % 2);
+  const int k_lane = col * kRowBytes;
 
-  if (tiles > 0) gather(0, k_ring, v_ring);
-  if (tiles > 1) gather(1, k_ring + kStageBytes, v_ring + kStageBytes);
-  // Inside the loop the barriers are plain s_barrier: __syncthreads() would
-  // also wait for every outstanding gather and serialise the pipeline.  What
-  // the loop needs is ordering: a wave's LDS reads of a stage are consumed by
-  // its MFMAs before it reaches the next barrier, and each wave waits for its
-  // own gathers (vmcnt) before the barrier that hands a stage to compute.
+  // Tiles are gathered three ahead: tile t + 3 goes into the stage of tile
+  // t - 1 once every wave is past it (the barrier at the top of tile t).  A
+  // wave's four gathers of tile t are complete when at most the eight of
+  // tiles t + 1 and t + 2 are outstanding (loads count down in issue order).
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (t < tiles) gather(t, k_ring + t * kStageBytes, v_ring + t * kStageBytes);
   for (int t = 0; t < tiles; ++t) {
     const unsigned char *k_stage = k_ring + (t % kDmaStages) * kStageBytes;
     unsigned char *v_stage = v_ring + (t % kDmaStages) * kStageBytes;
-    if (t % 2 == 0) {
-      // Tiles t and t + 1 were gathered two tiles ago.  Once this wave's loads
-      // are complete, one barrier says both that every wave's loads of them
-      // have landed and that every wave is done with tiles t - 2 and t - 1,
-      // whose stages tiles t + 2 and t + 3 take over.
-      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
-      workgroup_barrier();
-      if (t + 2 < tiles)
-        gather(t + 2, k_ring + ((t + 2) % kDmaStages) * kStageBytes, v_ring + ((t + 2) % kDmaStages) * kStageBytes);
-      if (t + 3 < tiles)
-        gather(t + 3, k_ring + ((t + 3) % kDmaStages) * kStageBytes, v_ring + ((t + 3) % kDmaStages) * kStageBytes);
-    }
+    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF78);       // vmcnt(8)
+    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4)
+    else __builtin_amdgcn_s_waitcnt(0xF70);                     // vmcnt(0)
+    workgroup_barrier();
+    if (t + 3 < tiles)
+      gather(t + 3, k_ring + ((t + 3) % kDmaStages) * kStageBytes, v_ring + ((t + 3) % kDmaStages) * kStageBytes);
     const unsigned long long valid_bits = tile_valid[t];
     if (valid_bits != ~0ull) {
-      // Zero the V rows of tokens without a valid slot: their probability is
-      // 0, and 0 * V must not turn an Inf or NaN of slot 0's row into a NaN.
-      // Thread i owns bytes 16 i .. 16 i + 15 of the stage (token i / 16).
-      if (slot_lds[t * kTile + tid / kChunksPerRow] < 0)
-        *reinterpret_cast<u32x4 *>(v_stage + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+      // Zero the V rows of tokens without a valid slot (0 * Inf would be NaN).
+      for (int c = tid; c < kTile * kChunksPerRow; c += kM32Threads)
+        if (slot_lds[t * kTile + c / kChunksPerRow] < 0)
+          *reinterpret_cast<u32x4 *>(v_stage + c * 16) = u32x4{0u, 0u, 0u, 0u};
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       workgroup_barrier();
     }
     const int t0 = kv_begin + t * kTile;
-    if (!computes || t0 >= kv_stop) continue;
-    // Keep the per-lane LDS offsets below from being precomputed for every
-    // (dim tile, token half) and held across tiles: 16 addresses would not fit
-    // in the register budget of a 16-wave workgroup.
-    int k_lane = c * kChunksPerRow * 16;
-    int v_lane = lane_base;
-    asm volatile("" : "+v"(k_lane), "+v"(v_lane));
+    if (!wave_computes || t0 >= wave_stop) continue;
+    int k_addr = k_lane;
+    int v_addr = v_lane;
+    asm volatile("" : "+v"(k_addr), "+v"(v_addr));
 
-    f32x4 s[4];
+    f32x16 s[2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks) {
-        // Token 16 n + c: its swizzle key is c, so row chunk 4 ks + g sits at (4 ks + g) ^ c.
-        const int chunk = (4 * ks + g) ^ c;
-        const frag a = *reinterpret_cast<const frag *>(k_stage + k_lane + n * 16 * kChunksPerRow * 16 + chunk * 16);
-        s[n] = E::mfma(a, qf[ks], s[n]);
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+    // K fragments in batches of two 16-dim steps (both 32-token blocks), the
+    // next batch's reads issued before this batch's MFMAs so that the LDS
+    // latency hides under them.
+    frag kf[2][4];
+    auto load_k = [&](int batch, frag *dst) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int chunk = (2 * (2 * batch + j) + h) ^ (col % 16);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          dst[2 * j + kb] = *reinterpret_cast<const frag *>(k_stage + k_addr + kb * 32 * kRowBytes + chunk * 16);
       }
+    };
+    load_k(0, kf[0]);
+#pragma unroll
+    for (int batch = 0; batch < kKSteps / 2; ++batch) {
+      if (batch + 1 < kKSteps / 2) load_k(batch + 1, kf[(batch + 1) % 2]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) s[kb] = E::mfma32(kf[batch % 2][2 * j + kb], qf[2 * batch + j], s[kb]);
     }
-    const bool whole = valid_bits == ~0ull && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first batch's 4 LDS reads
+#pragma unroll
+    for (int batch = 0; batch < kKSteps / 2; ++batch) {
+      if (batch + 1 < kKSteps / 2) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // next batch's reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // this batch's MFMAs
+    }
+    const bool whole = valid_bits == ~0ull && t0 + kTile <= wave_unmasked;
     float tile_max = -INFINITY;
     if (whole) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[n][r]);
+        for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[kb][r]);
       if (!q_ok) tile_max = -INFINITY;
     } else {
-      // Token 16 n + 4 g + r is visible iff 16 n + r <= limit (positions below
-      // the split end and not after the query), and its slot is valid.
-      const int limit = q_ok ? min(kv_stop - 1, my_pos) - t0 - 4 * g : -1;
-      const unsigned long long lane_bits = valid_bits >> (4 * g);
+      // Register r of block kb holds token 32 kb + 8 (r / 4) + 4 h + r % 4:
+      // visible iff at or below the lane's limit and its slot is valid.
+      const int limit = q_ok ? min(my_stop - 1, my_pos) - t0 - 4 * h : -1;
+      const unsigned long long lane_bits = valid_bits >> (4 * h);
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool visible = 16 * n + r <= limit && ((lane_bits >> (16 * n + r)) & 1ull) != 0;
-          s[n][r] = visible ? s[n][r] : -INFINITY;
-          tile_max = fmaxf(tile_max, s[n][r]);
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * kb + 8 * (r / 4) + r % 4;
+          const bool visible = rel <= limit && ((lane_bits >> rel) & 1ull) != 0;
+          s[kb][r] = visible ? s[kb][r] : -INFINITY;
+          tile_max = fmaxf(tile_max, s[kb][r]);
         }
       }
     }
-    tile_max = quad_max(tile_max);
-    // The reference maximum m moves only when the tile's maximum exceeds it by
-    // more than kSlack in log2 units, so most tiles keep it and skip rescaling
-    // O.  Probabilities relative to m stay <= 2^kSlack: no overflow in the
-    // fp32 sums, and their bf16 rounding is relative, as before.
+    {
+      unsigned a = __builtin_bit_cast(unsigned, tile_max), b = a;
+      permlane32_swap(a, b);
+      tile_max = max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    }
     const bool raise = tile_max > m + slack;
     const float m_new = raise ? tile_max : m;
     const float bias = -m_new * scale_log2;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
-    }
+      for (int r = 0; r < 16; ++r) s[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], scale_log2, bias));
     if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform
       const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);
-      lsum *= alpha;
+      l *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
+      for (int b = 0; b < kDimBlocks; ++b) o[b] *= alpha;
     }
     m = m_new;
-    frag pb[2];
+    // P^T operands of the four 16-token steps (step 2 kb + st), and their sums.
+    frag pb[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 bits;
-      bits[0] = E::pack(s[2 * h][0], s[2 * h][1]);
-      bits[1] = E::pack(s[2 * h][2], s[2 * h][3]);
-      bits[2] = E::pack(s[2 * h + 1][0], s[2 * h + 1][1]);
-      bits[3] = E::pack(s[2 * h + 1][2], s[2 * h + 1][3]);
-      pb[h] = __builtin_bit_cast(frag, bits);
-    }
-    // V^T fragment of dim tile dt and token half h: two transposed reads; lane
-    // j of a 16-lane group addresses dims 16 dt + 4 (j % 4) .. +3 of token
-    // 32 h + 4 g + j / 4 (first read) or that + 16 (second read).  Those dims
-    // are row chunk 2 dt + (j % 4) / 2, stored at (2 dt + (j % 4) / 2) ^ 2 (x % 8)
-    // = 2 (dt ^ (x % 8)) + (j % 4) / 2, so the byte offset is
-    //   lane_base + 8192 h (+ 4096) + ((dt ^ (x % 8)) << 5).
-    // Within 32 lanes (x % 8 takes all 8 values) the 16-byte slots are distinct:
-    // every bank is read once.
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt) {
-      const int dim_offset = v_lane + ((dt ^ x8) << 5);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const unsigned char *lo = v_stage + dim_offset + h * 32 * kChunksPerRow * 16;
-        const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)lo);
-        const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lo + 16 * kChunksPerRow * 16));
+      for (int st = 0; st < 2; ++st) {
         u32x4 bits;
-        bits[0] = __builtin_bit_cast(u32x2, a_lo)[0];
-        bits[1] = __builtin_bit_cast(u32x2, a_lo)[1];
-        bits[2] = __builtin_bit_cast(u32x2, a_hi)[0];
-        bits[3] = __builtin_bit_cast(u32x2, a_hi)[1];
-        o[dt] = E::mfma(__builtin_bit_cast(frag, bits), pb[h], o[dt]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bits[j] = E::pack(s[kb][8 * st + 2 * j], s[kb][8 * st + 2 * j + 1]);
+          l = E::dot2_ones(bits[j], l);
+        }
+        pb[2 * kb + st] = __builtin_bit_cast(frag, bits);
       }
     }
+    // V^T fragments of one step (four dim blocks, two transposed reads each),
+    // the next step's reads issued before this step's MFMAs.  Step 2 kb + st
+    // covers tokens 32 kb + 16 st + 4 h + (0..3) and, 8 further, the second read.
+    frag vf[2][kDimBlocks];
+    auto load_v = [&](int step, frag *dst) {
+      const int token_base = 16 * step * kRowBytes;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) lsum = E::mfma(ones, pb[h], lsum);
+      for (int b = 0; b < kDimBlocks; ++b) {
+        const unsigned char *lo = v_stage + v_addr + token_base + ((b ^ vu) << 6);
+        const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)lo);
+        const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lo + 8 * kRowBytes));
+        u32x4 va;
+        va[0] = __builtin_bit_cast(u32x2, a_lo)[0];
+        va[1] = __builtin_bit_cast(u32x2, a_lo)[1];
+        va[2] = __builtin_bit_cast(u32x2, a_hi)[0];
+        va[3] = __builtin_bit_cast(u32x2, a_hi)[1];
+        dst[b] = __builtin_bit_cast(frag, va);
+      }
+    };
+    load_v(0, vf[0]);
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+      if (step + 1 < 4) load_v(step + 1, vf[(step + 1) % 2]);
+#pragma unroll
+      for (int b = 0; b < kDimBlocks; ++b) o[b] = E::mfma32(vf[step % 2][b], pb[step], o[b]);
+    }
   }
-  const float l = lsum[0];
-  if (!computes) return;
-  if (partial < 0) {
+  // The column's other half (lane l ^ 32) summed the other tokens.
+  {
+    unsigned a = __builtin_bit_cast(unsigned, l), b = a;
+    permlane32_swap(a, b);
+    l = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  }
+  if (!mine.computes) return;
+  // Register r of dim block b holds dim 32 b + 8 (r / 4) + 4 h + r % 4.
+  if (mine.partial < 0) {
     if (!q_ok) return;
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 4 * g;
+    uint16_t *dst = p.out + (static_cast<long long>(mine.q_index + qc) * p.hq + mine.hq) * D + 4 * h;
 #pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt) {
-      u32x2 packed;
-      packed[0] = E::pack(o[dt][0] * inv, o[dt][1] * inv);
-      packed[1] = E::pack(o[dt][2] * inv, o[dt][3] * inv);
-      *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
-    }
+    for (int b = 0; b < kDimBlocks; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        u32x2 packed;
+        packed[0] = E::pack(o[b][4 * rr] * inv, o[b][4 * rr + 1] * inv);
+        packed[1] = E::pack(o[b][4 * rr + 2] * inv, o[b][4 * rr + 3] * inv);
+        *reinterpret_cast<u32x2 *>(dst + 32 * b + 8 * rr) = packed;
+      }
   } else {
-    float *block = partial_block<D>(p, partial, hq);
+    float *block = partial_block<D>(p, mine.partial, mine.hq);
 #pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt)
-      *reinterpret_cast<f32x4 *>(block + c * D + 16 * dt + 4 * g) = o[dt];
-    if (g == 0) {
-      block[kQueries * D + 2 * c] = m * scale_log2;
-      block[kQueries * D + 2 * c + 1] = l;
+    for (int b = 0; b < kDimBlocks; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        *reinterpret_cast<f32x4 *>(block + qc * D + 32 * b + 8 * rr + 4 * h) =
+            f32x4{o[b][4 * rr], o[b][4 * rr + 1], o[b][4 * rr + 2], o[b][4 * rr + 3]};
+    if (h == 0) {
+      block[kQueries * D + 2 * qc] = m * scale_log2;
+      block[kQueries * D + 2 * qc + 1] = l;
     }
   }
 }
@@ -909,18 +991,12 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     }
   }
   const int64_t n_tiles = static_cast<int64_t>(tiles.size());
-  int64_t work = 0;
   // Groups of up to per_item consecutive tiles of one request.
   auto group_end = [&](int64_t first) {
     int64_t last = first + 1;
     while (last < n_tiles && last - first < per_item && tiles[last].kv_offset == tiles[first].kv_offset) ++last;
     return last;
   };
-  for (int64_t first = 0; first < n_tiles; first = group_end(first)) {
-    int64_t needed = 0;
-    for (int64_t t = first; t < group_end(first); ++t) needed = tiles[t].needed > needed ? tiles[t].needed : needed;
-    work += needed;
-  }
   int64_t split = split_tokens;
   if (split == 0) {
     // Pick the chunk length whose plan finishes first on a model of the
@@ -1106,8 +1182,8 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   const dim3 staged(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
-    if (f16) repair_attention_dma_kernel<F16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
-    else repair_attention_dma_kernel<Bf16><<<grid, dim3(kDmaThreads), 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    else repair_attention_m32_kernel<Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
   } else if (a->head_dim == 64) {
     if (f16) repair_attention_kernel<64, F16><<<grid, staged, 0, s>>>(p);
     else repair_attention_kernel<64, Bf16><<<grid, staged, 0, s>>>(p);
