@@ -62,6 +62,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--repair-attention", action="store_true",
                         help="time the sparse repair attention of the workload's repair spans "
                              "(one layer) instead of the link")
+    parser.add_argument("--tp", type=int, default=1,
+                        help="bench one tensor-parallel rank's share: kv_heads / tp heads of every layer "
+                             "(the link has no exchange step; each rank links its own head shard)")
     parser.add_argument("--storage", choices=["reference", "clone"], default="reference",
                         help="blocks read from pool slots (reference) or captured into a snapshot arena and "
                              "linked from it (clone); clone also times the capture and a group promotion")
@@ -286,9 +289,11 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
     from legolink_amd.workloads import make_workload
 
     device = torch.device("cuda", 0)
-    workload = make_workload(args.workload)
+    full = make_workload(args.workload)
+    group = 7 if full.shape.kv_heads == 4 else 8  # Qwen2.5-7B: 28 / 4; Qwen3-32B: 64 / 8
+    workload = tp_share(full, args.tp)
     shape = workload.shape
-    q_heads = 28 if shape.kv_heads == 4 else 64  # Qwen2.5-7B: 28 / 4; Qwen3-32B: 64 / 8
+    q_heads = group * shape.kv_heads
     generator = torch.Generator(device=device).manual_seed(20260824)
     key = torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, generator=generator,
                       device=device).to(torch.bfloat16)
@@ -352,6 +357,22 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
                      "kv_gather_GBps": round(kv_bytes / (ms / 1e3) / 1e9, 1)},
         "cpu_baseline": baseline,
     }), flush=True)
+
+
+def tp_share(workload, tp: int):
+    """The workload as one tensor-parallel rank sees it: kv_heads / tp heads of
+    every layer, the same tokens, slots and positions."""
+
+    import dataclasses
+
+    if tp < 1 or workload.shape.kv_heads % tp:
+        raise SystemExit(f"--tp {tp} must divide the {workload.shape.kv_heads} KV heads of {workload.name}")
+    if tp == 1:
+        return workload
+    shape = dataclasses.replace(workload.shape, kv_heads=workload.shape.kv_heads // tp)
+    return dataclasses.replace(workload, shape=shape,
+                               description=f"{workload.description}; TP rank share: {shape.kv_heads} "
+                                           f"of {workload.shape.kv_heads} KV heads")
 
 
 def cpu_attention_baseline(spans, query, key, value, q_heads: int, head_dim: int, gflop_budget: float) -> dict:
@@ -430,7 +451,7 @@ def main() -> int:
 
     device = torch.device("cuda", 0)
     host_start = time.perf_counter()
-    workload = make_workload(args.workload)
+    workload = tp_share(make_workload(args.workload), args.tp)
     shape = workload.shape
     log(f"workload {workload.name}: {workload.description}")
     keys, values = [], []
@@ -591,7 +612,7 @@ def main() -> int:
     value = total_bytes / (ms_per_step / 1e3) / 1e9
     link_avg_ms = float(np.mean(link_ms))
     achieved = bytes_info["link_bytes"] / (link_avg_ms / 1e3) / 1e9
-    traffic = load_traffic(workload.name, bytes_info["link_bytes"])
+    traffic = load_traffic(workload.name, bytes_info["link_bytes"]) if args.tp == 1 else None
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -617,6 +638,7 @@ def main() -> int:
             "requests": workload.requests,
             "prefix_token_count": workload.prefix_token_count,
             "algorithmic_bytes_per_step": total_bytes,
+            "tp_share": f"1/{args.tp} of the KV heads (one rank's head shard)" if args.tp > 1 else None,
         },
         "tokens_linked_per_s": round(workload.tokens / (ms_per_step / 1e3), 1),
         "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
