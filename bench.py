@@ -360,19 +360,10 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
 
 
 def tp_share(workload, tp: int):
-    """The workload as one tensor-parallel rank sees it: kv_heads / tp heads of
-    every layer, the same tokens, slots and positions."""
-
-    import dataclasses
-
-    if tp < 1 or workload.shape.kv_heads % tp:
-        raise SystemExit(f"--tp {tp} must divide the {workload.shape.kv_heads} KV heads of {workload.name}")
-    if tp == 1:
-        return workload
-    shape = dataclasses.replace(workload.shape, kv_heads=workload.shape.kv_heads // tp)
-    return dataclasses.replace(workload, shape=shape,
-                               description=f"{workload.description}; TP rank share: {shape.kv_heads} "
-                                           f"of {workload.shape.kv_heads} KV heads")
+    try:
+        return workload.rank_share(tp)
+    except ValueError as error:
+        raise SystemExit(f"--tp: {error}")
 
 
 def cpu_attention_baseline(spans, query, key, value, q_heads: int, head_dim: int, gflop_budget: float) -> dict:

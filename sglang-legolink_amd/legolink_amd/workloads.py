@@ -20,6 +20,7 @@ prefix); delta_b is clipped to <= start_b so that local = global - delta >= 0.
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -69,6 +70,20 @@ class LinkWorkload:
     theta: float = 1_000_000.0
     seed: int = BASE_SEED
     notes: dict = field(default_factory=dict)
+
+    def rank_share(self, tp: int) -> "LinkWorkload":
+        """The workload as one of ``tp`` tensor-parallel ranks sees it: kv_heads / tp
+        heads of every layer (the ranks' shards of srt/models/qwen2.py:127-141),
+        the same tokens, slots and positions."""
+
+        if tp < 1 or self.shape.kv_heads % tp:
+            raise ValueError(f"tp {tp} must divide the {self.shape.kv_heads} KV heads of {self.name}")
+        if tp == 1:
+            return self
+        shape = dataclasses.replace(self.shape, kv_heads=self.shape.kv_heads // tp)
+        return dataclasses.replace(self, shape=shape,
+                                   description=f"{self.description}; TP rank share: {shape.kv_heads} "
+                                               f"of {self.shape.kv_heads} KV heads")
 
     @property
     def tokens(self) -> int:

@@ -77,6 +77,20 @@ def test_algorithmic_bytes():
     assert c4.shape.bytes_per_token == 524_288
 
 
+def test_rank_share_keeps_tokens_and_divides_heads():
+    c4 = make_workload("c4")
+    for tp in (1, 2, 4, 8):
+        share = c4.rank_share(tp)
+        assert share.shape.kv_heads == 8 // tp and share.shape.layers == 64
+        assert np.array_equal(share.source_slots, c4.source_slots)
+        assert np.array_equal(share.global_positions, c4.global_positions)
+        assert share.algorithmic_bytes()["total_bytes"] * tp == c4.algorithmic_bytes()["total_bytes"]
+    with pytest.raises(ValueError, match="must divide"):
+        c4.rank_share(3)
+    with pytest.raises(ValueError, match="must divide"):
+        make_workload("c2").rank_share(8)
+
+
 def test_block_length_ranges():
     assert all(256 <= n <= 4096 for n in make_workload("c2").block_lengths)
     assert all(512 <= n <= 2048 for n in make_workload("c4").block_lengths)
