@@ -279,8 +279,9 @@ typedef struct ll_link_maps_args {
  * query head h reads KV head h / G:
  *     out[query_index + i][h] = sum_j softmax_j(scale * q . K[slot_j][h / G]) V[slot_j][h / G]
  * The softmax is computed online in fp32 with exp2; scores and probabilities
- * come from bf16 MFMA products accumulated in fp32 (probabilities are rounded
- * to bf16 for the value product), and the output is rounded once to bf16.
+ * come from bf16 (or fp16) MFMA products accumulated in fp32 (probabilities
+ * are rounded to the KV dtype for the value product), and the output is
+ * rounded once to the KV dtype.
  * Slots outside [0, num_slots) are invisible (never read).
  *
  * Two phases, like the reference's plan/run wrapper:
@@ -289,8 +290,9 @@ typedef struct ll_link_maps_args {
  *   kv_offset -- share a tile, so short repair spans fill it; rows must not
  *   overlap), writes every query's logical position into the positions
  *   table, groups consecutive tiles of one request into work items
- *   that share every staged K/V tile (as many tiles as 16 waves hold: 2 for 7
- *   or 8 query heads per KV head, 1 above 8), splits long KV ranges into chunks of
+ *   that share every staged K/V tile (as many tiles as 16 (tile, query head)
+ *   pairs allow: 2 for 7 or 8 query heads per KV head, 1 above 8), splits
+ *   long KV ranges into chunks of
  *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
  *   from a model of the device's workgroup rounds), and writes the item and
  *   combine tables; the caller copies them to the device once and reuses them
