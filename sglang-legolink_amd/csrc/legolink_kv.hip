@@ -58,6 +58,7 @@ constexpr int kLayerUnroll = LL_LAYER_UNROLL;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // Kernel parameters (passed by value in the kernarg segment; the per-layer
@@ -196,7 +197,17 @@ __device__ __forceinline__ void store_row_chunk(char *address, u32x4 value) {
 // Neox: x holds 8 elements of this lane's half, y the same 8 dims of the other
 // half.  out = x*dc + y*dsn, with dsn = -ds in the first half and +ds in the
 // second half:  first' = first*dc - second*ds,  second' = second*dc + first*ds.
-template <bool kBF16>
+// kChain (bf16 K with a bf16/fp16 cache): each product rounded to bf16 before
+// the sum, as the reference's bf16 arithmetic does; otherwise fp32 throughout.
+// RNE is symmetric under negation, so rounding y * dsn equals negating the
+// rounded y * ds.
+template <bool kChain>
+__device__ __forceinline__ float rot_term(float a, float b) {
+  if constexpr (kChain) return round_bf16(a * b);
+  else return a * b;
+}
+
+template <bool kBF16, bool kChain>
 __device__ __forceinline__ u32x4 rotate_neox(u32x4 x, u32x4 y, const float *dc,
                                              const float *dsn) {
   u32x4 out;
@@ -206,26 +217,60 @@ __device__ __forceinline__ u32x4 rotate_neox(u32x4 x, u32x4 y, const float *dc,
     const float x1 = hi_elem<kBF16>(x[w]);
     const float y0 = lo_elem<kBF16>(y[w]);
     const float y1 = hi_elem<kBF16>(y[w]);
-    const float r0 = x0 * dc[2 * w] + y0 * dsn[2 * w];
-    const float r1 = x1 * dc[2 * w + 1] + y1 * dsn[2 * w + 1];
+    const float r0 = rot_term<kChain>(x0, dc[2 * w]) + rot_term<kChain>(y0, dsn[2 * w]);
+    const float r1 = rot_term<kChain>(x1, dc[2 * w + 1]) + rot_term<kChain>(y1, dsn[2 * w + 1]);
     out[w] = pack2<kBF16>(r0, r1);
   }
   return out;
 }
 
 // GPT-J style: every 32-bit word holds one (first, second) pair.
-template <bool kBF16>
+template <bool kBF16, bool kChain>
 __device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const float *ds) {
   u32x4 out;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const float a = lo_elem<kBF16>(x[w]);
     const float b = hi_elem<kBF16>(x[w]);
-    const float r0 = a * dc[w] - b * ds[w];
-    const float r1 = b * dc[w] + a * ds[w];
+    const float r0 = rot_term<kChain>(a, dc[w]) - rot_term<kChain>(b, ds[w]);
+    const float r1 = rot_term<kChain>(b, dc[w]) + rot_term<kChain>(a, ds[w]);
     out[w] = pack2<kBF16>(r0, r1);
   }
   return out;
+}
+
+// N consecutive cos/sin table entries from element `offset`, widened to fp32
+// (exactly: bf16 and fp16 values are fp32 values).  kCache: 1 = fp16,
+// 2 = bf16, 3 = fp32.  The address is 16-byte aligned (8-byte for four
+// 16-bit entries).
+template <int kCache, int N>
+__device__ __forceinline__ void load_table(const void *cs, long long offset, float *out) {
+  if constexpr (kCache == 3) {
+#pragma unroll
+    for (int e = 0; e < N; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(cs) + offset + e);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[e + k] = v[k];
+    }
+  } else {
+    const uint16_t *base = static_cast<const uint16_t *>(cs) + offset;
+    uint32_t w[N / 2];
+    if constexpr (N == 8) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(base);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = v[k];
+    } else {
+      static_assert(N == 4, "four or eight entries");
+      const u32x2 v = *reinterpret_cast<const u32x2 *>(base);
+      w[0] = v[0];
+      w[1] = v[1];
+    }
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+      out[2 * k] = lo_elem<kCache == 2>(w[k]);
+      out[2 * k + 1] = hi_elem<kCache == 2>(w[k]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -237,14 +282,18 @@ __device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const flo
 //   CU's L1 instead of being fetched once per layer group.
 //   grid.x = chunk-waves / (W / G), grid.y = layer groups / G.
 // Requirements (checked on the host): key_head_dim == value_head_dim ==
-// rotary_dim == kD, fp32 cos/sin cache with unit column stride and 16-byte
-// aligned rows, 16-byte aligned layer buffers.
+// rotary_dim == kD, an fp32, bf16 or fp16 cos/sin cache (kCache) with unit
+// column stride and 16-byte aligned rows, 16-byte aligned layer buffers.
 // ---------------------------------------------------------------------------
-template <bool kBF16, int kD, bool kNeox, typename Index>
+template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache>
 __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   constexpr int kChunksPerHead = kD / 8;
+  constexpr int kRotChunks = kR / 8;     // chunks of a head that rotate; the rest are copied
   constexpr int kPairs = kNeox ? 8 : 4;  // rotary pairs touched by one lane
-  constexpr int kHalf = kD / 2;
+  // bf16 K with a 16-bit cache follows the reference's bf16-rounded chain.
+  constexpr bool kChain = kBF16 && kCache != 3;
+  constexpr int kHalf = kR / 2;
+  static_assert(kR == kD || kR * 2 == kD, "full or half rotary");
 
   const int lane = threadIdx.x & (kWave - 1);
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
@@ -266,6 +315,7 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   // Chunk index inside the head; chunks_per_row is a multiple of
   // kChunksPerHead and kChunksPerHead divides 64, so this is lane-aligned.
   const int q = lane % kChunksPerHead;
+  const bool rotating = kR == kD || q < kRotChunks;
 
   // The token's maps: five independent loads with no branch between them, so
   // they are in flight together (t < num_tokens always holds).  Without a
@@ -319,25 +369,30 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     const bool use = remap && positions_ok;
     const long long lrow_index = use ? lp : 0;
     const long long grow_index = use ? gp : 0;
-    const int pb = kNeox ? (q % (kChunksPerHead / 2)) * 8 : q * 4;
-    const float *lrow = static_cast<const float *>(p.cs) + lrow_index * p.cs_stride_row + pb;
-    const float *grow = static_cast<const float *>(p.cs) + grow_index * p.cs_stride_row + pb;
+    // Lanes past the rotary dims read the first pairs' entries (unused), so
+    // the reads stay inside the row.
+    const int pb = kNeox ? (q % (kRotChunks / 2)) * 8 : (rotating ? q : 0) * 4;
+    const long long lrow = lrow_index * p.cs_stride_row + pb;
+    const long long grow = grow_index * p.cs_stride_row + pb;
+    float lc[kPairs], ls[kPairs], gc[kPairs], gs[kPairs];
+    load_table<kCache, kPairs>(p.cs, lrow, lc);
+    load_table<kCache, kPairs>(p.cs, lrow + kHalf, ls);
+    load_table<kCache, kPairs>(p.cs, grow, gc);
+    load_table<kCache, kPairs>(p.cs, grow + kHalf, gs);
 #pragma unroll
-    for (int e = 0; e < kPairs; e += 4) {
-      const f32x4 lc = *reinterpret_cast<const f32x4 *>(lrow + e);
-      const f32x4 ls = *reinterpret_cast<const f32x4 *>(lrow + kHalf + e);
-      const f32x4 gc = *reinterpret_cast<const f32x4 *>(grow + e);
-      const f32x4 gs = *reinterpret_cast<const f32x4 *>(grow + kHalf + e);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        dc[e + k] = gc[k] * lc[k] + gs[k] * ls[k];
-        ds[e + k] = gs[k] * lc[k] - gc[k] * ls[k];
+    for (int e = 0; e < kPairs; ++e) {
+      if constexpr (kChain) {
+        dc[e] = round_bf16(round_bf16(gc[e] * lc[e]) + round_bf16(gs[e] * ls[e]));
+        ds[e] = round_bf16(round_bf16(gs[e] * lc[e]) - round_bf16(gc[e] * ls[e]));
+      } else {
+        dc[e] = gc[e] * lc[e] + gs[e] * ls[e];
+        ds[e] = gs[e] * lc[e] - gc[e] * ls[e];
       }
     }
   }
   float dsn[kPairs];
   if constexpr (kNeox) {
-    const bool second_half = q >= kChunksPerHead / 2;
+    const bool second_half = q >= kRotChunks / 2;
 #pragma unroll
     for (int e = 0; e < kPairs; ++e) dsn[e] = second_half ? ds[e] : -ds[e];
   }
@@ -356,10 +411,10 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
       u32x4 kout = kin[u];
       if constexpr (kNeox) {
         // Every lane takes part in the exchange (uniform control flow here).
-        const u32x4 partner = xor_lane4<kChunksPerHead / 2>(kin[u]);
-        if (remap) kout = rotate_neox<kBF16>(kin[u], partner, dc, dsn);
+        const u32x4 partner = xor_lane4<kRotChunks / 2>(kin[u]);
+        if (remap && rotating) kout = rotate_neox<kBF16, kChain>(kin[u], partner, dc, dsn);
       } else {
-        if (remap) kout = rotate_gptj<kBF16>(kin[u], dc, ds);
+        if (remap && rotating) kout = rotate_gptj<kBF16, kChain>(kin[u], dc, ds);
       }
       if (ok && l + u < l1) {
         store_row_chunk(p.k_layers[l + u] + k_dst, kout);
@@ -656,9 +711,11 @@ bool vector_kernel_fits(const ll_kv_link_args *a) {
       a->global_positions_dtype != a->source_slots_dtype)
     return false;
   if (!(d == 32 || d == 64 || d == 128 || d == 256)) return false;
-  if (a->value_head_dim != d || a->rotary_dim != d) return false;
-  if (a->cos_sin_dtype != LL_DTYPE_FLOAT32 || a->cos_sin_stride_col != 1) return false;
-  if ((a->cos_sin_stride_row % 4) != 0 || !aligned16(a->cos_sin_cache)) return false;
+  if (a->value_head_dim != d) return false;
+  if (a->rotary_dim != d && !(a->rotary_dim * 2 == d && d >= 32)) return false;
+  if (a->cos_sin_stride_col != 1 || !aligned16(a->cos_sin_cache)) return false;
+  // Rows 16-byte aligned: 4 fp32 or 8 16-bit entries per 16 bytes.
+  if ((a->cos_sin_stride_row % (a->cos_sin_dtype == LL_DTYPE_FLOAT32 ? 4 : 8)) != 0) return false;
   for (int64_t l = 0; l < a->num_layers; ++l)
     if (!aligned16(a->key_layers[l]) || !aligned16(a->value_layers[l])) return false;
   if (a->source_key_layers != nullptr)
@@ -690,9 +747,9 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   const bool fits = vector_kernel_fits(a);
   if (a->kernel == LL_KERNEL_VECTOR && !fits)
     return fail(LL_ERR_UNSUPPORTED_KERNEL,
-                "vector kernel needs key_head_dim == value_head_dim == rotary_dim in "
-                "{32,64,128,256}, one index type for the four token maps, an fp32 "
-                "unit-stride cache and 16-byte aligned buffers");
+                "vector kernel needs key_head_dim == value_head_dim in {32,64,128,256}, "
+                "rotary_dim equal to it or half of it, one index type for the four token maps, a unit-stride "
+                "cache with 16-byte aligned rows and 16-byte aligned buffers");
   plan->kernel = (a->kernel == LL_KERNEL_GENERIC || !fits) ? LL_KERNEL_GENERIC : LL_KERNEL_VECTOR;
   const int waves_per_block = a->waves_per_block ? static_cast<int>(a->waves_per_block) : 4;
   plan->block_threads = waves_per_block * kWave;
@@ -729,25 +786,41 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   return LL_OK;
 }
 
-template <bool kBF16, int kD>
+template <bool kBF16, int kD, int kR, int kCache>
 void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   const bool index64 = (p.idx64 & 15) == 15;  // the vector kernel needs one index type
   if (neox) {
-    if (index64) kv_link_vec_kernel<kBF16, kD, true, long long><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, true, int><<<grid, block, 0, s>>>(p);
+    if (index64) kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache><<<grid, block, 0, s>>>(p);
   } else {
-    if (index64) kv_link_vec_kernel<kBF16, kD, false, long long><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, false, int><<<grid, block, 0, s>>>(p);
+    if (index64) kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache><<<grid, block, 0, s>>>(p);
+  }
+}
+
+template <bool kBF16, int kD, int kCache>
+void launch_vec_rotary(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+  if (p.rotary_dim == kD) launch_vec_neox<kBF16, kD, kD, kCache>(grid, block, s, p, neox);
+  else launch_vec_neox<kBF16, kD, kD / 2, kCache>(grid, block, s, p, neox);
+}
+
+template <bool kBF16, int kCache>
+void launch_vec_dim(int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+  switch (d) {
+    case 32: launch_vec_rotary<kBF16, 32, kCache>(grid, block, s, p, neox); break;
+    case 64: launch_vec_rotary<kBF16, 64, kCache>(grid, block, s, p, neox); break;
+    case 128: launch_vec_rotary<kBF16, 128, kCache>(grid, block, s, p, neox); break;
+    default: launch_vec_rotary<kBF16, 256, kCache>(grid, block, s, p, neox); break;
   }
 }
 
 template <bool kBF16>
-void launch_vec(int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
-  switch (d) {
-    case 32: launch_vec_neox<kBF16, 32>(grid, block, s, p, neox); break;
-    case 64: launch_vec_neox<kBF16, 64>(grid, block, s, p, neox); break;
-    case 128: launch_vec_neox<kBF16, 128>(grid, block, s, p, neox); break;
-    default: launch_vec_neox<kBF16, 256>(grid, block, s, p, neox); break;
+void launch_vec(int cache_dtype, int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p,
+                bool neox) {
+  switch (cache_dtype) {
+    case LL_DTYPE_FLOAT32: launch_vec_dim<kBF16, 3>(d, grid, block, s, p, neox); break;
+    case LL_DTYPE_BFLOAT16: launch_vec_dim<kBF16, 2>(d, grid, block, s, p, neox); break;
+    default: launch_vec_dim<kBF16, 1>(d, grid, block, s, p, neox); break;
   }
 }
 
@@ -890,8 +963,9 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
       const dim3 grid(static_cast<unsigned>(plan.grid_x),
                       static_cast<unsigned>((layer_groups + plan.layer_groups_per_block - 1) /
                                             plan.layer_groups_per_block));
-      if (bf16) launch_vec<true>(p.kdim, grid, block, s, p, p.neox != 0);
-      else launch_vec<false>(p.kdim, grid, block, s, p, p.neox != 0);
+      const int cache = static_cast<int>(a->cos_sin_dtype);
+      if (bf16) launch_vec<true>(cache, p.kdim, grid, block, s, p, p.neox != 0);
+      else launch_vec<false>(cache, p.kdim, grid, block, s, p, p.neox != 0);
     } else {
       p.layers_per_wave = 1;
       p.layer_groups_per_block = 1;

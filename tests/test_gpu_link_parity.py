@@ -42,10 +42,22 @@ CASES = [
     ("fp16_vec", torch.float16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 0, 0.1, 2, 150, "vector"),
     ("fp16_generic", torch.float16, torch.float32, 4, 128, 128, 128, True, GENERIC, torch.int64, 0, 0.1, 2, 150, "generic"),
     ("fp16_gptj_d64", torch.float16, torch.float32, 2, 64, 64, 64, False, AUTO, torch.int32, 0, 0.1, 2, 150, "vector"),
-    ("bf16_key_bf16_cache", torch.bfloat16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
-    ("bf16_key_fp16_cache", torch.bfloat16, torch.float16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
-    ("fp16_key_bf16_cache", torch.float16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "generic"),
-    ("partial_rotary", torch.bfloat16, torch.float32, 4, 128, 128, 64, True, AUTO, torch.int64, 0, 0.1, 2, 150, "generic"),
+    # 16-bit cos/sin tables: widened exactly to fp32, then the same arithmetic.
+    ("bf16_key_bf16_cache", torch.bfloat16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "vector"),
+    ("bf16_key_fp16_cache", torch.bfloat16, torch.float16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "vector"),
+    ("fp16_key_bf16_cache", torch.float16, torch.bfloat16, 4, 128, 128, 128, True, AUTO, torch.int64, 4, 0.1, 2, 150, "vector"),
+    ("bf16_cache_gptj_d64", torch.bfloat16, torch.bfloat16, 2, 64, 64, 64, False, AUTO, torch.int32, 3, 0.1, 2, 150, "vector"),
+    ("fp16_cache_d256", torch.bfloat16, torch.float16, 2, 256, 256, 256, True, AUTO, torch.int64, 0, 0.1, 2, 90, "vector"),
+    ("bf16_cache_gptj_d32", torch.float16, torch.bfloat16, 4, 32, 32, 32, False, AUTO, torch.int64, 2, 0.1, 2, 150, "vector"),
+    ("bf16_key_bf16_cache_generic", torch.bfloat16, torch.bfloat16, 4, 128, 128, 128, True, GENERIC, torch.int64, 4, 0.1, 2, 150, "generic"),
+    ("fp16_key_fp16_cache_generic", torch.float16, torch.float16, 4, 128, 128, 128, False, GENERIC, torch.int64, 4, 0.1, 2, 150, "generic"),
+    # Half rotary (dims past rotary_dim copied): the vector kernel; other partial widths: generic.
+    ("partial_rotary", torch.bfloat16, torch.float32, 4, 128, 128, 64, True, AUTO, torch.int64, 0, 0.1, 2, 150, "vector"),
+    ("half_rotary_gptj_bf16_cache", torch.bfloat16, torch.bfloat16, 2, 128, 128, 64, False, AUTO, torch.int32, 3, 0.1, 2, 150, "vector"),
+    ("half_rotary_d32_fp16", torch.float16, torch.float32, 4, 32, 32, 16, True, AUTO, torch.int64, 2, 0.1, 2, 150, "vector"),
+    ("half_rotary_d256_gptj", torch.bfloat16, torch.float16, 2, 256, 256, 128, False, VECTOR, torch.int64, 0, 0.1, 2, 90, "vector"),
+    ("partial_rotary_generic", torch.bfloat16, torch.float32, 4, 128, 128, 64, True, GENERIC, torch.int64, 0, 0.1, 2, 150, "generic"),
+    ("quarter_rotary", torch.bfloat16, torch.float32, 4, 128, 128, 32, True, AUTO, torch.int64, 0, 0.1, 2, 150, "generic"),
     ("value_dim_differs", torch.bfloat16, torch.float32, 2, 128, 64, 128, True, AUTO, torch.int64, 0, 0.1, 2, 150, "generic"),
     ("odd_dims_gptj", torch.bfloat16, torch.float32, 3, 40, 24, 16, False, AUTO, torch.int64, 2, 0.1, 2, 150, "generic"),
     ("prefix_is_everything", torch.bfloat16, torch.float32, 4, 128, 128, 128, True, AUTO, torch.int64, 150, 0.0, 2, 150, "vector"),

@@ -108,8 +108,12 @@ def test_kernel_choice_and_launch_shape():
     assert info.block_threads == 256 and info.grid_x == 32768 // 4
     assert info.layers_per_wave == 2 and info.grid_y == 1  # capped by the two layers of the CPU pool
     del keepalive
-    # Partial rotary falls back to the generic kernel; forcing the vector kernel fails.
+    # Half rotary stays on the vector kernel; other partial widths fall back to
+    # the generic kernel, and forcing the vector kernel on them fails.
     args, keepalive = _cpu_args(rotary_dim=64)
+    assert _native.kv_link_describe(args).kernel == _native.KERNEL_VECTOR
+    del keepalive
+    args, keepalive = _cpu_args(rotary_dim=32)
     assert _native.kv_link_describe(args).kernel == _native.KERNEL_GENERIC
     args.kernel = _native.KERNEL_VECTOR
     with pytest.raises(_native.NativeCallError) as error:
