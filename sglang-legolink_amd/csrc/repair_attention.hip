@@ -23,9 +23,9 @@
 //      accumulators (the token order inside the K step is free, as long as
 //      A uses the same one), A = V^T from transposed LDS reads.
 //
-// Head dim 128 runs repair_attention_m32_kernel: two pairs per wave on
+// Head dims 64 and 128 run repair_attention_m32_kernel: two pairs per wave on
 // v_mfma_f32_32x32x16, rows gathered into an LDS ring by global_load_lds.
-// Head dims 64 and 256 run repair_attention_kernel: one pair per wave on
+// Head dim 256 runs repair_attention_kernel: one pair per wave on
 // v_mfma_f32_16x16x32, each tile staged through registers.  Its lane layouts
 // (checked on the device): A/B lane l element e -> row/column l % 16,
 // k = 8 (l / 16) + e; accumulator register r -> row 4 (l / 16) + r, column
@@ -479,7 +479,7 @@ __device__ inline void workgroup_barrier() {
 }
 
 
-// Head dim 128 on v_mfma_f32_32x32x16 (issues at ~34 cycles for twice the work
+// Head dims 64 and 128 on v_mfma_f32_32x32x16 (issues at ~34 cycles for twice the work
 // of a 16x16x32 at ~20, and hides about four VALU instructions in the wave
 // that issued it, against two).  Each wave owns two (query tile, head) pairs,
 // 32 MFMA columns: column n = 16 (pair - 2 wave) + query.  Lane layouts
@@ -494,18 +494,28 @@ __device__ inline void workgroup_barrier() {
 //   reads giving each lane one dim of that token order.
 // Each lane sums its bf16/fp16 probabilities with v_dot2 against ones (the
 // values the value product sees); the two lanes of a column add at the end.
-// K rows keep the chunk swizzle c ^ (t % 16); V rows use c ^ 4 (t % 4), under
-// which the 32 lanes of one transposed read (4 tokens x 64 bytes) cover the 64
-// banks once.  Each of the 8 waves issues four of a tile's 32 gathers.
+// Chunk swizzles (chunk c of token t is stored at c ^ swizzle(t)), chosen so
+// that the 16 lanes of a K read (16 tokens, one chunk each) and the 32 lanes
+// of a transposed V read (4 tokens x 64 bytes) each cover the 64 banks once:
+//   head dim 128 (256-byte rows): K c ^ (t % 16), V c ^ 4 (t % 4);
+//   head dim 64 (128-byte rows, two per bank row): K c ^ ((t / 2) % 8),
+//   V c ^ 4 ((t / 2) % 2).
+// Each of the 8 waves issues 1/8 of a tile's K and V gathers.
 constexpr int kM32Threads = 512;
 
-template <typename E>
+template <int D>
+__host__ __device__ constexpr int m32_k_swizzle(int t) { return D == 128 ? t % 16 : (t / 2) % 8; }
+template <int D>
+__host__ __device__ constexpr int m32_v_swizzle(int t) { return D == 128 ? 4 * (t % 4) : 4 * ((t / 2) % 2); }
+
+template <int D, typename E>
 __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const AttnParams p) {
   typedef typename E::frag frag;
-  constexpr int D = 128;
+  static_assert(D == 64 || D == 128, "head dims 64 and 128");
   constexpr int kKSteps = D / 16;                        // 16-dim steps of the score MFMAs
   constexpr int kDimBlocks = D / 32;                     // 32-dim blocks of O^T
-  constexpr int kChunksPerRow = D / 8;                   // 16-byte chunks per row: 16
+  constexpr int kChunksPerRow = D / 8;                   // 16-byte chunks per row
+  constexpr int kGathers = kChunksPerRow / (kM32Threads / kWave);  // per wave, per tile, of K and of V
   constexpr int kRowBytes = D * 2;
   constexpr int kStageBytes = kTile * kRowBytes;         // one K or V tile: 16 KB
   constexpr int kRangeTiles = kDmaMaxRange / kTile;
@@ -606,21 +616,21 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
   // (P % 16) ^ swizzle(token) (each swizzle is its own inverse).
   const long long row_stride = static_cast<long long>(p.hkv) * D;
   const bool have_slots = p.num_slots > 0;
-  int g_token[2], g_kchunk[2], g_vchunk[2];
+  int g_token[kGathers], g_kchunk[kGathers], g_vchunk[kGathers];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int chunk_index = (2 * wave + j) * kWave + lane;
+  for (int j = 0; j < kGathers; ++j) {
+    const int chunk_index = (kGathers * wave + j) * kWave + lane;
     g_token[j] = chunk_index / kChunksPerRow;
-    g_kchunk[j] = (chunk_index % kChunksPerRow) ^ (g_token[j] % 16);
-    g_vchunk[j] = (chunk_index % kChunksPerRow) ^ (4 * (g_token[j] % 4));
+    g_kchunk[j] = (chunk_index % kChunksPerRow) ^ m32_k_swizzle<D>(g_token[j]);
+    g_vchunk[j] = (chunk_index % kChunksPerRow) ^ m32_v_swizzle<D>(g_token[j]);
   }
   auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kGathers; ++j) {
       const int slot = max(slot_lds[t * kTile + g_token[j]], 0);
       const long long row = slot * row_stride + hk * D;
-      const int offset = (2 * wave + j) * kWave * 16;
+      const int offset = (kGathers * wave + j) * kWave * 16;
       dma_pair(p.k + row + g_kchunk[j] * 8, k_dst + offset, p.v + row + g_vchunk[j] * 8, v_dst + offset);
     }
   };
@@ -655,8 +665,9 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
   for (int t = 0; t < tiles; ++t) {
     const unsigned char *k_stage = k_ring + (t % kDmaStages) * kStageBytes;
     unsigned char *v_stage = v_ring + (t % kDmaStages) * kStageBytes;
-    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF78);       // vmcnt(8)
-    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4)
+    // 2 kGathers loads per tile and wave: vmcnt(4 kGathers) or vmcnt(2 kGathers).
+    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (4 * kGathers));
+    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kGathers));
     else __builtin_amdgcn_s_waitcnt(0xF70);                     // vmcnt(0)
     workgroup_barrier();
     if (t + 3 < tiles)
@@ -688,7 +699,7 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
     auto load_k = [&](int batch, frag *dst) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int chunk = (2 * (2 * batch + j) + h) ^ (col % 16);
+        const int chunk = (2 * (2 * batch + j) + h) ^ m32_k_swizzle<D>(col);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
           dst[2 * j + kb] = *reinterpret_cast<const frag *>(k_stage + k_addr + kb * 32 * kRowBytes + chunk * 16);
@@ -775,7 +786,7 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
       const int token_base = 16 * step * kRowBytes;
 #pragma unroll
       for (int b = 0; b < kDimBlocks; ++b) {
-        const unsigned char *lo = v_stage + v_addr + token_base + ((b ^ vu) << 6);
+        const unsigned char *lo = v_stage + v_addr + token_base + ((b ^ (m32_v_swizzle<D>(vu) / 4)) << 6);
         const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)lo);
         const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lo + 8 * kRowBytes));
         u32x4 va;
@@ -1182,11 +1193,11 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   const dim3 staged(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
-    if (f16) repair_attention_m32_kernel<F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
-    else repair_attention_m32_kernel<Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
   } else if (a->head_dim == 64) {
-    if (f16) repair_attention_kernel<64, F16><<<grid, staged, 0, s>>>(p);
-    else repair_attention_kernel<64, Bf16><<<grid, staged, 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
   } else {
     if (f16) repair_attention_kernel<256, F16><<<grid, staged, 0, s>>>(p);
     else repair_attention_kernel<256, Bf16><<<grid, staged, 0, s>>>(p);
