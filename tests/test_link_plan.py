@@ -242,3 +242,9 @@ def test_batched_capture_rejects_before_any_registration():
     with pytest.raises(ValueError, match="slot count"):
         executor.capture_blocks(pool, [{"cache_key": "t", "token_ids": [1, 2, 3], "slots": [0]}])
     assert registry.get_legolink_block_tokens("t") is None
+    # A key registered twice in one batch: the entries before it are evicted again.
+    with pytest.raises(ValueError, match="already registered"):
+        executor.capture_blocks(pool, [{"cache_key": "u", "token_ids": [1], "slots": [9]},
+                                       {"cache_key": "u", "token_ids": [2], "slots": [10]}])
+    assert registry.get_legolink_block_tokens("u") is None
+    assert registry.get_legolink_block_tokens("r") == (1, 2)  # earlier blocks untouched
