@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 7
+#define LL_ABI_VERSION 8
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -165,6 +165,12 @@ typedef struct ll_kv_link_args {
                                       read sources from key_layers */
   void *const *source_value_layers;/* host array [num_layers], or NULL (with source_key_layers) */
   int64_t source_num_slots;        /* rows of every source buffer (when the tables are set) */
+  int64_t stream_source_rows;      /* 1: each source row is read once (no reuse within the launch)
+                                      and the rows exceed the caches: the vector kernel's
+                                      full-rotary fp32-table variants read them with non-temporal
+                                      loads (+1-2 % on random rows); 0: rows may repeat (batched
+                                      requests sharing blocks) or be cache-resident and stay
+                                      cacheable.  The result is the same either way.  (ABI 8) */
 } ll_kv_link_args;
 
 /*

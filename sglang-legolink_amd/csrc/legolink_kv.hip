@@ -95,6 +95,7 @@ struct LinkParams {
   int rotary_dim;
   int idx64;                 // bit0 src, bit1 dst, bit2 local, bit3 global are int64
   int neox;
+  int stream_rows;           // vector kernel: non-temporal row loads (rows read once)
 };
 
 struct ScatterParams {
@@ -184,6 +185,16 @@ __device__ __forceinline__ u32x4 xor_lane4(u32x4 v) {
   r.z = xor_lane<kXor>(v.z);
   r.w = xor_lane<kXor>(v.w);
   return r;
+}
+
+// A row chunk of the source pool; non-temporal when each row is read once.
+// (A compile-time choice: with a runtime one the compiler merges both loads
+// into one plain load.)
+template <bool kStream>
+__device__ __forceinline__ u32x4 load_row(const char *address) {
+  const u32x4 *chunk = reinterpret_cast<const u32x4 *>(address);
+  if constexpr (kStream) return __builtin_nontemporal_load(chunk);
+  else return *chunk;
 }
 
 __device__ __forceinline__ void store_row_chunk(char *address, u32x4 value) {
@@ -285,7 +296,7 @@ __device__ __forceinline__ void load_table(const void *cs, long long offset, flo
 // rotary_dim == kD, an fp32, bf16 or fp16 cos/sin cache (kCache) with unit
 // column stride and 16-byte aligned rows, 16-byte aligned layer buffers.
 // ---------------------------------------------------------------------------
-template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache>
+template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache, bool kStream>
 __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   constexpr int kChunksPerHead = kD / 8;
   constexpr int kRotChunks = kR / 8;     // chunks of a head that rotate; the rest are copied
@@ -351,8 +362,8 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
 #pragma unroll
   for (int u = 0; u < kLayerUnroll; ++u) {
     const int lu = min(l0 + u, l1 - 1);
-    kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[lu] + k_src);
-    vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[lu] + v_src);
+    kin[u] = load_row<kStream>(p.sk_layers[lu] + k_src);
+    vin[u] = load_row<kStream>(p.sv_layers[lu] + v_src);
   }
 
   // fp32 delta of this lane's rotary pairs.  Rows are clamped to 0 where the
@@ -402,8 +413,8 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
 #pragma unroll
       for (int u = 0; u < kLayerUnroll; ++u) {
         const int lu = min(l + u, l1 - 1);
-        kin[u] = *reinterpret_cast<const u32x4 *>(p.sk_layers[lu] + k_src);
-        vin[u] = *reinterpret_cast<const u32x4 *>(p.sv_layers[lu] + v_src);
+        kin[u] = load_row<kStream>(p.sk_layers[lu] + k_src);
+        vin[u] = load_row<kStream>(p.sv_layers[lu] + v_src);
       }
     }
 #pragma unroll
@@ -786,16 +797,29 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   return LL_OK;
 }
 
-template <bool kBF16, int kD, int kR, int kCache>
-void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+template <bool kBF16, int kD, int kR, int kCache, bool kStream>
+void launch_vec_index(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   const bool index64 = (p.idx64 & 15) == 15;  // the vector kernel needs one index type
   if (neox) {
-    if (index64) kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache><<<grid, block, 0, s>>>(p);
+    if (index64) kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream><<<grid, block, 0, s>>>(p);
   } else {
-    if (index64) kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache><<<grid, block, 0, s>>>(p);
+    if (index64) kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache, kStream><<<grid, block, 0, s>>>(p);
+    else kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache, kStream><<<grid, block, 0, s>>>(p);
   }
+}
+
+// Streamed (non-temporal) row loads are built for the full-rotary fp32-table
+// kernels only, the production shape; other shapes load rows as usual.
+template <bool kBF16, int kD, int kR, int kCache>
+void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
+  if constexpr (kR == kD && kCache == 3) {
+    if (p.stream_rows) {
+      launch_vec_index<kBF16, kD, kR, kCache, true>(grid, block, s, p, neox);
+      return;
+    }
+  }
+  launch_vec_index<kBF16, kD, kR, kCache, false>(grid, block, s, p, neox);
 }
 
 template <bool kBF16, int kD, int kCache>
@@ -918,6 +942,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.num_tokens = a->num_tokens;
   p.num_slots = a->num_slots;
   p.src_num_slots = a->source_key_layers != nullptr ? a->source_num_slots : a->num_slots;
+  p.stream_rows = a->stream_source_rows != 0 ? 1 : 0;
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;

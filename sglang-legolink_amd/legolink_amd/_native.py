@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -100,6 +100,7 @@ class LinkArgs(ctypes.Structure):
         ("source_key_layers", _ptr),
         ("source_value_layers", _ptr),
         ("source_num_slots", _i64),
+        ("stream_source_rows", _i64),
     ]
 
 

@@ -441,6 +441,7 @@ class PreparedKVLink:
         layer_groups_per_block: int = 0,
         source_key_buffers: Sequence[torch.Tensor] | None = None,
         source_value_buffers: Sequence[torch.Tensor] | None = None,
+        stream_source_rows: bool = False,
     ) -> None:
         key_buffers = list(key_buffers)
         value_buffers = list(value_buffers)
@@ -512,6 +513,8 @@ class PreparedKVLink:
             source_value_buffers,
         )
         self._args.struct_size = ctypes.sizeof(_native.LinkArgs)
+        # Rows read once (no source repeats within the launch) take non-temporal loads.
+        self._args.stream_source_rows = 1 if stream_source_rows else 0
         # Keep every tensor the argument block points at alive.
         self._tensors = (
             key_buffers, value_buffers, source_slots, destination_slots,
@@ -581,12 +584,14 @@ def fused_kv_link_layers_inplace(
     layer_groups_per_block: int = 0,
     source_key_buffers: Sequence[torch.Tensor] | None = None,
     source_value_buffers: Sequence[torch.Tensor] | None = None,
+    stream_source_rows: bool = False,
 ) -> None:
     """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
     64 layers, on the current stream.  Per layer the result equals
     ``fused_kv_link_inplace``.  With ``source_key_buffers``/``source_value_buffers``
     (one per layer, same row layout) the source rows are read from that pool
-    instead of the destination pool."""
+    instead of the destination pool.  ``stream_source_rows`` says that no source
+    row repeats within the link (non-temporal loads; the result is the same)."""
 
     prepared = PreparedKVLink(
         key_buffers=key_buffers,
@@ -609,6 +614,7 @@ def fused_kv_link_layers_inplace(
         layer_groups_per_block=layer_groups_per_block,
         source_key_buffers=source_key_buffers,
         source_value_buffers=source_value_buffers,
+        stream_source_rows=stream_source_rows,
     )
     prepared()
 

@@ -371,3 +371,26 @@ def test_layer_groups_per_block_shapes_match_oracle(gpu_device, waves, groups, l
     for layer in range(layers):
         assert np.array_equal(bits(keys[layer]), expected_k[layer]), f"K layer {layer}"
         assert np.array_equal(bits(values[layer]), expected_v[layer]), f"V layer {layer}"
+
+
+def test_streamed_row_loads_give_the_same_pool(gpu_device):
+    """stream_source_rows only changes how rows are loaded (non-temporal)."""
+
+    report("streamed vs cached row loads")
+    layers, tokens = 3, 400
+    rng = np.random.default_rng(77)
+    pools = []
+    for stream in (False, True):
+        keys, values = make_pool(layers, 2048, 4, 128, 128, torch.bfloat16, gpu_device, 77)
+        perm = rng.permutation(2048) if not pools else perm
+        maps = [torch.from_numpy(a).to(gpu_device) for a in (
+            perm[:tokens], perm[tokens:2 * tokens], np.arange(tokens) % 700, np.arange(tokens) + 100)]
+        kv_link.fused_kv_link_layers_inplace(
+            key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+            local_positions=maps[2], global_positions=maps[3], cos_sin_cache=build_cos_sin_cache(1024, 128).to(gpu_device),
+            prefix_token_count=5, rotary_dim=128, is_neox_style=True, kernel=VECTOR, stream_source_rows=stream)
+        torch.cuda.synchronize(gpu_device)
+        pools.append(([bits(k) for k in keys], [bits(v) for v in values]))
+    for layer in range(layers):
+        assert np.array_equal(pools[0][0][layer], pools[1][0][layer])
+        assert np.array_equal(pools[0][1][layer], pools[1][1][layer])
