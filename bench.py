@@ -549,7 +549,7 @@ def main() -> int:
         raise RuntimeError("prepared link does not match the workload's token and repair-row counts")
     link = prepared.launch
     scatter = prepared.prepare_write_repaired(repaired_k, repaired_v)
-    launch = prepared.launch_info[0]
+    launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows))
     log(f"setup {setup_s:.1f}s; host prepare {host_prepare_ms:.2f} ms; link launch {launch}")
 
     for _ in range(args.warmup):
