@@ -308,3 +308,18 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
     torch.cuda.synchronize(gpu_device)
     for a, b in zip(pool_a.k_buffer + pool_a.v_buffer, pool_b.k_buffer + pool_b.v_buffer):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_streamed_single_request_link_matches_oracle(gpu_device, monkeypatch):
+    """With the memory-side-cache threshold lowered to 0 a single request's link
+    takes the non-temporal row loads; it still matches the oracle bit for bit
+    (the flow helper checks every layer), and small links keep cached loads."""
+
+    from legolink_amd import link_runtime
+
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=13)
+    assert not prepared.stream_source_rows  # a few MB: may be cache-resident
+    monkeypatch.setattr(link_runtime, "MEMORY_SIDE_CACHE_BYTES", 0)
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=13)
+    assert prepared.stream_source_rows
+    assert all(info["kernel"] == "vector" for info in prepared.launch_info)
