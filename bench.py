@@ -350,8 +350,7 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
                    "spans": len(spans), "queries": plan.num_queries, "q_heads": q_heads,
                    "kv_heads": shape.kv_heads, "head_dim": shape.head_dim,
                    "algorithmic_flops": flops, "plan": plan.info, "host_plan_ms": round(plan_ms, 3)},
-        "roofline": {"bound": "mfma", "kernel": (f"repair_attention_m32_kernel<{shape.head_dim}>" if shape.head_dim in (64, 128)
-                                                        else f"repair_attention_kernel<{shape.head_dim}>"), "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": f"repair_attention_m32_kernel<{shape.head_dim}>", "achieved": round(achieved, 2),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(achieved / 2500.0, 4),
                      "kv_bytes_gathered": kv_bytes,
                      "kv_gather_GBps": round(kv_bytes / (ms / 1e3) / 1e9, 1)},

@@ -8,9 +8,10 @@
 //   workgroup = (item, KV head); the item's (query tile, query head) pairs
 //   -- pair n is query tile n / G, query head hk * G + n % G (G query heads
 //   share one KV head) -- are spread over its waves, so each K/V tile staged
-//   in LDS serves every query tile and head of the item.  With more than 16
-//   query heads per KV head, items have one tile and each KV head gets
-//   ceil(G / 16) workgroups of 16 heads.
+//   in LDS serves every query tile and head of the item.  A workgroup holds
+//   P = 16 pairs (8 for head dim 256); with more than P query heads per KV
+//   head, items have one tile and each KV head gets ceil(G / P) workgroups of
+//   P heads.
 //
 // Per 64-token KV tile:
 //   1. gather the tile's K and V rows of this KV head into LDS by slot;
@@ -23,13 +24,9 @@
 //      accumulators (the token order inside the K step is free, as long as
 //      A uses the same one), A = V^T from transposed LDS reads.
 //
-// Head dims 64 and 128 run repair_attention_m32_kernel: two pairs per wave on
-// v_mfma_f32_32x32x16, rows gathered into an LDS ring by global_load_lds.
-// Head dim 256 runs repair_attention_kernel: one pair per wave on
-// v_mfma_f32_16x16x32, each tile staged through registers.  Its lane layouts
-// (checked on the device): A/B lane l element e -> row/column l % 16,
-// k = 8 (l / 16) + e; accumulator register r -> row 4 (l / 16) + r, column
-// l % 16.
+// Every head dim (64, 128, 256) runs repair_attention_m32_kernel: two pairs
+// per wave on v_mfma_f32_32x32x16, rows gathered into an LDS ring by
+// global_load_lds.
 //
 // Roofline: MFMA-bound in principle.  Algorithmic work per (query, visible
 // key) pair and query head: 4 * head_dim flops (QK and PV); KV bytes are read
@@ -70,7 +67,7 @@ constexpr int kMaxTiles = 4;    // 16-query tiles per work item
 constexpr int kItemInts = 24;
 constexpr int kTileInts = 5;
 constexpr int kCombineInts = 4;
-constexpr int kMaxWaves = 16;  // waves per workgroup: (query tile, query head) pairs = waves per workgroup
+constexpr int kMaxPairs = 16;  // (query tile, query head) pairs per workgroup (head dims 64 and 128)
 
 int fail(int code, const char *fmt, ...) {
   va_list ap;
@@ -109,9 +106,6 @@ struct AttnParams {
 struct Bf16 {
   typedef bf16x8 frag;
   static constexpr uint32_t kOnes = 0x3F803F80u;  // two 1.0s
-  __device__ static f32x4 mfma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
   __device__ static uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
   }
@@ -127,9 +121,6 @@ struct Bf16 {
 struct F16 {
   typedef f16x8 frag;
   static constexpr uint32_t kOnes = 0x3C003C00u;
-  __device__ static f32x4 mfma(frag a, frag b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
   __device__ static uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   }
@@ -141,9 +132,9 @@ struct F16 {
   }
 };
 
-// Query tiles per work item for a GQA group: as many as 16 waves hold.
+// Query tiles per work item for a GQA group: as many as 16 pairs hold.
 __host__ __device__ inline int tiles_per_item(int group) {
-  const int tiles = kMaxWaves / group;
+  const int tiles = kMaxPairs / group;
   return tiles < 1 ? 1 : (tiles > kMaxTiles ? kMaxTiles : tiles);
 }
 
@@ -158,18 +149,12 @@ __device__ inline float *partial_block(const AttnParams &p, int partial, int h) 
   return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
 }
 
-// Max over the four lanes of one query column (l % 16 fixed).
-// v_permlane16_swap a, b exchanges the odd 16-lane rows of a with the even
-// rows of b, v_permlane32_swap the upper half of a with the lower half of b;
-// from two copies of x they leave (x[l], x[l ^ 16]) and then
-// (y[l], y[l ^ 32]) in the lane, up to order -- the operands of xor shuffles
-// 16 and 32.  (Inline assembly: the compiler builtins lose the second result
-// when both operands hold the same value.)  The s_nop covers the wait states
-// between a VALU write of an operand and the permute.
-__device__ inline void permlane16_swap(unsigned &a, unsigned &b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
+// v_permlane32_swap a, b exchanges the upper half of a with the lower half of
+// b: from two copies of x it leaves (x[l], x[l ^ 32]) in the lane, up to
+// order -- the operands of an xor shuffle 32.  (Inline assembly: the compiler
+// builtin loses the second result when both operands hold the same value.)
+// The s_nop covers the wait states between a VALU write of an operand and the
+// permute.
 __device__ inline void permlane32_swap(unsigned &a, unsigned &b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
@@ -183,256 +168,16 @@ __device__ inline float max_f32(float a, float b) {
   return r;
 }
 
-__device__ inline float quad_max(float x) {
-  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-  permlane16_swap(a, b);
-  x = max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-  a = __builtin_bit_cast(unsigned, x);
-  b = a;
-  permlane32_swap(a, b);
-  return max_f32(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
-
 constexpr float kSlack = 8.f;  // log2 headroom of the lazily updated softmax maximum
 constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score units)
 
-// Waves per workgroup of the register-staged kernel: head dim 256 needs twice
-// the registers per wave (256 at 8 waves per CU).
-__host__ __device__ constexpr int staged_max_waves(int d) { return d == 256 ? kMaxWaves / 2 : kMaxWaves; }
+// (Query tile, query head) pairs per workgroup, two per wave: head dim 256
+// needs twice the registers and LDS per wave, so its workgroups hold 4 waves.
+__host__ __device__ constexpr int max_pairs(int d) { return d == 256 ? kMaxPairs / 2 : kMaxPairs; }
 
-template <int D, typename E>
-__global__ void __launch_bounds__(kWave * staged_max_waves(D)) repair_attention_kernel(const AttnParams p) {
-  typedef typename E::frag frag;
-  constexpr int kSteps = D / 32;     // k-steps of S^T = K Q^T
-  constexpr int kDimTiles = D / 16;  // 16-row tiles of O^T
-  constexpr int kKRow = D + 8;       // LDS row stride of K (elements), spreads banks
-  constexpr int kVRow = kTile + 8;   // LDS row stride of transposed V
-  constexpr int kParts = D / 8;      // 16-byte chunks per head row
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTile * kKRow];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * kVRow];
-  __shared__ unsigned char token_ok[kTile];
-  __shared__ int tile_invalid;  // tokens of the current tile that are out of range or invalid
-
-  const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
-  const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
-  const int hk = blockIdx.y / p.head_chunks;
-  const int head_base = (blockIdx.y % p.head_chunks) * p.heads_per_wg;
-  // Items come from the planner; a malformed one is skipped whole (uniform).
-  if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
-      static_cast<long long>(kv_off) + kv_end > p.slots_len || hk >= p.hkv)
-    return;
-
-  const int tid = threadIdx.x;
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  const int g = lane / 16;   // lane group: k (or row) block of the MFMA operands
-  const int c = lane % 16;   // query of this lane in the S^T / O^T accumulators
-  // Wave w computes query head hk * G + head_base + w % H for the item's query
-  // tile w / H, H = heads_per_wg (G itself unless G > 16).
-  const int tile = wave / p.heads_per_wg;
-  const int head = head_base + wave % p.heads_per_wg;
-  const int hq = hk * p.group + head;
-  const int *entry = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
-  const int q_index = entry[0], q_pos = entry[1], q_count = entry[2], partial = entry[3], needed = entry[4];
-  const bool computes = tile < n_tiles && head < p.group && q_count >= 1 && q_count <= kQueries && q_index >= 0 &&
-                        static_cast<long long>(q_index) + q_count <= p.num_queries && q_pos >= 0 &&
-                        needed > q_pos && (partial == -1 || (partial >= 0 && partial < p.ws_items));
-  const bool q_ok = computes && c < q_count;
-  // A tile's queries are consecutive rows of one request, not always
-  // consecutive positions (several short repair spans share a tile).
-  const int my_pos = q_ok ? p.positions[q_index + c] : 0;
-  // The wave's keys end where its furthest query's do; the workgroup loads up
-  // to the furthest of its tiles.
-  const int kv_stop = computes ? min(kv_end, needed) : kv_begin;
-  int load_stop = kv_begin;
-  for (int t = 0; t < n_tiles; ++t) {
-    const int *e = it + 4 + kTileInts * t;
-    if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
-  }
-
-  // The wave's queries as the B operand of S^T = K Q^T: query c, dims 32 ks + 8 g + e.
-  frag qf[kSteps];
-  {
-    const uint16_t *qrow = p.q + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
-      u32x4 bits = {0u, 0u, 0u, 0u};
-      if (q_ok) bits = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
-      qf[ks] = __builtin_bit_cast(frag, bits);
-    }
-  }
-
-  // The softmax state: a lazily raised maximum from a finite floor (as in
-  // repair_attention_m32_kernel), denominators from a value MFMA with a
-  // 16-row A operand of ones.
-  float m = kScoreFloor;
-  f32x4 o[kDimTiles];
-#pragma unroll
-  for (int dt = 0; dt < kDimTiles; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
-  const frag ones = __builtin_bit_cast(frag, u32x4{E::kOnes, E::kOnes, E::kOnes, E::kOnes});
-
-  const long long row_stride = static_cast<long long>(p.hkv) * D;  // elements per slot
-  const float scale_log2 = p.scale_log2;
-  const float slack = kSlack / scale_log2;
-  for (int t0 = kv_begin; t0 < load_stop; t0 += kTile) {
-    __syncthreads();  // the previous tile's LDS reads are done
-    if (tid == 0) tile_invalid = 0;
-    __syncthreads();
-    // K: token-major (16 lanes cover one 256-byte row: coalesced), V: token-minor
-    // (consecutive lanes write consecutive tokens of a transposed row).
-    for (int ci = tid; ci < kTile * kParts; ci += blockDim.x) {
-      {
-        const int tok = ci / kParts, part = ci % kParts;
-        const int j = t0 + tok;
-        u32x4 kc = {0u, 0u, 0u, 0u};
-        if (j < load_stop) {
-          const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
-          if (slot >= 0 && slot < p.num_slots)
-            kc = *reinterpret_cast<const u32x4 *>(p.k + slot * row_stride + hk * D + part * 8);
-        }
-        *reinterpret_cast<u32x4 *>(&k_lds[tok * kKRow + part * 8]) = kc;
-      }
-      {
-        const int tok = ci % kTile, part = ci / kTile;
-        const int j = t0 + tok;
-        u32x4 vc = {0u, 0u, 0u, 0u};
-        bool ok = false;
-        if (j < load_stop) {
-          const long long slot = slot_at(p, static_cast<long long>(kv_off) + j);
-          ok = slot >= 0 && slot < p.num_slots;
-          if (ok) vc = *reinterpret_cast<const u32x4 *>(p.v + slot * row_stride + hk * D + part * 8);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v_lds[(part * 8 + 2 * e) * kVRow + tok] = static_cast<uint16_t>(vc[e] & 0xffffu);
-          v_lds[(part * 8 + 2 * e + 1) * kVRow + tok] = static_cast<uint16_t>(vc[e] >> 16);
-        }
-        if (part == 0) {
-          token_ok[tok] = ok ? 1 : 0;
-          if (!ok) atomicAdd(&tile_invalid, 1);
-        }
-      }
-    }
-    __syncthreads();
-    if (!computes || t0 >= kv_stop) continue;  // this wave's tile has no keys here
-
-    // S^T tile: lane holds tokens 16 n + 4 g + r for query c.
-    f32x4 s[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks) {
-        const frag a = *reinterpret_cast<const frag *>(&k_lds[(16 * n + c) * kKRow + 32 * ks + 8 * g]);
-        s[n] = E::mfma(a, qf[ks], s[n]);
-      }
-    }
-    // Raw scores are kept unscaled: the max commutes with the positive scale,
-    // which is folded into the exponent (one FMA and one v_exp_f32 per score).
-    // A tile that every query sees whole, with every slot valid, needs no mask.
-    const bool whole = tile_invalid == 0 && t0 + kTile <= q_pos && t0 + kTile <= kv_stop;
-    float tile_max = -INFINITY;
-    if (whole) {
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[n][r]);
-      if (!q_ok) tile_max = -INFINITY;
-    } else {
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = 16 * n + 4 * g + r;
-          const int j = t0 + tok;
-          const bool visible = q_ok && j < kv_stop && j <= my_pos && token_ok[tok];
-          s[n][r] = visible ? s[n][r] : -INFINITY;
-          tile_max = fmaxf(tile_max, s[n][r]);
-        }
-      }
-    }
-    tile_max = quad_max(tile_max);
-    // The maximum moves only past kSlack (log2 units) above the current one.
-    const bool raise = tile_max > m + slack;
-    const float m_new = raise ? tile_max : m;
-    const float bias = -m_new * scale_log2;
-    float pv[4][4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pv[n][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[n][r], scale_log2, bias));
-    }
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform
-      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);
-      lsum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < kDimTiles; ++dt) o[dt] *= alpha;
-    }
-    m = m_new;
-    // P^T as the B operand of 16x16x32 MFMAs over 32 tokens: k-step h takes the
-    // accumulators of token tiles 2h and 2h + 1, so lane group g holds tokens
-    // 32 h + 4 g + {0..3} and 32 h + 16 + 4 g + {0..3}; the A operand (V^T)
-    // reads the same tokens for its dim row.
-    frag pb[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 bits;
-      bits[0] = E::pack(pv[2 * h][0], pv[2 * h][1]);
-      bits[1] = E::pack(pv[2 * h][2], pv[2 * h][3]);
-      bits[2] = E::pack(pv[2 * h + 1][0], pv[2 * h + 1][1]);
-      bits[3] = E::pack(pv[2 * h + 1][2], pv[2 * h + 1][3]);
-      pb[h] = __builtin_bit_cast(frag, bits);
-    }
-#pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint16_t *row = &v_lds[(16 * dt + c) * kVRow + 32 * h + 4 * g];
-        u32x4 bits;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(row);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(row + 16);
-        bits[0] = lo[0];
-        bits[1] = lo[1];
-        bits[2] = hi[0];
-        bits[3] = hi[1];
-        o[dt] = E::mfma(__builtin_bit_cast(frag, bits), pb[h], o[dt]);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) lsum = E::mfma(ones, pb[h], lsum);
-  }
-
-  const float l = lsum[0];
-  if (!computes) return;
-  // o[dt][r] = O^T[dim 16 dt + 4 g + r][query c].
-  if (partial < 0) {
-    if (!q_ok) return;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + hq) * D + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt) {
-      u32x2 packed;
-      packed[0] = E::pack(o[dt][0] * inv, o[dt][1] * inv);
-      packed[1] = E::pack(o[dt][2] * inv, o[dt][3] * inv);
-      *reinterpret_cast<u32x2 *>(dst + 16 * dt) = packed;
-    }
-  } else {
-    float *block = partial_block<D>(p, partial, hq);
-#pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt)
-      *reinterpret_cast<f32x4 *>(block + c * D + 16 * dt + 4 * g) = o[dt];
-    if (g == 0) {  // the running max in the combine's units: log2-scaled scores
-      block[kQueries * D + 2 * c] = m * scale_log2;
-      block[kQueries * D + 2 * c + 1] = l;
-    }
-  }
-}
-
-// Head dim 128 gathers K and V rows straight into a four-stage LDS ring with
-// global_load_lds, three tiles ahead of the MFMAs, so no registers stage them.
-// Rows are stored token-major with their sixteen 16-byte chunks XOR-swizzled
-// by token, which keeps the fragment reads free of bank conflicts.  V^T
+// K and V rows are gathered straight into an LDS ring with global_load_lds,
+// up to three tiles ahead of the MFMAs, so no registers stage them.  Rows are
+// stored token-major with their 16-byte chunks XOR-swizzled by token, which keeps the fragment reads free of bank conflicts.  V^T
 // fragments come from ds_read_b64_tr_b16: within a group of 16 lanes it
 // returns to lane i, element e, element i % 4 of the 8 bytes that lane
 // 4 e + i / 4 addressed (checked on the device), so lanes addressing 4 dims of
@@ -479,7 +224,7 @@ __device__ inline void workgroup_barrier() {
 }
 
 
-// Head dims 64 and 128 on v_mfma_f32_32x32x16 (issues at ~34 cycles for twice the work
+// Attention on v_mfma_f32_32x32x16 (issues at ~34 cycles for twice the work
 // of a 16x16x32 at ~20, and hides about four VALU instructions in the wave
 // that issued it, against two).  Each wave owns two (query tile, head) pairs,
 // 32 MFMA columns: column n = 16 (pair - 2 wave) + query.  Lane layouts
@@ -497,31 +242,40 @@ __device__ inline void workgroup_barrier() {
 // Chunk swizzles (chunk c of token t is stored at c ^ swizzle(t)), chosen so
 // that the 16 lanes of a K read (16 tokens, one chunk each) and the 32 lanes
 // of a transposed V read (4 tokens x 64 bytes) each cover the 64 banks once:
-//   head dim 128 (256-byte rows): K c ^ (t % 16), V c ^ 4 (t % 4);
+//   head dims 128 and 256 (256- and 512-byte rows, each starting a bank
+//   row): K c ^ (t % 16), V c ^ 4 (t % 4);
 //   head dim 64 (128-byte rows, two per bank row): K c ^ ((t / 2) % 8),
 //   V c ^ 4 ((t / 2) % 2).
-// Each of the 8 waves issues 1/8 of a tile's K and V gathers.
-constexpr int kM32Threads = 512;
+// Each wave issues an equal share of a tile's K and V gathers.
+// Head dims 64 and 128: 8 waves and a four-stage ring; head dim 256 (twice the
+// registers and LDS per tile): 4 waves, one per SIMD, and a two-stage ring.
+template <int D>
+__host__ __device__ constexpr int m32_threads() { return D == 256 ? 256 : 512; }
+template <int D>
+__host__ __device__ constexpr int m32_stages() { return D == 256 ? 2 : kDmaStages; }
 
 template <int D>
-__host__ __device__ constexpr int m32_k_swizzle(int t) { return D == 128 ? t % 16 : (t / 2) % 8; }
+__host__ __device__ constexpr int m32_k_swizzle(int t) { return D >= 128 ? t % 16 : (t / 2) % 8; }
 template <int D>
-__host__ __device__ constexpr int m32_v_swizzle(int t) { return D == 128 ? 4 * (t % 4) : 4 * ((t / 2) % 2); }
+__host__ __device__ constexpr int m32_v_swizzle(int t) { return D >= 128 ? 4 * (t % 4) : 4 * ((t / 2) % 2); }
 
 template <int D, typename E>
-__global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(const AttnParams p) {
   typedef typename E::frag frag;
-  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static_assert(D == 64 || D == 128 || D == 256, "head dims 64, 128 and 256");
+  constexpr int kM32Threads = m32_threads<D>();
+  constexpr int kStages = m32_stages<D>();
+  constexpr int kLead = kStages - 1;  // tiles gathered ahead of the one computed
   constexpr int kKSteps = D / 16;                        // 16-dim steps of the score MFMAs
   constexpr int kDimBlocks = D / 32;                     // 32-dim blocks of O^T
   constexpr int kChunksPerRow = D / 8;                   // 16-byte chunks per row
   constexpr int kGathers = kChunksPerRow / (kM32Threads / kWave);  // per wave, per tile, of K and of V
   constexpr int kRowBytes = D * 2;
-  constexpr int kStageBytes = kTile * kRowBytes;         // one K or V tile: 16 KB
+  constexpr int kStageBytes = kTile * kRowBytes;         // one K or V tile
   constexpr int kRangeTiles = kDmaMaxRange / kTile;
-  static_assert(kM32Threads / kWave * 2 == kMaxWaves, "two (tile, head) pairs per wave");
-  __shared__ __attribute__((aligned(16))) unsigned char k_ring[kDmaStages * kStageBytes];
-  __shared__ __attribute__((aligned(16))) unsigned char v_ring[kDmaStages * kStageBytes];
+  static_assert(kM32Threads / kWave * 2 == max_pairs(D), "two (tile, head) pairs per wave");
+  __shared__ __attribute__((aligned(16))) unsigned char k_ring[kStages * kStageBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char v_ring[kStages * kStageBytes];
   __shared__ int slot_lds[kDmaMaxRange];
   __shared__ unsigned long long tile_valid[kRangeTiles];
 
@@ -610,10 +364,11 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
   __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): queries and slots are in
   __syncthreads();
 
-  // Gather of tile t: 16 K and 16 V instructions of 64 lanes; wave w issues
-  // instructions 2 w and 2 w + 1 of each.  Instruction k fills stage chunks
-  // 64 k .. 64 k + 63: chunk P holds token P / 16 and, of its row, chunk
-  // (P % 16) ^ swizzle(token) (each swizzle is its own inverse).
+  // Gather of tile t: D / 8 K and D / 8 V instructions of 64 lanes; wave w
+  // issues instructions kGathers w .. kGathers w + kGathers - 1 of each.
+  // Instruction k fills stage chunks 64 k .. 64 k + 63: chunk P holds token
+  // P / kChunksPerRow and, of its row, chunk (P % kChunksPerRow) ^
+  // swizzle(token) (each swizzle is its own inverse).
   const long long row_stride = static_cast<long long>(p.hkv) * D;
   const bool have_slots = p.num_slots > 0;
   int g_token[kGathers], g_kchunk[kGathers], g_vchunk[kGathers];
@@ -655,23 +410,24 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
   const int v_lane = (4 * h + vu) * kRowBytes + (2 * ((lane / 16) % 2) + (li % 4) / 2) * 16 + 8 * (li % 2);
   const int k_lane = col * kRowBytes;
 
-  // Tiles are gathered three ahead: tile t + 3 goes into the stage of tile
-  // t - 1 once every wave is past it (the barrier at the top of tile t).  A
-  // wave's four gathers of tile t are complete when at most the eight of
-  // tiles t + 1 and t + 2 are outstanding (loads count down in issue order).
+  // Tiles are gathered kLead ahead: tile t + kLead goes into the stage of
+  // tile t - 1 once every wave is past it (the barrier at the top of tile t).
+  // A wave's 2 kGathers loads of tile t are complete when at most those of
+  // tiles t + 1 .. t + kLead - 1 are outstanding (loads count down in issue
+  // order).
 #pragma unroll
-  for (int t = 0; t < 3; ++t)
+  for (int t = 0; t < kLead; ++t)
     if (t < tiles) gather(t, k_ring + t * kStageBytes, v_ring + t * kStageBytes);
   for (int t = 0; t < tiles; ++t) {
-    const unsigned char *k_stage = k_ring + (t % kDmaStages) * kStageBytes;
-    unsigned char *v_stage = v_ring + (t % kDmaStages) * kStageBytes;
-    // 2 kGathers loads per tile and wave: vmcnt(4 kGathers) or vmcnt(2 kGathers).
-    if (t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (4 * kGathers));
-    else if (t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kGathers));
-    else __builtin_amdgcn_s_waitcnt(0xF70);                     // vmcnt(0)
+    const unsigned char *k_stage = k_ring + (t % kStages) * kStageBytes;
+    unsigned char *v_stage = v_ring + (t % kStages) * kStageBytes;
+    if (kLead >= 3 && t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (4 * kGathers));
+    else if (kLead >= 2 && t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kGathers));
+    else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
     workgroup_barrier();
-    if (t + 3 < tiles)
-      gather(t + 3, k_ring + ((t + 3) % kDmaStages) * kStageBytes, v_ring + ((t + 3) % kDmaStages) * kStageBytes);
+    if (t + kLead < tiles)
+      gather(t + kLead, k_ring + ((t + kLead) % kStages) * kStageBytes,
+             v_ring + ((t + kLead) % kStages) * kStageBytes);
     const unsigned long long valid_bits = tile_valid[t];
     if (valid_bits != ~0ull) {
       // Zero the V rows of tokens without a valid slot (0 * Inf would be NaN).
@@ -778,7 +534,7 @@ __global__ void __launch_bounds__(kM32Threads) repair_attention_m32_kernel(const
         pb[2 * kb + st] = __builtin_bit_cast(frag, bits);
       }
     }
-    // V^T fragments of one step (four dim blocks, two transposed reads each),
+    // V^T fragments of one step (every dim block, two transposed reads each),
     // the next step's reads issued before this step's MFMAs.  Step 2 kb + st
     // covers tokens 32 kb + 16 st + 4 h + (0..3) and, 8 further, the second read.
     frag vf[2][kDimBlocks];
@@ -1179,8 +935,7 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
   // A workgroup holds every (tile, head) pair of its item when the waves
   // allow, else the heads are split over several workgroups per KV head.
-  const int max_waves = a->head_dim == 128 ? kMaxWaves : staged_max_waves(static_cast<int>(a->head_dim));
-  const int head_room = max_waves / tiles_per_item(p.group);
+  const int head_room = max_pairs(static_cast<int>(a->head_dim)) / tiles_per_item(p.group);
   p.heads_per_wg = p.group < head_room ? p.group : head_room;
   p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
   p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
@@ -1190,17 +945,16 @@ int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
   if (a->num_kv_heads * p.head_chunks > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
-  const dim3 staged(static_cast<unsigned>(kWave * p.heads_per_wg * tiles_per_item(p.group)));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
-    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
-    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
   } else if (a->head_dim == 64) {
-    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(kM32Threads), 0, s>>>(p);
-    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(kM32Threads), 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
   } else {
-    if (f16) repair_attention_kernel<256, F16><<<grid, staged, 0, s>>>(p);
-    else repair_attention_kernel<256, Bf16><<<grid, staged, 0, s>>>(p);
+    if (f16) repair_attention_m32_kernel<256, F16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<256, Bf16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
