@@ -20,6 +20,7 @@ plain device copy of known size, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -70,6 +71,8 @@ def parse_args() -> argparse.Namespace:
                              "linked from it (clone); clone also times the capture and a group promotion")
     parser.add_argument("--split-tokens", type=int, default=0,
                         help="repair attention: KV tokens per work item (0: the planner's choice)")
+    parser.add_argument("--head-dim", type=int, default=0, choices=[0, 64, 128, 256],
+                        help="repair attention: head dim in place of the workload's (same spans and heads)")
     return parser.parse_args()
 
 
@@ -293,6 +296,8 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
     group = 7 if full.shape.kv_heads == 4 else 8  # Qwen2.5-7B: 28 / 4; Qwen3-32B: 64 / 8
     workload = tp_share(full, args.tp)
     shape = workload.shape
+    if args.head_dim:
+        shape = dataclasses.replace(shape, head_dim=args.head_dim)
     q_heads = group * shape.kv_heads
     generator = torch.Generator(device=device).manual_seed(20260824)
     key = torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, generator=generator,
