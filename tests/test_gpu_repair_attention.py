@@ -90,9 +90,11 @@ CASES = [
     ("group12", 24, 2, 128, [(50, 70), (400, 416)], 2048, 0, None),
     ("mqa_group32", 32, 1, 128, [(100, 133)], 2048, 256, None),
     ("mqa_group71_head_dim64", 71, 1, 64, [(20, 37), (900, 905)], 2048, 0, None),
-    # Head dim 256: at most 8 waves per workgroup, so 7 heads x 2 tiles take two workgroups.
+    # Head dim 256: at most 8 (tile, head) pairs per workgroup, so 7 heads x 2
+    # tiles take two workgroups, and 20 heads of one tile take three (8, 8, 4).
     ("head_dim256_group2", 8, 4, 256, [(10, 40), (600, 616)], 2048, 0, None),
     ("head_dim256_group7_split", 28, 4, 256, [(1500, 1520)], 4096, 512, None),
+    ("head_dim256_mqa_group20", 20, 1, 256, [(300, 345)], 2048, 0, None),
 ]
 
 
