@@ -58,8 +58,11 @@ def parse_args() -> argparse.Namespace:
                         help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
                         help="time a plain device copy of this many MiB instead of the link")
-    parser.add_argument("--ceiling", action="store_true",
-                        help="measure memory ceilings next to the link instead of the step")
+    parser.add_argument("--run-sweep", action="store_true",
+                        help="time the link kernel on maps whose sources and destinations come in "
+                             "contiguous runs of 1..64 slots, for several launch shapes")
+    parser.add_argument("--sweep-detail-run", type=int, default=64,
+                        help="run length that gets every launch-shape variant (besides 1)")
     parser.add_argument("--repair-attention", action="store_true",
                         help="time the sparse repair attention of the workload's repair spans "
                              "(one layer) instead of the link")
@@ -184,26 +187,49 @@ def _median_ms(torch, run, steps: int, warmup: int) -> float:
     return sorted(s.elapsed_time(e) for s, e in events)[steps // 2]
 
 
-def ceiling(args: argparse.Namespace) -> None:
-    """The link next to pure-copy probes over the same rows: how close the
-    kernel is to what the memory system delivers for this access pattern."""
+RUN_LENGTHS = (1, 2, 4, 8, 16, 64)
 
-    import ctypes
+
+def run_length_maps(workload, run: int, seed: int):
+    """Token maps of ``workload``'s tokens whose source and destination slots
+    come in contiguous runs of ``run`` rows: the pool is cut into runs of
+    ``run`` slots, distinct runs are drawn at random for the sources and for
+    the destinations, and token t reads row t % run of its source run and
+    writes row t % run of its destination run.  run = 1 is a fully fragmented
+    pool (page size 1, random permutation), as the workload itself."""
+
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    tokens = workload.tokens
+    runs_needed = -(-tokens // run)
+    runs = rng.permutation(workload.num_slots // run)[: 2 * runs_needed].astype(np.int64)
+    if runs.size < 2 * runs_needed:
+        raise ValueError("pool too small for these runs")
+    offsets = np.arange(tokens, dtype=np.int64)
+    src = runs[offsets // run] * run + offsets % run
+    dst = runs[runs_needed + offsets // run] * run + offsets % run
+    return src, dst
+
+
+def run_sweep(args: argparse.Namespace) -> None:
+    """The link kernel itself on maps of growing contiguity: how fast the
+    kernel moves the workload's rows when sources and destinations come in
+    runs of 1 (fully fragmented), 2, 4, ... 64 consecutive slots, for several
+    launch shapes.  Every launch links all of the workload's tokens (repair
+    rows included) with the workload's positions; GB/s counts each token's K
+    and V rows of every layer read once and written once.  Prints one JSON line
+    with a row per (run length, variant) and the order of their launches (for
+    matching rocprofv3 dispatches)."""
 
     import numpy as np
     import torch
 
-    from legolink_amd import _native, kv_link
-    from legolink_amd.build import PROBE_OUTPUT
+    from legolink_amd import kv_link
     from legolink_amd.rope import build_cos_sin_cache
     from legolink_amd.workloads import make_workload
 
     device = torch.device("cuda", 0)
-    _native.load_library()  # binds the HIP runtime torch loaded
-    probe = ctypes.CDLL(str(PROBE_OUTPUT))
-    probe.llp_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
-    probe.llp_row_copy.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
-                                   ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_void_p]
     workload = make_workload(args.workload)
     shape = workload.shape
     generator = torch.Generator(device=device).manual_seed(20260824)
@@ -212,51 +238,48 @@ def ceiling(args: argparse.Namespace) -> None:
     values = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
                           device=device, generator=generator) for _ in range(shape.layers)]
     table = build_cos_sin_cache(workload.max_position + 1, workload.rotary_dim, theta=workload.theta).to(device)
-    maps = torch.from_numpy(np.stack([workload.source_slots, workload.destination_slots,
-                                      workload.local_positions, workload.global_positions])).to(device)
-    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)  # noqa: E731
-
-    def link_with_prefix(prefix: int) -> kv_link.PreparedKVLink:
-        return kv_link.PreparedKVLink(
-            key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
-            local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table,
-            prefix_token_count=prefix, rotary_dim=workload.rotary_dim, is_neox_style=True,
-            num_warps=args.waves_per_block, layers_per_wave=args.layers_per_wave,
-            layer_groups_per_block=args.layer_groups_per_block,
-        )
-
-    buffers = (ctypes.c_void_p * (2 * shape.layers))(*[b.data_ptr() for b in keys + values])
-
-    def row_copy() -> None:
-        rc = probe.llp_row_copy(buffers, 2 * shape.layers, maps[0].data_ptr(), maps[1].data_ptr(),
-                                workload.tokens, workload.num_slots, shape.row_bytes, stream())
-        if rc != 0:
-            raise RuntimeError(f"llp_row_copy failed ({rc})")
-
+    local = torch.from_numpy(workload.local_positions).to(device)
+    glob = torch.from_numpy(workload.global_positions).to(device)
     link_bytes = workload.tokens * shape.bytes_per_token
-    results = {}
-    for name, run in (("link", link_with_prefix(workload.prefix_token_count)),
-                      ("link_without_rotation", link_with_prefix(workload.tokens)),
-                      ("row_copy_probe", row_copy)):
-        ms = _median_ms(torch, run, args.steps, args.warmup)
-        results[name] = {"ms": round(ms, 5), "GBps": round(link_bytes / ms / 1e6, 1)}
-        log(f"{name}: {ms:.4f} ms, {link_bytes / ms / 1e6:.1f} GB/s")
-    del keys, values, pool, prepared, link, scatter
-    torch.cuda.empty_cache()
-    nbytes = 4 << 30
-    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    dst = torch.empty_like(src)
-
-    def stream_copy() -> None:
-        if probe.llp_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, stream()) != 0:
-            raise RuntimeError("llp_stream_copy failed")
-
-    ms = _median_ms(torch, stream_copy, args.steps, args.warmup)
-    results["stream_copy_4GiB"] = {"ms": round(ms, 5), "GBps": round(2 * nbytes / ms / 1e6, 1)}
-    ms = _median_ms(torch, lambda: dst.copy_(src), args.steps, args.warmup)
-    results["torch_copy_4GiB"] = {"ms": round(ms, 5), "GBps": round(2 * nbytes / ms / 1e6, 1)}
-    print(json.dumps({"ceiling": results, "workload": workload.name,
-                      "bytes_per_row_pass": link_bytes, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
+    # (name, launch keywords); the first is the executor's choice for a single request.
+    default = {"num_warps": 4, "layers_per_wave": 0, "stream_source_rows": True}
+    variants = [("default", {})]
+    detailed = {1, int(args.sweep_detail_run)}
+    extra = [
+        ("cached_loads", {"stream_source_rows": False}),
+        ("rotation_off", {"rotation_off": True}),
+        ("layers_per_wave_1", {"layers_per_wave": 1}),
+        ("layers_per_wave_2", {"layers_per_wave": 2}),
+        ("layers_per_wave_7", {"layers_per_wave": 7}),
+        ("layers_per_wave_28", {"layers_per_wave": 28}),
+        ("waves_per_block_1", {"num_warps": 1}),
+        ("waves_per_block_8", {"num_warps": 8}),
+    ]
+    rows, schedule, dispatch = [], [], 0
+    for run in RUN_LENGTHS:
+        src, dst = run_length_maps(workload, run, seed=20260824 + run)
+        src_t = torch.from_numpy(src).to(device)
+        dst_t = torch.from_numpy(dst).to(device)
+        for name, changes in variants + (extra if run in detailed else []):
+            options = dict(default, **changes)
+            rotation_off = options.pop("rotation_off", False)
+            prepared = kv_link.PreparedKVLink(
+                key_buffers=keys, value_buffers=values, source_slots=src_t, destination_slots=dst_t,
+                local_positions=local, global_positions=glob, cos_sin_cache=table,
+                prefix_token_count=workload.tokens if rotation_off else workload.prefix_token_count,
+                rotary_dim=workload.rotary_dim, is_neox_style=True, **options)
+            ms = _median_ms(torch, prepared, args.steps, args.warmup)
+            launches = prepared.launch["launches"] * (args.steps + args.warmup)
+            schedule.append({"run": run, "variant": name, "first_dispatch": dispatch, "dispatches": launches})
+            dispatch += launches
+            rows.append({"run": run, "variant": name, "ms": round(ms, 5),
+                         "GBps": round(link_bytes / ms / 1e6, 1),
+                         "frac": round(link_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                         "launch": prepared.launch})
+            log(f"run {run:3d} {name:20s} {ms:.4f} ms  {link_bytes / ms / 1e6:8.1f} GB/s")
+    print(json.dumps({"sweep": rows, "schedule": schedule, "workload": workload.name,
+                      "tokens": workload.tokens, "bytes_per_launch": link_bytes,
+                      "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 
 def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
@@ -429,8 +452,8 @@ def main() -> int:
     if args.copy_calibration:
         copy_calibration(args)
         return 0
-    if args.ceiling:
-        ceiling(args)
+    if args.run_sweep:
+        run_sweep(args)
         return 0
     if args.repair_attention:
         repair_attention_bench(args)

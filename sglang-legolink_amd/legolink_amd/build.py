@@ -22,9 +22,6 @@ SOURCE = PACKAGE_DIR.parent / "csrc" / "legolink_kv.hip"
 SOURCES = (SOURCE, PACKAGE_DIR.parent / "csrc" / "repair_attention.hip")
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
-# Memory-ceiling probes used by bench.py --ceiling (not part of the link ABI).
-PROBE_SOURCE = PACKAGE_DIR.parent / "csrc" / "row_copy_probe.hip"
-PROBE_OUTPUT = PACKAGE_DIR / "lib" / "librow_copy_probe.so"
 OFFLOAD_ARCH = "gfx950"
 
 
@@ -58,10 +55,9 @@ def compile_command(output: Path, sources=SOURCES) -> list[str]:
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile the link library and the probe library; outputs are replaced atomically."""
+    """Compile the link library; the output is replaced atomically."""
 
     _compile(SOURCES, OUTPUT, verbose)
-    _compile((PROBE_SOURCE,), PROBE_OUTPUT, verbose)
     return OUTPUT
 
 
