@@ -69,6 +69,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--tp", type=int, default=1,
                         help="bench one tensor-parallel rank's share: kv_heads / tp heads of every layer "
                              "(the link has no exchange step; each rank links its own head shard)")
+    parser.add_argument("--rounding", choices=["fused", "eager"], default="fused",
+                        help="rounding of re-rotated K: the reference's fused kernel (default) or its "
+                             "torch path")
     parser.add_argument("--storage", choices=["reference", "clone"], default="reference",
                         help="blocks read from pool slots (reference) or captured into a snapshot arena and "
                              "linked from it (clone); clone also times the capture and a group promotion")
@@ -499,10 +502,16 @@ def main() -> int:
         arena = SnapshotArena.allocate(num_slots=sum(source.size for source, _ in blocks.values()),
                                        num_layers=shape.layers, num_heads=shape.kv_heads,
                                        head_dim=shape.head_dim, device=device)
+    # The fused rounding (fp32 rotation, one rounding at the store) is what the
+    # link is measured on; clone blocks take the reference's torch-path rounding
+    # ("auto" falls back to it, as the reference does).  --rounding eager times
+    # the torch path's rounding on the same kernel.
+    fused_mode = "disabled" if args.rounding == "eager" else ("auto" if clone else "required")
     executor = KVLinkExecutor(registry, RotarySpec(table, rotary_dim=workload.rotary_dim),
                               end_layer=shape.layers, num_warps=args.waves_per_block,
                               layers_per_wave=args.layers_per_wave,
-                              layer_groups_per_block=args.layer_groups_per_block, arena=arena)
+                              layer_groups_per_block=args.layer_groups_per_block, arena=arena,
+                              fused_mode=fused_mode)
     pool = KVPool(keys, values)
     row_bytes = 2 * shape.kv_heads * shape.head_dim * 2  # one token's K and V row, one layer
     storage = {"mode": args.storage}
@@ -576,7 +585,8 @@ def main() -> int:
         raise RuntimeError("prepared link does not match the workload's token and repair-row counts")
     link = prepared.launch
     scatter = prepared.prepare_write_repaired(repaired_k, repaired_v)
-    launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows))
+    launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows),
+                  rounding=prepared.rounding)
     log(f"setup {setup_s:.1f}s; host prepare {host_prepare_ms:.2f} ms; link launch {launch}")
 
     for _ in range(args.warmup):

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 8
+#define LL_ABI_VERSION 9
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -63,6 +63,23 @@ enum {
   LL_KERNEL_AUTO = 0,   /* vectorised kernel when the shape allows, else generic */
   LL_KERNEL_VECTOR = 1, /* 16-byte row-chunk kernel; LL_ERR_UNSUPPORTED_KERNEL if the shape does not fit */
   LL_KERNEL_GENERIC = 2 /* element-wise kernel for every eligible shape */
+};
+
+/*
+ * Rounding of re-rotated K (ll_kv_link_args.rounding).  The reference computes
+ * the link in two ways that round differently; both are available:
+ *   LL_ROUNDING_FUSED  its fused kernel (legolink_triton.py:413-470), which its
+ *                      link uses when the fused mode is on and every block is
+ *                      read from pool slots;
+ *   LL_ROUNDING_EAGER  its torch path (pic_runtime.py:6025-6058 with
+ *                      _apply_rotary_emb, :1868-1885), which it uses by default
+ *                      (fused mode off, :1307-1308), for every link that holds
+ *                      a clone-mode block (:5034-5035) and for group promotion
+ *                      (:5914-5919).
+ */
+enum {
+  LL_ROUNDING_FUSED = 0,
+  LL_ROUNDING_EAGER = 1
 };
 
 /*
@@ -110,11 +127,17 @@ enum {
  * with (lc, ls) = cos_sin_cache[local][i], cos_sin_cache[local][i + rotary_dim/2]
  * and  (gc, gs) the same at the global position; pairs are (i, i + rotary_dim/2)
  * for neox style and (2i, 2i + 1) otherwise.  Dims >= rotary_dim are copied.
- * Rounding (legolink_triton.py:413-470): bf16 K with an fp32 cache uses fp32
- * with every multiply and add rounded to nearest even (no fused multiply-add)
- * and one round-to-nearest-even to bf16 at the store; bf16 K with a bf16 or fp16
- * cache rounds every product and sum to bf16; fp16 K computes in fp32 and rounds
- * once to fp16.
+ * Every multiply and add is a separate round-to-nearest-even op (no fused
+ * multiply-add).  Rounding points:
+ *   LL_ROUNDING_FUSED (legolink_triton.py:413-470): bf16 K with an fp32 cache
+ *     computes the delta and the rotation in fp32 and rounds once to bf16 at
+ *     the store; bf16 K with a bf16 or fp16 cache rounds every product and sum
+ *     (delta and rotation) to bf16; fp16 K computes in fp32 and rounds once to
+ *     fp16.
+ *   LL_ROUNDING_EAGER (pic_runtime.py:6039-6058, :1874-1885): every product
+ *     and sum of the delta is rounded to the cache's dtype (fp32 ops for an
+ *     fp32 cache), dc and ds are then rounded to the key dtype, and every
+ *     product and sum of the rotation is rounded to the key dtype.
  *
  * Replaces, with num_layers == 1, fused_kv_link_inplace
  * (patched_sglang_files/python/sglang/srt/legolink_triton.py:550-645), and with
@@ -171,6 +194,7 @@ typedef struct ll_kv_link_args {
                                       loads (+1-2 % on random rows); 0: rows may repeat (batched
                                       requests sharing blocks) or be cache-resident and stay
                                       cacheable.  The result is the same either way.  (ABI 8) */
+  int64_t rounding;                /* LL_ROUNDING_FUSED or LL_ROUNDING_EAGER (ABI 9) */
 } ll_kv_link_args;
 
 /*

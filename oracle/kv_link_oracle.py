@@ -4,12 +4,16 @@ TEST INFRASTRUCTURE ONLY: only tests/, __graft_entry__.smoke() and bench.py's
 CPU-baseline leg may import this module, and only as the checker.  The product
 path (legolink_amd) never calls it.
 
-Two independent restatements of the per-token K arithmetic of the reference's
-fused link kernel (patched_sglang_files/python/sglang/srt/legolink_triton.py:
-302-547), which the tests check against each other bit for bit:
+Two independent restatements of the per-token K arithmetic of the reference,
+which the tests check against each other bit for bit:
 
 * ``rerotate_rows_c``      plain C (ll_oracle.c), one element at a time;
 * ``rerotate_rows_numpy``  numpy float32 ufuncs, one rounding per operation.
+
+Both take ``rounding``: ``FUSED`` (the default) follows the reference's fused
+link kernel (patched_sglang_files/python/sglang/srt/legolink_triton.py:
+302-547); ``EAGER`` follows its torch path (pic_runtime.py:6039-6058 and
+:1874-1885), whose rounding points differ.
 
 plus the pool-level semantics around them:
 
@@ -36,6 +40,7 @@ C_SOURCE = ORACLE_DIR / "ll_oracle.c"
 C_LIBRARY = ORACLE_DIR / "libll_oracle.so"
 
 F16, BF16, F32 = 1, 2, 3
+FUSED, EAGER = 0, 1
 _DTYPE_CODES = {"float16": F16, "bfloat16": BF16, "float32": F32}
 
 
@@ -78,7 +83,7 @@ def c_oracle() -> ctypes.CDLL:
         i64 = ctypes.c_int64
         lib.llo_rerotate_rows.argtypes = [
             ptr, ptr, i64, i64, i64, ctypes.c_int, ptr, ctypes.c_int,
-            i64, i64, i64, ptr, ptr, i64, ctypes.c_int, i64,
+            i64, i64, i64, ptr, ptr, i64, ctypes.c_int, i64, ctypes.c_int,
         ]
         lib.llo_rerotate_rows.restype = ctypes.c_int
         lib.llo_f32_to_bf16.argtypes = [ctypes.c_float]
@@ -152,6 +157,14 @@ def _round_bf16(values: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(f32_to_bf16_bits(values))
 
 
+def _stored_as(values: np.ndarray, dtype: int) -> np.ndarray:
+    """fp32 values stored in ``dtype`` and read back (F32: unchanged)."""
+
+    if dtype == F32:
+        return np.asarray(values, dtype=np.float32)
+    return _to_f32(_from_f32(values, dtype), dtype)
+
+
 def cache_to_f32(cache: np.ndarray, cache_dtype: int) -> np.ndarray:
     if cache_dtype == F32:
         return np.asarray(cache, dtype=np.float32)
@@ -172,6 +185,7 @@ def rerotate_rows_numpy(
     rotary_dim: int,
     neox: bool,
     prefix: int,
+    rounding: int = FUSED,
 ) -> np.ndarray:
     """rows [T, H, D] uint16 -> re-rotated rows (t >= prefix), copies (t < prefix)."""
 
@@ -195,7 +209,16 @@ def rerotate_rows_numpy(
         d2 = d1 + 1
     x1 = _to_f32(rows[tail][:, :, d1], key_dtype)
     x2 = _to_f32(rows[tail][:, :, d2], key_dtype)
-    if key_dtype == BF16 and cache_dtype != F32:
+    if rounding == EAGER:
+        # the delta as tensors of the cache's dtype, cast to the key dtype,
+        # then the rotation as tensors of the key dtype
+        dc = _stored_as(_stored_as(gc * lc, cache_dtype) + _stored_as(gs * ls, cache_dtype), cache_dtype)
+        ds = _stored_as(_stored_as(gs * lc, cache_dtype) - _stored_as(gc * ls, cache_dtype), cache_dtype)
+        dc = _stored_as(dc, key_dtype)
+        ds = _stored_as(ds, key_dtype)
+        o1 = _from_f32(_stored_as(x1 * dc, key_dtype) - _stored_as(x2 * ds, key_dtype), key_dtype)
+        o2 = _from_f32(_stored_as(x2 * dc, key_dtype) + _stored_as(x1 * ds, key_dtype), key_dtype)
+    elif key_dtype == BF16 and cache_dtype != F32:
         dc = _round_bf16(_round_bf16(gc * lc) + _round_bf16(gs * ls))
         ds = _round_bf16(_round_bf16(gs * lc) - _round_bf16(gc * ls))
         first_cos = _round_bf16(x1 * dc)
@@ -227,6 +250,7 @@ def rerotate_rows_c(
     rotary_dim: int,
     neox: bool,
     prefix: int,
+    rounding: int = FUSED,
 ) -> np.ndarray:
     rows = np.ascontiguousarray(rows, dtype=np.uint16)
     local = np.ascontiguousarray(local, dtype=np.int64)
@@ -252,6 +276,7 @@ def rerotate_rows_c(
         rotary_dim,
         1 if neox else 0,
         int(prefix),
+        int(rounding),
     )
     if rc != 0:
         raise IndexError("a remapped token's position is outside the cos/sin cache")
@@ -279,6 +304,7 @@ def link_pool(
     rerotate=rerotate_rows_c,
     source_key_layers: list[np.ndarray] | None = None,
     source_value_layers: list[np.ndarray] | None = None,
+    rounding: int = FUSED,
 ) -> tuple[list[np.ndarray], list[np.ndarray]]:
     """Expected pool after the link; the inputs are not modified.  Source rows
     come from ``source_*_layers`` when given, else from the pool itself."""
@@ -304,6 +330,7 @@ def link_pool(
             rotary_dim=rotary_dim,
             neox=neox,
             prefix=prefix,
+            rounding=rounding,
         )
         new_k = key.copy()
         new_v = value.copy()

@@ -19,6 +19,12 @@
  *                        :469-470  fp16 K: fp32 rotation, one RNE to fp16
  *                        :471-486  prefix tokens stored unrotated
  *                        :488-519  dims >= rotary_dim copied
+ *                      and, with rounding = 1 ("eager"), the reference's torch
+ *                      path instead, patched_sglang_files/python/sglang/srt/
+ *                      pic_runtime.py:6039-6058 (_remap_key_positions: the
+ *                      delta's products and sums in the cache's dtype) and
+ *                      :1874-1885 (_apply_rotary_emb: delta cast to the key
+ *                      dtype, every product and sum in the key dtype)
  *   llo_f32_to_bf16 / llo_f32_to_f16   round-to-nearest-even conversions.
  *
  * Compiled with gcc -O2 -ffp-contract=off: on x86-64 every float operation
@@ -105,6 +111,13 @@ void llo_f16_to_f32_array(const uint16_t *in, float *out, int64_t n) {
 
 static float round_bf16(float f) { return llo_bf16_to_f32(llo_f32_to_bf16(f)); }
 
+/* An fp32 result stored in `dtype` and read back (fp32: unchanged). */
+static float stored_as(float f, int dtype) {
+  if (dtype == LLO_BF16) return round_bf16(f);
+  if (dtype == LLO_F16) return llo_f16_to_f32(llo_f32_to_f16(f));
+  return f;
+}
+
 static float key_to_f32(uint16_t bits, int key_dtype) {
   return key_dtype == LLO_BF16 ? llo_bf16_to_f32(bits) : llo_f16_to_f32(bits);
 }
@@ -121,14 +134,15 @@ static float cache_at(const void *cache, int cache_dtype, int64_t offset) {
 
 /*
  * out[t] = in[t] re-rotated from local[t] to global[t] (t >= prefix) or copied
- * (t < prefix).  Returns 0, or -1 if a remapped token's position is outside
+ * (t < prefix); rounding 0 = the fused kernel's rounding points, 1 = the torch
+ * path's.  Returns 0, or -1 if a remapped token's position is outside
  * [0, cache_rows).
  */
 int llo_rerotate_rows(const uint16_t *in, uint16_t *out, int64_t num_tokens, int64_t num_heads,
                       int64_t head_dim, int key_dtype, const void *cache, int cache_dtype,
                       int64_t cache_rows, int64_t cs_stride_row, int64_t cs_stride_col,
                       const int64_t *local, const int64_t *global, int64_t rotary_dim, int neox,
-                      int64_t prefix) {
+                      int64_t prefix, int rounding) {
   const int64_t half = rotary_dim / 2;
   const int64_t row = num_heads * head_dim;
   for (int64_t t = 0; t < num_tokens; ++t) {
@@ -149,7 +163,25 @@ int llo_rerotate_rows(const uint16_t *in, uint16_t *out, int64_t num_tokens, int
         const float x1 = key_to_f32(src[h * head_dim + d1], key_dtype);
         const float x2 = key_to_f32(src[h * head_dim + d2], key_dtype);
         uint16_t o1, o2;
-        if (key_dtype == LLO_BF16 && cache_dtype != LLO_F32) {
+        if (rounding == 1) {
+          /* pic_runtime.py:6050-6051: torch tensors of the cache's dtype */
+          const float cos_local = stored_as(gc * lc, cache_dtype);
+          const float sin_local = stored_as(gs * ls, cache_dtype);
+          const float dcc = stored_as(cos_local + sin_local, cache_dtype);
+          const float sin_cos = stored_as(gs * lc, cache_dtype);
+          const float cos_sin = stored_as(gc * ls, cache_dtype);
+          const float dsc = stored_as(sin_cos - cos_sin, cache_dtype);
+          /* pic_runtime.py:1874-1882: cos/sin cast to the key dtype, then
+           * tensors of the key dtype */
+          const float dck = stored_as(dcc, key_dtype);
+          const float dsk = stored_as(dsc, key_dtype);
+          const float first_cos = stored_as(x1 * dck, key_dtype);
+          const float second_sin = stored_as(x2 * dsk, key_dtype);
+          const float second_cos = stored_as(x2 * dck, key_dtype);
+          const float first_sin = stored_as(x1 * dsk, key_dtype);
+          o1 = f32_to_key(first_cos - second_sin, key_dtype);
+          o2 = f32_to_key(second_cos + first_sin, key_dtype);
+        } else if (key_dtype == LLO_BF16 && cache_dtype != LLO_F32) {
           /* legolink_triton.py:437-468 */
           const float p1 = round_bf16(gc * lc);
           const float p2 = round_bf16(gs * ls);

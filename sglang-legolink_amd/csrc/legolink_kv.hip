@@ -20,10 +20,15 @@
 //
 // kv_scatter_kernel writes repaired boundary rows into the pool.
 //
-// Rounding follows patched_sglang_files/python/sglang/srt/legolink_triton.py:
-// 413-470: multiplies and adds are separate round-to-nearest-even fp32 ops (the
-// file is compiled with contraction off, so no FMA is formed) and K is rounded
-// once to bf16/fp16 at the store.
+// Two rounding semantics, both with separate round-to-nearest-even multiplies
+// and adds (the file is compiled with contraction off, so no FMA is formed):
+//   fused  the reference's fused kernel, patched_sglang_files/python/sglang/srt/
+//          legolink_triton.py:413-470: the delta and the rotation in fp32 and K
+//          rounded once at the store (bf16 K with a bf16/fp16 cache: every
+//          product and sum rounded to bf16);
+//   eager  the reference's torch path, pic_runtime.py:6025-6058 and :1868-1885:
+//          the delta computed in the cache's dtype and cast to the key dtype,
+//          then every product and sum of the rotation rounded to the key dtype.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -96,6 +101,7 @@ struct LinkParams {
   int idx64;                 // bit0 src, bit1 dst, bit2 local, bit3 global are int64
   int neox;
   int stream_rows;           // vector kernel: non-temporal row loads (rows read once)
+  int eager;                 // LL_ROUNDING_EAGER: the torch path's rounding points
 };
 
 struct ScatterParams {
@@ -140,9 +146,22 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return __half_as_ushort(__float2half_rn(f));
 }
 
-// Round an fp32 value to the nearest bf16 and widen it back.
+// Round an fp32 value to the nearest bf16 / fp16 and widen it back.
 __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+__device__ __forceinline__ float round_f16(float f) {
+  return f16_bits_to_f32(f32_to_f16_bits(f));
+}
+
+// Storage-type codes of the rounding helpers (the kernels' kCache / kKey
+// codes): 1 = fp16, 2 = bf16, 3 = fp32 (an fp32 op result is already rounded).
+template <int kTo>
+__device__ __forceinline__ float round_to(float f) {
+  if constexpr (kTo == 2) return round_bf16(f);
+  else if constexpr (kTo == 1) return round_f16(f);
+  else return f;
 }
 
 template <bool kBF16>
@@ -208,17 +227,17 @@ __device__ __forceinline__ void store_row_chunk(char *address, u32x4 value) {
 // Neox: x holds 8 elements of this lane's half, y the same 8 dims of the other
 // half.  out = x*dc + y*dsn, with dsn = -ds in the first half and +ds in the
 // second half:  first' = first*dc - second*ds,  second' = second*dc + first*ds.
-// kChain (bf16 K with a bf16/fp16 cache): each product rounded to bf16 before
-// the sum, as the reference's bf16 arithmetic does; otherwise fp32 throughout.
-// RNE is symmetric under negation, so rounding y * dsn equals negating the
-// rounded y * ds.
-template <bool kChain>
+// kProd rounds each product before the sum (round_to codes): to bf16 for the
+// fused bf16 chain (bf16 K with a bf16/fp16 cache) and to the key dtype for
+// the eager semantics; 3 keeps fp32.  The sum is rounded to the key dtype when
+// packed.  RNE is symmetric under negation, so rounding y * dsn equals
+// negating the rounded y * ds.
+template <int kProd>
 __device__ __forceinline__ float rot_term(float a, float b) {
-  if constexpr (kChain) return round_bf16(a * b);
-  else return a * b;
+  return round_to<kProd>(a * b);
 }
 
-template <bool kBF16, bool kChain>
+template <bool kBF16, int kProd>
 __device__ __forceinline__ u32x4 rotate_neox(u32x4 x, u32x4 y, const float *dc,
                                              const float *dsn) {
   u32x4 out;
@@ -228,26 +247,48 @@ __device__ __forceinline__ u32x4 rotate_neox(u32x4 x, u32x4 y, const float *dc,
     const float x1 = hi_elem<kBF16>(x[w]);
     const float y0 = lo_elem<kBF16>(y[w]);
     const float y1 = hi_elem<kBF16>(y[w]);
-    const float r0 = rot_term<kChain>(x0, dc[2 * w]) + rot_term<kChain>(y0, dsn[2 * w]);
-    const float r1 = rot_term<kChain>(x1, dc[2 * w + 1]) + rot_term<kChain>(y1, dsn[2 * w + 1]);
+    const float r0 = rot_term<kProd>(x0, dc[2 * w]) + rot_term<kProd>(y0, dsn[2 * w]);
+    const float r1 = rot_term<kProd>(x1, dc[2 * w + 1]) + rot_term<kProd>(y1, dsn[2 * w + 1]);
     out[w] = pack2<kBF16>(r0, r1);
   }
   return out;
 }
 
 // GPT-J style: every 32-bit word holds one (first, second) pair.
-template <bool kBF16, bool kChain>
+template <bool kBF16, int kProd>
 __device__ __forceinline__ u32x4 rotate_gptj(u32x4 x, const float *dc, const float *ds) {
   u32x4 out;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const float a = lo_elem<kBF16>(x[w]);
     const float b = hi_elem<kBF16>(x[w]);
-    const float r0 = rot_term<kChain>(a, dc[w]) - rot_term<kChain>(b, ds[w]);
-    const float r1 = rot_term<kChain>(b, dc[w]) + rot_term<kChain>(a, ds[w]);
+    const float r0 = rot_term<kProd>(a, dc[w]) - rot_term<kProd>(b, ds[w]);
+    const float r1 = rot_term<kProd>(b, dc[w]) + rot_term<kProd>(a, ds[w]);
     out[w] = pack2<kBF16>(r0, r1);
   }
   return out;
+}
+
+// Rounding points of one rounding semantics (round_to codes).  The delta's
+// products and sums round to kDelta, the delta is then cast to kCast, and the
+// rotation's products round to kProd.
+template <bool kBF16, int kCache, bool kEager>
+struct Rounding {
+  static constexpr int kKey = kBF16 ? 2 : 1;
+  // Fused: bf16 K with a 16-bit cache follows the reference's bf16 chain
+  // (legolink_triton.py:437-468), everything else stays fp32 (:413-436, :469-470).
+  static constexpr bool kFusedChain = kBF16 && kCache != 3;
+  static constexpr int kDelta = kEager ? kCache : (kFusedChain ? 2 : 3);
+  static constexpr int kCast = kEager ? (kCache == kKey ? 3 : kKey) : 3;
+  static constexpr int kProd = kEager ? kKey : (kFusedChain ? 2 : 3);
+};
+
+// The delta rotation of one pair: dc = gc*lc + gs*ls, ds = gs*lc - gc*ls.
+template <int kDelta, int kCast>
+__device__ __forceinline__ void delta_pair(float lc, float ls, float gc, float gs, float &dc,
+                                           float &ds) {
+  dc = round_to<kCast>(round_to<kDelta>(round_to<kDelta>(gc * lc) + round_to<kDelta>(gs * ls)));
+  ds = round_to<kCast>(round_to<kDelta>(round_to<kDelta>(gs * lc) - round_to<kDelta>(gc * ls)));
 }
 
 // N consecutive cos/sin table entries from element `offset`, widened to fp32
@@ -296,13 +337,13 @@ __device__ __forceinline__ void load_table(const void *cs, long long offset, flo
 // rotary_dim == kD, an fp32, bf16 or fp16 cos/sin cache (kCache) with unit
 // column stride and 16-byte aligned rows, 16-byte aligned layer buffers.
 // ---------------------------------------------------------------------------
-template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache, bool kStream>
+template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache, bool kStream,
+          bool kEager>
 __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   constexpr int kChunksPerHead = kD / 8;
   constexpr int kRotChunks = kR / 8;     // chunks of a head that rotate; the rest are copied
   constexpr int kPairs = kNeox ? 8 : 4;  // rotary pairs touched by one lane
-  // bf16 K with a 16-bit cache follows the reference's bf16-rounded chain.
-  constexpr bool kChain = kBF16 && kCache != 3;
+  using Round = Rounding<kBF16, kCache, kEager>;
   constexpr int kHalf = kR / 2;
   static_assert(kR == kD || kR * 2 == kD, "full or half rotary");
 
@@ -391,15 +432,8 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     load_table<kCache, kPairs>(p.cs, grow, gc);
     load_table<kCache, kPairs>(p.cs, grow + kHalf, gs);
 #pragma unroll
-    for (int e = 0; e < kPairs; ++e) {
-      if constexpr (kChain) {
-        dc[e] = round_bf16(round_bf16(gc[e] * lc[e]) + round_bf16(gs[e] * ls[e]));
-        ds[e] = round_bf16(round_bf16(gs[e] * lc[e]) - round_bf16(gc[e] * ls[e]));
-      } else {
-        dc[e] = gc[e] * lc[e] + gs[e] * ls[e];
-        ds[e] = gs[e] * lc[e] - gc[e] * ls[e];
-      }
-    }
+    for (int e = 0; e < kPairs; ++e)
+      delta_pair<Round::kDelta, Round::kCast>(lc[e], ls[e], gc[e], gs[e], dc[e], ds[e]);
   }
   float dsn[kPairs];
   if constexpr (kNeox) {
@@ -423,9 +457,9 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
       if constexpr (kNeox) {
         // Every lane takes part in the exchange (uniform control flow here).
         const u32x4 partner = xor_lane4<kRotChunks / 2>(kin[u]);
-        if (remap && rotating) kout = rotate_neox<kBF16, kChain>(kin[u], partner, dc, dsn);
+        if (remap && rotating) kout = rotate_neox<kBF16, Round::kProd>(kin[u], partner, dc, dsn);
       } else {
-        if (remap && rotating) kout = rotate_gptj<kBF16, kChain>(kin[u], dc, ds);
+        if (remap && rotating) kout = rotate_gptj<kBF16, Round::kProd>(kin[u], dc, ds);
       }
       if (ok && l + u < l1) {
         store_row_chunk(p.k_layers[l + u] + k_dst, kout);
@@ -460,8 +494,9 @@ __device__ __forceinline__ uint16_t f32_to_key(float f) {
   else return static_cast<uint16_t>(f32_to_f16_bits(f));
 }
 
-template <int kKey, int kCache>
+template <int kKey, int kCache, bool kEager>
 __global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p) {
+  using Round = Rounding<kKey == 2, kCache, kEager>;
   const int layer = blockIdx.y;
   const uint16_t *kbase = reinterpret_cast<const uint16_t *>(p.sk_layers[layer]);
   uint16_t *kout = reinterpret_cast<uint16_t *>(p.k_layers[layer]);
@@ -508,22 +543,14 @@ __global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p
               load_cache<kCache>(p.cs, gp * p.cs_stride_row + (i + half) * p.cs_stride_col);
           const float x1 = key_to_f32<kKey>(b1);
           const float x2 = key_to_f32<kKey>(b2);
-          if constexpr (kKey == 2 && kCache != 3) {
-            // bf16 K with a bf16/fp16 cache: every product and sum rounded to bf16.
-            const float dcb = round_bf16(round_bf16(gc * lc) + round_bf16(gs * ls));
-            const float dsb = round_bf16(round_bf16(gs * lc) - round_bf16(gc * ls));
-            const float first_cos = round_bf16(x1 * dcb);
-            const float second_sin = round_bf16(x2 * dsb);
-            const float second_cos = round_bf16(x2 * dcb);
-            const float first_sin = round_bf16(x1 * dsb);
-            o1 = static_cast<uint16_t>(f32_to_bf16_bits(first_cos - second_sin));
-            o2 = static_cast<uint16_t>(f32_to_bf16_bits(second_cos + first_sin));
-          } else {
-            const float dc = gc * lc + gs * ls;
-            const float ds = gs * lc - gc * ls;
-            o1 = f32_to_key<kKey>(x1 * dc - x2 * ds);
-            o2 = f32_to_key<kKey>(x2 * dc + x1 * ds);
-          }
+          float dc, ds;
+          delta_pair<Round::kDelta, Round::kCast>(lc, ls, gc, gs, dc, ds);
+          const float first_cos = round_to<Round::kProd>(x1 * dc);
+          const float second_sin = round_to<Round::kProd>(x2 * ds);
+          const float second_cos = round_to<Round::kProd>(x2 * dc);
+          const float first_sin = round_to<Round::kProd>(x1 * ds);
+          o1 = f32_to_key<kKey>(first_cos - second_sin);
+          o2 = f32_to_key<kKey>(second_cos + first_sin);
         }
         kd[h * p.kdim + d1] = o1;
         kd[h * p.kdim + d2] = o2;
@@ -707,6 +734,8 @@ int validate_link(const ll_kv_link_args *a) {
       a->waves_per_block != 4 && a->waves_per_block != 8)
     return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0, 1, 2, 4 or 8");
   if (a->layers_per_wave < 0) return fail(LL_ERR_LAUNCH_CONFIG, "layers_per_wave is negative");
+  if (a->rounding != LL_ROUNDING_FUSED && a->rounding != LL_ROUNDING_EAGER)
+    return fail(LL_ERR_INVALID_ARGUMENT, "unknown rounding %lld", static_cast<long long>(a->rounding));
   if (a->layer_groups_per_block < 0 ||
       (a->layer_groups_per_block > 0 &&
        ((a->waves_per_block ? a->waves_per_block : 4) % a->layer_groups_per_block) != 0))
@@ -797,64 +826,82 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
   return LL_OK;
 }
 
-template <bool kBF16, int kD, int kR, int kCache, bool kStream>
+template <bool kBF16, int kD, int kR, int kCache, bool kStream, bool kEager>
 void launch_vec_index(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   const bool index64 = (p.idx64 & 15) == 15;  // the vector kernel needs one index type
   if (neox) {
-    if (index64) kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream><<<grid, block, 0, s>>>(p);
+    if (index64)
+      kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+    else
+      kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
   } else {
-    if (index64) kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache, kStream><<<grid, block, 0, s>>>(p);
-    else kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache, kStream><<<grid, block, 0, s>>>(p);
+    if (index64)
+      kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+    else
+      kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
   }
 }
 
 // Streamed (non-temporal) row loads are built for the full-rotary fp32-table
 // kernels only, the production shape; other shapes load rows as usual.
-template <bool kBF16, int kD, int kR, int kCache>
+template <bool kBF16, int kD, int kR, int kCache, bool kEager>
 void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   if constexpr (kR == kD && kCache == 3) {
     if (p.stream_rows) {
-      launch_vec_index<kBF16, kD, kR, kCache, true>(grid, block, s, p, neox);
+      launch_vec_index<kBF16, kD, kR, kCache, true, kEager>(grid, block, s, p, neox);
       return;
     }
   }
-  launch_vec_index<kBF16, kD, kR, kCache, false>(grid, block, s, p, neox);
+  launch_vec_index<kBF16, kD, kR, kCache, false, kEager>(grid, block, s, p, neox);
 }
 
-template <bool kBF16, int kD, int kCache>
+template <bool kBF16, int kD, int kCache, bool kEager>
 void launch_vec_rotary(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
-  if (p.rotary_dim == kD) launch_vec_neox<kBF16, kD, kD, kCache>(grid, block, s, p, neox);
-  else launch_vec_neox<kBF16, kD, kD / 2, kCache>(grid, block, s, p, neox);
+  if (p.rotary_dim == kD) launch_vec_neox<kBF16, kD, kD, kCache, kEager>(grid, block, s, p, neox);
+  else launch_vec_neox<kBF16, kD, kD / 2, kCache, kEager>(grid, block, s, p, neox);
 }
 
-template <bool kBF16, int kCache>
+template <bool kBF16, int kCache, bool kEager>
 void launch_vec_dim(int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   switch (d) {
-    case 32: launch_vec_rotary<kBF16, 32, kCache>(grid, block, s, p, neox); break;
-    case 64: launch_vec_rotary<kBF16, 64, kCache>(grid, block, s, p, neox); break;
-    case 128: launch_vec_rotary<kBF16, 128, kCache>(grid, block, s, p, neox); break;
-    default: launch_vec_rotary<kBF16, 256, kCache>(grid, block, s, p, neox); break;
+    case 32: launch_vec_rotary<kBF16, 32, kCache, kEager>(grid, block, s, p, neox); break;
+    case 64: launch_vec_rotary<kBF16, 64, kCache, kEager>(grid, block, s, p, neox); break;
+    case 128: launch_vec_rotary<kBF16, 128, kCache, kEager>(grid, block, s, p, neox); break;
+    default: launch_vec_rotary<kBF16, 256, kCache, kEager>(grid, block, s, p, neox); break;
+  }
+}
+
+template <bool kBF16, bool kEager>
+void launch_vec_cache(int cache_dtype, int d, dim3 grid, dim3 block, hipStream_t s,
+                      const LinkParams &p, bool neox) {
+  switch (cache_dtype) {
+    case LL_DTYPE_FLOAT32: launch_vec_dim<kBF16, 3, kEager>(d, grid, block, s, p, neox); break;
+    case LL_DTYPE_BFLOAT16: launch_vec_dim<kBF16, 2, kEager>(d, grid, block, s, p, neox); break;
+    default: launch_vec_dim<kBF16, 1, kEager>(d, grid, block, s, p, neox); break;
   }
 }
 
 template <bool kBF16>
 void launch_vec(int cache_dtype, int d, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p,
                 bool neox) {
+  if (p.eager) launch_vec_cache<kBF16, true>(cache_dtype, d, grid, block, s, p, neox);
+  else launch_vec_cache<kBF16, false>(cache_dtype, d, grid, block, s, p, neox);
+}
+
+template <int kKey, bool kEager>
+void launch_generic_cache(int cache_dtype, dim3 grid, dim3 block, hipStream_t s,
+                          const LinkParams &p) {
   switch (cache_dtype) {
-    case LL_DTYPE_FLOAT32: launch_vec_dim<kBF16, 3>(d, grid, block, s, p, neox); break;
-    case LL_DTYPE_BFLOAT16: launch_vec_dim<kBF16, 2>(d, grid, block, s, p, neox); break;
-    default: launch_vec_dim<kBF16, 1>(d, grid, block, s, p, neox); break;
+    case LL_DTYPE_FLOAT32: kv_link_generic_kernel<kKey, 3, kEager><<<grid, block, 0, s>>>(p); break;
+    case LL_DTYPE_BFLOAT16: kv_link_generic_kernel<kKey, 2, kEager><<<grid, block, 0, s>>>(p); break;
+    default: kv_link_generic_kernel<kKey, 1, kEager><<<grid, block, 0, s>>>(p); break;
   }
 }
 
 template <int kKey>
 void launch_generic(int cache_dtype, dim3 grid, dim3 block, hipStream_t s, const LinkParams &p) {
-  switch (cache_dtype) {
-    case LL_DTYPE_FLOAT32: kv_link_generic_kernel<kKey, 3><<<grid, block, 0, s>>>(p); break;
-    case LL_DTYPE_BFLOAT16: kv_link_generic_kernel<kKey, 2><<<grid, block, 0, s>>>(p); break;
-    default: kv_link_generic_kernel<kKey, 1><<<grid, block, 0, s>>>(p); break;
-  }
+  if (p.eager) launch_generic_cache<kKey, true>(cache_dtype, grid, block, s, p);
+  else launch_generic_cache<kKey, false>(cache_dtype, grid, block, s, p);
 }
 
 }  // namespace
@@ -943,6 +990,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.num_slots = a->num_slots;
   p.src_num_slots = a->source_key_layers != nullptr ? a->source_num_slots : a->num_slots;
   p.stream_rows = a->stream_source_rows != 0 ? 1 : 0;
+  p.eager = a->rounding == LL_ROUNDING_EAGER ? 1 : 0;
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;

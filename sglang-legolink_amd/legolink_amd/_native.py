@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -27,6 +27,9 @@ DTYPE_FLOAT32 = 3
 DTYPE_INT32 = 4
 DTYPE_INT64 = 5
 DTYPE_UINT8 = 6
+
+ROUNDING_FUSED = 0
+ROUNDING_EAGER = 1
 
 KERNEL_AUTO = 0
 KERNEL_VECTOR = 1
@@ -101,6 +104,7 @@ class LinkArgs(ctypes.Structure):
         ("source_value_layers", _ptr),
         ("source_num_slots", _i64),
         ("stream_source_rows", _i64),
+        ("rounding", _i64),
     ]
 
 

@@ -32,15 +32,12 @@ def hipcc_path() -> str:
     return candidate
 
 
-def compile_command(output: Path, sources=SOURCES) -> list[str]:
-    sources = [sources] if isinstance(sources, Path) else list(sources)
+def _flags() -> list[str]:
     return [
-        hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
         "-O3",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         "-ffp-contract=off",
         "-Xclang",
         "-target-feature",
@@ -48,45 +45,52 @@ def compile_command(output: Path, sources=SOURCES) -> list[str]:
         "-packed-fp32-ops",
         "-Wall",
         f"-I{INCLUDE_DIR}",
-        "-o",
-        str(output),
-        *[str(source) for source in sources],
     ]
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile the link library; the output is replaced atomically."""
+def compile_command(output: Path, sources=SOURCES) -> list[str]:
+    """One hipcc call that compiles and links ``sources`` into ``output``."""
 
-    _compile(SOURCES, OUTPUT, verbose)
+    sources = [sources] if isinstance(sources, Path) else list(sources)
+    return [hipcc_path(), *_flags(), "-shared", "-o", str(output), *[str(source) for source in sources]]
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every translation unit in parallel, then link the library; the
+    output is replaced atomically."""
+
+    OUTPUT.parent.mkdir(parents=True, exist_ok=True)
+    with tempfile.TemporaryDirectory(dir=OUTPUT.parent, prefix=".build.") as scratch:
+        objects = [Path(scratch) / f"{source.stem}.o" for source in SOURCES]
+        jobs = [
+            (subprocess.Popen([hipcc_path(), *_flags(), "-c", "-o", str(obj), str(source)],
+                              stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True), source)
+            for source, obj in zip(SOURCES, objects)
+        ]
+        failures = []
+        for job, source in jobs:
+            output, _ = job.communicate()
+            messages = _messages(output)
+            if job.returncode != 0:
+                failures.append(f"hipcc failed on {source.name}:\n" + "\n".join(messages))
+            elif verbose and messages:
+                print("\n".join(messages), file=sys.stderr)
+        if failures:
+            raise RuntimeError("\n".join(failures))
+        temporary = Path(scratch) / OUTPUT.name
+        result = subprocess.run([hipcc_path(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o",
+                                 str(temporary), *[str(obj) for obj in objects]],
+                                capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + "\n".join(_messages(result.stdout + result.stderr)))
+        os.replace(temporary, OUTPUT)
     return OUTPUT
 
 
-def _compile(sources, output: Path, verbose: bool) -> None:
-    output.parent.mkdir(parents=True, exist_ok=True)
-    with tempfile.NamedTemporaryFile(
-        dir=output.parent, prefix=f".{output.stem}.", suffix=".so.tmp", delete=False
-    ) as handle:
-        temporary = Path(handle.name)
-    command = compile_command(temporary, sources)
-    try:
-        result = subprocess.run(command, capture_output=True, text=True)
-        # hipcc's host pass does not know the packed-fp32 target feature; that
-        # warning is expected and harmless.
-        messages = [
-            line
-            for line in (result.stdout + result.stderr).splitlines()
-            if "packed-fp32-ops" not in line and line.strip()
-        ]
-        if result.returncode != 0:
-            raise RuntimeError(
-                "hipcc failed:\n" + " ".join(command) + "\n" + "\n".join(messages)
-            )
-        if verbose and messages:
-            print("\n".join(messages), file=sys.stderr)
-        os.replace(temporary, output)
-    finally:
-        if temporary.exists():
-            temporary.unlink()
+def _messages(text: str) -> list[str]:
+    # hipcc's host pass does not know the packed-fp32 target feature; that
+    # warning is expected and harmless.
+    return [line for line in text.splitlines() if "packed-fp32-ops" not in line and line.strip()]
 
 
 if __name__ == "__main__":

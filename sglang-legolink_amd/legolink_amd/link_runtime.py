@@ -20,6 +20,15 @@ Also here, all on the same kernel:
   a linked range copied into new slots with K rotated from its global
   positions back to 0..n-1.
 
+Rounding of re-rotated K follows the reference's dispatch
+(pic_runtime.py:1307-1323, :5033-5035, :5153-5165): with the fused mode off
+(``SGLANG_PIC_TRITON_FUSED_KV_LINK`` = 0, its default) the reference runs its
+torch path, so the link uses the "eager" rounding points; with the mode on
+("1" / "auto") it uses the fused kernel's, unless a block is stored in clone
+mode ("required" then fails, "auto" falls back to eager).  Group promotion is
+always eager (``_remap_key_positions``, :5914-5919).  Both run on the same HIP
+kernels.
+
 Differences from the reference that keep the result identical:
 * repair rows (``imp_indices`` inside blocks) are dropped from the maps instead
   of being passed as a mask when ``compact_repair_rows`` is on (no empty waves);
@@ -47,6 +56,40 @@ from .rope import RotarySpec
 
 def _env_flag(name: str, default: str) -> bool:
     return os.getenv(name, default).strip().lower() in ("1", "true", "yes", "on")
+
+
+_FUSED_MODE_ALIASES = {
+    "0": "disabled", "false": "disabled", "off": "disabled", "disabled": "disabled",
+    "1": "required", "true": "required", "on": "required", "required": "required",
+    "auto": "auto",
+}
+
+
+def get_fused_kv_link_mode(raw: Optional[str] = None) -> str:
+    """"disabled", "required" or "auto", from ``raw`` or the environment
+    (get_triton_fused_kv_link_mode, pic_runtime.py:1307-1323: same variable,
+    aliases, default and error)."""
+
+    mode = (os.getenv("SGLANG_PIC_TRITON_FUSED_KV_LINK", "0") if raw is None else str(raw)).strip().lower()
+    normalized = _FUSED_MODE_ALIASES.get(mode)
+    if normalized is None:
+        raise LinkRuntimeError("SGLANG_PIC_TRITON_FUSED_KV_LINK must be 0, 1, or auto.")
+    return normalized
+
+
+def link_rounding(mode: str, has_clone_blocks: bool) -> tuple[str, Optional[str]]:
+    """(rounding, fallback reason) of a link under the fused ``mode``: the
+    reference runs its fused kernel only with the mode on and every block read
+    from pool slots (pic_runtime.py:5033-5035), else its torch path; "required"
+    fails where the fused kernel cannot run (:5153-5157)."""
+
+    if mode == "disabled":
+        return "eager", None
+    if has_clone_blocks:
+        if mode == "required":
+            raise LinkRuntimeError("Required Triton LegoLink fusion is unavailable: reference_storage_required")
+        return "eager", "reference_storage_required"
+    return "fused", None
 
 
 class KVPool:
@@ -273,7 +316,8 @@ class PreparedLink:
                  groups: list[tuple[list[int], RotarySpec]], boundary_repair_aware: bool,
                  compact_repair_rows: bool, num_warps: Optional[int], layers_per_wave: int,
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
-                 layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None) -> None:
+                 layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None,
+                 fused_mode: str = "required") -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -283,8 +327,11 @@ class PreparedLink:
         value_buffers = [pool.get_value_buffer(layer) for layer in layers]
         self.key_buffers, self.value_buffers = key_buffers, value_buffers
         token_count = maps.token_count
-        if bool((maps.blocks.sets == 1).any()) and arena is None:
+        has_clone = bool((maps.blocks.sets == 1).any())
+        if has_clone and arena is None:
             raise LinkRuntimeError("PIC link of clone-mode blocks needs the snapshot arena.")
+        self.fused_mode = fused_mode
+        self.rounding, self.fallback_reason = link_rounding(fused_mode, has_clone)
         repair_positions = maps.repair_positions if boundary_repair_aware else np.zeros(0, dtype=np.int64)
         plan = link_maps.plan_segments(maps.blocks, repair_positions, compact=compact_repair_rows,
                                        leading_blocks=maps.leading_blocks)
@@ -351,6 +398,7 @@ class PreparedLink:
                     source_value_buffers=(None if source_arena is None else
                                           [source_arena.get_value_buffer(layer) for layer in group_layers]),
                     stream_source_rows=self.stream_source_rows,
+                    rounding=self.rounding,
                 ))
         key_row = int(key_buffers[0][0].numel()) * key_buffers[0].element_size()
         value_row = int(value_buffers[0][0].numel()) * value_buffers[0].element_size()
@@ -405,6 +453,9 @@ class PreparedLink:
                               for handle, start in zip(self.maps.handles, blocks.starts.tolist())],
             "storage_modes": [handle.storage_mode for handle in self.maps.handles],
             "map_runs": int(self.segment_plan.table.shape[0]),
+            "fused_mode": self.fused_mode,
+            "rounding": self.rounding,
+            "fallback_reason": self.fallback_reason,
             **self.traffic,
         }
 
@@ -415,8 +466,13 @@ class KVLinkExecutor:
     def __init__(self, registry: LegoLinkBlockRegistry, rotary: RotarySpec | Mapping[int, RotarySpec], *,
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
                  layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
-                 layer_groups_per_block: int = 0) -> None:
+                 layer_groups_per_block: int = 0, fused_mode: Optional[str] = None) -> None:
+        """``fused_mode`` ("disabled" / "required" / "auto", or the reference's
+        aliases) fixes the link's rounding; None reads
+        ``SGLANG_PIC_TRITON_FUSED_KV_LINK`` at every link, as the reference does."""
+
         self.registry = registry
+        self.fused_mode = None if fused_mode is None else get_fused_kv_link_mode(fused_mode)
         self.start_layer = int(start_layer)
         self.end_layer = int(end_layer)
         if isinstance(rotary, RotarySpec):
@@ -431,6 +487,9 @@ class KVLinkExecutor:
     @property
     def layers(self) -> list[int]:
         return list(range(self.start_layer, self.end_layer))
+
+    def _fused_mode(self) -> str:
+        return self.fused_mode if self.fused_mode is not None else get_fused_kv_link_mode()
 
     # -- maps ---------------------------------------------------------------
     def build_link_maps(self, destination_slots: torch.Tensor, link_plan: Mapping[str, Any],
@@ -529,7 +588,7 @@ class KVLinkExecutor:
             boundary_repair_aware=bool(boundary_repair_aware), compact_repair_rows=compact_repair_rows,
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
-            layer_groups_per_block=self.layer_groups_per_block,
+            layer_groups_per_block=self.layer_groups_per_block, fused_mode=self._fused_mode(),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -562,6 +621,7 @@ class KVLinkExecutor:
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, order_by_source=order_by_source,
+            fused_mode=self._fused_mode(),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -604,7 +664,7 @@ class KVLinkExecutor:
 
     def _copy_rows(self, *, destination: Any, source: Any, source_slots: torch.Tensor,
                    destination_slots: torch.Tensor, local: torch.Tensor, global_: torch.Tensor,
-                   prefix: int) -> None:
+                   prefix: int, rounding: str = "fused") -> None:
         """One link launch between two pools (or within one) over every layer."""
 
         max_position = int(max(int(local.max()), int(global_.max()))) if prefix < local.numel() else 0
@@ -628,6 +688,7 @@ class KVLinkExecutor:
                 source_value_buffers=None if same_pool else [source.get_value_buffer(layer) for layer in group_layers],
                 stream_source_rows=(int(source_slots.numel()) * len(group_layers)
                                     * _row_bytes(source, group_layers[0]) > MEMORY_SIDE_CACHE_BYTES),
+                rounding=rounding,
             )
 
     def capture_block(self, pool: Any, cache_key: str, token_ids: Sequence[int], slots: torch.Tensor, *,
@@ -736,7 +797,8 @@ class KVLinkExecutor:
         with K rotated from its global positions back to 0..n-1, and register
         the copy as a block (_promote_reconstructed_group,
         pic_runtime.py:5901-5922).  Like the reference, the rotation runs even
-        when the group starts at position 0."""
+        when the group starts at position 0, with the torch path's rounding
+        (``_remap_key_positions``, :5914-5919) whatever the fused mode."""
 
         _validate_pool(pool)
         count = int(group_end) - int(group_start)
@@ -754,6 +816,6 @@ class KVLinkExecutor:
         self._copy_rows(destination=pool, source=pool,
                         source_slots=destination_slots[group_start:group_end].contiguous(),
                         destination_slots=new_slots, local=global_positions, global_=local_positions,
-                        prefix=0)
+                        prefix=0, rounding="eager")
         return self.registry.register_legolink_block(cache_key, token_ids, new_slots,
                                                      storage_mode="reference")

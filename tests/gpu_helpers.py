@@ -47,6 +47,42 @@ def row_checksums(buffer: torch.Tensor) -> torch.Tensor:
     return buffer.view(torch.int16).sum(dim=(1, 2), dtype=torch.int64)
 
 
+def _link_through_executor(workload: LinkWorkload, keys, values, table, repaired_k, repaired_v,
+                           device, *, fused_mode: str, with_scatter: bool) -> dict:
+    """The link step exactly as bench.py runs it: blocks registered, the plan
+    prepared by the executor (map builder on the device, repair rows left out
+    of the maps, non-temporal row loads for a single request larger than the
+    memory-side cache), then the link launch and the repaired-row write-back."""
+
+    from legolink_amd.link_runtime import KVLinkExecutor, KVPool
+    from legolink_amd.registry import LegoLinkBlockRegistry
+    from legolink_amd.rope import RotarySpec
+
+    registry = LegoLinkBlockRegistry()
+    blocks, requests = workload.link_requests()
+    for key, (source, local) in blocks.items():
+        registry.register_legolink_block(key, range(source.size), torch.from_numpy(source).to(device),
+                                         compile_local_positions=local.tolist())
+    executor = KVLinkExecutor(registry, RotarySpec(table, rotary_dim=workload.rotary_dim),
+                              end_layer=workload.shape.layers, fused_mode=fused_mode)
+    pool = KVPool(keys, values)
+    requests = [(torch.from_numpy(slots).to(device), plan) for slots, plan in requests]
+    if len(requests) == 1:
+        prepared = executor.prepare_link(pool, requests[0][0], requests[0][1], boundary_repair_aware=True,
+                                         compact_repair_rows=True)
+    else:
+        prepared = executor.prepare_links(pool, requests, boundary_repair_aware=True, compact_repair_rows=True)
+    assert prepared.linked_token_count == workload.tokens - workload.repair_rows
+    assert np.array_equal(prepared.repair_destination_slots.cpu().numpy(), workload.repair_destination_slots)
+    launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows),
+                  rounding=prepared.rounding)
+    report(f"[{workload.name}] executor link {launch}")
+    prepared.launch()
+    if with_scatter:
+        prepared.write_repaired(repaired_k, repaired_v)
+    return launch
+
+
 def check_workload(
     workload: LinkWorkload,
     device: torch.device,
@@ -55,9 +91,14 @@ def check_workload(
     with_scatter: bool = True,
     kernel: int = 0,
     seed: int = 7,
+    rounding: str = "fused",
+    via_executor: bool = False,
 ) -> dict:
     """Run one link step (link + repaired-row scatter) of ``workload`` on the GPU
-    and compare it with the oracle.  Returns summary counts."""
+    and compare it with the oracle.  ``via_executor`` runs it through
+    KVLinkExecutor.prepare_link as bench.py does (then the fused mode follows
+    ``rounding``: "required" for fused, "disabled" for eager); otherwise
+    through the all-layer operator with a repair mask.  Returns summary counts."""
 
     shape = workload.shape
     report(f"[{workload.name}] pool {workload.num_slots} slots x {shape.layers} layers, "
@@ -92,18 +133,24 @@ def check_workload(
                        row_checksums(key), row_checksums(value)))
     torch.cuda.synchronize(device)
 
-    report(f"[{workload.name}] link launch {kv_link.describe_link_launch(key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst, local_positions=local, global_positions=glob, cos_sin_cache=table, prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim, is_neox_style=True, repair_mask=mask, kernel=kernel)}")
-    kv_link.fused_kv_link_layers_inplace(
-        key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
-        local_positions=local, global_positions=glob, cos_sin_cache=table,
-        prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
-        is_neox_style=True, repair_mask=mask, kernel=kernel,
-    )
-    if with_scatter:
-        kv_link.scatter_kv_rows_inplace(
-            key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
-            repaired_keys=repaired_k, repaired_values=repaired_v,
+    launch = None
+    if via_executor:
+        launch = _link_through_executor(workload, keys, values, table, repaired_k, repaired_v, device,
+                                        fused_mode="required" if rounding == "fused" else "disabled",
+                                        with_scatter=with_scatter)
+    else:
+        report(f"[{workload.name}] link launch {kv_link.describe_link_launch(key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst, local_positions=local, global_positions=glob, cos_sin_cache=table, prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim, is_neox_style=True, repair_mask=mask, kernel=kernel)}")
+        kv_link.fused_kv_link_layers_inplace(
+            key_buffers=keys, value_buffers=values, source_slots=src, destination_slots=dst,
+            local_positions=local, global_positions=glob, cos_sin_cache=table,
+            prefix_token_count=workload.prefix_token_count, rotary_dim=workload.rotary_dim,
+            is_neox_style=True, repair_mask=mask, kernel=kernel, rounding=rounding,
         )
+        if with_scatter:
+            kv_link.scatter_kv_rows_inplace(
+                key_buffers=keys, value_buffers=values, destination_slots=repair_slots,
+                repaired_keys=repaired_k, repaired_values=repaired_v,
+            )
     torch.cuda.synchronize(device)
     report(f"[{workload.name}] kernels done; comparing {len(tokens)} tokens with the oracle")
 
@@ -125,6 +172,7 @@ def check_workload(
         expected_k = ko.rerotate_rows_c(
             bits(src_k), local_t, global_t, table_host, key_dtype=ko.BF16, cache_dtype=ko.F32,
             rotary_dim=workload.rotary_dim, neox=True, prefix=prefix_t,
+            rounding=ko.EAGER if rounding == "eager" else ko.FUSED,
         )
         expected_v = bits(src_v)
         if with_scatter:
@@ -144,7 +192,7 @@ def check_workload(
             f"{workload.name} layer {layer}: K rows outside the destinations changed")
         assert torch.equal(row_checksums(value)[untouched], ck_v[untouched]), (
             f"{workload.name} layer {layer}: V rows outside the destinations changed")
-    report(f"[{workload.name}] all {shape.layers} layers bit-exact")
+    report(f"[{workload.name}] all {shape.layers} layers bit-exact ({rounding} rounding)")
     del keys, values, before
     torch.cuda.empty_cache()
-    return {"tokens_checked": len(tokens), "mismatches": mismatches}
+    return {"tokens_checked": len(tokens), "mismatches": mismatches, "launch": launch}

@@ -1,7 +1,9 @@
 """GPU parity of the HIP link and repair-row scatter against the CPU oracle.
 
 Bar: bit-exact on every element (V and copied K are bit copies; re-rotated K
-follows the fused rounding exactly, which implies <= 1 bf16 ulp).
+follows the chosen rounding -- the reference's fused kernel or its torch path
+-- exactly, which for the fused rounding implies <= 1 bf16 ulp of the exact
+rotation).
 """
 
 from __future__ import annotations
@@ -71,11 +73,11 @@ CASES = [
 ]
 
 
-def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense"):
+def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense", rounding="fused"):
     (name, dtype, cache_dtype, heads, kdim, vdim, rotary, neox, kernel, index_dtype, prefix,
      mask_fraction, layers, tokens, expected_kernel) = case
     report(f"case {name}: layers={layers} heads={heads} kdim={kdim} vdim={vdim} rotary={rotary} "
-           f"neox={neox} tokens={tokens} kernel={kernel}")
+           f"neox={neox} tokens={tokens} kernel={kernel} rounding={rounding}")
     slots = 2 * tokens + 41
     rng = np.random.default_rng(seed)
     perm = rng.permutation(slots)
@@ -103,6 +105,7 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         key_np, value_np, src_np, dst_np, local_np, global_np, cache_host(table),
         key_dtype=TORCH_TO_CODE[dtype], cache_dtype=TORCH_TO_CODE[cache_dtype],
         rotary_dim=rotary, neox=neox, prefix=prefix, repair_mask=mask_np if mask is not None else None,
+        rounding=ko.EAGER if rounding == "eager" else ko.FUSED,
     )
     launch = kv_link.describe_link_launch(
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
@@ -115,7 +118,7 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
         local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
         prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
-        kernel=kernel,
+        kernel=kernel, rounding=rounding,
     )
     torch.cuda.synchronize(device)
     for layer in range(layers):
@@ -131,6 +134,13 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
 @pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])
 def test_link_matches_oracle(gpu_device, case):
     _run_case(gpu_device, case)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])
+def test_eager_link_matches_oracle(gpu_device, case):
+    """The torch path's rounding points (pic_runtime.py:6025-6058) on every shape."""
+
+    _run_case(gpu_device, case, rounding="eager")
 
 
 def test_bool_mask_and_strided_cache(gpu_device):
@@ -336,6 +346,31 @@ def test_full_size_workload(gpu_device, name, sample):
 
 def test_full_size_workload_generic_kernel(gpu_device):
     result = check_workload(make_workload("c1"), gpu_device, kernel=GENERIC)
+    assert result["mismatches"] == 0
+
+
+@pytest.mark.parametrize("name", ["c2", "c5"])
+def test_full_size_link_as_benched(gpu_device, name):
+    """The exact link bench.py times: the executor with repair rows left out of
+    the device-built maps, non-temporal row loads, fused rounding."""
+
+    result = check_workload(make_workload(name), gpu_device, via_executor=True, rounding="fused")
+    assert result["mismatches"] == 0
+    assert result["launch"]["stream_source_rows"] and result["launch"]["kernel"] == "vector"
+
+
+@pytest.mark.parametrize("name", ["c2", "c5"])
+def test_full_size_eager_link(gpu_device, name):
+    """The reference's default link (fused mode off: its torch path's rounding)
+    through the executor at full size."""
+
+    result = check_workload(make_workload(name), gpu_device, via_executor=True, rounding="eager")
+    assert result["mismatches"] == 0
+    assert result["launch"]["rounding"] == "eager"
+
+
+def test_full_size_eager_link_generic_kernel(gpu_device):
+    result = check_workload(make_workload("c1"), gpu_device, kernel=GENERIC, rounding="eager")
     assert result["mismatches"] == 0
 
 

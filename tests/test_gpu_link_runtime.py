@@ -72,8 +72,9 @@ def test_first_block_remap_cases(gpu_device, case):
                                   ko.f32_to_bf16_bits(compiled.astype(np.float32)))
 
 
-def _flow(device, *, boundary_repair_aware, compact, seed=3):
-    """Register 5 blocks, derive a plan, link, write repaired rows."""
+def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="required"):
+    """Register 5 blocks, derive a plan, link, write repaired rows; the result is
+    checked with the oracle of the rounding the fused mode selects."""
 
     rng = np.random.default_rng(seed)
     layers, heads, dim, slots = 6, 4, 128, 8192
@@ -102,7 +103,7 @@ def _flow(device, *, boundary_repair_aware, compact, seed=3):
     linked = resolve_link_plan(registry.get_legolink_block_tokens, host_tokens, plan)
     destination = torch.from_numpy(perm[cursor : cursor + len(linked)]).to(device)
     rotary = RotarySpec(build_cos_sin_cache(2048, dim), rotary_dim=dim)
-    executor = KVLinkExecutor(registry, rotary, end_layer=layers)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode=fused_mode)
     before_k = [bits(k) for k in pool.k_buffer]
     before_v = [bits(v) for v in pool.v_buffer]
     prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=boundary_repair_aware,
@@ -122,6 +123,7 @@ def _flow(device, *, boundary_repair_aware, compact, seed=3):
         maps.local_positions, maps.global_positions, rotary.cos_sin_cache.cpu().numpy(),
         key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=dim, neox=True,
         prefix=maps.prefix_token_count, repair_mask=mask if repair_rows else None,
+        rounding=ko.EAGER if prepared.rounding == "eager" else ko.FUSED,
     )
     if repair_rows:
         expected_k, expected_v = ko.scatter_rows(expected_k, expected_v,
@@ -139,6 +141,22 @@ def test_plan_link_repair_flow_matches_oracle(gpu_device):
     assert prepared.repair_offsets.size == 4 * 16
     assert prepared.maps.block_specs[3]["needs_rope_remap"]
     assert prepared.linked_token_count == prepared.maps.token_count - 64
+
+
+@pytest.mark.parametrize("fused_mode,rounding", [("disabled", "eager"), ("auto", "fused"), ("1", "fused")])
+def test_fused_mode_selects_the_rounding(gpu_device, fused_mode, rounding):
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=21, fused_mode=fused_mode)
+    assert prepared.rounding == rounding
+    assert prepared.record()["rounding"] == rounding
+
+
+def test_fused_mode_defaults_to_the_environment(gpu_device, monkeypatch):
+    monkeypatch.delenv("SGLANG_PIC_TRITON_FUSED_KV_LINK", raising=False)
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=22, fused_mode=None)
+    assert prepared.rounding == "eager"  # the reference's default: its torch path
+    monkeypatch.setenv("SGLANG_PIC_TRITON_FUSED_KV_LINK", "required")
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=22, fused_mode=None)
+    assert prepared.rounding == "fused"
 
 
 def test_compacted_and_masked_links_agree(gpu_device):
@@ -169,7 +187,7 @@ def test_executor_matches_the_per_layer_drop_in_operator(gpu_device):
                                                      {"start_token": 300, "end_token": 1000}]}
     destination = torch.from_numpy(perm[1000:2000]).to(gpu_device)
     rotary = RotarySpec(build_cos_sin_cache(2048, 128), rotary_dim=128)
-    executor = KVLinkExecutor(registry, rotary, end_layer=layers)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode="required")
     executor.copy_linked_kv(KVPool(keys, values), destination, plan)
     maps = executor.build_link_maps(destination, plan)
     local = torch.from_numpy(maps.local_positions).to(gpu_device)
@@ -233,8 +251,9 @@ def test_prepared_link_replays_in_a_hip_graph(gpu_device):
             assert np.array_equal(a, b), f"replay {replay}"
 
 
+@pytest.mark.parametrize("fused_mode", ["disabled", "auto"])
 @pytest.mark.parametrize("order_by_source", [True, False])
-def test_batched_link_equals_request_by_request_links(gpu_device, order_by_source):
+def test_batched_link_equals_request_by_request_links(gpu_device, order_by_source, fused_mode):
     """prepare_links over several requests -- identity first blocks, a request
     behind a chat prefix, a block compiled behind a prefix, clone blocks in
     the snapshot arena, shared blocks, repair rows -- leaves the pool
@@ -256,7 +275,7 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
                                    device=gpu_device)
     registry = LegoLinkBlockRegistry()
     rotary = RotarySpec(build_cos_sin_cache(8192, dim), rotary_dim=dim)
-    executor = KVLinkExecutor(registry, rotary, end_layer=layers, arena=arena)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers, arena=arena, fused_mode=fused_mode)
     perm = rng.permutation(slots)
     cursor = 0
     lengths = [120, 64, 300, 45, 200, 90]
@@ -289,6 +308,9 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
 
     batched = executor.prepare_links(pool_a, requests, boundary_repair_aware=True, order_by_source=order_by_source)
     assert batched.order_by_source == order_by_source
+    # Every request holds a clone block: the reference's torch path either way.
+    assert batched.rounding == "eager"
+    assert batched.fallback_reason == (None if fused_mode == "disabled" else "reference_storage_required")
     batched.launch()
     rows = int(batched.repair_offsets.size)
     repaired_k = torch.randn(layers, rows, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
@@ -323,3 +345,23 @@ def test_streamed_single_request_link_matches_oracle(gpu_device, monkeypatch):
     prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True, seed=13)
     assert prepared.stream_source_rows
     assert all(info["kernel"] == "vector" for info in prepared.launch_info)
+
+
+def test_required_fused_mode_refuses_clone_blocks(gpu_device):
+    """pic_runtime.py:5033-5035, :5153-5157: the fused kernel needs every block in
+    pool slots; "required" fails with the reference's message."""
+
+    from legolink_amd.errors import LinkRuntimeError
+    from legolink_amd.link_runtime import SnapshotArena
+
+    layers, slots = 2, 1024
+    pool = KVPool.allocate(num_slots=slots, num_layers=layers, num_heads=4, head_dim=128, device=gpu_device)
+    arena = SnapshotArena.allocate(num_slots=256, num_layers=layers, num_heads=4, head_dim=128, device=gpu_device)
+    registry = LegoLinkBlockRegistry()
+    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(1024, 128), rotary_dim=128),
+                              end_layer=layers, arena=arena, fused_mode="required")
+    executor.capture_block(pool, "c", list(range(50)), torch.arange(50, device=gpu_device), storage_mode="clone")
+    plan = {"cache_keys": ["c"], "block_ranges": [{"start_token": 10, "end_token": 60}]}
+    with pytest.raises(LinkRuntimeError, match="Required Triton LegoLink fusion is unavailable: "
+                                               "reference_storage_required"):
+        executor.prepare_link(pool, torch.arange(100, 200, device=gpu_device), plan)

@@ -114,8 +114,10 @@ def test_clone_blocks_survive_reuse_of_their_pool_slots(gpu_device):
         original_k, original_v, original_src, maps.destination_slots.cpu().numpy(),
         maps.local_positions, maps.global_positions, build_cos_sin_cache(4096, 128).numpy(),
         key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=128, neox=True,
-        prefix=maps.prefix_token_count, repair_mask=mask,
+        prefix=maps.prefix_token_count, repair_mask=mask, rounding=ko.EAGER,
     )
+    # The reference links clone blocks on its torch path (pic_runtime.py:5033-5035).
+    assert prepared.rounding == "eager"
     written = maps.destination_slots.cpu().numpy()[mask == 0]
     for layer in range(pool.layer_num):
         assert np.array_equal(bits(pool.k_buffer[layer])[written], expected_k[layer][written])
@@ -159,9 +161,11 @@ def test_group_promotion_round_trip(gpu_device):
     torch.cuda.synchronize(gpu_device)
     table = build_cos_sin_cache(4096, 128).numpy()
     for layer in range(pool.layer_num):
+        # _promote_reconstructed_group remaps with _remap_key_positions
+        # (pic_runtime.py:5914-5919): the torch path's rounding.
         expected = ko.rerotate_rows_c(linked[layer], np.arange(group["start_token"], group["end_token"]),
                                       np.arange(n_b), table, key_dtype=ko.BF16, cache_dtype=ko.F32,
-                                      rotary_dim=128, neox=True, prefix=0)
+                                      rotary_dim=128, neox=True, prefix=0, rounding=ko.EAGER)
         assert np.array_equal(bits(pool.k_buffer[layer])[new_slots.cpu().numpy()], expected)
     promoted = pool.k_buffer[0][new_slots].float().cpu().numpy()
     assert np.abs(promoted - compiled_b).max() < 0.06  # two bf16 re-rotations away from the original
@@ -232,8 +236,10 @@ def test_batched_capture_matches_block_by_block_capture(gpu_device):
         original_k, original_v, original_src, maps.destination_slots.cpu().numpy(),
         maps.local_positions, maps.global_positions, build_cos_sin_cache(4096, 128).numpy(),
         key_dtype=ko.BF16, cache_dtype=ko.F32, rotary_dim=128, neox=True,
-        prefix=maps.prefix_token_count, repair_mask=mask,
+        prefix=maps.prefix_token_count, repair_mask=mask, rounding=ko.EAGER,
     )
+    # The reference links clone blocks on its torch path (pic_runtime.py:5033-5035).
+    assert prepared.rounding == "eager"
     written = maps.destination_slots.cpu().numpy()[mask == 0]
     for layer in range(pool.layer_num):
         assert np.array_equal(bits(pool.k_buffer[layer])[written], expected_k[layer][written])

@@ -1,4 +1,5 @@
-"""Pins of the CPU oracle (no GPU).
+"""Pins of the CPU oracle (no GPU); the rounding branches beyond the fused
+fp32-table path are pinned in test_oracle_rounding_pins.py.
 
 The oracle is trusted only because of these checks:
 * conversions against library routines (torch bf16 cast, numpy fp16 cast);
@@ -111,12 +112,14 @@ def _case(
 @pytest.mark.parametrize("cache_dtype", [ko.F32, ko.BF16, ko.F16])
 @pytest.mark.parametrize("neox", [True, False])
 @pytest.mark.parametrize("rotary_dim,prefix", [(64, 0), (32, 17), (64, 96)])
-def test_c_and_numpy_restatements_agree(key_dtype, cache_dtype, neox, rotary_dim, prefix):
+@pytest.mark.parametrize("rounding", [ko.FUSED, ko.EAGER])
+def test_c_and_numpy_restatements_agree(key_dtype, cache_dtype, neox, rotary_dim, prefix, rounding):
     rows, local, global_, cache = _case(
         key_dtype=key_dtype, cache_dtype=cache_dtype, rotary_dim=rotary_dim
     )
     kwargs = dict(
-        key_dtype=key_dtype, cache_dtype=cache_dtype, rotary_dim=rotary_dim, neox=neox, prefix=prefix
+        key_dtype=key_dtype, cache_dtype=cache_dtype, rotary_dim=rotary_dim, neox=neox, prefix=prefix,
+        rounding=rounding,
     )
     from_c = ko.rerotate_rows_c(rows, local, global_, cache, **kwargs)
     from_numpy = ko.rerotate_rows_numpy(rows, local, global_, cache, **kwargs)
