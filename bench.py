@@ -193,6 +193,34 @@ def _median_ms(torch, run, steps: int, warmup: int) -> float:
 RUN_LENGTHS = (1, 2, 4, 8, 16, 64)
 
 
+SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", "contiguous")
+
+
+def ordered_maps(workload, run: int, order: str, seed: int):
+    """``run_length_maps`` visited in ``order``: "random" (as drawn),
+    "sorted_source" / "sorted_destination" (tokens reordered so that one map
+    increases; positions move with their tokens), "sorted_both" (each map
+    sorted on its own: the same slots, both increasing), "contiguous" (sources
+    [0, T), destinations [T, 2T)).  Returns src, dst, local, global."""
+
+    import numpy as np
+
+    local, glob = workload.local_positions, workload.global_positions
+    if order == "contiguous":
+        tokens = np.arange(workload.tokens, dtype=np.int64)
+        return tokens, tokens + workload.tokens, local, glob
+    src, dst = run_length_maps(workload, run, seed)
+    if order == "sorted_source":
+        index = np.argsort(src, kind="stable")
+        return src[index], dst[index], local[index], glob[index]
+    if order == "sorted_destination":
+        index = np.argsort(dst, kind="stable")
+        return src[index], dst[index], local[index], glob[index]
+    if order == "sorted_both":
+        return np.sort(src), np.sort(dst), local, glob
+    return src, dst, local, glob
+
+
 def run_length_maps(workload, run: int, seed: int):
     """Token maps of ``workload``'s tokens whose source and destination slots
     come in contiguous runs of ``run`` rows: the pool is cut into runs of
@@ -241,8 +269,6 @@ def run_sweep(args: argparse.Namespace) -> None:
     values = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
                           device=device, generator=generator) for _ in range(shape.layers)]
     table = build_cos_sin_cache(workload.max_position + 1, workload.rotary_dim, theta=workload.theta).to(device)
-    local = torch.from_numpy(workload.local_positions).to(device)
-    glob = torch.from_numpy(workload.global_positions).to(device)
     link_bytes = workload.tokens * shape.bytes_per_token
     # (name, launch keywords); the first is the executor's choice for a single request.
     default = {"num_warps": 4, "layers_per_wave": 0, "stream_source_rows": True}
@@ -259,11 +285,16 @@ def run_sweep(args: argparse.Namespace) -> None:
         ("waves_per_block_8", {"num_warps": 8}),
     ]
     rows, schedule, dispatch = [], [], 0
-    for run in RUN_LENGTHS:
-        src, dst = run_length_maps(workload, run, seed=20260824 + run)
+    cases = [(run, "random") for run in RUN_LENGTHS]
+    cases += [(1, order) for order in SWEEP_ORDERS if order != "random"]
+    for run, order in cases:
+        src, dst, local_np, global_np = ordered_maps(workload, run, order, seed=20260824 + run)
         src_t = torch.from_numpy(src).to(device)
         dst_t = torch.from_numpy(dst).to(device)
-        for name, changes in variants + (extra if run in detailed else []):
+        local = torch.from_numpy(np.ascontiguousarray(local_np)).to(device)
+        glob = torch.from_numpy(np.ascontiguousarray(global_np)).to(device)
+        chosen = variants + (extra if (run in detailed and order == "random") or order == "contiguous" else [])
+        for name, changes in chosen:
             options = dict(default, **changes)
             rotation_off = options.pop("rotation_off", False)
             prepared = kv_link.PreparedKVLink(
@@ -273,13 +304,14 @@ def run_sweep(args: argparse.Namespace) -> None:
                 rotary_dim=workload.rotary_dim, is_neox_style=True, **options)
             ms = _median_ms(torch, prepared, args.steps, args.warmup)
             launches = prepared.launch["launches"] * (args.steps + args.warmup)
-            schedule.append({"run": run, "variant": name, "first_dispatch": dispatch, "dispatches": launches})
+            schedule.append({"run": run, "order": order, "variant": name, "first_dispatch": dispatch,
+                             "dispatches": launches})
             dispatch += launches
-            rows.append({"run": run, "variant": name, "ms": round(ms, 5),
+            rows.append({"run": run, "order": order, "variant": name, "ms": round(ms, 5),
                          "GBps": round(link_bytes / ms / 1e6, 1),
                          "frac": round(link_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
                          "launch": prepared.launch})
-            log(f"run {run:3d} {name:20s} {ms:.4f} ms  {link_bytes / ms / 1e6:8.1f} GB/s")
+            log(f"run {run:3d} {order:18s} {name:20s} {ms:.4f} ms  {link_bytes / ms / 1e6:8.1f} GB/s")
     print(json.dumps({"sweep": rows, "schedule": schedule, "workload": workload.name,
                       "tokens": workload.tokens, "bytes_per_launch": link_bytes,
                       "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
