@@ -385,6 +385,29 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
                              ll_repair_attention_plan_info *info);
 int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream);
 
+/*
+ * Allocation-free repair attention.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, semantics and output as ll_repair_attention, except that
+ * args->workspace must be NULL: the split partial results go to a device array
+ * of LL_REPAIR_SCRATCH_BYTES that the library holds on every GPU it runs on,
+ * from its first use there until the process ends (args->workspace_items
+ * still gives the plan's partial count).  A plan whose partials need more --
+ * workspace_items * num_q_heads * (16 * head_dim + 32) * 4 bytes -- is
+ * rejected with LL_ERR_INVALID_ARGUMENT before any launch.  Nothing needs
+ * clearing: every partial the combine reads is written by the same call.
+ * Calls that overlap on one GPU (two streams, or two threads) share that
+ * GPU's array and race; serialise them.  The entry allocates nothing and
+ * calls no allocating routine; the first call on a device looks up the
+ * array's address there (hipGetSymbolAddress).
+ */
+#define LL_REPAIR_SCRATCH_BYTES (64LL << 20)
+int ll_repair_attention_noalloc(const ll_repair_attention_args *args, ll_stream_t stream);
+/* LL_REPAIR_SCRATCH_BYTES, as built into the library. */
+int64_t ll_repair_scratch_bytes(void);
+
 /* Which kernel and launch shape ll_kv_link would use (no GPU work). */
 typedef struct ll_launch_info {
   int64_t kernel;                  /* LL_KERNEL_VECTOR or LL_KERNEL_GENERIC */

@@ -39,6 +39,7 @@
 
 #include <algorithm>
 #include <functional>
+#include <mutex>
 #include <queue>
 #include <vector>
 
@@ -694,6 +695,145 @@ bool aligned(const void *ptr, uintptr_t bytes) {
   return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0;
 }
 
+// Split partial results of ll_repair_attention_noalloc: one array per device,
+// held from the library's load on that device until the process ends.  Host
+// code must not use the array's name as a device address (it is a host-side
+// stand-in); scratch_on() returns the device's own address of it.
+constexpr long long kScratchBytes = LL_REPAIR_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices];
+
+// The scratch array's address on `device`, looked up once per device with that
+// device current.  Returns nullptr (and records the error) on failure.
+float *scratch_on(int device) {
+  if (device < 0 || device >= kMaxDevices) {
+    fail(LL_ERR_INVALID_ARGUMENT, "device %d is outside the %d devices the scratch table covers", device,
+         kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] != nullptr) return g_scratch_ptr[device];
+  int current = -1;
+  hipError_t err = hipGetDevice(&current);
+  if (err == hipSuccess && current != device) err = hipSetDevice(device);
+  void *ptr = nullptr;
+  if (err == hipSuccess) err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (current >= 0 && current != device) {
+    const hipError_t restore = hipSetDevice(current);
+    if (err == hipSuccess) err = restore;
+  }
+  if (err != hipSuccess || ptr == nullptr) {
+    fail(LL_ERR_HIP, "scratch address on device %d: %s", device,
+         err != hipSuccess ? hipGetErrorString(err) : "null address");
+    return nullptr;
+  }
+  g_scratch_ptr[device] = static_cast<float *>(ptr);
+  return g_scratch_ptr[device];
+}
+
+// Checks of the repair attention's arguments other than the workspace.
+int check_attention_args(const ll_repair_attention_args *a) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_repair_attention_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_repair_attention_args));
+  if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
+    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes fp16 or bf16 queries and KV");
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64, 128 or 256");
+  if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
+      a->num_q_heads > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
+                "num_q_heads must be a multiple of num_kv_heads, at most 65535");
+  if (a->num_queries < 0 || a->num_slots < 0 || a->kv_slots_len < 0 || a->num_items < 0 ||
+      a->num_combine < 0 || a->workspace_items < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "counts must be >= 0");
+  if (a->num_slots > 0x7fffffff) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots must be below 2^31");
+  if (!(a->softmax_scale > 0.0) || !isfinite(a->softmax_scale))
+    return fail(LL_ERR_INVALID_ARGUMENT, "softmax_scale must be finite and > 0");
+  if (a->num_items == 0) return LL_OK;
+  if (a->num_items > 0x7fffffff || a->num_combine > 0x7fffffff)
+    return fail(LL_ERR_INVALID_ARGUMENT, "too many items");
+  if (a->query == nullptr || a->output == nullptr || a->key_buffer == nullptr ||
+      a->value_buffer == nullptr || a->kv_slots == nullptr || a->items == nullptr ||
+      a->query_positions == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "query/output/key/value/kv_slots/items/query_positions pointer is NULL");
+  if (a->kv_slots_dtype != LL_DTYPE_INT32 && a->kv_slots_dtype != LL_DTYPE_INT64)
+    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "kv_slots must be int32 or int64");
+  if (a->num_combine > 0 && a->combine == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split items need the combine table");
+  if (!aligned(a->query, 16) || !aligned(a->key_buffer, 16) || !aligned(a->value_buffer, 16) ||
+      !aligned(a->output, 8))
+    return fail(LL_ERR_INVALID_ARGUMENT, "query/key/value (16-byte) and output (8-byte) must be aligned");
+  return LL_OK;
+}
+
+// Launches the attention (and the combine of split items) with the partial
+// results in `ws` (ws_items partial slots); the arguments are checked.
+int launch_attention(const ll_repair_attention_args *a, float *ws, long long ws_items, hipStream_t s) {
+  AttnParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t *>(a->query);
+  p.out = static_cast<uint16_t *>(a->output);
+  p.k = static_cast<const uint16_t *>(a->key_buffer);
+  p.v = static_cast<const uint16_t *>(a->value_buffer);
+  p.slots = a->kv_slots;
+  p.items = a->items;
+  p.combine = a->combine;
+  p.positions = a->query_positions;
+  p.ws = ws;
+  p.num_queries = a->num_queries;
+  p.num_slots = a->num_slots;
+  p.slots_len = a->kv_slots_len;
+  p.ws_items = ws != nullptr ? ws_items : 0;
+  p.hq = static_cast<int>(a->num_q_heads);
+  p.hkv = static_cast<int>(a->num_kv_heads);
+  p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
+  // A workgroup holds every (tile, head) pair of its item when the waves
+  // allow, else the heads are split over several workgroups per KV head.
+  const int head_room = max_pairs(static_cast<int>(a->head_dim)) / tiles_per_item(p.group);
+  p.heads_per_wg = p.group < head_room ? p.group : head_room;
+  p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
+  p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
+  p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
+
+  if (a->num_kv_heads * p.head_chunks > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
+  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
+  const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
+  if (a->head_dim == 128) {
+    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
+  } else if (a->head_dim == 64) {
+    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
+  } else {
+    if (f16) repair_attention_m32_kernel<256, F16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
+    else repair_attention_m32_kernel<256, Bf16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  if (a->num_combine > 0) {
+    const dim3 cgrid(static_cast<unsigned>(a->num_combine), static_cast<unsigned>(a->num_q_heads));
+    if (a->head_dim == 128) {
+      if (f16) repair_combine_kernel<128, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<128, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    } else if (a->head_dim == 64) {
+      if (f16) repair_combine_kernel<64, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<64, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    } else {
+      if (f16) repair_combine_kernel<256, F16><<<cgrid, dim3(256), 0, s>>>(p);
+      else repair_combine_kernel<256, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
+    }
+    err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return LL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -881,99 +1021,43 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
 }
 
 int ll_repair_attention(const ll_repair_attention_args *a, ll_stream_t stream) {
-  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
-  if (a->struct_size != static_cast<int64_t>(sizeof(ll_repair_attention_args)))
-    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
-                static_cast<long long>(a->struct_size), sizeof(ll_repair_attention_args));
-  if (a->kv_dtype != LL_DTYPE_BFLOAT16 && a->kv_dtype != LL_DTYPE_FLOAT16)
-    return fail(LL_ERR_FP16_OR_BF16_REQUIRED, "repair attention takes fp16 or bf16 queries and KV");
-  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
-    return fail(LL_ERR_HEAD_DIMENSION_OUT_OF_RANGE, "head_dim must be 64, 128 or 256");
-  if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0 ||
-      a->num_q_heads > 65535)
-    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH,
-                "num_q_heads must be a multiple of num_kv_heads, at most 65535");
-  if (a->num_queries < 0 || a->num_slots < 0 || a->kv_slots_len < 0 || a->num_items < 0 ||
-      a->num_combine < 0 || a->workspace_items < 0)
-    return fail(LL_ERR_INVALID_ARGUMENT, "counts must be >= 0");
-  if (a->num_slots > 0x7fffffff) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots must be below 2^31");
-  if (!(a->softmax_scale > 0.0) || !isfinite(a->softmax_scale))
-    return fail(LL_ERR_INVALID_ARGUMENT, "softmax_scale must be finite and > 0");
-  if (a->num_items == 0) return LL_OK;
-  if (a->num_items > 0x7fffffff || a->num_combine > 0x7fffffff)
-    return fail(LL_ERR_INVALID_ARGUMENT, "too many items");
-  if (a->query == nullptr || a->output == nullptr || a->key_buffer == nullptr ||
-      a->value_buffer == nullptr || a->kv_slots == nullptr || a->items == nullptr ||
-      a->query_positions == nullptr)
-    return fail(LL_ERR_INVALID_ARGUMENT, "query/output/key/value/kv_slots/items/query_positions pointer is NULL");
-  if (a->kv_slots_dtype != LL_DTYPE_INT32 && a->kv_slots_dtype != LL_DTYPE_INT64)
-    return fail(LL_ERR_INTEGER_TOKEN_MAPS_REQUIRED, "kv_slots must be int32 or int64");
-  if (a->num_combine > 0 && (a->combine == nullptr || a->workspace == nullptr || a->workspace_items < 1))
+  int rc = check_attention_args(a);
+  if (rc != LL_OK || a->num_items == 0) return rc;
+  if (a->num_combine > 0 && (a->workspace == nullptr || a->workspace_items < 1))
     return fail(LL_ERR_INVALID_ARGUMENT, "split items need the combine table and a workspace");
-  if (!aligned(a->query, 16) || !aligned(a->key_buffer, 16) || !aligned(a->value_buffer, 16) ||
-      !aligned(a->output, 8) || !aligned(a->workspace, 16))
-    return fail(LL_ERR_INVALID_ARGUMENT, "query/key/value (16-byte), output (8-byte) and workspace "
-                "(16-byte) must be aligned");
-
-  AttnParams p;
-  memset(&p, 0, sizeof(p));
-  p.q = static_cast<const uint16_t *>(a->query);
-  p.out = static_cast<uint16_t *>(a->output);
-  p.k = static_cast<const uint16_t *>(a->key_buffer);
-  p.v = static_cast<const uint16_t *>(a->value_buffer);
-  p.slots = a->kv_slots;
-  p.items = a->items;
-  p.combine = a->combine;
-  p.positions = a->query_positions;
-  p.ws = a->workspace;
-  p.num_queries = a->num_queries;
-  p.num_slots = a->num_slots;
-  p.slots_len = a->kv_slots_len;
-  p.ws_items = a->workspace != nullptr ? a->workspace_items : 0;
-  p.hq = static_cast<int>(a->num_q_heads);
-  p.hkv = static_cast<int>(a->num_kv_heads);
-  p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
-  // A workgroup holds every (tile, head) pair of its item when the waves
-  // allow, else the heads are split over several workgroups per KV head.
-  const int head_room = max_pairs(static_cast<int>(a->head_dim)) / tiles_per_item(p.group);
-  p.heads_per_wg = p.group < head_room ? p.group : head_room;
-  p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
-  p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
-  p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-
-  if (a->num_kv_heads * p.head_chunks > 65535)
-    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
-  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
-  const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
-  if (a->head_dim == 128) {
-    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
-  } else if (a->head_dim == 64) {
-    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
-  } else {
-    if (f16) repair_attention_m32_kernel<256, F16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<256, Bf16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
-  }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-  if (a->num_combine > 0) {
-    const dim3 cgrid(static_cast<unsigned>(a->num_combine), static_cast<unsigned>(a->num_q_heads));
-    if (a->head_dim == 128) {
-      if (f16) repair_combine_kernel<128, F16><<<cgrid, dim3(256), 0, s>>>(p);
-      else repair_combine_kernel<128, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
-    } else if (a->head_dim == 64) {
-      if (f16) repair_combine_kernel<64, F16><<<cgrid, dim3(256), 0, s>>>(p);
-      else repair_combine_kernel<64, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
-    } else {
-      if (f16) repair_combine_kernel<256, F16><<<cgrid, dim3(256), 0, s>>>(p);
-      else repair_combine_kernel<256, Bf16><<<cgrid, dim3(256), 0, s>>>(p);
-    }
-    err = hipGetLastError();
-    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-  }
-  return LL_OK;
+  if (!aligned(a->workspace, 16)) return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  return launch_attention(a, a->workspace, a->workspace_items, reinterpret_cast<hipStream_t>(stream));
 }
+
+int ll_repair_attention_noalloc(const ll_repair_attention_args *a, ll_stream_t stream) {
+  int rc = check_attention_args(a);
+  if (rc != LL_OK) return rc;
+  if (a->workspace != nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be NULL: the partial results go to the "
+                "library's scratch array");
+  if (a->num_items == 0) return LL_OK;
+  // Every (partial, query head) block holds 16 queries x (head_dim outputs) and
+  // a (maximum, sum) pair per query, in fp32.
+  const long long block_floats = 16 * a->head_dim + 32;
+  const long long needed = a->workspace_items * a->num_q_heads * block_floats * 4;
+  if (a->workspace_items > kScratchBytes || needed > kScratchBytes)
+    return fail(LL_ERR_INVALID_ARGUMENT, "the plan's %lld split partials need %lld bytes; the scratch array "
+                "holds %lld (LL_REPAIR_SCRATCH_BYTES)", static_cast<long long>(a->workspace_items), needed,
+                kScratchBytes);
+  if (a->num_combine > 0 && a->workspace_items < 1)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split items need workspace_items partial slots");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int device = -1;
+  const hipError_t err = s != nullptr ? hipStreamGetDevice(s, &device) : hipGetDevice(&device);
+  if (err != hipSuccess) return fail(LL_ERR_HIP, "stream device: %s", hipGetErrorString(err));
+  float *ws = nullptr;
+  if (a->num_combine > 0) {
+    ws = scratch_on(device);
+    if (ws == nullptr) return LL_ERR_HIP;
+  }
+  return launch_attention(a, ws, a->workspace_items, s);
+}
+
+int64_t ll_repair_scratch_bytes(void) { return kScratchBytes; }
 
 }  // extern "C"

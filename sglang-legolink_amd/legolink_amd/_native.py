@@ -57,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "ll_repair_attention_plan",
     "ll_repair_attention",
     "ll_repair_attention_args_size",
+    "ll_repair_attention_noalloc",
+    "ll_repair_scratch_bytes",
 )
 
 _i64 = ctypes.c_int64
@@ -309,6 +311,10 @@ def load_library() -> ctypes.CDLL:
         lib.ll_repair_attention.restype = ctypes.c_int
         lib.ll_repair_attention_args_size.argtypes = []
         lib.ll_repair_attention_args_size.restype = _i64
+        lib.ll_repair_attention_noalloc.argtypes = [ctypes.POINTER(RepairAttentionArgs), _ptr]
+        lib.ll_repair_attention_noalloc.restype = ctypes.c_int
+        lib.ll_repair_scratch_bytes.argtypes = []
+        lib.ll_repair_scratch_bytes.restype = _i64
         if lib.ll_abi_version() != ABI_VERSION:
             raise NativeLibraryUnavailable(
                 f"{LIB_PATH} has ABI {lib.ll_abi_version()}, expected {ABI_VERSION}; rebuild it"
@@ -400,3 +406,15 @@ def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_token
 def repair_attention(args: RepairAttentionArgs, stream: int) -> None:
     args.struct_size = ctypes.sizeof(RepairAttentionArgs)
     _check(load_library().ll_repair_attention(ctypes.byref(args), _ptr(int(stream))))
+
+
+def repair_attention_noalloc(args: RepairAttentionArgs, stream: int) -> None:
+    """ll_repair_attention_noalloc: the split partials go to the library's
+    device scratch array (``args.workspace`` must be NULL)."""
+
+    args.struct_size = ctypes.sizeof(RepairAttentionArgs)
+    _check(load_library().ll_repair_attention_noalloc(ctypes.byref(args), _ptr(int(stream))))
+
+
+def repair_scratch_bytes() -> int:
+    return int(load_library().ll_repair_scratch_bytes())

@@ -54,11 +54,16 @@ class RepairAttentionPlan:
     With ``validate`` (the reference always checks, :1235-1236) every slot of
     every span is checked against ``pool_size`` once, here (one device sync);
     without it, slots outside the pool are treated as invisible keys.
+
+    With ``allocation_free`` no workspace is allocated: ``run`` calls
+    ``ll_repair_attention_noalloc``, whose split partials live in the
+    library's device scratch array (plans that need more than it holds are
+    rejected when they run; runs that overlap on one GPU race).
     """
 
     def __init__(self, spans: Sequence[tuple[torch.Tensor, int, int]], *, num_q_heads: int,
                  num_kv_heads: int, head_dim: int, pool_size: Optional[int] = None,
-                 split_tokens: int = 0, validate: bool = True) -> None:
+                 split_tokens: int = 0, validate: bool = True, allocation_free: bool = False) -> None:
         if not spans:
             raise SparseRepairAttentionError("no repair spans")
         self.num_q_heads = int(num_q_heads)
@@ -105,8 +110,9 @@ class RepairAttentionPlan:
         self.combine = self._tables[items.size : items.size + combine.size]
         self.positions = self._tables[items.size + combine.size :]
         per_item = self.num_q_heads * (16 * self.head_dim + 32)
+        self.allocation_free = bool(allocation_free)
         self.workspace = (torch.empty(info.workspace_items * per_item, dtype=torch.float32, device=device)
-                          if info.workspace_items else None)
+                          if info.workspace_items and not self.allocation_free else None)
 
     @property
     def algorithmic_flops(self) -> int:
@@ -177,7 +183,10 @@ class RepairAttentionPlan:
         args.workspace_items = self.info["workspace_items"]
         if stream is None:
             stream = torch.cuda.current_stream(query.device)
-        _native.repair_attention(args, stream.cuda_stream)
+        if self.allocation_free:
+            _native.repair_attention_noalloc(args, stream.cuda_stream)
+        else:
+            _native.repair_attention(args, stream.cuda_stream)
         return output
 
 
