@@ -193,7 +193,9 @@ def _median_ms(torch, run, steps: int, warmup: int) -> float:
 RUN_LENGTHS = (1, 2, 4, 8, 16, 64)
 
 
-SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", "contiguous")
+SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", "contiguous",
+                "random_source_contiguous_destination", "contiguous_source_random_destination",
+                "random_in_first_65536_slots", "random_in_first_131072_slots")
 
 
 def ordered_maps(workload, run: int, order: str, seed: int):
@@ -206,9 +208,24 @@ def ordered_maps(workload, run: int, order: str, seed: int):
     import numpy as np
 
     local, glob = workload.local_positions, workload.global_positions
+    tokens = np.arange(workload.tokens, dtype=np.int64)
     if order == "contiguous":
-        tokens = np.arange(workload.tokens, dtype=np.int64)
         return tokens, tokens + workload.tokens, local, glob
+    if order.startswith("random_in_first_"):
+        # Every row of a smaller slot range is read or written: random order,
+        # smaller footprint per buffer.
+        span = int(order.rsplit("_", 2)[1])
+        perm = np.random.default_rng(seed).permutation(span).astype(np.int64)
+        return perm[: workload.tokens], perm[workload.tokens : 2 * workload.tokens], local, glob
+    if order in ("random_source_contiguous_destination", "contiguous_source_random_destination"):
+        # One side is the last T slots in token order, the other random rows
+        # of the slots before them.
+        block = tokens + workload.num_slots - workload.tokens
+        scattered = np.random.default_rng(seed).permutation(workload.num_slots - workload.tokens)
+        scattered = scattered[: workload.tokens].astype(np.int64)
+        if order == "random_source_contiguous_destination":
+            return scattered, block, local, glob
+        return block, scattered, local, glob
     src, dst = run_length_maps(workload, run, seed)
     if order == "sorted_source":
         index = np.argsort(src, kind="stable")
@@ -272,7 +289,7 @@ def run_sweep(args: argparse.Namespace) -> None:
     link_bytes = workload.tokens * shape.bytes_per_token
     # (name, launch keywords); the first is the executor's choice for a single request.
     default = {"num_warps": 4, "layers_per_wave": 0, "stream_source_rows": True}
-    variants = [("default", {})]
+    variants = [("default", {}), ("staged_deltas", {"delta_staging": "workgroup"})]
     detailed = {1, int(args.sweep_detail_run)}
     extra = [
         ("cached_loads", {"stream_source_rows": False}),
@@ -283,6 +300,9 @@ def run_sweep(args: argparse.Namespace) -> None:
         ("layers_per_wave_28", {"layers_per_wave": 28}),
         ("waves_per_block_1", {"num_warps": 1}),
         ("waves_per_block_8", {"num_warps": 8}),
+        ("staged_deltas", {"delta_staging": "workgroup"}),
+        ("staged_deltas_layers_per_wave_2", {"delta_staging": "workgroup", "layers_per_wave": 2}),
+        ("staged_deltas_layers_per_wave_7", {"delta_staging": "workgroup", "layers_per_wave": 7}),
     ]
     rows, schedule, dispatch = [], [], 0
     cases = [(run, "random") for run in RUN_LENGTHS]
@@ -293,7 +313,8 @@ def run_sweep(args: argparse.Namespace) -> None:
         dst_t = torch.from_numpy(dst).to(device)
         local = torch.from_numpy(np.ascontiguousarray(local_np)).to(device)
         glob = torch.from_numpy(np.ascontiguousarray(global_np)).to(device)
-        chosen = variants + (extra if (run in detailed and order == "random") or order == "contiguous" else [])
+        chosen = variants + ([v for v in extra if v[0] != "staged_deltas"]
+                             if (run in detailed and order == "random") or order == "contiguous" else [])
         for name, changes in chosen:
             options = dict(default, **changes)
             rotation_off = options.pop("rotation_off", False)

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 9
+#define LL_ABI_VERSION 10
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -80,6 +80,25 @@ enum {
 enum {
   LL_ROUNDING_FUSED = 0,
   LL_ROUNDING_EAGER = 1
+};
+
+/*
+ * Where the vector kernel computes each token's RoPE delta
+ * (ll_kv_link_args.delta_staging).  The result is the same either way.
+ *   LL_DELTA_PER_WAVE   every wave computes its lanes' pairs from the cos/sin
+ *                       table itself (each layer group of a token reads the
+ *                       token's two table rows again);
+ *   LL_DELTA_WORKGROUP  one workgroup holds every layer group of its tokens
+ *                       and computes each token's delta once into LDS (the
+ *                       two table rows read once per token); neox links
+ *                       with full rotary and an fp32 table only, else per
+ *                       wave;
+ *   LL_DELTA_AUTO       the library's choice for the shape.
+ */
+enum {
+  LL_DELTA_AUTO = 0,
+  LL_DELTA_PER_WAVE = 1,
+  LL_DELTA_WORKGROUP = 2
 };
 
 /*
@@ -195,6 +214,9 @@ typedef struct ll_kv_link_args {
                                       requests sharing blocks) or be cache-resident and stay
                                       cacheable.  The result is the same either way.  (ABI 8) */
   int64_t rounding;                /* LL_ROUNDING_FUSED or LL_ROUNDING_EAGER (ABI 9) */
+  int64_t delta_staging;           /* LL_DELTA_*; with LL_DELTA_WORKGROUP, waves_per_block (0..16,
+                                      0 = 16) caps the workgroup and layer_groups_per_block
+                                      must be 0 (ABI 10) */
 } ll_kv_link_args;
 
 /*
@@ -417,6 +439,7 @@ typedef struct ll_launch_info {
   int64_t block_threads;
   int64_t layers_per_wave;
   int64_t layer_groups_per_block;
+  int64_t delta_staging;           /* LL_DELTA_PER_WAVE or LL_DELTA_WORKGROUP (vector kernel), else 0 */
 } ll_launch_info;
 
 int ll_kv_link(const ll_kv_link_args *args, ll_stream_t stream);

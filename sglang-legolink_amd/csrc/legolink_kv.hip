@@ -59,6 +59,9 @@ namespace {
 
 constexpr int kMaxLayersPerLaunch = 64;
 constexpr int kWave = 64;
+// Workgroup-staged deltas: tokens whose deltas one workgroup stages in LDS.
+constexpr int kMaxStagedTokens = 18;
+constexpr int kMaxWavesPerBlock = 16;
 constexpr int kLayerUnroll = LL_LAYER_UNROLL;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -102,6 +105,7 @@ struct LinkParams {
   int neox;
   int stream_rows;           // vector kernel: non-temporal row loads (rows read once)
   int eager;                 // LL_ROUNDING_EAGER: the torch path's rounding points
+  int staged;                // vector kernel: deltas staged once per workgroup in LDS
 };
 
 struct ScatterParams {
@@ -329,17 +333,22 @@ __device__ __forceinline__ void load_table(const void *cs, long long offset, flo
 // Vectorised link kernel.
 //   Waves cover num_tokens * chunks_per_row chunks, 64 per wave; the launch's
 //   layers are split into groups of layers_per_wave.  A block of W waves holds
-//   W / G chunk-waves x G layer groups (G = layer_groups_per_block): its G waves
-//   of one chunk-wave read the same cos/sin rows, which then come from the
-//   CU's L1 instead of being fetched once per layer group.
+//   W / G chunk-waves x G layer groups (G = layer_groups_per_block).
 //   grid.x = chunk-waves / (W / G), grid.y = layer groups / G.
+//   Deltas: per wave (each lane reads its token's cos/sin entries and computes
+//   its 8 pairs' delta itself), or, with kStaged, once per workgroup: G covers
+//   every layer group of the launch, the workgroup computes each of its tokens'
+//   deltas once into LDS (every table entry read once per token), and every
+//   wave reads its lanes' pairs from there.
 // Requirements (checked on the host): key_head_dim == value_head_dim ==
 // rotary_dim == kD, an fp32, bf16 or fp16 cos/sin cache (kCache) with unit
-// column stride and 16-byte aligned rows, 16-byte aligned layer buffers.
+// column stride and 16-byte aligned rows, 16-byte aligned layer buffers; for
+// kStaged also an fp32 cache and at most kMaxStagedTokens tokens per block.
 // ---------------------------------------------------------------------------
 template <bool kBF16, int kD, int kR, bool kNeox, typename Index, int kCache, bool kStream,
-          bool kEager>
-__global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
+          bool kEager, bool kStaged>
+__global__ void __launch_bounds__(kStaged ? kMaxWavesPerBlock * kWave : 512)
+kv_link_vec_kernel(const LinkParams p) {
   constexpr int kChunksPerHead = kD / 8;
   constexpr int kRotChunks = kR / 8;     // chunks of a head that rotate; the rest are copied
   constexpr int kPairs = kNeox ? 8 : 4;  // rotary pairs touched by one lane
@@ -358,7 +367,12 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   const int layer_group = blockIdx.y * groups + wave_in_block % groups;
   const int l0 = layer_group * p.layers_per_wave;
   const int l1 = min(l0 + p.layers_per_wave, p.num_layers);
-  if (l0 >= l1) return;  // whole wave: a layer group past the last layer
+  // A whole wave whose layer group lies past the last layer has no rows; with
+  // staged deltas it still helps stage and meets the barrier.
+  if constexpr (!kStaged) {
+    if (l0 >= l1) return;
+  }
+  const bool has_layers = l0 < l1;
   const long long g = wave * kWave + lane;
   const long long C = p.chunks_per_row;
   const bool in_range = g < p.num_tokens * C;
@@ -400,11 +414,13 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
   // read again (uniform clamp) and not stored.
   u32x4 kin[kLayerUnroll];
   u32x4 vin[kLayerUnroll];
+  if (has_layers) {
 #pragma unroll
-  for (int u = 0; u < kLayerUnroll; ++u) {
-    const int lu = min(l0 + u, l1 - 1);
-    kin[u] = load_row<kStream>(p.sk_layers[lu] + k_src);
-    vin[u] = load_row<kStream>(p.sv_layers[lu] + v_src);
+    for (int u = 0; u < kLayerUnroll; ++u) {
+      const int lu = min(l0 + u, l1 - 1);
+      kin[u] = load_row<kStream>(p.sk_layers[lu] + k_src);
+      vin[u] = load_row<kStream>(p.sv_layers[lu] + v_src);
+    }
   }
 
   // fp32 delta of this lane's rotary pairs.  Rows are clamped to 0 where the
@@ -417,7 +433,49 @@ __global__ void __launch_bounds__(512) kv_link_vec_kernel(const LinkParams p) {
     dc[e] = 1.0f;
     ds[e] = 0.0f;
   }
-  if (p.cs_rows > 0) {
+  if constexpr (kStaged) {
+    // The workgroup's tokens [t_first, t_end): entry (token, pair) of the LDS
+    // table holds that token's (dc, ds) for the pair; identity where the delta
+    // is not used.  Consecutive threads take consecutive pairs of a token, so
+    // the table reads are coalesced.
+    constexpr int kTokenPairs = kR / 2;
+    __shared__ float staged_cos[kMaxStagedTokens * kTokenPairs];
+    __shared__ float staged_sin[kMaxStagedTokens * kTokenPairs];
+    const long long block_chunks = static_cast<long long>(blockDim.x / kWave / groups) * kWave;
+    const long long first_chunk = static_cast<long long>(blockIdx.x) * block_chunks;
+    const long long t_first = first_chunk / C;
+    const long long t_end = min((first_chunk + block_chunks + C - 1) / C, p.num_tokens);
+    const int entries = static_cast<int>(t_end - t_first) * kTokenPairs;
+    const float *table = static_cast<const float *>(p.cs);
+    for (int e = threadIdx.x; e < entries; e += blockDim.x) {
+      const int token = e / kTokenPairs;
+      const int i = e - token * kTokenPairs;
+      const long long tt = t_first + token;
+      float sc = 1.0f, ss = 0.0f;
+      if (tt >= p.prefix) {
+        const long long lpe = static_cast<long long>(static_cast<const Index *>(p.lpos)[tt]);
+        const long long gpe = static_cast<long long>(static_cast<const Index *>(p.gpos)[tt]);
+        if (lpe >= 0 && lpe < p.cs_rows && gpe >= 0 && gpe < p.cs_rows) {
+          const float lc = table[lpe * p.cs_stride_row + i];
+          const float ls = table[lpe * p.cs_stride_row + i + kHalf];
+          const float gc = table[gpe * p.cs_stride_row + i];
+          const float gs = table[gpe * p.cs_stride_row + i + kHalf];
+          delta_pair<Round::kDelta, Round::kCast>(lc, ls, gc, gs, sc, ss);
+        }
+      }
+      staged_cos[e] = sc;
+      staged_sin[e] = ss;
+    }
+    __syncthreads();
+    if (!has_layers) return;
+    const int token = in_range ? static_cast<int>(t - t_first) : 0;
+    const int pb = kNeox ? (q % (kRotChunks / 2)) * 8 : (rotating ? q : 0) * 4;
+#pragma unroll
+    for (int e = 0; e < kPairs; ++e) {
+      dc[e] = staged_cos[token * kTokenPairs + pb + e];
+      ds[e] = staged_sin[token * kTokenPairs + pb + e];
+    }
+  } else if (p.cs_rows > 0) {
     const bool use = remap && positions_ok;
     const long long lrow_index = use ? lp : 0;
     const long long grow_index = use ? gp : 0;
@@ -730,9 +788,17 @@ int validate_link(const ll_kv_link_args *a) {
   if (a->kernel < LL_KERNEL_AUTO || a->kernel > LL_KERNEL_GENERIC)
     return fail(LL_ERR_LAUNCH_CONFIG, "unknown kernel selector %lld",
                 static_cast<long long>(a->kernel));
-  if (a->waves_per_block != 0 && a->waves_per_block != 1 && a->waves_per_block != 2 &&
-      a->waves_per_block != 4 && a->waves_per_block != 8)
+  if (a->delta_staging < LL_DELTA_AUTO || a->delta_staging > LL_DELTA_WORKGROUP)
+    return fail(LL_ERR_LAUNCH_CONFIG, "unknown delta_staging %lld", static_cast<long long>(a->delta_staging));
+  if (a->delta_staging == LL_DELTA_WORKGROUP) {
+    if (a->waves_per_block < 0 || a->waves_per_block > kMaxWavesPerBlock)
+      return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0..16 with workgroup-staged deltas");
+    if (a->layer_groups_per_block != 0)
+      return fail(LL_ERR_LAUNCH_CONFIG, "workgroup-staged deltas choose layer_groups_per_block themselves");
+  } else if (a->waves_per_block != 0 && a->waves_per_block != 1 && a->waves_per_block != 2 &&
+             a->waves_per_block != 4 && a->waves_per_block != 8) {
     return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0, 1, 2, 4 or 8");
+  }
   if (a->layers_per_wave < 0) return fail(LL_ERR_LAUNCH_CONFIG, "layers_per_wave is negative");
   if (a->rounding != LL_ROUNDING_FUSED && a->rounding != LL_ROUNDING_EAGER)
     return fail(LL_ERR_INVALID_ARGUMENT, "unknown rounding %lld", static_cast<long long>(a->rounding));
@@ -771,7 +837,14 @@ struct LinkPlan {
   int layers_per_wave;  // vector kernel
   int layer_groups_per_block;  // vector kernel
   int launches;
+  bool staged;  // vector kernel: workgroup-staged deltas
 };
+
+// Workgroup-staged deltas need the production shape (neox, full rotary, fp32
+// table) on the vector kernel.
+bool staging_fits(const ll_kv_link_args *a) {
+  return a->is_neox_style && a->rotary_dim == a->key_head_dim && a->cos_sin_dtype == LL_DTYPE_FLOAT32;
+}
 
 // Launch shape of the vector kernel.  Short runs of layers per wave keep the
 // GPU's in-flight rows within few layer buffers at a time.  Measured on gfx950
@@ -791,7 +864,8 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
                 "rotary_dim equal to it or half of it, one index type for the four token maps, a unit-stride "
                 "cache with 16-byte aligned rows and 16-byte aligned buffers");
   plan->kernel = (a->kernel == LL_KERNEL_GENERIC || !fits) ? LL_KERNEL_GENERIC : LL_KERNEL_VECTOR;
-  const int waves_per_block = a->waves_per_block ? static_cast<int>(a->waves_per_block) : 4;
+  const int waves_per_block =
+      a->waves_per_block && a->delta_staging != LL_DELTA_WORKGROUP ? static_cast<int>(a->waves_per_block) : 4;
   plan->block_threads = waves_per_block * kWave;
   const int layers_first = static_cast<int>(
       a->num_layers < kMaxLayersPerLaunch ? a->num_layers : kMaxLayersPerLaunch);
@@ -817,42 +891,78 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     }
     if (lpw > layers_first) lpw = layers_first;
     plan->layers_per_wave = lpw;
+    plan->staged = false;
+    if (a->delta_staging == LL_DELTA_WORKGROUP && staging_fits(a)) {
+      // Every layer group of a token in one workgroup: G groups of
+      // layers_per_wave layers (at most 16, so lpw grows for deep models),
+      // times as many chunk-waves as fit in the wave budget and the LDS table.
+      int groups = (layers_first + lpw - 1) / lpw;
+      if (groups > kMaxWavesPerBlock) {
+        lpw = (layers_first + kMaxWavesPerBlock - 1) / kMaxWavesPerBlock;
+        plan->layers_per_wave = lpw;
+        groups = (layers_first + lpw - 1) / lpw;
+      }
+      const int budget = a->waves_per_block ? static_cast<int>(a->waves_per_block) : kMaxWavesPerBlock;
+      int chunk_waves = budget / groups;
+      const long long row_chunks = chunks;
+      while (chunk_waves > 1 &&
+             (chunk_waves * kWave + row_chunks - 1) / row_chunks + 1 > kMaxStagedTokens)
+        --chunk_waves;
+      if (chunk_waves >= 1 && (chunk_waves * kWave + row_chunks - 1) / row_chunks + 1 <= kMaxStagedTokens) {
+        plan->staged = true;
+        plan->layer_groups_per_block = groups;
+        plan->block_threads = chunk_waves * groups * kWave;
+        plan->grid_x = (waves_x + chunk_waves - 1) / chunk_waves;
+      }
+    }
   } else {
     plan->grid_x = a->num_tokens < 65536 ? a->num_tokens : 65536;
     plan->layers_per_wave = 1;
     plan->layer_groups_per_block = 1;
+    plan->staged = false;
   }
   if (plan->grid_x > 0x7fffffffLL) return fail(LL_ERR_LAUNCH_CONFIG, "link too large for one grid");
   return LL_OK;
 }
 
-template <bool kBF16, int kD, int kR, int kCache, bool kStream, bool kEager>
+template <bool kBF16, int kD, int kR, int kCache, bool kStream, bool kEager, bool kStaged>
 void launch_vec_index(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   const bool index64 = (p.idx64 & 15) == 15;  // the vector kernel needs one index type
-  if (neox) {
+  if constexpr (kStaged) {  // neox only (the plan checks)
     if (index64)
-      kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+      kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream, kEager, true><<<grid, block, 0, s>>>(p);
     else
-      kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+      kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream, kEager, true><<<grid, block, 0, s>>>(p);
+  } else if (neox) {
+    if (index64)
+      kv_link_vec_kernel<kBF16, kD, kR, true, long long, kCache, kStream, kEager, false><<<grid, block, 0, s>>>(p);
+    else
+      kv_link_vec_kernel<kBF16, kD, kR, true, int, kCache, kStream, kEager, false><<<grid, block, 0, s>>>(p);
   } else {
     if (index64)
-      kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+      kv_link_vec_kernel<kBF16, kD, kR, false, long long, kCache, kStream, kEager, false><<<grid, block, 0, s>>>(p);
     else
-      kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache, kStream, kEager><<<grid, block, 0, s>>>(p);
+      kv_link_vec_kernel<kBF16, kD, kR, false, int, kCache, kStream, kEager, false><<<grid, block, 0, s>>>(p);
   }
 }
 
-// Streamed (non-temporal) row loads are built for the full-rotary fp32-table
-// kernels only, the production shape; other shapes load rows as usual.
+// Streamed (non-temporal) row loads and workgroup-staged deltas are built for
+// the full-rotary fp32-table kernels only, the production shape; other shapes
+// load rows as usual and compute deltas per wave.
 template <bool kBF16, int kD, int kR, int kCache, bool kEager>
 void launch_vec_neox(dim3 grid, dim3 block, hipStream_t s, const LinkParams &p, bool neox) {
   if constexpr (kR == kD && kCache == 3) {
+    if (p.staged) {
+      if (p.stream_rows) launch_vec_index<kBF16, kD, kR, kCache, true, kEager, true>(grid, block, s, p, neox);
+      else launch_vec_index<kBF16, kD, kR, kCache, false, kEager, true>(grid, block, s, p, neox);
+      return;
+    }
     if (p.stream_rows) {
-      launch_vec_index<kBF16, kD, kR, kCache, true, kEager>(grid, block, s, p, neox);
+      launch_vec_index<kBF16, kD, kR, kCache, true, kEager, false>(grid, block, s, p, neox);
       return;
     }
   }
-  launch_vec_index<kBF16, kD, kR, kCache, false, kEager>(grid, block, s, p, neox);
+  launch_vec_index<kBF16, kD, kR, kCache, false, kEager, false>(grid, block, s, p, neox);
 }
 
 template <bool kBF16, int kD, int kCache, bool kEager>
@@ -967,6 +1077,7 @@ int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info) {
   info->block_threads = plan.block_threads;
   info->layers_per_wave = plan.layers_per_wave;
   info->layer_groups_per_block = plan.layer_groups_per_block;
+  info->delta_staging = plan.kernel != LL_KERNEL_VECTOR ? 0 : (plan.staged ? LL_DELTA_WORKGROUP : LL_DELTA_PER_WAVE);
   return LL_OK;
 }
 
@@ -991,6 +1102,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.src_num_slots = a->source_key_layers != nullptr ? a->source_num_slots : a->num_slots;
   p.stream_rows = a->stream_source_rows != 0 ? 1 : 0;
   p.eager = a->rounding == LL_ROUNDING_EAGER ? 1 : 0;
+  p.staged = plan.staged ? 1 : 0;
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;

@@ -18,7 +18,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "liblegolink_kv.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -30,6 +30,10 @@ DTYPE_UINT8 = 6
 
 ROUNDING_FUSED = 0
 ROUNDING_EAGER = 1
+
+DELTA_AUTO = 0
+DELTA_PER_WAVE = 1
+DELTA_WORKGROUP = 2
 
 KERNEL_AUTO = 0
 KERNEL_VECTOR = 1
@@ -107,6 +111,7 @@ class LinkArgs(ctypes.Structure):
         ("source_num_slots", _i64),
         ("stream_source_rows", _i64),
         ("rounding", _i64),
+        ("delta_staging", _i64),
     ]
 
 
@@ -243,6 +248,7 @@ class LaunchInfo(ctypes.Structure):
         ("block_threads", _i64),
         ("layers_per_wave", _i64),
         ("layer_groups_per_block", _i64),
+        ("delta_staging", _i64),
     ]
 
 

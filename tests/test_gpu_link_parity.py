@@ -73,7 +73,8 @@ CASES = [
 ]
 
 
-def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense", rounding="fused"):
+def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense", rounding="fused",
+              **link_options):
     (name, dtype, cache_dtype, heads, kdim, vdim, rotary, neox, kernel, index_dtype, prefix,
      mask_fraction, layers, tokens, expected_kernel) = case
     report(f"case {name}: layers={layers} heads={heads} kdim={kdim} vdim={vdim} rotary={rotary} "
@@ -111,14 +112,16 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
         local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
         prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
-        kernel=kernel,
+        kernel=kernel, **link_options,
     )
     assert launch["kernel"] == expected_kernel, launch
+    if link_options.get("delta_staging") == "workgroup":
+        assert launch["delta_staging"] == "workgroup", launch
     kv_link.fused_kv_link_layers_inplace(
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
         local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
         prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
-        kernel=kernel, rounding=rounding,
+        kernel=kernel, rounding=rounding, **link_options,
     )
     torch.cuda.synchronize(device)
     for layer in range(layers):
@@ -134,6 +137,32 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
 @pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])
 def test_link_matches_oracle(gpu_device, case):
     _run_case(gpu_device, case)
+
+
+# Workgroup-staged deltas (neox, full rotary, fp32 table): name, kv dtype, heads, dim,
+# layers, tokens, prefix, mask fraction, layers per wave, index dtype.
+STAGED_CASES = [
+    ("qwen7b_28_layers", torch.bfloat16, 4, 128, 28, 301, 17, 0.1, 0, torch.int64),
+    ("qwen7b_two_layers_per_wave", torch.bfloat16, 4, 128, 28, 130, 0, 0.1, 2, torch.int32),
+    ("one_layer_per_wave_raised", torch.bfloat16, 4, 128, 28, 70, 3, 0.0, 1, torch.int64),
+    ("qwen3_32b_64_layers", torch.bfloat16, 8, 128, 64, 90, 5, 0.1, 0, torch.int64),
+    ("seventy_layers_two_launches", torch.bfloat16, 2, 128, 70, 64, 3, 0.1, 0, torch.int64),
+    ("one_head_four_tokens_per_wave", torch.bfloat16, 1, 128, 28, 333, 6, 0.1, 0, torch.int32),
+    ("head_dim_256", torch.bfloat16, 2, 256, 5, 150, 0, 0.1, 0, torch.int64),
+    ("head_dim_64_fp16", torch.float16, 4, 64, 7, 171, 9, 0.1, 0, torch.int64),
+    ("head_dim_32_small_link", torch.bfloat16, 4, 32, 3, 45, 2, 0.1, 0, torch.int64),
+    ("single_token", torch.bfloat16, 4, 128, 28, 1, 0, 0.0, 0, torch.int64),
+    ("prefix_is_everything", torch.bfloat16, 4, 128, 6, 100, 100, 0.0, 0, torch.int64),
+]
+
+
+@pytest.mark.parametrize("rounding", ["fused", "eager"])
+@pytest.mark.parametrize("staged", STAGED_CASES, ids=[case[0] for case in STAGED_CASES])
+def test_workgroup_staged_deltas_match_oracle(gpu_device, staged, rounding):
+    name, dtype, heads, dim, layers, tokens, prefix, mask_fraction, lpw, index_dtype = staged
+    case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
+            mask_fraction, layers, tokens, "vector")
+    _run_case(gpu_device, case, rounding=rounding, delta_staging="workgroup", layers_per_wave=lpw)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])

@@ -148,6 +148,52 @@ def test_small_links_split_layers_across_waves():
     assert info["grid_y"] * info["layers_per_wave"] >= 28 and info["grid_y"] > 1
 
 
+def _describe(layers, heads, dim, tokens, **options):
+    keys = [torch.zeros(8, heads, dim, dtype=torch.bfloat16) for _ in range(layers)]
+    index = torch.arange(tokens)
+    return kv_link.describe_link_launch(
+        key_buffers=keys, value_buffers=keys, source_slots=index, destination_slots=index,
+        local_positions=index, global_positions=index, cos_sin_cache=build_cos_sin_cache(8, dim),
+        prefix_token_count=0, rotary_dim=dim, is_neox_style=True, **options)
+
+
+@pytest.mark.parametrize("layers,heads,dim,lpw,groups,threads", [
+    (28, 4, 128, 0, 7, 14 * 64),    # Qwen2.5-7B: 7 groups of 4 layers x 2 tokens
+    (28, 4, 128, 2, 14, 14 * 64),   # 14 groups x 1 token
+    (28, 4, 128, 1, 14, 14 * 64),   # 28 groups would exceed 16 waves: 2 layers per wave
+    (64, 8, 128, 0, 16, 16 * 64),   # Qwen3-32B: 16 groups x 1 wave (half a token)
+    (28, 1, 128, 0, 7, 14 * 64),    # one head: 4 tokens per wave, 2 waves fit the LDS table
+    (3, 2, 64, 0, 2, 8 * 64),       # a small link splits its 3 layers in 2 groups; 16-chunk rows:
+                                    # 4 chunk-waves (17 tokens) fill the LDS table
+])
+def test_workgroup_staged_launch_shape(layers, heads, dim, lpw, groups, threads):
+    info = _describe(layers, heads, dim, 32768, layers_per_wave=lpw, delta_staging="workgroup")
+    assert info["delta_staging"] == "workgroup"
+    assert info["layer_groups_per_block"] == groups and info["grid_y"] == 1
+    assert info["block_threads"] == threads
+    chunk_waves = threads // 64 // groups
+    tokens_per_block = -(-chunk_waves * 64 // (heads * dim // 8)) + 1
+    assert tokens_per_block <= 18  # the kernel's LDS table
+    assert info["grid_x"] == -(-(32768 * heads * dim // 8 // 64) // chunk_waves)
+
+
+def test_workgroup_staging_falls_back_to_per_wave_deltas():
+    # GPT-J pairs and bf16 tables keep per-wave deltas; the default is per wave.
+    assert _describe(28, 4, 128, 4096)["delta_staging"] == "per_wave"
+    keys = [torch.zeros(8, 4, 128, dtype=torch.bfloat16) for _ in range(4)]
+    index = torch.arange(64)
+    common = dict(key_buffers=keys, value_buffers=keys, source_slots=index, destination_slots=index,
+                  local_positions=index, global_positions=index, prefix_token_count=0, rotary_dim=128,
+                  delta_staging="workgroup")
+    assert kv_link.describe_link_launch(cos_sin_cache=build_cos_sin_cache(8, 128), is_neox_style=False,
+                                        **common)["delta_staging"] == "per_wave"
+    assert kv_link.describe_link_launch(cos_sin_cache=build_cos_sin_cache(8, 128).bfloat16(),
+                                        is_neox_style=True, **common)["delta_staging"] == "per_wave"
+    with pytest.raises(_native.NativeCallError, match="layer_groups_per_block"):
+        kv_link.describe_link_launch(cos_sin_cache=build_cos_sin_cache(8, 128), is_neox_style=True,
+                                     layer_groups_per_block=2, **common)
+
+
 def test_cpu_tensors_are_not_eligible():
     keys = torch.zeros(16, 2, 8, dtype=torch.bfloat16)
     result = kv_link.check_fused_kv_link_eligibility(
