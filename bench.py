@@ -54,6 +54,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--layers-per-wave", type=int, default=0)
     parser.add_argument("--waves-per-block", type=int, default=4)
     parser.add_argument("--layer-groups-per-block", type=int, default=0)
+    parser.add_argument("--delta-staging", choices=["auto", "per_wave", "workgroup"], default="auto",
+                        help="where the link kernel computes its RoPE deltas (same result)")
     parser.add_argument("--repair-rows", choices=["compact", "mask"], default="compact",
                         help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
@@ -355,6 +357,21 @@ def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
         return None
 
 
+def load_pattern_ceiling(workload_name: str) -> dict | None:
+    """The committed run-length sweep's ceiling for this workload's access
+    pattern (the fastest link variant on its fully fragmented rows, and on
+    contiguous rows), or None when there is none."""
+
+    path = PROFILES / f"pattern_ceiling_kv_link_{workload_name}.json"
+    if not path.is_file():
+        return None
+    data = json.loads(path.read_text())
+    best = data["fragmented_rows_best"]["GBps"]
+    return {"GBps": best, "frac": round(best / HBM_PEAK_GBPS, 4),
+            "what": data["fragmented_rows_best"]["what"],
+            "contiguous_rows_GBps": data["contiguous_rows_best"]["GBps"], "source": data["source"]}
+
+
 def repair_attention_bench(args: argparse.Namespace) -> None:
     """The repair pass's attention for the workload's repair spans, one layer
     of the Qwen2.5-7B shape (28 query heads over 4 KV heads, head dim 128):
@@ -564,7 +581,7 @@ def main() -> int:
                               end_layer=shape.layers, num_warps=args.waves_per_block,
                               layers_per_wave=args.layers_per_wave,
                               layer_groups_per_block=args.layer_groups_per_block, arena=arena,
-                              fused_mode=fused_mode)
+                              fused_mode=fused_mode, delta_staging=args.delta_staging)
     pool = KVPool(keys, values)
     row_bytes = 2 * shape.kv_heads * shape.head_dim * 2  # one token's K and V row, one layer
     storage = {"mode": args.storage}
@@ -739,6 +756,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic if not clone else None,
             "algorithmic_bytes_per_launch": bytes_info["link_bytes"],
+            "pattern_ceiling": load_pattern_ceiling(workload.name) if args.tp == 1 else None,
         },
         "cpu_baseline": None,
     }

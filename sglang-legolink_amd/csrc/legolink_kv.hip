@@ -892,7 +892,13 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     if (lpw > layers_first) lpw = layers_first;
     plan->layers_per_wave = lpw;
     plan->staged = false;
-    if (a->delta_staging == LL_DELTA_WORKGROUP && staging_fits(a)) {
+    // Staged deltas by default where they fit (they cut the table reads from
+    // one per token and layer group to one per token: c2 reads 1.094x ->
+    // 1.018x the row bytes, and c2/c4 link 2 % faster); an explicit
+    // layer_groups_per_block asks for per-wave deltas.
+    const bool want_staged = a->delta_staging == LL_DELTA_WORKGROUP ||
+                             (a->delta_staging == LL_DELTA_AUTO && a->layer_groups_per_block == 0);
+    if (want_staged && staging_fits(a)) {
       // Every layer group of a token in one workgroup: G groups of
       // layers_per_wave layers (at most 16, so lpw grows for deep models),
       // times as many chunk-waves as fit in the wave budget and the LDS table.
@@ -902,7 +908,8 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
         plan->layers_per_wave = lpw;
         groups = (layers_first + lpw - 1) / lpw;
       }
-      const int budget = a->waves_per_block ? static_cast<int>(a->waves_per_block) : kMaxWavesPerBlock;
+      const int budget = a->delta_staging == LL_DELTA_WORKGROUP && a->waves_per_block
+                             ? static_cast<int>(a->waves_per_block) : kMaxWavesPerBlock;
       int chunk_waves = budget / groups;
       const long long row_chunks = chunks;
       while (chunk_waves > 1 &&

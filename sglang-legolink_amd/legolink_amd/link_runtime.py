@@ -317,7 +317,7 @@ class PreparedLink:
                  compact_repair_rows: bool, num_warps: Optional[int], layers_per_wave: int,
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None,
-                 fused_mode: str = "required") -> None:
+                 fused_mode: str = "required", delta_staging: str = "auto") -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -399,6 +399,7 @@ class PreparedLink:
                                           [source_arena.get_value_buffer(layer) for layer in group_layers]),
                     stream_source_rows=self.stream_source_rows,
                     rounding=self.rounding,
+                    delta_staging=delta_staging,
                 ))
         key_row = int(key_buffers[0][0].numel()) * key_buffers[0].element_size()
         value_row = int(value_buffers[0][0].numel()) * value_buffers[0].element_size()
@@ -466,13 +467,17 @@ class KVLinkExecutor:
     def __init__(self, registry: LegoLinkBlockRegistry, rotary: RotarySpec | Mapping[int, RotarySpec], *,
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
                  layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
-                 layer_groups_per_block: int = 0, fused_mode: Optional[str] = None) -> None:
+                 layer_groups_per_block: int = 0, fused_mode: Optional[str] = None,
+                 delta_staging: str = "auto") -> None:
         """``fused_mode`` ("disabled" / "required" / "auto", or the reference's
         aliases) fixes the link's rounding; None reads
-        ``SGLANG_PIC_TRITON_FUSED_KV_LINK`` at every link, as the reference does."""
+        ``SGLANG_PIC_TRITON_FUSED_KV_LINK`` at every link, as the reference does.
+        ``delta_staging`` ("auto" / "per_wave" / "workgroup") picks where the
+        link kernel computes its RoPE deltas (the result is the same)."""
 
         self.registry = registry
         self.fused_mode = None if fused_mode is None else get_fused_kv_link_mode(fused_mode)
+        self.delta_staging = delta_staging
         self.start_layer = int(start_layer)
         self.end_layer = int(end_layer)
         if isinstance(rotary, RotarySpec):
@@ -589,6 +594,7 @@ class KVLinkExecutor:
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, fused_mode=self._fused_mode(),
+            delta_staging=self.delta_staging,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -621,7 +627,7 @@ class KVLinkExecutor:
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, order_by_source=order_by_source,
-            fused_mode=self._fused_mode(),
+            fused_mode=self._fused_mode(), delta_staging=self.delta_staging,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared

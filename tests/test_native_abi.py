@@ -103,10 +103,16 @@ def test_kernel_choice_and_launch_shape():
     # Qwen2.5-7B: 4 heads x 128 dims = 64 chunks of 16 bytes per row = one wave per token.
     args, keepalive = _cpu_args(source_slots=torch.arange(32768), destination_slots=torch.arange(32768),
                                 local_positions=torch.arange(32768), global_positions=torch.arange(32768))
+    args.delta_staging = _native.DELTA_PER_WAVE
     info = _native.kv_link_describe(args)
-    assert info.kernel == _native.KERNEL_VECTOR
+    assert info.kernel == _native.KERNEL_VECTOR and info.delta_staging == _native.DELTA_PER_WAVE
     assert info.block_threads == 256 and info.grid_x == 32768 // 4
     assert info.layers_per_wave == 2 and info.grid_y == 1  # capped by the two layers of the CPU pool
+    # By default the deltas are staged: the two layers' groups x 16 chunk-waves per workgroup.
+    args.delta_staging = _native.DELTA_AUTO
+    info = _native.kv_link_describe(args)
+    assert info.delta_staging == _native.DELTA_WORKGROUP
+    assert info.block_threads == 1024 and info.grid_x == 32768 // 16 and info.layer_groups_per_block == 1
     del keepalive
     # Half rotary stays on the vector kernel; other partial widths fall back to
     # the generic kernel, and forcing the vector kernel on them fails.
@@ -145,7 +151,9 @@ def test_small_links_split_layers_across_waves():
         prefix_token_count=0, rotary_dim=128, is_neox_style=True,
     )
     assert info["kernel"] == "vector"
-    assert info["grid_y"] * info["layers_per_wave"] >= 28 and info["grid_y"] > 1
+    # Layer groups across the grid (per-wave deltas) or within a workgroup (staged).
+    groups = info["grid_y"] * info["layer_groups_per_block"]
+    assert groups * info["layers_per_wave"] >= 28 and groups > 1
 
 
 def _describe(layers, heads, dim, tokens, **options):
@@ -178,8 +186,10 @@ def test_workgroup_staged_launch_shape(layers, heads, dim, lpw, groups, threads)
 
 
 def test_workgroup_staging_falls_back_to_per_wave_deltas():
-    # GPT-J pairs and bf16 tables keep per-wave deltas; the default is per wave.
-    assert _describe(28, 4, 128, 4096)["delta_staging"] == "per_wave"
+    # GPT-J pairs and bf16 tables keep per-wave deltas, and so does an explicit
+    # layer_groups_per_block; the default stages where it fits.
+    assert _describe(28, 4, 128, 4096)["delta_staging"] == "workgroup"
+    assert _describe(28, 4, 128, 4096, layer_groups_per_block=2, num_warps=4)["delta_staging"] == "per_wave"
     keys = [torch.zeros(8, 4, 128, dtype=torch.bfloat16) for _ in range(4)]
     index = torch.arange(64)
     common = dict(key_buffers=keys, value_buffers=keys, source_slots=index, destination_slots=index,
