@@ -93,9 +93,10 @@ enum {
  *                       two table rows read once per token); neox links
  *                       with full rotary and an fp32 table only, else per
  *                       wave;
- *   LL_DELTA_AUTO       workgroup where it fits and layer_groups_per_block
- *                       is 0 (waves_per_block then sizes per-wave blocks
- *                       only), else per wave.
+ *   LL_DELTA_AUTO       workgroup where it fits, the source rows are streamed
+ *                       (stream_source_rows) and layer_groups_per_block is 0
+ *                       (waves_per_block then sizes per-wave blocks only),
+ *                       else per wave.
  */
 enum {
   LL_DELTA_AUTO = 0,

@@ -892,12 +892,16 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     if (lpw > layers_first) lpw = layers_first;
     plan->layers_per_wave = lpw;
     plan->staged = false;
-    // Staged deltas by default where they fit (they cut the table reads from
-    // one per token and layer group to one per token: c2 reads 1.094x ->
-    // 1.018x the row bytes, and c2/c4 link 2 % faster); an explicit
-    // layer_groups_per_block asks for per-wave deltas.
-    const bool want_staged = a->delta_staging == LL_DELTA_WORKGROUP ||
-                             (a->delta_staging == LL_DELTA_AUTO && a->layer_groups_per_block == 0);
+    // By default, staged deltas where they fit and the source rows are
+    // streamed (read once, beyond the caches): there they cut the table reads
+    // from one per token and layer group to one per token (c2 reads 1.094x ->
+    // 1.018x the row bytes) and the DRAM-bound link gains 0.4-2 % (c2, c4, c5).
+    // Links whose rows come partly from cache (batched requests sharing
+    // blocks) run faster with per-wave deltas (c3: 8.34 against 8.91 ms).  An
+    // explicit layer_groups_per_block asks for per-wave deltas.
+    const bool want_staged =
+        a->delta_staging == LL_DELTA_WORKGROUP ||
+        (a->delta_staging == LL_DELTA_AUTO && a->layer_groups_per_block == 0 && a->stream_source_rows != 0);
     if (want_staged && staging_fits(a)) {
       // Every layer group of a token in one workgroup: G groups of
       // layers_per_wave layers (at most 16, so lpw grows for deep models),

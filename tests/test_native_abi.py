@@ -108,8 +108,11 @@ def test_kernel_choice_and_launch_shape():
     assert info.kernel == _native.KERNEL_VECTOR and info.delta_staging == _native.DELTA_PER_WAVE
     assert info.block_threads == 256 and info.grid_x == 32768 // 4
     assert info.layers_per_wave == 2 and info.grid_y == 1  # capped by the two layers of the CPU pool
-    # By default the deltas are staged: the two layers' groups x 16 chunk-waves per workgroup.
+    # By default the deltas of streamed rows are staged: the two layers' groups
+    # x 16 chunk-waves per workgroup.
     args.delta_staging = _native.DELTA_AUTO
+    assert _native.kv_link_describe(args).delta_staging == _native.DELTA_PER_WAVE
+    args.stream_source_rows = 1
     info = _native.kv_link_describe(args)
     assert info.delta_staging == _native.DELTA_WORKGROUP
     assert info.block_threads == 1024 and info.grid_x == 32768 // 16 and info.layer_groups_per_block == 1
@@ -187,9 +190,8 @@ def test_workgroup_staged_launch_shape(layers, heads, dim, lpw, groups, threads)
 
 def test_workgroup_staging_falls_back_to_per_wave_deltas():
     # GPT-J pairs and bf16 tables keep per-wave deltas, and so does an explicit
-    # layer_groups_per_block; the default stages where it fits.
-    assert _describe(28, 4, 128, 4096)["delta_staging"] == "workgroup"
-    assert _describe(28, 4, 128, 4096, layer_groups_per_block=2, num_warps=4)["delta_staging"] == "per_wave"
+    # layer_groups_per_block; the default stages streamed rows where it fits.
+    assert _describe(28, 4, 128, 4096)["delta_staging"] == "per_wave"
     keys = [torch.zeros(8, 4, 128, dtype=torch.bfloat16) for _ in range(4)]
     index = torch.arange(64)
     common = dict(key_buffers=keys, value_buffers=keys, source_slots=index, destination_slots=index,
