@@ -305,6 +305,57 @@ typedef struct ll_link_segment {
   int64_t repair_offset;           /* index of the run's first repair row, or -1: not recorded */
 } ll_link_segment;
 
+/*
+ * A link's blocks, in plan order, for the run planner.  Block b covers request
+ * positions [start_token, start_token + token_count); its tokens' destination
+ * indices start at start_token + destination_base (0 for one request; the
+ * offset of the block's request when several requests' slots are
+ * concatenated).
+ */
+typedef struct ll_link_block {
+  const int64_t *source_slots;     /* device [token_count] */
+  const int64_t *local_positions;  /* device [token_count], or NULL: local_start + i */
+  int64_t token_count;             /* 0 .. 2^31 - 1 */
+  int64_t start_token;
+  int64_t destination_base;
+  int64_t local_start;
+  int64_t map_set;                 /* 0: pool slots, 1: snapshot arena */
+  int64_t leading;                 /* 1: an identity block (no token needs a remap): its runs
+                                      take the first map entries of its set */
+} ll_link_block;
+
+typedef struct ll_link_run_plan_info {
+  int64_t num_segments;            /* runs written (or needed, when the outputs are NULL) */
+  int64_t map_count[2];            /* map entries of set 0 and set 1 */
+  int64_t set_repair_rows[2];      /* repair rows whose tokens belong to each set */
+  int64_t set_prefix[2];           /* identity entries heading each set's maps */
+  int64_t repair_count;            /* repair rows in blocks (write-back order: plan order) */
+} ll_link_run_plan_info;
+
+/*
+ * Run planner (host only): cuts a link's blocks into the runs of
+ * ll_kv_build_link_maps.  repair_positions are destination indices (request
+ * positions for one request), in any order, duplicates allowed; only those
+ * inside a block count.  A run is a stretch of one block holding at most one
+ * contiguous stretch of repair rows; runs are in plan order.  With compact
+ * the repair rows take no map entry (else they are flagged in the set's
+ * mask).  Leading blocks' runs head their set's maps (the identity prefix);
+ * the other runs follow in plan order.  Outputs: the runs (segments), the
+ * block of every run (segment_blocks), and the concatenation offset of every
+ * repair row in plan order (repair_offsets); any of them may be NULL, and
+ * with all three NULL the call only fills info (sizing).  A run count of at
+ * most num_blocks + num_repair_positions fits every plan.
+ *
+ * Replaces the host loops of _copy_linked_kv_batched_blocks that find the
+ * repair rows inside blocks (patched_sglang_files/python/sglang/srt/
+ * pic_runtime.py:4981-5003: offset + position - start for every imp_indices
+ * entry inside a block).
+ */
+int ll_plan_link_runs(const ll_link_block *blocks, int64_t num_blocks, const int64_t *repair_positions,
+                      int64_t num_repair_positions, int64_t compact, ll_link_segment *segments,
+                      int64_t segment_capacity, int64_t *segment_blocks, int64_t *repair_offsets,
+                      int64_t repair_offsets_capacity, ll_link_run_plan_info *info);
+
 typedef struct ll_link_maps_args {
   int64_t struct_size;             /* sizeof(ll_link_maps_args) */
   int64_t num_segments;            /* >= 0 */

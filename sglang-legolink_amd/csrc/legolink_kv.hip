@@ -37,7 +37,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "legolink_kv.h"
 #include "ll_internal.h"
@@ -1025,6 +1027,19 @@ void launch_generic(int cache_dtype, dim3 grid, dim3 block, hipStream_t s, const
   else launch_generic_cache<kKey, false>(cache_dtype, grid, block, s, p);
 }
 
+// Host scratch of the run planner, kept per thread so that repeated plans
+// reuse its capacity instead of mapping fresh pages on every call.
+struct PlanScratch {
+  struct Seg { int64_t block, a, b, rb, re; };
+  std::vector<int64_t> dstart, offset, positions, by_start, hit_block, hit_offset, bucket, fill, rows, map_offset;
+  std::vector<Seg> segs;
+};
+
+PlanScratch &plan_scratch() {
+  thread_local PlanScratch scratch_space;
+  return scratch_space;
+}
+
 }  // namespace
 
 int ll_record_error(int code, const char *fmt, va_list ap) {
@@ -1251,6 +1266,170 @@ int ll_kv_scatter_rows(const ll_kv_scatter_args *a, ll_stream_t stream) {
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
       return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return LL_OK;
+}
+
+int ll_plan_link_runs(const ll_link_block *blocks, int64_t num_blocks, const int64_t *repair_positions,
+                      int64_t num_repair_positions, int64_t compact, ll_link_segment *segments,
+                      int64_t segment_capacity, int64_t *segment_blocks, int64_t *repair_offsets,
+                      int64_t repair_offsets_capacity, ll_link_run_plan_info *info) {
+  if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
+  if (num_blocks < 0 || (num_blocks > 0 && blocks == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "blocks must be a host array of num_blocks >= 0 entries");
+  if (num_repair_positions < 0 || (num_repair_positions > 0 && repair_positions == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "repair_positions must be a host array of >= 0 entries");
+  if (segment_capacity < 0 || repair_offsets_capacity < 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "capacities must be >= 0");
+  constexpr int64_t kLimit = static_cast<int64_t>(1) << 62;
+  PlanScratch &w = plan_scratch();
+  // Destination index of every block's first token, and its concatenation
+  // offset (blocks back to back in plan order).
+  std::vector<int64_t> &dstart = w.dstart, &offset = w.offset;
+  dstart.resize(static_cast<size_t>(num_blocks));
+  offset.resize(static_cast<size_t>(num_blocks));
+  int64_t total = 0;
+  for (int64_t b = 0; b < num_blocks; ++b) {
+    const ll_link_block &k = blocks[b];
+    if (k.token_count < 0 || k.token_count > 0x7fffffff || k.start_token < 0 || k.start_token > kLimit ||
+        k.destination_base < 0 || k.destination_base > kLimit || (k.map_set != 0 && k.map_set != 1) ||
+        total > kLimit - k.token_count)
+      return fail(LL_ERR_INVALID_ARGUMENT, "block %lld: token_count in [0, 2^31), start_token and "
+                  "destination_base >= 0, map_set 0 or 1", static_cast<long long>(b));
+    dstart[static_cast<size_t>(b)] = k.start_token + k.destination_base;
+    offset[static_cast<size_t>(b)] = total;
+    total += k.token_count;
+  }
+  // Repair positions inside blocks, per block, in increasing order.
+  std::vector<int64_t> &positions = w.positions;
+  positions.assign(repair_positions, repair_positions + num_repair_positions);
+  if (!std::is_sorted(positions.begin(), positions.end()))  // plans list them in order
+    std::sort(positions.begin(), positions.end());
+  positions.erase(std::unique(positions.begin(), positions.end()), positions.end());
+  std::vector<int64_t> &by_start = w.by_start;
+  by_start.resize(static_cast<size_t>(num_blocks));
+  for (int64_t b = 0; b < num_blocks; ++b) by_start[static_cast<size_t>(b)] = b;
+  // Plans lay their blocks out in position order; sort only when they do not.
+  const bool in_order = std::is_sorted(dstart.begin(), dstart.end());
+  if (!in_order)
+    std::stable_sort(by_start.begin(), by_start.end(), [&](int64_t x, int64_t y) {
+      return dstart[static_cast<size_t>(x)] < dstart[static_cast<size_t>(y)];
+    });
+  // Each position belongs to the last block starting at or before it, if it
+  // lies inside that block: one walk over the sorted positions and the blocks
+  // in start order.  Hits are then bucketed by block (counting sort), in
+  // increasing offset order within a block.
+  std::vector<int64_t> &hit_block = w.hit_block, &hit_offset = w.hit_offset;
+  hit_block.clear();
+  hit_offset.clear();
+  size_t k = 0;
+  for (const int64_t position : positions) {
+    while (k + 1 < by_start.size() && dstart[static_cast<size_t>(by_start[k + 1])] <= position) ++k;
+    if (by_start.empty() || dstart[static_cast<size_t>(by_start[k])] > position) continue;
+    const int64_t b = by_start[k];
+    const int64_t inside = position - dstart[static_cast<size_t>(b)];
+    if (inside < blocks[b].token_count) {
+      hit_block.push_back(b);
+      hit_offset.push_back(inside);
+    }
+  }
+  std::vector<int64_t> &bucket = w.bucket, &fill = w.fill, &rows = w.rows;
+  bucket.assign(static_cast<size_t>(num_blocks) + 1, 0);
+  for (const int64_t b : hit_block) ++bucket[static_cast<size_t>(b) + 1];
+  for (size_t b = 0; b < static_cast<size_t>(num_blocks); ++b) bucket[b + 1] += bucket[b];
+  if (in_order) {
+    rows.swap(hit_offset);  // hits of blocks in position order come grouped by block
+  } else {
+    rows.resize(hit_block.size());  // offsets inside blocks, grouped by block
+    fill.assign(bucket.begin(), bucket.end() - 1);
+    for (size_t i = 0; i < hit_block.size(); ++i)
+      rows[static_cast<size_t>(fill[static_cast<size_t>(hit_block[i])]++)] = hit_offset[i];
+  }
+  // Segments in plan order: a block's repair rows cut it into runs of
+  // consecutive offsets; segment j of a block spans [first ? 0 : begin_j,
+  // last ? count : begin_{j+1}) and holds repair run j.
+  std::vector<PlanScratch::Seg> &segs = w.segs;
+  segs.clear();
+  for (int64_t b = 0; b < num_blocks; ++b) {
+    const int64_t *r = rows.data() + bucket[static_cast<size_t>(b)];
+    const int64_t hits = bucket[static_cast<size_t>(b) + 1] - bucket[static_cast<size_t>(b)];
+    const int64_t count = blocks[b].token_count;
+    if (hits == 0) {
+      if (count > 0) segs.push_back(PlanScratch::Seg{b, 0, count, 0, 0});
+      continue;
+    }
+    // Runs of consecutive offsets [r[i], r[j]]: segment of run starting at i.
+    int64_t i = 0;
+    bool first_run = true;
+    while (i < hits) {
+      int64_t j = i;
+      while (j + 1 < hits && r[j + 1] == r[j] + 1) ++j;
+      const int64_t a = first_run ? 0 : r[i];
+      const int64_t e = j + 1 == hits ? count : r[j + 1];
+      segs.push_back(PlanScratch::Seg{b, a, e, r[i] - a, r[j] + 1 - a});
+      first_run = false;
+      i = j + 1;
+    }
+  }
+  const int64_t n = static_cast<int64_t>(segs.size());
+  // Map offsets per set: the identity (leading) blocks' runs first, then the
+  // others, each in plan order.  Repair rows are numbered in plan order.
+  int64_t map_count[2] = {0, 0}, set_repair[2] = {0, 0}, set_prefix[2] = {0, 0};
+  std::vector<int64_t> &map_offset = w.map_offset;
+  map_offset.resize(static_cast<size_t>(n));
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int64_t i = 0; i < n; ++i) {
+      const PlanScratch::Seg &g = segs[static_cast<size_t>(i)];
+      const bool lead = blocks[g.block].leading != 0;
+      if (lead != (pass == 0)) continue;
+      const int set = static_cast<int>(blocks[g.block].map_set);
+      const int64_t entries = (g.b - g.a) - (compact ? g.re - g.rb : 0);
+      map_offset[static_cast<size_t>(i)] = map_count[set];
+      map_count[set] += entries;
+      set_repair[set] += g.re - g.rb;
+      if (lead) set_prefix[set] += entries;
+    }
+  }
+  int64_t repair_count = 0;
+  for (const PlanScratch::Seg &g : segs) repair_count += g.re - g.rb;
+  info->num_segments = n;
+  info->map_count[0] = map_count[0];
+  info->map_count[1] = map_count[1];
+  info->set_repair_rows[0] = set_repair[0];
+  info->set_repair_rows[1] = set_repair[1];
+  info->set_prefix[0] = set_prefix[0];
+  info->set_prefix[1] = set_prefix[1];
+  info->repair_count = repair_count;
+  if (segments == nullptr && segment_blocks == nullptr && repair_offsets == nullptr) return LL_OK;
+  if (n > segment_capacity)
+    return fail(LL_ERR_INVALID_ARGUMENT, "segment_capacity %lld is below the %lld runs",
+                static_cast<long long>(segment_capacity), static_cast<long long>(n));
+  if (repair_offsets != nullptr && repair_count > repair_offsets_capacity)
+    return fail(LL_ERR_INVALID_ARGUMENT, "repair_offsets_capacity %lld is below the %lld repair rows",
+                static_cast<long long>(repair_offsets_capacity), static_cast<long long>(repair_count));
+  int64_t repair_seen = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const PlanScratch::Seg &g = segs[static_cast<size_t>(i)];
+    const ll_link_block &k = blocks[g.block];
+    if (segments != nullptr) {
+      ll_link_segment &out = segments[i];
+      out.source_slots = k.source_slots + g.a;
+      out.local_positions = k.local_positions != nullptr ? k.local_positions + g.a : nullptr;
+      out.token_count = g.b - g.a;
+      out.start_token = k.start_token + g.a;
+      out.destination_start = dstart[static_cast<size_t>(g.block)] + g.a;
+      out.local_start = k.local_start + g.a;
+      out.repair_begin = g.rb;
+      out.repair_end = g.re;
+      out.map_set = k.map_set;
+      out.map_offset = map_offset[static_cast<size_t>(i)];
+      out.repair_offset = repair_seen;
+    }
+    if (segment_blocks != nullptr) segment_blocks[i] = g.block;
+    if (repair_offsets != nullptr)
+      for (int64_t r = g.rb; r < g.re; ++r)
+        repair_offsets[repair_seen + (r - g.rb)] = offset[static_cast<size_t>(g.block)] + g.a + r;
+    repair_seen += g.re - g.rb;
   }
   return LL_OK;
 }

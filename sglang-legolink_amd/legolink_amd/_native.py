@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "ll_repair_attention_args_size",
     "ll_repair_attention_noalloc",
     "ll_repair_scratch_bytes",
+    "ll_plan_link_runs",
 )
 
 _i64 = ctypes.c_int64
@@ -159,6 +160,37 @@ class LinkSegment(ctypes.Structure):
 
 
 SEGMENT_FIELDS = tuple(name for name, _ in LinkSegment._fields_)
+
+
+class LinkBlock(ctypes.Structure):
+    """Mirror of ``ll_link_block`` (eight 8-byte fields: an int64 ``[n, 8]``
+    array has the same memory layout as ``n`` of these)."""
+
+    _fields_ = [
+        ("source_slots", _ptr),
+        ("local_positions", _ptr),
+        ("token_count", _i64),
+        ("start_token", _i64),
+        ("destination_base", _i64),
+        ("local_start", _i64),
+        ("map_set", _i64),
+        ("leading", _i64),
+    ]
+
+
+BLOCK_FIELDS = tuple(name for name, _ in LinkBlock._fields_)
+
+
+class LinkRunPlanInfo(ctypes.Structure):
+    """Mirror of ``ll_link_run_plan_info``."""
+
+    _fields_ = [
+        ("num_segments", _i64),
+        ("map_count", _i64 * 2),
+        ("set_repair_rows", _i64 * 2),
+        ("set_prefix", _i64 * 2),
+        ("repair_count", _i64),
+    ]
 
 
 class LinkMapsArgs(ctypes.Structure):
@@ -317,6 +349,9 @@ def load_library() -> ctypes.CDLL:
         lib.ll_repair_attention.restype = ctypes.c_int
         lib.ll_repair_attention_args_size.argtypes = []
         lib.ll_repair_attention_args_size.restype = _i64
+        lib.ll_plan_link_runs.argtypes = [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _i64,
+                                          ctypes.POINTER(LinkRunPlanInfo)]
+        lib.ll_plan_link_runs.restype = ctypes.c_int
         lib.ll_repair_attention_noalloc.argtypes = [ctypes.POINTER(RepairAttentionArgs), _ptr]
         lib.ll_repair_attention_noalloc.restype = ctypes.c_int
         lib.ll_repair_scratch_bytes.argtypes = []
@@ -407,6 +442,32 @@ def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_token
                                         positions.ctypes.data if positions.size else None, positions.size,
                                         ctypes.byref(info)))
     return items, combine, positions, info
+
+
+def plan_link_runs(blocks, repair_positions, compact: bool):
+    """ll_plan_link_runs over ``blocks`` (int64 ``[B, 8]`` ll_link_block
+    records) and ``repair_positions`` (int64 ``[R]``): returns the runs (int64
+    ``[S, 11]`` ll_link_segment records), the block of every run, the repair
+    rows' concatenation offsets and the plan info."""
+
+    import numpy as np
+
+    blocks = np.ascontiguousarray(blocks, dtype=np.int64)
+    repair_positions = np.ascontiguousarray(repair_positions, dtype=np.int64)
+    capacity = blocks.shape[0] + repair_positions.size
+    segments = np.empty((capacity, len(SEGMENT_FIELDS)), dtype=np.int64)
+    segment_blocks = np.empty(capacity, dtype=np.int64)
+    repair_offsets = np.empty(repair_positions.size, dtype=np.int64)
+    info = LinkRunPlanInfo()
+    _check(load_library().ll_plan_link_runs(
+        blocks.ctypes.data if blocks.size else None, blocks.shape[0],
+        repair_positions.ctypes.data if repair_positions.size else None, repair_positions.size,
+        1 if compact else 0, segments.ctypes.data if capacity else None, capacity,
+        segment_blocks.ctypes.data if capacity else None,
+        repair_offsets.ctypes.data if repair_offsets.size else None, repair_offsets.size,
+        ctypes.byref(info)))
+    count = int(info.num_segments)
+    return segments[:count], segment_blocks[:count], repair_offsets[: int(info.repair_count)], info
 
 
 def repair_attention(args: RepairAttentionArgs, stream: int) -> None:

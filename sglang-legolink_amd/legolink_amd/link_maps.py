@@ -114,9 +114,13 @@ def _sorted_unique(values: np.ndarray) -> np.ndarray:
     return values
 
 
+_BLOCK_FIELD = {name: index for index, name in enumerate(_native.BLOCK_FIELDS)}
+
+
 def plan_segments(blocks: BlockTable, repair_positions: np.ndarray, *, compact: bool,
                   leading_blocks: Optional[np.ndarray] = None) -> SegmentPlan:
-    """Cut the blocks into runs with at most one contiguous repair run each.
+    """Cut the blocks into runs with at most one contiguous repair run each
+    (``ll_plan_link_runs``, host C++).
 
     ``repair_positions`` are destination indices (request positions for one
     request; sorted or not, duplicates allowed); only those inside blocks
@@ -129,82 +133,29 @@ def plan_segments(blocks: BlockTable, repair_positions: np.ndarray, *, compact: 
     """
 
     count_blocks = int(blocks.counts.size)
-    block, offset = repair_rows_in_blocks(blocks, repair_positions)
-    # Runs: consecutive offsets of one block.
-    if block.size:
-        new_run = np.ones(block.size, dtype=bool)
-        new_run[1:] = (block[1:] != block[:-1]) | (offset[1:] != offset[:-1] + 1)
-        run_start = np.flatnonzero(new_run)
-        run_stop = np.concatenate((run_start[1:], [block.size]))
-        run_block = block[run_start]
-        run_begin = offset[run_start]
-        run_end = offset[run_stop - 1] + 1
-    else:
-        run_block = run_begin = run_end = np.zeros(0, dtype=np.int64)
-    # Runs of a block, in order: segment j spans [first ? 0 : begin_j, last ? count : begin_{j+1}).
-    first = np.ones(run_block.size, dtype=bool)
-    first[1:] = run_block[1:] != run_block[:-1]
-    last = np.ones(run_block.size, dtype=bool)
-    last[:-1] = run_block[:-1] != run_block[1:]
-    next_begin = np.concatenate((run_begin[1:], [0])) if run_block.size else run_begin
-    seg_a = np.where(first, 0, run_begin)
-    seg_b = np.where(last, blocks.counts[run_block], next_begin)
-    seg_block = run_block
-    seg_rb = run_begin - seg_a
-    seg_re = run_end - seg_a
-    # Blocks without repair rows are one run each.
-    plain = np.ones(count_blocks, dtype=bool)
-    plain[run_block] = False
-    plain_blocks = np.flatnonzero(plain)
-    seg_block = np.concatenate((seg_block, plain_blocks)).astype(np.int64)
-    seg_a = np.concatenate((seg_a, np.zeros(plain_blocks.size, dtype=np.int64)))
-    seg_b = np.concatenate((seg_b, blocks.counts[plain_blocks]))
-    seg_rb = np.concatenate((seg_rb, np.zeros(plain_blocks.size, dtype=np.int64)))
-    seg_re = np.concatenate((seg_re, np.zeros(plain_blocks.size, dtype=np.int64)))
-    ordering = np.argsort(blocks.offsets[seg_block] + seg_a, kind="stable")
-    seg_block, seg_a, seg_b = seg_block[ordering], seg_a[ordering], seg_b[ordering]
-    seg_rb, seg_re = seg_rb[ordering], seg_re[ordering]
-
-    count = seg_b - seg_a
-    repair_rows = seg_re - seg_rb
-    entries = count - repair_rows if compact else count
-    sets = blocks.sets[seg_block]
-    lead = (np.zeros(count.size, dtype=bool) if leading_blocks is None
-            else np.asarray(leading_blocks, dtype=bool)[seg_block])
-    map_offset = np.zeros(count.size, dtype=np.int64)
-    map_counts = []
-    set_repairs = []
-    set_prefix = []
-    for s in (0, 1):
-        head = np.flatnonzero((sets == s) & lead)
-        tail = np.flatnonzero((sets == s) & ~lead)
-        ordered = np.concatenate((head, tail))
-        map_offset[ordered] = _exclusive_cumsum(entries[ordered])
-        map_counts.append(int(entries[ordered].sum()))
-        set_repairs.append(int(repair_rows[ordered].sum()))
-        set_prefix.append(int(entries[head].sum()))
-    table = np.empty((count.size, len(_FIELD)), dtype=np.int64)
-    local_ptr = blocks.local_ptrs[seg_block]
-    table[:, _FIELD["source_slots"]] = blocks.source_ptrs[seg_block] + 8 * seg_a
-    table[:, _FIELD["local_positions"]] = np.where(local_ptr != 0, local_ptr + 8 * seg_a, 0)
-    table[:, _FIELD["token_count"]] = count
-    table[:, _FIELD["start_token"]] = blocks.starts[seg_block] + seg_a
-    table[:, _FIELD["destination_start"]] = blocks.destination_starts[seg_block] + seg_a
-    table[:, _FIELD["local_start"]] = blocks.local_starts[seg_block] + seg_a
-    table[:, _FIELD["repair_begin"]] = seg_rb
-    table[:, _FIELD["repair_end"]] = seg_re
-    table[:, _FIELD["map_set"]] = sets
-    table[:, _FIELD["map_offset"]] = map_offset
-    table[:, _FIELD["repair_offset"]] = _exclusive_cumsum(repair_rows)
-    block_entries = np.bincount(seg_block, weights=entries, minlength=count_blocks).astype(np.int64)
+    records = np.empty((count_blocks, len(_BLOCK_FIELD)), dtype=np.int64)
+    records[:, _BLOCK_FIELD["source_slots"]] = blocks.source_ptrs
+    records[:, _BLOCK_FIELD["local_positions"]] = blocks.local_ptrs
+    records[:, _BLOCK_FIELD["token_count"]] = blocks.counts
+    records[:, _BLOCK_FIELD["start_token"]] = blocks.starts
+    records[:, _BLOCK_FIELD["destination_base"]] = (0 if blocks.destination_bases is None
+                                                    else blocks.destination_bases)
+    records[:, _BLOCK_FIELD["local_start"]] = blocks.local_starts
+    records[:, _BLOCK_FIELD["map_set"]] = blocks.sets
+    records[:, _BLOCK_FIELD["leading"]] = (0 if leading_blocks is None
+                                           else np.asarray(leading_blocks, dtype=np.int64))
+    table, segment_blocks, repair_offsets, info = _native.plan_link_runs(
+        records, np.asarray(repair_positions, dtype=np.int64).reshape(-1), compact)
+    entries = table[:, _FIELD["token_count"]] - (
+        table[:, _FIELD["repair_end"]] - table[:, _FIELD["repair_begin"]] if compact else 0)
     return SegmentPlan(
         table=table,
-        map_counts=(map_counts[0], map_counts[1]),
-        set_repair_rows=(set_repairs[0], set_repairs[1]),
-        repair_count=int(repair_rows.sum()),
-        repair_offsets=(blocks.offsets[block] + offset).astype(np.int64),
-        block_entries=block_entries,
-        set_prefix=(set_prefix[0], set_prefix[1]),
+        map_counts=(int(info.map_count[0]), int(info.map_count[1])),
+        set_repair_rows=(int(info.set_repair_rows[0]), int(info.set_repair_rows[1])),
+        repair_count=int(info.repair_count),
+        repair_offsets=repair_offsets,
+        block_entries=np.bincount(segment_blocks, weights=entries, minlength=count_blocks).astype(np.int64),
+        set_prefix=(int(info.set_prefix[0]), int(info.set_prefix[1])),
     )
 
 

@@ -39,6 +39,9 @@ Differences from the reference that keep the result identical:
 
 from __future__ import annotations
 
+import array
+import itertools
+import operator
 import os
 import threading
 import time
@@ -271,6 +274,37 @@ class LinkMaps:
                 "repair_token_count": int(repairs[index]),
             })
         return specs
+
+
+_RANGE_FIELDS = operator.itemgetter("start_token", "end_token")
+
+
+def _range_bounds(ranges: Sequence[Mapping[str, Any]]) -> np.ndarray:
+    """int64 ``[B, 2]`` (start_token, end_token) of the plan's block ranges."""
+
+    try:
+        flat = np.fromiter(itertools.chain.from_iterable(map(_RANGE_FIELDS, ranges)), dtype=np.int64,
+                           count=2 * len(ranges))
+    except (TypeError, ValueError):  # entries that are not plain integers
+        flat = np.array([int(value) for r in ranges for value in _RANGE_FIELDS(r)], dtype=np.int64)
+    return flat.reshape(-1, 2)
+
+
+def _index_array(values: Any) -> np.ndarray:
+    """imp_indices as a flat int64 array: a Python list (the reference's plan
+    format) through array.array, the cheapest conversion (about 17 ns per
+    entry against 26 for numpy's); arrays and tensors as they are."""
+
+    if values is None:
+        return np.zeros(0, dtype=np.int64)
+    if isinstance(values, torch.Tensor):
+        return values.detach().reshape(-1).to("cpu", torch.int64).numpy()
+    if isinstance(values, np.ndarray):
+        return values.astype(np.int64, copy=False).reshape(-1)
+    try:
+        return np.frombuffer(array.array("q", values), dtype=np.int64)
+    except TypeError:  # entries that are not Python ints (numpy scalars, ...)
+        return np.asarray(values, dtype=np.int64).reshape(-1)
 
 
 def _needs_rope_remap(handle: LegoLinkBlockHandle, start: int) -> bool:
@@ -510,11 +544,12 @@ class KVLinkExecutor:
             raise LinkRuntimeError("PIC block range and cache key counts differ.")
         if not cache_keys:
             raise LinkRuntimeError("PIC link plan has no blocks.")
-        lookup = self.registry.lookup_legolink_blocks(str(key) for key in cache_keys)
-        unavailable = [*lookup.missing_blocks, *lookup.stale_blocks]
+        handles, unavailable = self.registry.link_handles([str(key) for key in cache_keys])
         if unavailable:
+            missing = [key for key, handle in zip(cache_keys, handles) if handle is None]
+            stale = [key for key, handle in zip(cache_keys, handles) if handle is not None and not handle.valid]
             raise LinkRuntimeError(
-                f"PIC RadixCache lookup cannot safely link block(s): {', '.join(unavailable)}"
+                f"PIC RadixCache lookup cannot safely link block(s): {', '.join(map(str, missing + stale))}"
             )
         device = destination_slots.device if device is None else device
         request_slots = destination_slots
@@ -522,12 +557,10 @@ class KVLinkExecutor:
             request_slots = request_slots.to(device=device, dtype=torch.int64)
         request_slots = request_slots.contiguous()
         total = int(request_slots.numel())
-        matched = lookup.matched_blocks
-        handles = [matched[str(key)] for key in cache_keys]
         # Per block: the handle's cached record (count, slot and position
         # addresses, local start, set, max local position) and the plan range.
-        records = np.array([handle.link_record(device) for handle in handles], dtype=np.int64)
-        bounds = np.array([(int(r["start_token"]), int(r["end_token"])) for r in ranges], dtype=np.int64)
+        records = self.registry.link_records(handles, device)
+        bounds = _range_bounds(ranges)
         starts, ends = bounds[:, 0].copy(), bounds[:, 1]
         counts = records[:, 0].copy()
         mismatch = np.flatnonzero(ends - starts != counts)
@@ -548,10 +581,8 @@ class KVLinkExecutor:
         max_position = int(max(int(ends.max()) - 1, int(records[:, 5].max())))
         blocks = link_maps.BlockTable(starts=starts, counts=counts, source_ptrs=source_ptrs,
                                       local_ptrs=local_ptrs, local_starts=local_starts, sets=sets)
-        imp = link_plan.get("imp_indices")
-        repair = np.asarray(imp if imp is not None else [], dtype=np.int64).reshape(-1)
-        if repair.size > 1 and not bool(np.all(repair[1:] > repair[:-1])):
-            repair = np.unique(repair)
+        # Sorted or not, duplicates allowed: the run planner sorts and dedups.
+        repair = _index_array(link_plan.get("imp_indices"))
         identity = not _needs_rope_remap(handles[0], int(starts[0]))
         leading = np.zeros(len(handles), dtype=bool)
         leading[0] = identity

@@ -41,6 +41,8 @@ class LegoLinkBlockHandle:
     max_local_position: int = -1
     # Per-device copies the link reads (int64 slots; non-consecutive positions).
     _device_tensors: dict = field(default_factory=dict, repr=False, compare=False)
+    # Row of the handle in its registry's per-device record tables.
+    row: int = -1
 
     @property
     def token_count(self) -> int:
@@ -120,6 +122,9 @@ class LegoLinkBlockRegistry:
         self._blocks: dict[str, LegoLinkBlockHandle] = {}
         self._lock = threading.Lock()
         self._generation = 0
+        self._rows = 0
+        # Per device: the link records of every handle by row, and which rows are filled.
+        self._records: dict[tuple[str, Optional[int]], tuple[np.ndarray, np.ndarray]] = {}
 
     def register_legolink_block(
         self,
@@ -166,7 +171,9 @@ class LegoLinkBlockRegistry:
                 storage_mode=storage_mode,
                 local_start=local_start,
                 max_local_position=max_local,
+                row=self._rows,
             )
+            self._rows += 1
             self._blocks[str(cache_key)] = handle
             return handle
 
@@ -188,6 +195,41 @@ class LegoLinkBlockRegistry:
                     result.kv_slot_ranges[cache_key] = handle.kv_slots
                     result.matched_handles.append(handle)
         return result
+
+    def link_handles(self, cache_keys: Sequence[str]) -> tuple[list[Optional[LegoLinkBlockHandle]], list[str]]:
+        """The valid handle of every key, in order (None where missing or
+        stale), and the keys that cannot be linked: ``lookup_legolink_blocks``
+        reduced to what a link reads, in one pass."""
+
+        with self._lock:
+            handles = [self._blocks.get(key) for key in cache_keys]
+        unavailable = [str(key) for key, handle in zip(cache_keys, handles) if handle is None or not handle.valid]
+        return handles, unavailable
+
+    def link_records(self, handles: Sequence[LegoLinkBlockHandle], device: torch.device) -> np.ndarray:
+        """int64 ``[len(handles), 6]``: every handle's ``link_record(device)``,
+        gathered from a per-device table (filled once per handle and device),
+        so that a link of many blocks reads them with one index."""
+
+        rows = np.fromiter((handle.row for handle in handles), dtype=np.int64, count=len(handles))
+        key = (device.type, device.index)
+        with self._lock:
+            table, filled = self._records.get(key, (None, None))
+            if table is None or table.shape[0] < self._rows:
+                capacity = max(64, 2 * self._rows)
+                grown = np.zeros((capacity, 6), dtype=np.int64)
+                grown_filled = np.zeros(capacity, dtype=bool)
+                if table is not None:
+                    grown[: table.shape[0]] = table
+                    grown_filled[: filled.shape[0]] = filled
+                table, filled = grown, grown_filled
+                self._records[key] = (table, filled)
+            missing = np.flatnonzero(~filled[rows])
+            for index in missing.tolist():
+                handle = handles[index]
+                table[handle.row] = handle.link_record(device)
+                filled[handle.row] = True
+            return table[rows]
 
     def acquire_legolink_blocks(self, handles: Iterable[LegoLinkBlockHandle]) -> list[LegoLinkBlockHandle]:
         handles = list(handles)
