@@ -316,8 +316,8 @@ typedef struct ll_link_block {
   const int64_t *source_slots;     /* device [token_count] */
   const int64_t *local_positions;  /* device [token_count], or NULL: local_start + i */
   int64_t token_count;             /* 0 .. 2^31 - 1 */
-  int64_t start_token;
-  int64_t destination_base;
+  int64_t start_token;             /* 0 .. 2^62 - 1 */
+  int64_t destination_base;        /* 0 .. 2^62 - 1 */
   int64_t local_start;
   int64_t map_set;                 /* 0: pool slots, 1: snapshot arena */
   int64_t leading;                 /* 1: an identity block (no token needs a remap): its runs

@@ -1291,11 +1291,13 @@ int ll_plan_link_runs(const ll_link_block *blocks, int64_t num_blocks, const int
   int64_t total = 0;
   for (int64_t b = 0; b < num_blocks; ++b) {
     const ll_link_block &k = blocks[b];
-    if (k.token_count < 0 || k.token_count > 0x7fffffff || k.start_token < 0 || k.start_token > kLimit ||
-        k.destination_base < 0 || k.destination_base > kLimit || (k.map_set != 0 && k.map_set != 1) ||
+    // Both starts below 2^62 keep their sum, and every position difference
+    // taken from it, inside int64.
+    if (k.token_count < 0 || k.token_count > 0x7fffffff || k.start_token < 0 || k.start_token >= kLimit ||
+        k.destination_base < 0 || k.destination_base >= kLimit || (k.map_set != 0 && k.map_set != 1) ||
         total > kLimit - k.token_count)
       return fail(LL_ERR_INVALID_ARGUMENT, "block %lld: token_count in [0, 2^31), start_token and "
-                  "destination_base >= 0, map_set 0 or 1", static_cast<long long>(b));
+                  "destination_base in [0, 2^62), map_set 0 or 1", static_cast<long long>(b));
     dstart[static_cast<size_t>(b)] = k.start_token + k.destination_base;
     offset[static_cast<size_t>(b)] = total;
     total += k.token_count;

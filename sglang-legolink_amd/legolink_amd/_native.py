@@ -13,11 +13,14 @@ There is no fallback: when the library is missing every entry raises
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
-LIB_PATH = LIB_DIR / "liblegolink_kv.so"
+# LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
+# one of the CPU sanitizer test).
+LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
 ABI_VERSION = 10
 
 # Element type codes (include/legolink_kv.h).

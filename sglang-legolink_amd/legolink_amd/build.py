@@ -22,6 +22,13 @@ SOURCE = PACKAGE_DIR.parent / "csrc" / "legolink_kv.hip"
 SOURCES = (SOURCE, PACKAGE_DIR.parent / "csrc" / "repair_attention.hip")
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
+# The same library with its host code under AddressSanitizer and
+# UndefinedBehaviorSanitizer (device code unchanged), for the CPU tests of the
+# host entries; never loaded on a GPU.
+SANITIZED_OUTPUT = PACKAGE_DIR / "lib" / "host_sanitized" / "liblegolink_kv.so"
+SANITIZE_FLAGS = ["-g", "-fno-omit-frame-pointer", "-shared-libsan",
+                  "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=all"]
 OFFLOAD_ARCH = "gfx950"
 
 
@@ -55,36 +62,54 @@ def compile_command(output: Path, sources=SOURCES) -> list[str]:
     return [hipcc_path(), *_flags(), "-shared", "-o", str(output), *[str(source) for source in sources]]
 
 
-def build_library(verbose: bool = False) -> Path:
+def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path:
     """Compile every translation unit in parallel, then link the library; the
-    output is replaced atomically."""
+    output is replaced atomically.  ``sanitize_host`` builds the host-sanitized
+    copy (SANITIZED_OUTPUT) instead."""
 
-    OUTPUT.parent.mkdir(parents=True, exist_ok=True)
-    with tempfile.TemporaryDirectory(dir=OUTPUT.parent, prefix=".build.") as scratch:
+    output = SANITIZED_OUTPUT if sanitize_host else OUTPUT
+    extra = SANITIZE_FLAGS if sanitize_host else []
+    output.parent.mkdir(parents=True, exist_ok=True)
+    with tempfile.TemporaryDirectory(dir=output.parent, prefix=".build.") as scratch:
         objects = [Path(scratch) / f"{source.stem}.o" for source in SOURCES]
         jobs = [
-            (subprocess.Popen([hipcc_path(), *_flags(), "-c", "-o", str(obj), str(source)],
+            (subprocess.Popen([hipcc_path(), *_flags(), *extra, "-c", "-o", str(obj), str(source)],
                               stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True), source)
             for source, obj in zip(SOURCES, objects)
         ]
         failures = []
         for job, source in jobs:
-            output, _ = job.communicate()
-            messages = _messages(output)
+            printed, _ = job.communicate()
+            messages = _messages(printed)
             if job.returncode != 0:
                 failures.append(f"hipcc failed on {source.name}:\n" + "\n".join(messages))
             elif verbose and messages:
                 print("\n".join(messages), file=sys.stderr)
         if failures:
             raise RuntimeError("\n".join(failures))
-        temporary = Path(scratch) / OUTPUT.name
-        result = subprocess.run([hipcc_path(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o",
-                                 str(temporary), *[str(obj) for obj in objects]],
+        temporary = Path(scratch) / output.name
+        result = subprocess.run([hipcc_path(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *extra,
+                                 "-o", str(temporary), *[str(obj) for obj in objects]],
                                 capture_output=True, text=True)
         if result.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + "\n".join(_messages(result.stdout + result.stderr)))
-        os.replace(temporary, OUTPUT)
-    return OUTPUT
+        os.replace(temporary, output)
+    return output
+
+
+def sanitizer_runtime() -> Path:
+    """The AddressSanitizer runtime of the compiler that builds the sanitized
+    library (to preload into the process that loads it)."""
+
+    clang = Path(hipcc_path()).resolve().parent.parent / "lib" / "llvm" / "bin" / "clang"
+    if not clang.exists():
+        clang = Path("/opt/rocm/lib/llvm/bin/clang")
+    result = subprocess.run([str(clang), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                            capture_output=True, text=True, check=True)
+    runtime = Path(result.stdout.strip())
+    if not runtime.is_file():
+        raise FileNotFoundError(f"AddressSanitizer runtime not found ({runtime})")
+    return runtime
 
 
 def _messages(text: str) -> list[str]:
