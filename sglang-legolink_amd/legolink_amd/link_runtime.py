@@ -498,12 +498,13 @@ class PreparedLink:
 class KVLinkExecutor:
     """Links registered blocks into request slots on one GPU."""
 
-    def __init__(self, registry: LegoLinkBlockRegistry, rotary: RotarySpec | Mapping[int, RotarySpec], *,
+    def __init__(self, registry: LegoLinkBlockRegistry, rotary: Any, *,
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
                  layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, fused_mode: Optional[str] = None,
                  delta_staging: str = "auto") -> None:
-        """``fused_mode`` ("disabled" / "required" / "auto", or the reference's
+        """``rotary`` is a RotarySpec, a model's rotary module, or a mapping of
+        layer to either.  ``fused_mode`` ("disabled" / "required" / "auto", or the reference's
         aliases) fixes the link's rounding; None reads
         ``SGLANG_PIC_TRITON_FUSED_KV_LINK`` at every link, as the reference does.
         ``delta_staging`` ("auto" / "per_wave" / "workgroup") picks where the
@@ -514,10 +515,22 @@ class KVLinkExecutor:
         self.delta_staging = delta_staging
         self.start_layer = int(start_layer)
         self.end_layer = int(end_layer)
-        if isinstance(rotary, RotarySpec):
-            self.rotary_by_layer = {layer: rotary for layer in range(self.start_layer, self.end_layer)}
+        # A model's rotary module (sglang's RotaryEmbedding and the like) is
+        # wrapped once, so layers sharing a module share one spec.
+        wrapped: dict[int, RotarySpec] = {}
+
+        def spec_of(value: Any) -> RotarySpec:
+            if isinstance(value, RotarySpec):
+                return value
+            if id(value) not in wrapped:
+                wrapped[id(value)] = RotarySpec.from_module(value)
+            return wrapped[id(value)]
+
+        if isinstance(rotary, Mapping):
+            self.rotary_by_layer = {int(layer): spec_of(value) for layer, value in rotary.items()}
         else:
-            self.rotary_by_layer = dict(rotary)
+            spec = spec_of(rotary)
+            self.rotary_by_layer = {layer: spec for layer in range(self.start_layer, self.end_layer)}
         self.num_warps = num_warps
         self.layers_per_wave = layers_per_wave
         self.layer_groups_per_block = layer_groups_per_block

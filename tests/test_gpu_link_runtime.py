@@ -13,7 +13,7 @@ from legolink_amd import kv_link
 from legolink_amd.link_plan import resolve_link_plan
 from legolink_amd.link_runtime import KVLinkExecutor, KVPool
 from legolink_amd.registry import LegoLinkBlockRegistry
-from legolink_amd.rope import RotarySpec, build_cos_sin_cache
+from legolink_amd.rope import RotarySpec
 from oracle import kv_link_oracle as ko
 from tests import rope_math
 from tests.gpu_helpers import bits, report
@@ -57,7 +57,7 @@ def test_first_block_remap_cases(gpu_device, case):
     destination = torch.arange(total, device=gpu_device)
     plan = {"cache_keys": list(raws),
             "block_ranges": [{"start_token": s, "end_token": s + c} for s, c in case["blocks"]]}
-    rotary_spec = RotarySpec(build_cos_sin_cache(4096, rotary, theta=theta), rotary_dim=rotary)
+    rotary_spec = RotarySpec.for_theta(4096, rotary, theta=theta)
     executor = KVLinkExecutor(registry, rotary_spec, end_layer=1)
     record = executor.copy_linked_kv(pool, destination, plan)
     torch.cuda.synchronize(gpu_device)
@@ -102,7 +102,7 @@ def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="require
     host_tokens = rng.integers(0, 50_000, size=5 + 40).tolist()
     linked = resolve_link_plan(registry.get_legolink_block_tokens, host_tokens, plan)
     destination = torch.from_numpy(perm[cursor : cursor + len(linked)]).to(device)
-    rotary = RotarySpec(build_cos_sin_cache(2048, dim), rotary_dim=dim)
+    rotary = RotarySpec.for_theta(2048, dim)
     executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode=fused_mode)
     before_k = [bits(k) for k in pool.k_buffer]
     before_v = [bits(v) for v in pool.v_buffer]
@@ -186,7 +186,7 @@ def test_executor_matches_the_per_layer_drop_in_operator(gpu_device):
     plan = {"cache_keys": ["y", "x"], "block_ranges": [{"start_token": 0, "end_token": 300},
                                                      {"start_token": 300, "end_token": 1000}]}
     destination = torch.from_numpy(perm[1000:2000]).to(gpu_device)
-    rotary = RotarySpec(build_cos_sin_cache(2048, 128), rotary_dim=128)
+    rotary = RotarySpec.for_theta(2048, 128)
     executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode="required")
     executor.copy_linked_kv(KVPool(keys, values), destination, plan)
     maps = executor.build_link_maps(destination, plan)
@@ -221,7 +221,7 @@ def test_prepared_link_replays_in_a_hip_graph(gpu_device):
     plan = {"cache_keys": ["a", "b"], "recompute_initial_tokens": 8}
     resolve_link_plan(registry.get_legolink_block_tokens, [1, 2, 3], plan)
     destination = torch.from_numpy(perm[650:1400]).to(gpu_device)
-    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(1024, dim), rotary_dim=dim), end_layer=layers)
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(1024, dim), end_layer=layers)
     prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=True)
     repaired_k = torch.randn(layers, int(prepared.repair_offsets.size), heads, dim, dtype=torch.bfloat16,
                              device=gpu_device, generator=generator)
@@ -274,7 +274,7 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
     arena = SnapshotArena.allocate(num_slots=2048, num_layers=layers, num_heads=heads, head_dim=dim,
                                    device=gpu_device)
     registry = LegoLinkBlockRegistry()
-    rotary = RotarySpec(build_cos_sin_cache(8192, dim), rotary_dim=dim)
+    rotary = RotarySpec.for_theta(8192, dim)
     executor = KVLinkExecutor(registry, rotary, end_layer=layers, arena=arena, fused_mode=fused_mode)
     perm = rng.permutation(slots)
     cursor = 0
@@ -358,7 +358,7 @@ def test_required_fused_mode_refuses_clone_blocks(gpu_device):
     pool = KVPool.allocate(num_slots=slots, num_layers=layers, num_heads=4, head_dim=128, device=gpu_device)
     arena = SnapshotArena.allocate(num_slots=256, num_layers=layers, num_heads=4, head_dim=128, device=gpu_device)
     registry = LegoLinkBlockRegistry()
-    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(1024, 128), rotary_dim=128),
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(1024, 128),
                               end_layer=layers, arena=arena, fused_mode="required")
     executor.capture_block(pool, "c", list(range(50)), torch.arange(50, device=gpu_device), storage_mode="clone")
     plan = {"cache_keys": ["c"], "block_ranges": [{"start_token": 10, "end_token": 60}]}

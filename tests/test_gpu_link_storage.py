@@ -71,7 +71,7 @@ def _setup(device, *, layers=4, slots=4096, arena_slots=2048, seed=31):
     arena = SnapshotArena([torch.zeros(arena_slots, 4, 128, dtype=torch.bfloat16, device=device) for _ in range(layers)],
                           [torch.zeros(arena_slots, 4, 128, dtype=torch.bfloat16, device=device) for _ in range(layers)])
     registry = LegoLinkBlockRegistry()
-    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(4096, 128), rotary_dim=128),
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(4096, 128),
                               end_layer=layers, arena=arena)
     return pool, arena, registry, executor
 

@@ -13,7 +13,7 @@ from legolink_amd.errors import LinkRuntimeError
 from legolink_amd.link_plan import ResolvedLinkPlan, contiguous_ranges, resolve_link_plan
 from legolink_amd.link_runtime import KVLinkExecutor, KVPool
 from legolink_amd.registry import LegoLinkBlockRegistry
-from legolink_amd.rope import RotarySpec, build_cos_sin_cache
+from legolink_amd.rope import RotarySpec
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
 
@@ -109,7 +109,7 @@ def _executor(blocks, *, layers=1, compile_positions=None):
         registry.register_legolink_block(key, list(range(count)), torch.arange(slot, slot + count),
                                          compile_local_positions=positions)
         slot += count
-    rotary = RotarySpec(build_cos_sin_cache(64, 8, theta=1e4), rotary_dim=8)
+    rotary = RotarySpec.for_theta(64, 8, theta=1e4)
     return KVLinkExecutor(registry, rotary, start_layer=0, end_layer=layers)
 
 
@@ -207,7 +207,7 @@ def test_storage_modes_in_registry_and_maps():
         registry.register_legolink_block("x", [1], torch.tensor([0]), storage_mode="paged")
     registry.register_legolink_block("r", [1, 2], torch.tensor([10, 11]))
     registry.register_legolink_block("c", [3, 4, 5], torch.tensor([0, 1, 2]), storage_mode="clone")
-    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(16, 8, theta=1e4), rotary_dim=8),
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(16, 8, theta=1e4),
                               end_layer=1)
     plan = {"cache_keys": ["c", "r"], "block_ranges": [{"start_token": 0, "end_token": 3},
                                                        {"start_token": 3, "end_token": 5}]}
@@ -223,7 +223,7 @@ def test_batched_capture_rejects_before_any_registration():
     """capture_blocks checks every entry before it copies or registers one."""
 
     registry = LegoLinkBlockRegistry()
-    executor = KVLinkExecutor(registry, RotarySpec(build_cos_sin_cache(16, 8, theta=1e4), rotary_dim=8),
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(16, 8, theta=1e4),
                               end_layer=1)
     pool = KVPool.allocate(num_slots=32, num_layers=1, num_heads=1, head_dim=8, device="cpu")
     reference = {"cache_key": "r", "token_ids": [1, 2], "slots": [3, 4]}
