@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 10
+#define LL_ABI_VERSION 11
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -220,6 +220,13 @@ typedef struct ll_kv_link_args {
   int64_t delta_staging;           /* LL_DELTA_*; with LL_DELTA_WORKGROUP, waves_per_block (0..16,
                                       0 = 16) caps the workgroup and layer_groups_per_block
                                       must be 0 (ABI 10) */
+  uint64_t *skipped_rows;          /* device counter, or NULL (ABI 11): the link adds the number of
+                                      unmasked tokens it skipped because a slot lies outside its
+                                      pool or, for a remapped token, a position lies outside the
+                                      cos/sin table; each such token once per call.  The caller
+                                      zeroes it and reads it after the stream's work.  With a
+                                      counter, a pool of no rows is rejected (nothing would run
+                                      to count) */
 } ll_kv_link_args;
 
 /*

@@ -286,6 +286,36 @@ def rerotate_rows_c(
 # ---------------------------------------------------------------------------
 # Pool-level semantics.
 # ---------------------------------------------------------------------------
+def skipped_token_mask(
+    src: np.ndarray,
+    dst: np.ndarray,
+    local: np.ndarray,
+    global_: np.ndarray,
+    *,
+    source_slots: int,
+    destination_slots: int,
+    cache_rows: int,
+    prefix: int,
+    repair_mask: np.ndarray | None = None,
+) -> np.ndarray:
+    """Tokens the link skips for an out-of-range index: unmasked, and a slot
+    outside its pool, or (remapped tokens, t >= prefix) a position outside
+    the table.  The reference leaves such inputs undefined in its fused kernel
+    (legolink_triton.py:336-339 load the slots and positions unchecked) and
+    raises in its torch path (index_select, pic_runtime.py:5534-5599); the
+    library skips them and counts them, and this is that contract."""
+
+    src = np.asarray(src, dtype=np.int64)
+    dst = np.asarray(dst, dtype=np.int64)
+    local = np.asarray(local, dtype=np.int64)
+    global_ = np.asarray(global_, dtype=np.int64)
+    masked = np.zeros(src.shape[0], dtype=bool) if repair_mask is None else np.asarray(repair_mask) != 0
+    bad = (src < 0) | (src >= source_slots) | (dst < 0) | (dst >= destination_slots)
+    remap = np.arange(src.shape[0]) >= prefix
+    bad_position = (local < 0) | (local >= cache_rows) | (global_ < 0) | (global_ >= cache_rows)
+    return ~masked & (bad | (remap & bad_position))
+
+
 def link_pool(
     key_layers: list[np.ndarray],
     value_layers: list[np.ndarray],
@@ -316,6 +346,22 @@ def link_pool(
         keep = np.asarray(repair_mask) == 0
     source_key_layers = key_layers if source_key_layers is None else source_key_layers
     source_value_layers = value_layers if source_value_layers is None else source_value_layers
+    # Tokens with an out-of-range index are skipped (skipped_token_mask); the
+    # rows of the others are computed with those indices replaced by 0.
+    skipped = skipped_token_mask(src, dst, local, global_, source_slots=source_key_layers[0].shape[0],
+                                 destination_slots=key_layers[0].shape[0], cache_rows=cache.shape[0],
+                                 prefix=prefix, repair_mask=repair_mask)
+    keep = keep & ~skipped
+    # Masked and skipped tokens store nothing: read row 0 and position 0 for
+    # any index of theirs that is out of range.
+    local = np.asarray(local, dtype=np.int64)
+    global_ = np.asarray(global_, dtype=np.int64)
+    cache_rows = cache.shape[0]
+    src = np.where((src >= 0) & (src < source_key_layers[0].shape[0]), src, 0)
+    local = np.where((local >= 0) & (local < cache_rows), local, 0)
+    global_ = np.where((global_ >= 0) & (global_ < cache_rows), global_, 0)
+    if cache_rows == 0:  # every remapped token is skipped: nothing reads the table
+        prefix = src.shape[0]
     out_k, out_v = [], []
     for key, value, source_key, source_value in zip(
         key_layers, value_layers, source_key_layers, source_value_layers

@@ -108,6 +108,7 @@ struct LinkParams {
   int stream_rows;           // vector kernel: non-temporal row loads (rows read once)
   int eager;                 // LL_ROUNDING_EAGER: the torch path's rounding points
   int staged;                // vector kernel: deltas staged once per workgroup in LDS
+  unsigned long long *skipped;  // tokens skipped for an out-of-range index, or NULL
 };
 
 struct ScatterParams {
@@ -398,9 +399,13 @@ kv_link_vec_kernel(const LinkParams p) {
   const unsigned char mask_byte = mask_bytes[t];
   const bool remap = t >= p.prefix;
   const bool positions_ok = lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows;
-  const bool ok = in_range && !(p.mask != nullptr && mask_byte != 0) && src >= 0 &&
-                  src < p.src_num_slots && dst >= 0 && dst < p.num_slots &&
-                  (!remap || positions_ok);
+  const bool masked = p.mask != nullptr && mask_byte != 0;
+  const bool ok = in_range && !masked && src >= 0 && src < p.src_num_slots && dst >= 0 &&
+                  dst < p.num_slots && (!remap || positions_ok);
+  // An unmasked token skipped for an out-of-range index is counted once, by
+  // its first chunk's lane in layer group 0 (an ordinary global atomic).
+  if (p.skipped != nullptr && in_range && !ok && !masked && c == 0 && layer_group == 0)
+    atomicAdd(p.skipped, 1ull);
 
   // Row loads are unconditional so that no wait separates one layer's loads
   // from the next: a lane without a valid source reads row 0 (the host
@@ -572,16 +577,21 @@ __global__ void __launch_bounds__(512) kv_link_generic_kernel(const LinkParams p
   const long long v_row = static_cast<long long>(p.num_heads) * p.vdim;
 
   for (long long t = blockIdx.x; t < p.num_tokens; t += gridDim.x) {
+    if (p.mask != nullptr && p.mask[t] != 0) continue;
     const long long src = load_index(p.src, p.idx64 & 1, t);
     const long long dst = load_index(p.dst, p.idx64 & 2, t);
-    if (src < 0 || src >= p.src_num_slots || dst < 0 || dst >= p.num_slots) continue;
-    if (p.mask != nullptr && p.mask[t] != 0) continue;
+    bool bad = src < 0 || src >= p.src_num_slots || dst < 0 || dst >= p.num_slots;
     const bool remap = t >= p.prefix;
     long long lp = 0, gp = 0;
-    if (remap) {
+    if (remap && !bad) {
       lp = load_index(p.lpos, p.idx64 & 4, t);
       gp = load_index(p.gpos, p.idx64 & 8, t);
-      if (lp < 0 || lp >= p.cs_rows || gp < 0 || gp >= p.cs_rows) continue;
+      bad = lp < 0 || lp >= p.cs_rows || gp < 0 || gp >= p.cs_rows;
+    }
+    if (bad) {
+      // Counted once per token: by thread 0 of the first layer's workgroup.
+      if (p.skipped != nullptr && blockIdx.y == 0 && threadIdx.x == 0) atomicAdd(p.skipped, 1ull);
+      continue;
     }
     const uint16_t *ks = kbase + src * k_row;
     uint16_t *kd = kout + dst * k_row;
@@ -804,6 +814,8 @@ int validate_link(const ll_kv_link_args *a) {
   if (a->layers_per_wave < 0) return fail(LL_ERR_LAUNCH_CONFIG, "layers_per_wave is negative");
   if (a->rounding != LL_ROUNDING_FUSED && a->rounding != LL_ROUNDING_EAGER)
     return fail(LL_ERR_INVALID_ARGUMENT, "unknown rounding %lld", static_cast<long long>(a->rounding));
+  if (reinterpret_cast<uintptr_t>(a->skipped_rows) % alignof(uint64_t) != 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "skipped_rows must be 8-byte aligned");
   if (a->layer_groups_per_block < 0 ||
       (a->layer_groups_per_block > 0 &&
        ((a->waves_per_block ? a->waves_per_block : 4) % a->layer_groups_per_block) != 0))
@@ -1129,6 +1141,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.stream_rows = a->stream_source_rows != 0 ? 1 : 0;
   p.eager = a->rounding == LL_ROUNDING_EAGER ? 1 : 0;
   p.staged = plan.staged ? 1 : 0;
+  p.skipped = reinterpret_cast<unsigned long long *>(a->skipped_rows);
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;
@@ -1149,8 +1162,12 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   const dim3 block(plan.block_threads);
   // Every slot index is out of range for an empty pool: every token is
   // skipped, and no kernel runs (the vector kernel reads row 0 of the source
-  // pool unconditionally).
-  if (p.src_num_slots == 0 || p.num_slots == 0) return LL_OK;
+  // pool unconditionally), so none could be counted.
+  if (p.src_num_slots == 0 || p.num_slots == 0) {
+    if (a->skipped_rows != nullptr)
+      return fail(LL_ERR_INVALID_ARGUMENT, "skipped_rows is set and a pool has no rows");
+    return LL_OK;
+  }
 
   for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
     const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch
@@ -1187,6 +1204,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
       return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    p.skipped = nullptr;  // later launches see the same tokens: count them once
   }
   return LL_OK;
 }

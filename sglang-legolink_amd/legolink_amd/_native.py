@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -116,6 +116,7 @@ class LinkArgs(ctypes.Structure):
         ("stream_source_rows", _i64),
         ("rounding", _i64),
         ("delta_staging", _i64),
+        ("skipped_rows", _ptr),
     ]
 
 

@@ -351,7 +351,8 @@ class PreparedLink:
                  compact_repair_rows: bool, num_warps: Optional[int], layers_per_wave: int,
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None,
-                 fused_mode: str = "required", delta_staging: str = "auto") -> None:
+                 fused_mode: str = "required", delta_staging: str = "auto",
+                 skipped_rows: Optional[torch.Tensor] = None) -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -409,7 +410,7 @@ class PreparedLink:
                 if mask is not None:
                     mask = torch.cat([mask[:prefix], mask[order]])
                 self._kernel_maps.append(device_maps)
-            for group_layers, rotary in groups:
+            for group_index, (group_layers, rotary) in enumerate(groups):
                 indices = [index_of[layer] for layer in group_layers]
                 self._links.append(kv_link.PreparedKVLink(
                     key_buffers=[key_buffers[i] for i in indices],
@@ -434,6 +435,8 @@ class PreparedLink:
                     stream_source_rows=self.stream_source_rows,
                     rounding=self.rounding,
                     delta_staging=delta_staging,
+                    # Each set's tokens are counted once, by its first layer group.
+                    skipped_rows=skipped_rows if group_index == 0 else None,
                 ))
         key_row = int(key_buffers[0][0].numel()) * key_buffers[0].element_size()
         value_row = int(value_buffers[0][0].numel()) * value_buffers[0].element_size()
@@ -502,13 +505,16 @@ class KVLinkExecutor:
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
                  layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, fused_mode: Optional[str] = None,
-                 delta_staging: str = "auto") -> None:
+                 delta_staging: str = "auto", count_skipped_rows: bool = True) -> None:
         """``rotary`` is a RotarySpec, a model's rotary module, or a mapping of
         layer to either.  ``fused_mode`` ("disabled" / "required" / "auto", or the reference's
         aliases) fixes the link's rounding; None reads
         ``SGLANG_PIC_TRITON_FUSED_KV_LINK`` at every link, as the reference does.
         ``delta_staging`` ("auto" / "per_wave" / "workgroup") picks where the
-        link kernel computes its RoPE deltas (the result is the same)."""
+        link kernel computes its RoPE deltas (the result is the same).
+        ``count_skipped_rows`` has every link count, on the device, the
+        tokens its kernel skipped for an out-of-range slot or position
+        (``skipped_rows`` / ``check_skipped_rows`` read the count)."""
 
         self.registry = registry
         self.fused_mode = None if fused_mode is None else get_fused_kv_link_mode(fused_mode)
@@ -535,10 +541,43 @@ class KVLinkExecutor:
         self.layers_per_wave = layers_per_wave
         self.layer_groups_per_block = layer_groups_per_block
         self.arena = arena
+        self.count_skipped_rows = bool(count_skipped_rows)
+        self._skip_counters: dict[torch.device, torch.Tensor] = {}
 
     @property
     def layers(self) -> list[int]:
         return list(range(self.start_layer, self.end_layer))
+
+    def _skip_counter(self, device: torch.device) -> Optional[torch.Tensor]:
+        if not self.count_skipped_rows:
+            return None
+        device = torch.device(device)
+        counter = self._skip_counters.get(device)
+        if counter is None:
+            counter = torch.zeros(1, dtype=torch.int64, device=device)
+            self._skip_counters[device] = counter
+        return counter
+
+    def skipped_rows(self, *, reset: bool = True) -> int:
+        """Tokens the links so far skipped because a slot or position was out
+        of range (the kernels skip such rows; the reference's eager path raises
+        on them).  Reads the device counters, which waits for the work already
+        queued on the current stream; links launched on other streams must be
+        synchronised first.  ``reset`` zeroes the counters."""
+
+        total = 0
+        for counter in self._skip_counters.values():
+            total += int(counter.item())
+            if reset:
+                counter.zero_()
+        return total
+
+    def check_skipped_rows(self) -> None:
+        """Raise if any link since the last check skipped a token."""
+
+        skipped = self.skipped_rows(reset=True)
+        if skipped:
+            raise LinkRuntimeError(f"PIC link skipped {skipped} token(s): a slot or RoPE position was out of range.")
 
     def _fused_mode(self) -> str:
         return self.fused_mode if self.fused_mode is not None else get_fused_kv_link_mode()
@@ -638,7 +677,7 @@ class KVLinkExecutor:
             num_warps=self.num_warps, layers_per_wave=self.layers_per_wave,
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, fused_mode=self._fused_mode(),
-            delta_staging=self.delta_staging,
+            delta_staging=self.delta_staging, skipped_rows=self._skip_counter(device),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -672,6 +711,7 @@ class KVLinkExecutor:
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, order_by_source=order_by_source,
             fused_mode=self._fused_mode(), delta_staging=self.delta_staging,
+            skipped_rows=self._skip_counter(device),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -739,6 +779,7 @@ class KVLinkExecutor:
                 stream_source_rows=(int(source_slots.numel()) * len(group_layers)
                                     * _row_bytes(source, group_layers[0]) > MEMORY_SIDE_CACHE_BYTES),
                 rounding=rounding,
+                skipped_rows=self._skip_counter(source_slots.device) if group_layers is groups[0][0] else None,
             )
 
     def capture_block(self, pool: Any, cache_key: str, token_ids: Sequence[int], slots: torch.Tensor, *,

@@ -73,8 +73,20 @@ CASES = [
 ]
 
 
+def _corrupt(rng, fraction, src, dst, local, global_, slots, cache_rows):
+    """Plant out-of-range slots and positions in about ``fraction`` of the tokens."""
+
+    src, dst, local, global_ = (a.copy() for a in (src, dst, local, global_))
+    for t in np.flatnonzero(rng.random(src.shape[0]) < fraction):
+        kind = int(rng.integers(0, 8))
+        target = (src, dst, local, global_)[kind % 4]
+        limit = slots if kind % 4 < 2 else cache_rows
+        target[t] = -1 - int(rng.integers(0, 3)) if kind < 4 else limit + int(rng.integers(0, 3))
+    return src, dst, local, global_
+
+
 def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="dense", rounding="fused",
-              **link_options):
+              corrupt=0.0, **link_options):
     (name, dtype, cache_dtype, heads, kdim, vdim, rotary, neox, kernel, index_dtype, prefix,
      mask_fraction, layers, tokens, expected_kernel) = case
     report(f"case {name}: layers={layers} heads={heads} kdim={kdim} vdim={vdim} rotary={rotary} "
@@ -87,6 +99,12 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
     local_np = rng.integers(0, max_position, size=tokens)
     global_np = rng.integers(0, max_position, size=tokens)
     mask_np = (rng.random(tokens) < mask_fraction).astype(np.uint8)
+    skipped = None
+    if corrupt:
+        src_np, dst_np, local_np, global_np = _corrupt(rng, corrupt, src_np, dst_np, local_np, global_np,
+                                                       slots, max_position)
+        skipped = torch.zeros(1, dtype=torch.int64, device=device)
+        link_options = {**link_options, "skipped_rows": skipped}
     keys, values = make_pool(layers, slots, heads, kdim, vdim, dtype, device, seed)
     table = build_cos_sin_cache(max_position, rotary, theta=1e6).to(cache_dtype)
     if cache_layout == "strided":
@@ -108,11 +126,12 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         rotary_dim=rotary, neox=neox, prefix=prefix, repair_mask=mask_np if mask is not None else None,
         rounding=ko.EAGER if rounding == "eager" else ko.FUSED,
     )
+    describe_options = {key: value for key, value in link_options.items() if key != "skipped_rows"}
     launch = kv_link.describe_link_launch(
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
         local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
         prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=neox, repair_mask=mask,
-        kernel=kernel, **link_options,
+        kernel=kernel, **describe_options,
     )
     assert launch["kernel"] == expected_kernel, launch
     if link_options.get("delta_staging") == "workgroup":
@@ -132,6 +151,12 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         assert np.array_equal(got_v, expected_v[layer]), f"{name}: V layer {layer}"
         diff = np.argwhere(got_k != expected_k[layer])
         assert diff.size == 0, f"{name}: K layer {layer} differs at {diff[:5].tolist()}"
+    if skipped is not None:
+        expected_skips = ko.skipped_token_mask(
+            src_np, dst_np, local_np, global_np, source_slots=slots, destination_slots=slots,
+            cache_rows=max_position, prefix=prefix, repair_mask=mask_np if mask is not None else None)
+        assert expected_skips.any(), f"{name}: no token was corrupted"
+        assert int(skipped.item()) == int(expected_skips.sum()), f"{name}: skipped-row count"
 
 
 @pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])
@@ -163,6 +188,29 @@ def test_workgroup_staged_deltas_match_oracle(gpu_device, staged, rounding):
     case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
             mask_fraction, layers, tokens, "vector")
     _run_case(gpu_device, case, rounding=rounding, delta_staging="workgroup", layers_per_wave=lpw)
+
+
+SKIP_CASES = [case for case in CASES if case[0] in {
+    "qwen7b_vec", "qwen7b_vec_prefix_mask", "qwen7b_generic_prefix_mask", "tp_shard_one_head_int32",
+    "gptj_vec", "fp16_generic", "bf16_key_bf16_cache", "partial_rotary_generic", "seventy_layers",
+    "mixed_index_dtypes", "five_layers_odd_tail"}]
+
+
+@pytest.mark.parametrize("case", SKIP_CASES, ids=[case[0] for case in SKIP_CASES])
+def test_out_of_range_tokens_are_skipped_and_counted(gpu_device, case):
+    """Tokens with a slot or position out of range store nothing and are
+    counted once per call (over several launches too: seventy_layers)."""
+
+    _run_case(gpu_device, case, corrupt=0.15, seed=23)
+
+
+@pytest.mark.parametrize("staged", STAGED_CASES[:5], ids=[case[0] for case in STAGED_CASES[:5]])
+def test_out_of_range_tokens_are_counted_with_staged_deltas(gpu_device, staged):
+    name, dtype, heads, dim, layers, tokens, prefix, mask_fraction, lpw, index_dtype = staged
+    case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
+            mask_fraction, layers, tokens, "vector")
+    _run_case(gpu_device, case, delta_staging="workgroup", layers_per_wave=lpw, corrupt=0.15, seed=29,
+              rounding="eager")
 
 
 @pytest.mark.parametrize("case", CASES, ids=[case[0] for case in CASES])

@@ -11,7 +11,7 @@ import torch
 
 from legolink_amd import kv_link
 from legolink_amd.link_plan import resolve_link_plan
-from legolink_amd.link_runtime import KVLinkExecutor, KVPool
+from legolink_amd.link_runtime import KVLinkExecutor, KVPool, LinkRuntimeError
 from legolink_amd.registry import LegoLinkBlockRegistry
 from legolink_amd.rope import RotarySpec
 from oracle import kv_link_oracle as ko
@@ -365,3 +365,41 @@ def test_required_fused_mode_refuses_clone_blocks(gpu_device):
     with pytest.raises(LinkRuntimeError, match="Required Triton LegoLink fusion is unavailable: "
                                                "reference_storage_required"):
         executor.prepare_link(pool, torch.arange(100, 200, device=gpu_device), plan)
+
+
+def test_executor_counts_tokens_skipped_for_bad_slots(gpu_device):
+    """A block registered with slots outside the pool: the kernel skips those
+    tokens, the executor's device counter holds how many, and
+    check_skipped_rows raises once (then the count starts again at zero)."""
+
+    report("executor skipped-row counter: 2 blocks, 5 bad slots")
+    layers, slots, heads, dim = 3, 1500, 4, 128
+    rng = np.random.default_rng(8)
+    registry = LegoLinkBlockRegistry()
+    generator = torch.Generator(device=gpu_device).manual_seed(9)
+    pool = KVPool([torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)],
+                  [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator) for _ in range(layers)])
+    perm = rng.permutation(slots)
+    bad = perm[:300].copy()
+    bad[[3, 50, 51, 200, 299]] = slots + np.array([0, 1, 7, 100, 5])
+    registry.register_legolink_block("a", list(range(400)), torch.from_numpy(perm[300:700]).to(gpu_device))
+    registry.register_legolink_block("b", list(range(300)), torch.from_numpy(bad).to(gpu_device))
+    plan = {"cache_keys": ["a", "b"], "recompute_initial_tokens": 8}
+    resolve_link_plan(registry.get_legolink_block_tokens, [1, 2, 3], plan)
+    destination = torch.from_numpy(perm[700:1400]).to(gpu_device)
+    executor = KVLinkExecutor(registry, RotarySpec.for_theta(1024, dim), end_layer=layers)
+    before = [bits(k) for k in pool.k_buffer]
+    executor.prepare_link(pool, destination, plan, boundary_repair_aware=False).launch()
+    with pytest.raises(LinkRuntimeError, match="skipped 5 token"):
+        executor.check_skipped_rows()
+    executor.check_skipped_rows()  # reset by the failed check
+    # The skipped tokens' destinations (block b starts at request position 400) were not written.
+    untouched = destination.cpu().numpy()[400 + np.array([3, 50, 51, 200, 299])]
+    for layer in range(layers):
+        assert np.array_equal(bits(pool.k_buffer[layer])[untouched], before[layer][untouched])
+    # A clean link leaves the counter at zero.
+    registry.register_legolink_block("c", list(range(300)), torch.from_numpy(perm[:300]).to(gpu_device))
+    plan = {"cache_keys": ["a", "c"], "recompute_initial_tokens": 8}
+    resolve_link_plan(registry.get_legolink_block_tokens, [1, 2, 3], plan)
+    executor.prepare_link(pool, destination, plan, boundary_repair_aware=False).launch()
+    assert executor.skipped_rows() == 0

@@ -212,3 +212,19 @@ def test_allocation_free_attention_rejects_before_any_launch():
     args.num_items = 0
     args.workspace_items = 0
     assert lib.ll_repair_attention_noalloc(ctypes.byref(args), None) == _native.LL_OK  # nothing to do
+
+
+def test_link_rejects_a_misaligned_counter_and_a_counter_on_an_empty_pool():
+    from tests.test_native_abi import _cpu_args
+
+    args, keepalive = _cpu_args()
+    args.skipped_rows = 0x1004  # not 8-byte aligned
+    with pytest.raises(_native.NativeCallError, match="aligned"):
+        _native.kv_link_describe(args)
+    lib = _native.load_library()
+    args.skipped_rows = 0x1008
+    args.num_slots = 0  # nothing would run to count the skipped tokens
+    args.source_num_slots = 0
+    assert lib.ll_kv_link(ctypes.byref(args), None) == _native.LL_ERR_INVALID_ARGUMENT
+    assert "no rows" in lib.ll_last_error().decode()
+    del keepalive
