@@ -724,6 +724,9 @@ def main() -> int:
     end_to_end_link_ms = float(np.median(end_to_end_ms[1:]))
     del fresh
     log(f"end to end per link (fresh prepare + link + write-back): {end_to_end_link_ms:.3f} ms")
+    # Every link above counted the tokens its kernel skipped for a bad index:
+    # the synthetic plans have none.
+    executor.check_skipped_rows()
 
     bytes_info = workload.algorithmic_bytes()
     total_bytes = bytes_info["total_bytes"]
