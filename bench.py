@@ -81,6 +81,9 @@ def parse_args() -> argparse.Namespace:
                         help="repair attention: KV tokens per work item (0: the planner's choice)")
     parser.add_argument("--head-dim", type=int, default=0, choices=[0, 64, 128, 256],
                         help="repair attention: head dim in place of the workload's (same spans and heads)")
+    parser.add_argument("--heads", default="",
+                        help="repair attention: query/KV heads in place of the model's, e.g. 8/8 (MHA), "
+                             "32/8 (same spans)")
     return parser.parse_args()
 
 
@@ -394,6 +397,12 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
     shape = workload.shape
     if args.head_dim:
         shape = dataclasses.replace(shape, head_dim=args.head_dim)
+    if args.heads:
+        q_heads, kv_heads = (int(x) for x in args.heads.split("/"))
+        if q_heads < 1 or kv_heads < 1 or q_heads % kv_heads:
+            raise SystemExit("--heads takes Q/KV with Q a multiple of KV")
+        shape = dataclasses.replace(shape, kv_heads=kv_heads)
+        group = q_heads // kv_heads
     q_heads = group * shape.kv_heads
     generator = torch.Generator(device=device).manual_seed(20260824)
     key = torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, generator=generator,

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 11
+#define LL_ABI_VERSION 12
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -404,7 +404,8 @@ typedef struct ll_link_maps_args {
  *   overlap), writes every query's logical position into the positions
  *   table, groups consecutive tiles of one request into work items
  *   that share every staged K/V tile (as many tiles as 16 (tile, query head)
- *   pairs allow: 2 for 7 or 8 query heads per KV head, 1 above 8), splits
+ *   pairs allow: 16 for one query head per KV head, 2 for 7 or 8, 1 above
+ *   8), splits
  *   long KV ranges into chunks of
  *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
  *   from a model of the device's workgroup rounds), and writes the item and
@@ -429,7 +430,7 @@ typedef struct ll_repair_row {
 } ll_repair_row;
 
 typedef struct ll_repair_attention_plan_info {
-  int64_t num_items;               /* int32 [num_items, 24] work items */
+  int64_t num_items;               /* int32 [num_items, 84] work items (ABI 12) */
   int64_t num_combine;             /* int32 [num_combine, 4] combine items */
   int64_t workspace_items;         /* partial results (see ll_repair_attention_args.workspace) */
   int64_t split_tokens;            /* KV tokens per work item (the plan's choice when 0 was asked) */

@@ -2,16 +2,18 @@
 // repair rows over the linked KV, read through each request's slot list.
 //
 // Work decomposition (planned on the host by ll_repair_attention_plan):
-//   item = up to four 16-query tiles of one request (consecutive repair
-//   rows) and a KV range [kv_begin, kv_end) of logical positions; long ranges
-//   are split and the partial results merged by a combine pass.
+//   item = up to 16 / G 16-query tiles of one request (consecutive repair
+//   rows; G query heads share one KV head; at most 16 tiles, at least 1) and
+//   a KV range [kv_begin, kv_end) of logical positions; long ranges are
+//   split and the partial results merged by a combine pass.
 //   workgroup = (item, KV head); the item's (query tile, query head) pairs
-//   -- pair n is query tile n / G, query head hk * G + n % G (G query heads
-//   share one KV head) -- are spread over its waves, so each K/V tile staged
-//   in LDS serves every query tile and head of the item.  A workgroup holds
-//   P = 16 pairs (8 for head dim 256); with more than P query heads per KV
-//   head, items have one tile and each KV head gets ceil(G / P) workgroups of
-//   P heads.
+//   -- pair n is query tile n / G, query head hk * G + n % G -- are spread
+//   over its waves, so each K/V tile staged in LDS serves every query tile
+//   and head of the item.  A workgroup holds P = 16 pairs (8 for head dim
+//   256); with more than P query heads per KV head, items have one tile and
+//   each KV head gets ceil(G / P) workgroups of P heads, and where an item's
+//   tiles times G exceed P (head dim 256) its tiles are split over several
+//   workgroups the same way.
 //
 // Per 64-token KV tile:
 //   1. gather the tile's K and V rows of this KV head into LDS by slot;
@@ -62,11 +64,14 @@ typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
 constexpr int kTile = 64;     // KV tokens per LDS tile
-constexpr int kMaxTiles = 4;    // 16-query tiles per work item
+// 16-query tiles per work item: as many (tile, query head) pairs as a
+// workgroup of head dim 64 or 128 holds, so that MHA (one query head per KV
+// head) fills its waves with 16 tiles.
+constexpr int kMaxTiles = 16;
 // kv_offset, kv_begin, kv_end, tiles, then per tile (first query, lowest
 // position, query count (0: absent), partial slot (-1: none), key end).
-constexpr int kItemInts = 24;
 constexpr int kTileInts = 5;
+constexpr int kItemInts = 4 + kTileInts * kMaxTiles;  // 84
 constexpr int kCombineInts = 4;
 constexpr int kMaxPairs = 16;  // (query tile, query head) pairs per workgroup (head dims 64 and 128)
 
@@ -95,8 +100,10 @@ struct AttnParams {
   int hq;
   int hkv;
   int group;
-  int heads_per_wg;  // query heads of a KV head that one workgroup computes: min(group, 16)
-  int head_chunks;   // workgroups per (item, KV head): group / heads_per_wg, rounded up
+  int heads_per_wg;  // query heads of a KV head that one workgroup computes
+  int head_chunks;   // head groups per (item, KV head): group / heads_per_wg, rounded up
+  int tiles_per_wg;  // query tiles of an item that one workgroup computes
+  int tile_chunks;   // tile groups per (item, KV head): tiles per item / tiles_per_wg, rounded up
   int slots64;
   float scale_log2;
 };
@@ -282,15 +289,21 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
 
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
-  const int hk = blockIdx.y / p.head_chunks;
-  const int head_base = (blockIdx.y % p.head_chunks) * p.heads_per_wg;
+  // blockIdx.y = (KV head, head group, tile group).
+  const int chunks_per_head = p.head_chunks * p.tile_chunks;
+  const int hk = blockIdx.y / chunks_per_head;
+  const int head_base = (blockIdx.y % chunks_per_head) / p.tile_chunks * p.heads_per_wg;
+  const int tile_base = (blockIdx.y % p.tile_chunks) * p.tiles_per_wg;
   if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
       kv_end - kv_begin > kDmaMaxRange || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
       hk >= p.hkv)
     return;
 
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  // Wave-uniform values are made visibly uniform (readfirstlane), so that
+  // branches on them are scalar branches: otherwise the compiler evaluates
+  // both sides of the per-tile mask branch below on every tile.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   const int h = lane / 32;   // k half of the A/B operands, row group of the accumulators
   const int col = lane % 32;  // MFMA column of this lane
@@ -304,7 +317,8 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   };
   auto pair_info = [&](int pair) {
     PairInfo r;
-    const int tile = pair / p.heads_per_wg;
+    const int tile_in_wg = pair / p.heads_per_wg;
+    const int tile = tile_base + tile_in_wg;
     const int head = head_base + pair % p.heads_per_wg;
     const int *e = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
     r.q_index = e[0];
@@ -313,7 +327,8 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     r.partial = e[3];
     const int needed = e[4];
     r.hq = hk * p.group + head;
-    r.computes = tile < n_tiles && head < p.group && r.q_count >= 1 && r.q_count <= kQueries && r.q_index >= 0 &&
+    r.computes = tile_in_wg < p.tiles_per_wg && tile < n_tiles && head < p.group && r.q_count >= 1 &&
+                 r.q_count <= kQueries && r.q_index >= 0 &&
                  static_cast<long long>(r.q_index) + r.q_count <= p.num_queries && r.q_pos >= 0 &&
                  needed > r.q_pos && (r.partial == -1 || (r.partial >= 0 && r.partial < p.ws_items));
     r.stop = r.computes ? min(kv_end, needed) : kv_begin;
@@ -331,8 +346,9 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   const int my_pos = q_ok ? p.positions[mine.q_index + qc] : 0;
   const int my_stop = mine.stop;
 
+  // Keys this workgroup's tiles need.
   int load_stop = kv_begin;
-  for (int t = 0; t < n_tiles; ++t) {
+  for (int t = tile_base; t < n_tiles && t < tile_base + p.tiles_per_wg; ++t) {
     const int *e = it + 4 + kTileInts * t;
     if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
   }
@@ -429,7 +445,14 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     if (t + kLead < tiles)
       gather(t + kLead, k_ring + ((t + kLead) % kStages) * kStageBytes,
              v_ring + ((t + kLead) % kStages) * kStageBytes);
-    const unsigned long long valid_bits = tile_valid[t];
+    // readfirstlane returns int: each half goes through unsigned so that the
+    // low half is not sign-extended into the high one.
+    const unsigned long long valid_bits_lds = tile_valid[t];
+    const unsigned valid_lo =
+        static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(valid_bits_lds))));
+    const unsigned valid_hi = static_cast<unsigned>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(valid_bits_lds >> 32))));
+    const unsigned long long valid_bits = (static_cast<unsigned long long>(valid_hi) << 32) | valid_lo;
     if (valid_bits != ~0ull) {
       // Zero the V rows of tokens without a valid slot (0 * Inf would be NaN).
       for (int c = tid; c < kTile * kChunksPerRow; c += kM32Threads)
@@ -477,15 +500,10 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       if (batch + 1 < kKSteps / 2) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // next batch's reads
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // this batch's MFMAs
     }
+    // Tiles that every query of the wave sees whole (the common case) skip the
+    // mask: a scalar branch, since `whole` is wave-uniform.
     const bool whole = valid_bits == ~0ull && t0 + kTile <= wave_unmasked;
-    float tile_max = -INFINITY;
-    if (whole) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[kb][r]);
-      if (!q_ok) tile_max = -INFINITY;
-    } else {
+    if (!whole) {
       // Register r of block kb holds token 32 kb + 8 (r / 4) + 4 h + r % 4:
       // visible iff at or below the lane's limit and its slot is valid.
       const int limit = q_ok ? min(my_stop - 1, my_pos) - t0 - 4 * h : -1;
@@ -497,10 +515,15 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
           const int rel = 32 * kb + 8 * (r / 4) + r % 4;
           const bool visible = rel <= limit && ((lane_bits >> rel) & 1ull) != 0;
           s[kb][r] = visible ? s[kb][r] : -INFINITY;
-          tile_max = fmaxf(tile_max, s[kb][r]);
         }
       }
     }
+    float tile_max = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[kb][r]);
+    if (!q_ok) tile_max = -INFINITY;
     {
       unsigned a = __builtin_bit_cast(unsigned, tile_max), b = a;
       permlane32_swap(a, b);
@@ -793,16 +816,21 @@ int launch_attention(const ll_repair_attention_args *a, float *ws, long long ws_
   p.hkv = static_cast<int>(a->num_kv_heads);
   p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
   // A workgroup holds every (tile, head) pair of its item when the waves
-  // allow, else the heads are split over several workgroups per KV head.
-  const int head_room = max_pairs(static_cast<int>(a->head_dim)) / tiles_per_item(p.group);
-  p.heads_per_wg = p.group < head_room ? p.group : head_room;
+  // allow; else the heads (MQA-like groups) or the tiles (head dim 256, which
+  // holds half the pairs) are split over several workgroups per KV head.
+  const int pairs = max_pairs(static_cast<int>(a->head_dim));
+  const int item_tiles = tiles_per_item(p.group);
+  p.heads_per_wg = p.group < pairs ? p.group : pairs;
   p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
+  p.tiles_per_wg = std::max(1, std::min(item_tiles, pairs / p.heads_per_wg));
+  p.tile_chunks = (item_tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
   p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
   p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
 
-  if (a->num_kv_heads * p.head_chunks > 65535)
+  if (a->num_kv_heads * p.head_chunks * p.tile_chunks > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
-  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.head_chunks));
+  const dim3 grid(static_cast<unsigned>(a->num_items),
+                  static_cast<unsigned>(a->num_kv_heads * p.head_chunks * p.tile_chunks));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
     if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);

@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -268,7 +268,7 @@ class RepairAttentionArgs(ctypes.Structure):
     ]
 
 
-REPAIR_ITEM_INTS = 24
+REPAIR_ITEM_INTS = 84
 REPAIR_TILE_INTS = 5   # per tile of an item: first query, lowest position, count, partial, key end
 REPAIR_COMBINE_INTS = 4
 

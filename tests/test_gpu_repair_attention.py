@@ -95,6 +95,13 @@ CASES = [
     ("head_dim256_group2", 8, 4, 256, [(10, 40), (600, 616)], 2048, 0, None),
     ("head_dim256_group7_split", 28, 4, 256, [(1500, 1520)], 4096, 512, None),
     ("head_dim256_mqa_group20", 20, 1, 256, [(300, 345)], 2048, 0, None),
+    # Small groups: an item holds up to 16 / G tiles (MHA: 16).  At head dim
+    # 256 (8 pairs per workgroup) an item's tiles are split over workgroups.
+    ("mha_thirteen_tiles", 8, 8, 128, [(100, 300)], 4096, 0, None),
+    ("mha_tiles_with_forced_splits", 4, 4, 64, [(40, 60), (600, 900)], 4096, 256, None),
+    ("group2_eight_tiles", 16, 8, 128, [(10, 150)], 2048, 0, None),
+    ("head_dim256_mha_tile_split", 4, 4, 256, [(50, 250)], 4096, 0, None),
+    ("head_dim256_group3_tile_split", 12, 4, 256, [(30, 130)], 2048, 512, None),
 ]
 
 

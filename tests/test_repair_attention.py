@@ -133,7 +133,7 @@ def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
         cursor += count
     items, combine, positions, info = _plan(rows, q_heads, kv_heads, split)
     T = _native.REPAIR_TILE_INTS
-    per_item = max(1, min(4, 16 // (q_heads // kv_heads)))
+    per_item = max(1, min(16, 16 // (q_heads // kv_heads)))  # 16 (tile, head) pairs per workgroup
     assert info.split_tokens % 64 == 0 and (split == 0 or info.split_tokens == split)
     # The positions table holds every query's logical position.
     position, request = np.zeros(cursor, np.int64), np.zeros(cursor, np.int64)
@@ -143,6 +143,8 @@ def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
     assert info.num_queries == cursor and positions.tolist() == position.tolist()
     # Every item entry: its tile's keys, a chunk of them, and its partial slot.
     covered = {}
+    if q_heads == kv_heads:  # MHA: one head per KV head, items of more than four tiles
+        assert max(item[3] for item in items.tolist()) > 4
     for item in items.tolist():
         kv_off, kv_begin, kv_end, n_tiles = item[:4]
         assert 1 <= n_tiles <= per_item and kv_begin % 64 == 0 and kv_begin < kv_end
