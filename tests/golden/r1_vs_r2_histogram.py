@@ -16,7 +16,8 @@ enabled.  This script re-rotates the same rows both ways with the oracle (C
 restatement, ``rounding`` FUSED / EAGER) and reports, per case:
 
 * the histogram of |R1 - R2| in ulps of the key dtype (distance between the
-  16-bit patterns in value order; +0 and -0 are 0 apart);
+  16-bit patterns in value order; +0 and -0 are 0 apart), and the share more
+  than 1 ulp apart measured as |a - b| in ulps at max(|a|, |b|);
 * each rounding's error against the exact rotation by the table's entries
   (fp64): the share of elements within 1/2 ulp of the exact value
   (correctly rounded), and the largest and mean error in ulps of the pair's
@@ -124,6 +125,10 @@ def histogram_case(key_dtype: int, cache_dtype: int, distribution: str, seed: in
         inside = (apart >= low) if high is None else ((apart >= low) & (apart <= high))
         buckets[label] = int(np.count_nonzero(inside))
     to_f32 = ko.bf16_bits_to_f32 if key_dtype == ko.BF16 else ko.f16_bits_to_f32
+    # The same distance measured as |a - b| in ulps at max(|a|, |b|): a pair
+    # apart by one step across a power of two counts as half an ulp or one.
+    a, b = to_f32(r1).astype(np.float64).reshape(-1), to_f32(r2).astype(np.float64).reshape(-1)
+    at_larger = np.abs(a - b) / _ulp(np.maximum(np.abs(a), np.abs(b)), key_dtype)
     exact = _exact(to_f32(rows), local, global_, ko.cache_to_f32(cache, cache_dtype))
     # A rotation keeps each pair's norm: errors are also measured in ulps of
     # it, which cancellation in one element of the pair does not inflate.
@@ -145,6 +150,8 @@ def histogram_case(key_dtype: int, cache_dtype: int, distribution: str, seed: in
         "share_differing": round(1.0 - buckets["0"] / total, 6),
         "share_more_than_1_ulp": round(1.0 - (buckets["0"] + buckets["1"]) / total, 6),
         "max_ulp_apart": int(apart.max()),
+        "share_more_than_1_ulp_at_larger": round(float(np.mean(at_larger > 1.0 + 1e-9)), 6),
+        "max_ulp_at_larger": round(float(at_larger.max()), 3),
         "error_vs_exact": errors,
     }
 
@@ -166,7 +173,8 @@ if __name__ == "__main__":
     OUTPUT.write_text(json.dumps(result, indent=1) + "\n")
     for case in result["cases"]:
         print(f"{case['case']:20s} {case['k_distribution']:17s} differ {case['share_differing']:.4f} "
-              f">1ulp {case['share_more_than_1_ulp']:.4f} max {case['max_ulp_apart']}  "
+              f">1ulp {case['share_more_than_1_ulp']:.4f} max {case['max_ulp_apart']} "
+              f"(at larger: >1 {case['share_more_than_1_ulp_at_larger']:.4f} max {case['max_ulp_at_larger']})  "
               f"R1 exact {case['error_vs_exact']['R1']['correctly_rounded_share']:.4f} "
               f"(max {case['error_vs_exact']['R1']['max_pair_norm_ulps']})  "
               f"R2 exact {case['error_vs_exact']['R2']['correctly_rounded_share']:.4f} "
