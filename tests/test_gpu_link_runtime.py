@@ -403,3 +403,66 @@ def test_executor_counts_tokens_skipped_for_bad_slots(gpu_device):
     resolve_link_plan(registry.get_legolink_block_tokens, [1, 2, 3], plan)
     executor.prepare_link(pool, destination, plan, boundary_repair_aware=False).launch()
     assert executor.skipped_rows() == 0
+
+
+class _ScaledRotary:
+    """A model rotary module with linear position scaling (row p holds the
+    angles of p / scale): its table grows through its own method, as sglang's
+    rotary embeddings do."""
+
+    def __init__(self, rows, rotary_dim, theta, scale, device):
+        self.rotary_dim, self.is_neox_style = rotary_dim, True
+        self.theta, self.scale, self.device, self.grown_to = theta, scale, device, []
+        self.cos_sin_cache = self._table(rows)
+
+    def _table(self, rows):
+        inv_freq = 1.0 / self.theta ** (torch.arange(0, self.rotary_dim, 2, dtype=torch.float32) / self.rotary_dim)
+        angles = torch.outer(torch.arange(rows, dtype=torch.float32) / self.scale, inv_freq)
+        return torch.cat((angles.cos(), angles.sin()), dim=-1).to(self.device)
+
+    def _ensure_cos_sin_cache_length(self, needed_max_pos):
+        if needed_max_pos >= self.cos_sin_cache.shape[0]:
+            self.grown_to.append(needed_max_pos)
+            self.cos_sin_cache = self._table(needed_max_pos + 1)
+
+
+def test_link_grows_a_model_rotary_table_through_the_module(gpu_device):
+    """The executor given a model's rotary module: a link past the end of its
+    table grows it through the module (pic_runtime.py:5051-5053), keeping the
+    module's scaling, and the link is bit-exact against the oracle on the
+    grown table."""
+
+    report("rotary module growth: 2 blocks, positions up to 1099, table of 300 rows, scale 2")
+    layers, heads, dim, slots = 3, 4, 128, 4096
+    rng = np.random.default_rng(12)
+    generator = torch.Generator(device=gpu_device).manual_seed(12)
+    pool = KVPool([torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
+                   for _ in range(layers)],
+                  [torch.randn(slots, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
+                   for _ in range(layers)])
+    perm = rng.permutation(slots)
+    registry = LegoLinkBlockRegistry()
+    registry.register_legolink_block("a", list(range(200)), torch.from_numpy(perm[:200]).to(gpu_device))
+    registry.register_legolink_block("b", list(range(300)), torch.from_numpy(perm[200:500]).to(gpu_device))
+    destination = torch.from_numpy(perm[500:1600]).to(gpu_device)
+    plan = {"cache_keys": ["a", "b"],
+            "block_ranges": [{"start_token": 0, "end_token": 200}, {"start_token": 800, "end_token": 1100}]}
+    module = _ScaledRotary(300, dim, 1e6, 2.0, gpu_device)
+    executor = KVLinkExecutor(registry, module, end_layer=layers, fused_mode="required")
+    before_k = [bits(k) for k in pool.k_buffer]
+    before_v = [bits(v) for v in pool.v_buffer]
+    executor.copy_linked_kv(pool, destination, plan)
+    torch.cuda.synchronize(gpu_device)
+    assert module.grown_to and module.cos_sin_cache.shape[0] >= 1100
+    assert executor.rotary_by_layer[0].cos_sin_cache is module.cos_sin_cache
+    executor.check_skipped_rows()
+    src = perm[:500]
+    positions = np.concatenate([np.arange(200), np.arange(800, 1100)])
+    local = np.concatenate([np.arange(200), np.arange(300)])
+    dst = perm[500:1600][positions]
+    want_k, want_v = ko.link_pool(before_k, before_v, src, dst, local, positions,
+                                  module.cos_sin_cache.cpu().numpy(), key_dtype=ko.BF16, cache_dtype=ko.F32,
+                                  rotary_dim=dim, neox=True, prefix=200)
+    for layer in range(layers):
+        assert np.array_equal(bits(pool.k_buffer[layer]), want_k[layer]), f"K layer {layer}"
+        assert np.array_equal(bits(pool.v_buffer[layer]), want_v[layer]), f"V layer {layer}"
