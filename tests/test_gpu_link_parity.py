@@ -426,7 +426,7 @@ def test_full_size_workload_generic_kernel(gpu_device):
     assert result["mismatches"] == 0
 
 
-@pytest.mark.parametrize("name", ["c2", "c5"])
+@pytest.mark.parametrize("name", ["c2", "c5", "c4"])
 def test_full_size_link_as_benched(gpu_device, name):
     """The exact link bench.py times: the executor with repair rows left out of
     the device-built maps, non-temporal row loads, fused rounding."""
@@ -436,7 +436,7 @@ def test_full_size_link_as_benched(gpu_device, name):
     assert result["launch"]["stream_source_rows"] and result["launch"]["kernel"] == "vector"
 
 
-@pytest.mark.parametrize("name", ["c2", "c5"])
+@pytest.mark.parametrize("name", ["c2", "c5", "c4"])
 def test_full_size_eager_link(gpu_device, name):
     """The reference's default link (fused mode off: its torch path's rounding)
     through the executor at full size."""
