@@ -126,7 +126,12 @@ def cpu_baseline(workload, args) -> dict:
         lengths.append(length)
         total += length
     shape = workload.shape
-    slots = 4 * total
+    # The workload's own pool when the sample is the whole workload and the
+    # pool fits in 40 GB of host memory (c2: 262,144 slots, 15 GB); else a
+    # pool four times the sample.
+    pool_bytes = workload.num_slots * shape.layers * 2 * shape.kv_heads * shape.head_dim * 2
+    whole = len(lengths) == len(workload.block_lengths)
+    slots = workload.num_slots if whole and pool_bytes <= 40e9 else 4 * total
     sample = scaled_single_request(shape=shape, num_slots=slots, block_lengths=lengths,
                                    imp_per_seam=int(workload.notes.get("imp_per_seam", 16)),
                                    delta_range=None, seed=workload.seed, name="cpu_sample")
