@@ -532,8 +532,8 @@ def cpu_attention_baseline(spans, query, key, value, q_heads: int, head_dim: int
 def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures the link step on one GPU only; this build runs no multi-GPU "
-              "configuration (the link shards by KV head / request with no exchange step).",
+        print("bench.py measures the link step on one GPU only; there is no multi-GPU "
+              "configuration to run (the link shards by KV head / request with no exchange step).",
               file=sys.stderr)
         return 2
     if args.copy_calibration:

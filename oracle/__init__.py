@@ -1,7 +1,7 @@
 """CPU oracle of the LegoLink KV link step.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
-CPU-baseline leg may import anything here, and only as the checker (or, for
+CPU-baseline leg may import anything here, and only to check results (or, for
 bench.py, as the timed CPU baseline).  The product package ``legolink_amd``
 never imports it.
 

@@ -1,7 +1,7 @@
 """CPU oracle of the sparse repair attention.
 
-TEST INFRASTRUCTURE ONLY: only tests/ may import this module, as the checker
-of the repair attention kernel.  The product path never calls it.
+TEST INFRASTRUCTURE ONLY: only tests/ may import this module, to check the
+repair attention kernel.  The product path never calls it.
 
 Restates, in float64 numpy:
 

@@ -1,7 +1,7 @@
 """CPU oracle for the LegoLink KV link step.
 
 TEST INFRASTRUCTURE ONLY: only tests/, __graft_entry__.smoke() and bench.py's
-CPU-baseline leg may import this module, and only as the checker.  The product
+CPU-baseline leg may import this module, and only to check results.  The product
 path (legolink_amd) never calls it.
 
 Two independent restatements of the per-token K arithmetic of the reference,

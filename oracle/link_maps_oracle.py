@@ -1,7 +1,7 @@
 """CPU oracle of a link's token maps.
 
-TEST INFRASTRUCTURE ONLY: only tests/ may import this module, as the checker
-of the device map builder.  The product path never calls it.
+TEST INFRASTRUCTURE ONLY: only tests/ may import this module, to check the
+device map builder.  The product path never calls it.
 
 Restates, block by block in plan order, the map construction of
 ``_copy_linked_kv_batched_blocks``

@@ -1,8 +1,8 @@
 /*
  * ll_oracle.c - CPU restatement of the LegoLink KV link arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP kernels are compared
- * against; only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
+ * TEST INFRASTRUCTURE ONLY.  The HIP kernels are compared against this
+ * restatement; only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
  * leg may load it.  It is never part of the product path.
  *
  * What it restates (reference = Nyannyan222/sglang-Legolink):
