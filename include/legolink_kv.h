@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 12
+#define LL_ABI_VERSION 13
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -402,15 +402,16 @@ typedef struct ll_link_maps_args {
  *   (consecutive rows of one request -- contiguous query_index, same
  *   kv_offset -- share a tile, so short repair spans fill it; rows must not
  *   overlap), writes every query's logical position into the positions
- *   table, groups consecutive tiles of one request into work items
- *   that share every staged K/V tile (as many tiles as 16 (tile, query head)
- *   pairs allow: 16 for one query head per KV head, 2 for 7 or 8, 1 above
- *   8), splits
- *   long KV ranges into chunks of
+ *   table, cuts the (tile, query head) pairs of each run of consecutive tiles
+ *   of one request (tile-major: G pairs per tile) into work items of 16
+ *   consecutive pairs that share every staged K/V tile (a window may start
+ *   or end inside a tile, so groups that do not divide 16 still fill every
+ *   item), splits long KV ranges into chunks of
  *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
  *   from a model of the device's workgroup rounds), and writes the item and
  *   combine tables; the caller copies them to the device once and reuses them
- *   for every layer.  Call it with NULL tables to size them.
+ *   for every layer.  Call it with NULL tables to size them.  num_q_heads is
+ *   at most 65535.
  *   ll_repair_attention runs one layer; it takes tables made by this plan
  *   (items over more than 4096 keys are not computed) and num_slots < 2^31.
  *
@@ -430,7 +431,7 @@ typedef struct ll_repair_row {
 } ll_repair_row;
 
 typedef struct ll_repair_attention_plan_info {
-  int64_t num_items;               /* int32 [num_items, 84] work items (ABI 12) */
+  int64_t num_items;               /* int32 [num_items, 86] work items (ABI 13) */
   int64_t num_combine;             /* int32 [num_combine, 4] combine items */
   int64_t workspace_items;         /* partial results (see ll_repair_attention_args.workspace) */
   int64_t split_tokens;            /* KV tokens per work item (the plan's choice when 0 was asked) */

@@ -2,18 +2,20 @@
 // repair rows over the linked KV, read through each request's slot list.
 //
 // Work decomposition (planned on the host by ll_repair_attention_plan):
-//   item = up to 16 / G 16-query tiles of one request (consecutive repair
-//   rows; G query heads share one KV head; at most 16 tiles, at least 1) and
+//   The 16-query tiles of one request (consecutive repair rows) form a run;
+//   G query heads share one KV head, so a run of n tiles has n * G (query
+//   tile, query head) pairs, numbered tile-major: pair f is tile f / G, query
+//   head f % G of the KV head.  The run's pairs are cut into windows of 16
+//   consecutive pairs (the last may be shorter), so a window may start or end
+//   inside a tile: with G = 7, windows of 16 pairs keep every wave busy where
+//   whole tiles (2 x 7 = 14 pairs) would leave one of eight waves idle.
+//   item = one window (its tiles, at most 16, and its first pair's head) and
 //   a KV range [kv_begin, kv_end) of logical positions; long ranges are
 //   split and the partial results merged by a combine pass.
-//   workgroup = (item, KV head); the item's (query tile, query head) pairs
-//   -- pair n is query tile n / G, query head hk * G + n % G -- are spread
-//   over its waves, so each K/V tile staged in LDS serves every query tile
-//   and head of the item.  A workgroup holds P = 16 pairs (8 for head dim
-//   256); with more than P query heads per KV head, items have one tile and
-//   each KV head gets ceil(G / P) workgroups of P heads, and where an item's
-//   tiles times G exceed P (head dim 256) its tiles are split over several
-//   workgroups the same way.
+//   workgroup = (item, KV head); the window's pairs are spread over its
+//   waves, so each K/V tile staged in LDS serves every pair of the window.
+//   A workgroup holds P = 16 pairs (8 for head dim 256, whose windows take
+//   two workgroups per KV head).
 //
 // Per 64-token KV tile:
 //   1. gather the tile's K and V rows of this KV head into LDS by slot;
@@ -64,16 +66,18 @@ typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 constexpr int kWave = 64;
 constexpr int kQueries = 16;  // queries per item: one MFMA column tile
 constexpr int kTile = 64;     // KV tokens per LDS tile
-// 16-query tiles per work item: as many (tile, query head) pairs as a
-// workgroup of head dim 64 or 128 holds, so that MHA (one query head per KV
-// head) fills its waves with 16 tiles.
+constexpr int kMaxPairs = 16;  // (query tile, query head) pairs per window (and per workgroup at head dims 64, 128)
+// 16-query tiles a window touches: 16 for one query head per KV head (MHA),
+// at most 9 for larger groups.
 constexpr int kMaxTiles = 16;
-// kv_offset, kv_begin, kv_end, tiles, then per tile (first query, lowest
-// position, query count (0: absent), partial slot (-1: none), key end).
+// kv_offset, kv_begin, kv_end, tiles, the window's first pair (its head in
+// the first tile, 0 .. G - 1) and its pair count (1 .. 16), then per tile
+// (first query, lowest position, query count (0: absent), partial slot (-1:
+// none), key end).
+constexpr int kItemHeader = 6;
 constexpr int kTileInts = 5;
-constexpr int kItemInts = 4 + kTileInts * kMaxTiles;  // 84
+constexpr int kItemInts = kItemHeader + kTileInts * kMaxTiles;  // 86
 constexpr int kCombineInts = 4;
-constexpr int kMaxPairs = 16;  // (query tile, query head) pairs per workgroup (head dims 64 and 128)
 
 int fail(int code, const char *fmt, ...) {
   va_list ap;
@@ -100,10 +104,7 @@ struct AttnParams {
   int hq;
   int hkv;
   int group;
-  int heads_per_wg;  // query heads of a KV head that one workgroup computes
-  int head_chunks;   // head groups per (item, KV head): group / heads_per_wg, rounded up
-  int tiles_per_wg;  // query tiles of an item that one workgroup computes
-  int tile_chunks;   // tile groups per (item, KV head): tiles per item / tiles_per_wg, rounded up
+  int pair_chunks;   // workgroups per (item, KV head): 16 / (pairs per workgroup)
   int slots64;
   float scale_log2;
 };
@@ -139,12 +140,6 @@ struct F16 {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, kOnes), acc, false);
   }
 };
-
-// Query tiles per work item for a GQA group: as many as 16 pairs hold.
-__host__ __device__ inline int tiles_per_item(int group) {
-  const int tiles = kMaxPairs / group;
-  return tiles < 1 ? 1 : (tiles > kMaxTiles ? kMaxTiles : tiles);
-}
 
 __device__ inline long long slot_at(const AttnParams &p, long long i) {
   return p.slots64 ? static_cast<const long long *>(p.slots)[i]
@@ -287,16 +282,19 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   __shared__ int slot_lds[kDmaMaxRange];
   __shared__ unsigned long long tile_valid[kRangeTiles];
 
+  constexpr int kPairs = max_pairs(D);
   const int *it = p.items + static_cast<long long>(blockIdx.x) * kItemInts;
   const int kv_off = it[0], kv_begin = it[1], kv_end = it[2], n_tiles = it[3];
-  // blockIdx.y = (KV head, head group, tile group).
-  const int chunks_per_head = p.head_chunks * p.tile_chunks;
-  const int hk = blockIdx.y / chunks_per_head;
-  const int head_base = (blockIdx.y % chunks_per_head) / p.tile_chunks * p.heads_per_wg;
-  const int tile_base = (blockIdx.y % p.tile_chunks) * p.tiles_per_wg;
+  const int pair_first = it[4], pair_count = it[5];
+  // blockIdx.y = (KV head, pair chunk): this workgroup's pairs of the window
+  // are [wg_first, wg_end), counted from the item's first tile.
+  const int hk = blockIdx.y / p.pair_chunks;
+  const int wg_first = pair_first + static_cast<int>(blockIdx.y % p.pair_chunks) * kPairs;
+  const int wg_end = min(pair_first + pair_count, wg_first + kPairs);
   if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
       kv_end - kv_begin > kDmaMaxRange || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
-      hk >= p.hkv)
+      hk >= p.hkv || pair_first < 0 || pair_first >= p.group || pair_count < 1 || pair_count > kMaxPairs ||
+      wg_first >= wg_end || (wg_end - 1) / p.group >= n_tiles)
     return;
 
   const int tid = threadIdx.x;
@@ -317,18 +315,18 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   };
   auto pair_info = [&](int pair) {
     PairInfo r;
-    const int tile_in_wg = pair / p.heads_per_wg;
-    const int tile = tile_base + tile_in_wg;
-    const int head = head_base + pair % p.heads_per_wg;
-    const int *e = it + 4 + kTileInts * (tile < kMaxTiles ? tile : 0);
+    const int flat = wg_first + pair;  // pair index in the window's tiles
+    const int tile = flat / p.group;
+    const int head = flat - tile * p.group;
+    const bool in_window = flat < wg_end;  // and so tile < n_tiles (checked above)
+    const int *e = it + kItemHeader + kTileInts * (in_window ? tile : 0);
     r.q_index = e[0];
     r.q_pos = e[1];
     r.q_count = e[2];
     r.partial = e[3];
     const int needed = e[4];
     r.hq = hk * p.group + head;
-    r.computes = tile_in_wg < p.tiles_per_wg && tile < n_tiles && head < p.group && r.q_count >= 1 &&
-                 r.q_count <= kQueries && r.q_index >= 0 &&
+    r.computes = in_window && r.q_count >= 1 && r.q_count <= kQueries && r.q_index >= 0 &&
                  static_cast<long long>(r.q_index) + r.q_count <= p.num_queries && r.q_pos >= 0 &&
                  needed > r.q_pos && (r.partial == -1 || (r.partial >= 0 && r.partial < p.ws_items));
     r.stop = r.computes ? min(kv_end, needed) : kv_begin;
@@ -348,8 +346,8 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
 
   // Keys this workgroup's tiles need.
   int load_stop = kv_begin;
-  for (int t = tile_base; t < n_tiles && t < tile_base + p.tiles_per_wg; ++t) {
-    const int *e = it + 4 + kTileInts * t;
+  for (int t = wg_first / p.group; t <= (wg_end - 1) / p.group; ++t) {
+    const int *e = it + kItemHeader + kTileInts * t;
     if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
   }
   const int range = load_stop - kv_begin;
@@ -815,22 +813,15 @@ int launch_attention(const ll_repair_attention_args *a, float *ws, long long ws_
   p.hq = static_cast<int>(a->num_q_heads);
   p.hkv = static_cast<int>(a->num_kv_heads);
   p.group = static_cast<int>(a->num_q_heads / a->num_kv_heads);
-  // A workgroup holds every (tile, head) pair of its item when the waves
-  // allow; else the heads (MQA-like groups) or the tiles (head dim 256, which
-  // holds half the pairs) are split over several workgroups per KV head.
-  const int pairs = max_pairs(static_cast<int>(a->head_dim));
-  const int item_tiles = tiles_per_item(p.group);
-  p.heads_per_wg = p.group < pairs ? p.group : pairs;
-  p.head_chunks = (p.group + p.heads_per_wg - 1) / p.heads_per_wg;
-  p.tiles_per_wg = std::max(1, std::min(item_tiles, pairs / p.heads_per_wg));
-  p.tile_chunks = (item_tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
+  // A workgroup holds a whole window of 16 pairs, or half of it at head dim
+  // 256 (two workgroups per item and KV head).
+  p.pair_chunks = kMaxPairs / max_pairs(static_cast<int>(a->head_dim));
   p.slots64 = a->kv_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
   p.scale_log2 = static_cast<float>(a->softmax_scale * 1.4426950408889634);  // log2(e)
 
-  if (a->num_kv_heads * p.head_chunks * p.tile_chunks > 65535)
+  if (a->num_kv_heads * p.pair_chunks > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
-  const dim3 grid(static_cast<unsigned>(a->num_items),
-                  static_cast<unsigned>(a->num_kv_heads * p.head_chunks * p.tile_chunks));
+  const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.pair_chunks));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
   if (a->head_dim == 128) {
     if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
@@ -884,12 +875,13 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
                 kTile, kDmaMaxRange);
   constexpr int64_t kIntMax = 0x7fffffff;
-  const int per_item = tiles_per_item(static_cast<int>(num_q_heads / num_kv_heads));
+  if (num_q_heads > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be at most 65535");
+  const int64_t group = num_q_heads / num_kv_heads;
   // 16-query tiles in row order.  Consecutive rows of one request (the next
   // row's queries follow the last one's, same kv_offset) share a tile, so
   // short repair spans fill it; a tile records its lowest position and its
-  // key end (highest position + 1).  Consecutive tiles of one request share
-  // work items, up to per_item at a time.
+  // key end (highest position + 1).
   struct Tile { int64_t q_index, pos, count, kv_offset, needed; };
   int64_t num_queries = 0;
   for (int64_t r = 0; r < num_rows; ++r) {
@@ -926,11 +918,57 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     }
   }
   const int64_t n_tiles = static_cast<int64_t>(tiles.size());
-  // Groups of up to per_item consecutive tiles of one request.
-  auto group_end = [&](int64_t first) {
-    int64_t last = first + 1;
-    while (last < n_tiles && last - first < per_item && tiles[last].kv_offset == tiles[first].kv_offset) ++last;
-    return last;
+  // Windows: the (tile, query head) pairs of each run of consecutive tiles of
+  // one request, tile-major, cut into windows of at most kMaxPairs.  A window
+  // covers tiles [first, last), from head pair_first of its first tile,
+  // pair_count pairs, and costs its workgroup the keys of its furthest tile.
+  // Below 16 query heads per KV head the cut points are chosen by dynamic
+  // programming over the run's pairs, minimising the summed cost (key tiles
+  // of each window's furthest tile plus a per-item overhead), so windows
+  // cross tile boundaries freely: 16 pairs per workgroup where whole tiles of
+  // 7 heads would fill 14.  From 16 heads up every tile is cut on its own.
+  struct Window { int64_t first, last, pair_first, pair_count; };
+  std::vector<Window> windows;
+  std::vector<double> cost;
+  std::vector<int64_t> from;
+  for (int64_t run = 0; run < n_tiles;) {
+    int64_t run_end = run + 1;
+    while (run_end < n_tiles && tiles[run_end].kv_offset == tiles[run].kv_offset) ++run_end;
+    if (group >= kMaxPairs) {
+      for (int64_t t = run; t < run_end; ++t)
+        for (int64_t f = 0; f < group; f += kMaxPairs)
+          windows.push_back(Window{t, t + 1, f, group - f < kMaxPairs ? group - f : kMaxPairs});
+    } else {
+      const int64_t n = (run_end - run) * group;  // pairs of the run, below 16 per tile
+      cost.assign(static_cast<size_t>(n + 1), 0.0);
+      from.assign(static_cast<size_t>(n + 1), 0);
+      for (int64_t i = 1; i <= n; ++i) {
+        double best = -1.0;
+        int64_t furthest = 0;
+        for (int64_t j = i - 1; j >= 0 && j >= i - kMaxPairs; --j) {  // window [j, i)
+          const int64_t needed = tiles[run + j / group].needed;
+          furthest = needed > furthest ? needed : furthest;
+          const double c = cost[j] + static_cast<double>((furthest + kTile - 1) / kTile) + kItemOverheadTiles;
+          if (best < 0.0 || c <= best) {  // ties: the longer window
+            best = c;
+            from[i] = j;
+          }
+        }
+        cost[i] = best;
+      }
+      const size_t run_first = windows.size();
+      for (int64_t i = n; i > 0; i = from[i]) {
+        const int64_t j = from[i];
+        windows.push_back(Window{run + j / group, run + (i - 1) / group + 1, j % group, i - j});
+      }
+      std::reverse(windows.begin() + static_cast<std::ptrdiff_t>(run_first), windows.end());
+    }
+    run = run_end;
+  }
+  auto window_needed = [&](const Window &w) {
+    int64_t needed = 0;
+    for (int64_t t = w.first; t < w.last; ++t) needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+    return needed;
   };
   int64_t split = split_tokens;
   if (split == 0) {
@@ -945,15 +983,15 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     for (const int64_t candidate : kCandidates) {
       const double estimate = plan_cost_estimate(
           candidate, num_kv_heads, num_q_heads, [&](auto &&visit) {
-            for (int64_t first = 0; first < n_tiles; first = group_end(first)) {
-              const int64_t last = group_end(first);
-              int64_t needed = 0, partials = 0;
-              for (int64_t t = first; t < last; ++t) {
-                needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+            int64_t next_tile = 0;  // a tile's partials count with the first window that holds it
+            for (const Window &w : windows) {
+              int64_t partials = 0;
+              for (int64_t t = w.first > next_tile ? w.first : next_tile; t < w.last; ++t) {
                 const int64_t chunks = (tiles[t].needed + candidate - 1) / candidate;
                 partials += chunks > 1 ? chunks : 0;
               }
-              visit(needed, partials);
+              next_tile = w.last > next_tile ? w.last : next_tile;
+              visit(window_needed(w), partials);
             }
           });
       if (best < 0.0 || estimate <= best) {
@@ -962,38 +1000,32 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
       }
     }
   }
+  // Each tile's key chunks, and the partial slots and combine item of a tile
+  // with more than one.
   int64_t n_items = 0, n_combine = 0, n_partial = 0;
-  int rc = LL_OK;
-  for (int64_t first = 0; first < n_tiles && rc == LL_OK; first = group_end(first)) {
-    const int64_t last = group_end(first);
-    int64_t needed = 0;
-    int64_t base[kMaxTiles];
-    int64_t chunks[kMaxTiles];
-    for (int64_t t = first; t < last; ++t) {
-      needed = tiles[t].needed > needed ? tiles[t].needed : needed;
-      chunks[t - first] = (tiles[t].needed + split - 1) / split;
-      base[t - first] = -1;
-      if (chunks[t - first] > 1) {
-        if (combine != nullptr) {
-          if (n_combine >= combine_capacity) {
-            rc = fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
-                      static_cast<long long>(combine_capacity));
-            break;
-          }
-          int32_t *ci = combine + n_combine * kCombineInts;
-          ci[0] = static_cast<int32_t>(tiles[t].q_index);
-          ci[1] = static_cast<int32_t>(tiles[t].count);
-          ci[2] = static_cast<int32_t>(n_partial);
-          ci[3] = static_cast<int32_t>(chunks[t - first]);
-        }
-        base[t - first] = n_partial;
-        n_partial += chunks[t - first];
-        ++n_combine;
-      }
+  std::vector<int64_t> chunks(static_cast<size_t>(n_tiles)), base(static_cast<size_t>(n_tiles), -1);
+  for (int64_t t = 0; t < n_tiles; ++t) {
+    chunks[t] = (tiles[t].needed + split - 1) / split;
+    if (chunks[t] < 2) continue;
+    if (combine != nullptr) {
+      if (n_combine >= combine_capacity)
+        return fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
+                    static_cast<long long>(combine_capacity));
+      int32_t *ci = combine + n_combine * kCombineInts;
+      ci[0] = static_cast<int32_t>(tiles[t].q_index);
+      ci[1] = static_cast<int32_t>(tiles[t].count);
+      ci[2] = static_cast<int32_t>(n_partial);
+      ci[3] = static_cast<int32_t>(chunks[t]);
     }
-    if (rc != LL_OK) break;
-    const int64_t group_chunks = (needed + split - 1) / split;
-    for (int64_t s = 0; s < group_chunks; ++s) {
+    base[t] = n_partial;
+    n_partial += chunks[t];
+    ++n_combine;
+  }
+  int rc = LL_OK;
+  for (const Window &w : windows) {
+    const int64_t needed = window_needed(w);
+    const int64_t window_chunks = (needed + split - 1) / split;
+    for (int64_t s = 0; s < window_chunks; ++s) {
       if (items != nullptr) {
         if (n_items >= items_capacity) {
           rc = fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
@@ -1002,22 +1034,25 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
         }
         int32_t *it = items + n_items * kItemInts;
         for (int i = 0; i < kItemInts; ++i) it[i] = 0;
-        it[0] = static_cast<int32_t>(tiles[first].kv_offset);
+        it[0] = static_cast<int32_t>(tiles[w.first].kv_offset);
         it[1] = static_cast<int32_t>(s * split);
         it[2] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
-        it[3] = static_cast<int32_t>(last - first);
-        for (int64_t t = first; t < last; ++t) {
-          int32_t *e = it + 4 + kTileInts * (t - first);
+        it[3] = static_cast<int32_t>(w.last - w.first);
+        it[4] = static_cast<int32_t>(w.pair_first);
+        it[5] = static_cast<int32_t>(w.pair_count);
+        for (int64_t t = w.first; t < w.last; ++t) {
+          int32_t *e = it + kItemHeader + kTileInts * (t - w.first);
           e[0] = static_cast<int32_t>(tiles[t].q_index);
           e[1] = static_cast<int32_t>(tiles[t].pos);
-          const bool present = s < chunks[t - first];  // this chunk holds keys the tile sees
+          const bool present = s < chunks[t];  // this chunk holds keys the tile sees
           e[2] = present ? static_cast<int32_t>(tiles[t].count) : 0;
-          e[3] = !present || chunks[t - first] == 1 ? -1 : static_cast<int32_t>(base[t - first] + s);
+          e[3] = !present || chunks[t] == 1 ? -1 : static_cast<int32_t>(base[t] + s);
           e[4] = static_cast<int32_t>(tiles[t].needed);
         }
       }
       ++n_items;
     }
+    if (rc != LL_OK) break;
   }
   if (rc != LL_OK) return rc;
   if (n_items > kIntMax || n_partial > kIntMax)

@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -268,7 +268,8 @@ class RepairAttentionArgs(ctypes.Structure):
     ]
 
 
-REPAIR_ITEM_INTS = 84
+REPAIR_ITEM_INTS = 86
+REPAIR_ITEM_HEADER = 6  # kv_offset, kv_begin, kv_end, tiles, first pair's head, pair count
 REPAIR_TILE_INTS = 5   # per tile of an item: first query, lowest position, count, partial, key end
 REPAIR_COMBINE_INTS = 4
 
@@ -425,7 +426,7 @@ def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
 
 
 def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_tokens: int = 0):
-    """Host planning: returns (items int32 [n, 24], combine int32 [m, 4],
+    """Host planning: returns (items int32 [n, 86], combine int32 [m, 4],
     positions int32 [num_queries], info)."""
 
     import numpy as np

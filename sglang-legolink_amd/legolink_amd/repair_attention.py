@@ -125,9 +125,8 @@ class RepairAttentionPlan:
     def kv_bytes_read(self) -> int:
         """Bytes of K and V the kernel gathers: each work item reads its KV range
         [kv_begin, kv_end) once per KV head (2-byte elements).  A lower bound
-        where a KV head's (tile, head) pairs take several workgroups (more than
-        16 query heads per KV head, or small groups at head dim 256), each of
-        which gathers the keys its own tiles need."""
+        at head dim 256, where a work item's 16 (tile, head) pairs take two
+        workgroups, each of which gathers the keys its own tiles need."""
 
         items = self.items.view(-1, _native.REPAIR_ITEM_INTS).cpu().numpy().astype(np.int64)
         tokens = int((items[:, 2] - items[:, 1]).sum())

@@ -132,8 +132,8 @@ def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
         rows.append((cursor, start, count, int(rng.integers(0, 3)) * 5000))  # three requests
         cursor += count
     items, combine, positions, info = _plan(rows, q_heads, kv_heads, split)
-    T = _native.REPAIR_TILE_INTS
-    per_item = max(1, min(16, 16 // (q_heads // kv_heads)))  # 16 (tile, head) pairs per workgroup
+    T, H = _native.REPAIR_TILE_INTS, _native.REPAIR_ITEM_HEADER
+    group = q_heads // kv_heads
     assert info.split_tokens % 64 == 0 and (split == 0 or info.split_tokens == split)
     # The positions table holds every query's logical position.
     position, request = np.zeros(cursor, np.int64), np.zeros(cursor, np.int64)
@@ -141,16 +141,19 @@ def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
         position[q_index : q_index + count] = np.arange(start, start + count)
         request[q_index : q_index + count] = kv_off
     assert info.num_queries == cursor and positions.tolist() == position.tolist()
-    # Every item entry: its tile's keys, a chunk of them, and its partial slot.
-    covered = {}
-    if q_heads == kv_heads:  # MHA: one head per KV head, items of more than four tiles
-        assert max(item[3] for item in items.tolist()) > 4
+    # Every item is a window of at most 16 (tile, query head) pairs, tile-major
+    # from head pair_first of its first tile, ending in its last tile; every
+    # pair entry: its tile's keys, a chunk of them, and its partial slot.
+    covered, tiles = {}, set()
     for item in items.tolist():
-        kv_off, kv_begin, kv_end, n_tiles = item[:4]
-        assert 1 <= n_tiles <= per_item and kv_begin % 64 == 0 and kv_begin < kv_end
+        kv_off, kv_begin, kv_end, n_tiles, pair_first, pair_count = item[:H]
+        assert 1 <= n_tiles <= 16 and kv_begin % 64 == 0 and kv_begin < kv_end
+        assert 0 <= pair_first < group and 1 <= pair_count <= 16
+        assert (pair_first + pair_count - 1) // group == n_tiles - 1
         furthest = 0
-        for t in range(n_tiles):
-            q_index, low, q_count, partial, needed = item[4 + T * t : 4 + T * (t + 1)]
+        for f in range(pair_first, pair_first + pair_count):
+            t, head = divmod(f, group)
+            q_index, low, q_count, partial, needed = item[H + T * t : H + T * (t + 1)]
             if q_count == 0:
                 assert partial == -1
                 continue
@@ -159,35 +162,108 @@ def test_plan_covers_every_query_and_key_range_once(split, q_heads, kv_heads):
             assert (request[queries] == kv_off).all()          # one request per tile
             assert low == position[queries].min() and needed == position[queries].max() + 1
             furthest = max(furthest, needed)
-            covered.setdefault((q_index, q_count), []).append((kv_begin, min(kv_end, needed), partial, needed))
+            tiles.add((q_index, q_count, needed))
+            covered.setdefault((q_index, q_count, head), []).append((kv_begin, min(kv_end, needed), partial, needed))
         assert kv_end <= furthest  # an item never loads keys past its last present tile's
     # Tiles partition the queries; consecutive rows of a request share tiles.
     seen = np.zeros(cursor, np.int64)
-    for q_index, q_count in covered:
+    for q_index, q_count, _ in tiles:
         seen[q_index : q_index + q_count] += 1
     assert (seen == 1).all()
-    runs, expected_tiles = [], 0
+    runs = []
     for q_index, start, count, kv_off in rows:
         if runs and runs[-1][0] == kv_off:
             runs[-1][1] += count
         else:
             runs.append([kv_off, count])
-    assert len(covered) == sum((n + 15) // 16 for _, n in runs)
+    run_tiles = [(n + 15) // 16 for _, n in runs]
+    assert len(tiles) == sum(run_tiles)
+    if q_heads == kv_heads:  # MHA: one head per KV head, windows of up to 16 tiles
+        assert max(item[3] for item in items.tolist()) == min(16, max(run_tiles)) > 4
+    # Windows are cut per run, at most 16 pairs each, and cover its pairs once.
+    windows = {(item[H], item[4]): item[5] for item in items.tolist()}
+    assert len(windows) >= sum((n * group + 15) // 16 for n in run_tiles)
+    assert sum(windows.values()) == len(tiles) * group
+    # Every (tile, query head) pair of every tile covers its keys once, in
+    # chunks; its heads share the tile's partial slots.
+    assert len(covered) == len(tiles) * group
     partials = set()
     combine_rows = [tuple(r) for r in combine.tolist()]
-    for (q_index, q_count), ranges in covered.items():
+    slots_of = {}
+    for (q_index, q_count, head), ranges in covered.items():
         ranges.sort()
         needed = ranges[0][3]
         assert ranges[0][0] == 0 and ranges[-1][1] == needed
         assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+        ids = [r[2] for r in ranges]
+        assert slots_of.setdefault((q_index, q_count), ids) == ids
         if len(ranges) == 1:
-            assert ranges[0][2] == -1
+            assert ids == [-1]
         else:
-            ids = [r[2] for r in ranges]
             assert ids == list(range(ids[0], ids[0] + len(ids)))
             partials.update(ids)
             assert (q_index, q_count, ids[0], len(ids)) in combine_rows
     assert len(partials) == info.workspace_items == combine[:, 3].sum()
+
+
+def _windows(items):
+    """(first query of the first tile, tiles, first head, pairs, keys) of each window."""
+    H = _native.REPAIR_ITEM_HEADER
+    spans = {}
+    for item in items.tolist():
+        key = (item[H], item[3], item[4], item[5])
+        spans[key] = max(spans.get(key, 0), item[2])
+    return sorted(key + (end,) for key, end in spans.items())
+
+
+def test_plan_windows_cross_tiles_only_where_the_keys_match():
+    # One 160-query span (10 tiles whose key ends are 16 apart), 7 query heads
+    # per KV head: 70 pairs fit in five windows, four of 16 pairs crossing
+    # tile boundaries, the short one on the tiles with the fewest keys.
+    items, _, _, _ = _plan([(0, 5000, 160, 0)], 28, 4, 4096)
+    assert [w[:4] for w in _windows(items)] == [(0, 1, 0, 6), (0, 4, 6, 16), (48, 3, 1, 16), (80, 3, 3, 16),
+                                               (112, 3, 5, 16)]
+    # Ten 16-query spans 1,000 positions apart: the same cuts.  A window's
+    # cost is its furthest tile's keys, so the short window goes first (116
+    # keys) and each later one ends where the tile-aligned pairs of tiles
+    # (0-1, 2-3, ...) end: 2 + 49 + 80 + 112 + 143 key tiles against 18 + 49 +
+    # 80 + 112 + 143.
+    items, _, _, _ = _plan([(16 * i, 1000 * i + 100, 16, 0) for i in range(10)], 28, 4, 4096)
+    assert _windows(items) == [(0, 1, 0, 6, 116), (0, 4, 6, 16, 3116), (48, 3, 1, 16, 5116),
+                               (80, 3, 3, 16, 7116), (112, 3, 5, 16, 9116)]
+    # 8 query heads per KV head: windows are whole pairs of tiles either way.
+    items, _, _, _ = _plan([(0, 5000, 160, 0)], 64, 8, 4096)
+    assert [w[:4] for w in _windows(items)] == [(32 * i, 2, 0, 16) for i in range(5)]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_plan_windows_minimise_the_modelled_cost(seed):
+    # Brute force over every cut of a short run's pairs into windows of at
+    # most 16: the plan's windows cost the minimum of the planner's model
+    # (key tiles of the window's furthest tile + 3 per window).
+    rng = np.random.default_rng(seed)
+    group = int(rng.choice([3, 5, 7]))
+    n_tiles = 15 // group
+    rows, cursor = [], 0
+    for _ in range(n_tiles):
+        start = int(rng.integers(0, 3000))
+        rows.append((cursor, start, 16, 0))
+        cursor += 16
+    items, _, _, _ = _plan(rows, 4 * group, 4, 4096)
+    needed = [start + 16 for _, start, _, _ in rows]
+    pair_needed = [needed[p // group] for p in range(n_tiles * group)]
+
+    def cost(cuts):
+        bounds = [0, *cuts, len(pair_needed)]
+        return sum(-(-max(pair_needed[a:b]) // 64) + 3 for a, b in zip(bounds, bounds[1:]))
+
+    n = len(pair_needed)
+    best = min(cost([c for c in range(1, n) if mask >> (c - 1) & 1]) for mask in range(1 << (n - 1))
+               if all(b - a <= 16 for a, b in zip([0] + [c for c in range(1, n) if mask >> (c - 1) & 1],
+                                                    [c for c in range(1, n) if mask >> (c - 1) & 1] + [n])))
+    windows = _windows(items)
+    assert sum(pairs for _, _, _, pairs, _ in windows) == n
+    assert sum(-(-end // 64) + 3 for *_, end in windows) == best
 
 
 def test_plan_packs_short_spans_of_one_request_into_tiles():
@@ -196,9 +272,9 @@ def test_plan_packs_short_spans_of_one_request_into_tiles():
     rows = [(0, 100, 8, 0), (8, 300, 8, 0), (16, 500, 8, 0), (24, 700, 8, 0), (32, 40, 8, 9000),
             (48, 60, 4, 9000)]
     items, combine, positions, info = _plan(rows, 28, 4, 4096)
-    T = _native.REPAIR_TILE_INTS
-    tiles = sorted(tuple(item[4 + T * t : 4 + T * (t + 1)]) for item in items.tolist() for t in range(item[3])
-                   if item[4 + T * t + 2])
+    T, H = _native.REPAIR_TILE_INTS, _native.REPAIR_ITEM_HEADER
+    tiles = sorted({tuple(item[H + T * t : H + T * (t + 1)]) for item in items.tolist() for t in range(item[3])
+                    if item[H + T * t + 2]})
     assert tiles == [(0, 100, 16, -1, 308), (16, 500, 16, -1, 708), (32, 40, 8, -1, 48), (48, 60, 4, -1, 64)]
     assert positions[:16].tolist() == list(range(100, 108)) + list(range(300, 308))
 
