@@ -1101,12 +1101,15 @@ int ll_repair_attention_noalloc(const ll_repair_attention_args *a, ll_stream_t s
   if (a->num_items == 0) return LL_OK;
   // Every (partial, query head) block holds 16 queries x (head_dim outputs) and
   // a (maximum, sum) pair per query, in fp32.
+  // workspace_items is bounded before the product, which then stays below
+  // 2^56 (num_q_heads <= 65535 and head_dim <= 256 were checked).
   const long long block_floats = 16 * a->head_dim + 32;
-  const long long needed = a->workspace_items * a->num_q_heads * block_floats * 4;
-  if (a->workspace_items > kScratchBytes || needed > kScratchBytes)
-    return fail(LL_ERR_INVALID_ARGUMENT, "the plan's %lld split partials need %lld bytes; the scratch array "
-                "holds %lld (LL_REPAIR_SCRATCH_BYTES)", static_cast<long long>(a->workspace_items), needed,
-                kScratchBytes);
+  if (a->workspace_items > kScratchBytes ||
+      a->workspace_items * a->num_q_heads * block_floats * 4 > kScratchBytes)
+    return fail(LL_ERR_INVALID_ARGUMENT, "the plan's %lld split partials (%lld query heads, %lld bytes each) "
+                "exceed what the scratch array holds: %lld bytes (LL_REPAIR_SCRATCH_BYTES)",
+                static_cast<long long>(a->workspace_items), static_cast<long long>(a->num_q_heads),
+                block_floats * 4, kScratchBytes);
   if (a->num_combine > 0 && a->workspace_items < 1)
     return fail(LL_ERR_INVALID_ARGUMENT, "split items need workspace_items partial slots");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
