@@ -634,23 +634,46 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
   const int c = threadIdx.x / 16;
   const int part = threadIdx.x % 16;
   if (c >= q_count) return;
-  float big = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < count; ++s) big = fmaxf(big, partial_block<D>(p, first + s, h)[kQueries * D + 2 * c]);
+  // One pass in batches of kBatch partials whose loads are all in flight
+  // together; the running maximum rescales what is summed when a batch
+  // raises it.
+  constexpr int kBatch = 8;
+  float run_max = -INFINITY;
   float total = 0.f;
   f32x4 acc[kPer / 4];
 #pragma unroll
   for (int d = 0; d < kPer / 4; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Unrolled so that several partials' loads are in flight at once.
-#pragma unroll 4
-  for (int s = 0; s < count; ++s) {
-    const float *block = partial_block<D>(p, first + s, h);
-    const float ms = block[kQueries * D + 2 * c];
-    const float w = ms == -INFINITY ? 0.f : exp2f(ms - big);
-    total += block[kQueries * D + 2 * c + 1] * w;
-    const f32x4 *row = reinterpret_cast<const f32x4 *>(block + c * D + part * kPer);
+  for (int s0 = 0; s0 < count; s0 += kBatch) {
+    float ms[kBatch], ls[kBatch];
+    f32x4 rows[kBatch][kPer / 4];
 #pragma unroll
-    for (int d = 0; d < kPer / 4; ++d) acc[d] += w * row[d];
+    for (int i = 0; i < kBatch; ++i) {
+      const int s = min(s0 + i, count - 1);  // past the end: the last partial again, unused
+      const float *block = partial_block<D>(p, first + s, h);
+      ms[i] = block[kQueries * D + 2 * c];
+      ls[i] = block[kQueries * D + 2 * c + 1];
+      const f32x4 *row = reinterpret_cast<const f32x4 *>(block + c * D + part * kPer);
+#pragma unroll
+      for (int d = 0; d < kPer / 4; ++d) rows[i][d] = row[d];
+    }
+    float batch_max = run_max;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (s0 + i < count) batch_max = fmaxf(batch_max, ms[i]);
+    if (batch_max > run_max) {
+      const float scale = run_max == -INFINITY ? 0.f : exp2f(run_max - batch_max);
+      total *= scale;
+#pragma unroll
+      for (int d = 0; d < kPer / 4; ++d) acc[d] *= scale;
+      run_max = batch_max;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float w = s0 + i >= count || ms[i] == -INFINITY ? 0.f : exp2f(ms[i] - run_max);
+      total += ls[i] * w;
+#pragma unroll
+      for (int d = 0; d < kPer / 4; ++d) acc[d] += w * rows[i][d];
+    }
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
   uint16_t *dst = p.out + (static_cast<long long>(q_index + c) * p.hq + h) * D + part * kPer;
