@@ -86,22 +86,32 @@ CASES = [
     ("group8_head_dim64", 16, 2, 64, [(30, 50), (200, 201)], 2048, 0, None),
     ("group1", 8, 8, 128, [(10, 26)], 2048, 0, None),
     ("sharp_softmax", 28, 4, 128, [(3, 40), (300, 333)], 4096, 128, 1.0),
-    # GQA ratios above 8: one tile per item; above 16, several workgroups per KV head.
+    # GQA ratios above 8: windows of 16 pairs hold one tile or part of one;
+    # from 16 heads up each tile's heads take several windows.
     ("group12", 24, 2, 128, [(50, 70), (400, 416)], 2048, 0, None),
     ("mqa_group32", 32, 1, 128, [(100, 133)], 2048, 256, None),
     ("mqa_group71_head_dim64", 71, 1, 64, [(20, 37), (900, 905)], 2048, 0, None),
-    # Head dim 256: at most 8 (tile, head) pairs per workgroup, so 7 heads x 2
-    # tiles take two workgroups, and 20 heads of one tile take three (8, 8, 4).
+    # Head dim 256: 8 (tile, head) pairs per workgroup, so a window of 16
+    # pairs takes two workgroups, and 20 heads of one tile take two windows
+    # (16 and 4).
     ("head_dim256_group2", 8, 4, 256, [(10, 40), (600, 616)], 2048, 0, None),
     ("head_dim256_group7_split", 28, 4, 256, [(1500, 1520)], 4096, 512, None),
     ("head_dim256_mqa_group20", 20, 1, 256, [(300, 345)], 2048, 0, None),
-    # Small groups: an item holds up to 16 / G tiles (MHA: 16).  At head dim
-    # 256 (8 pairs per workgroup) an item's tiles are split over workgroups.
+    # Small groups: a window of 16 pairs holds 16 / G tiles (MHA: 16).  At head
+    # dim 256 (8 pairs per workgroup) a window is split over two workgroups.
     ("mha_thirteen_tiles", 8, 8, 128, [(100, 300)], 4096, 0, None),
     ("mha_tiles_with_forced_splits", 4, 4, 64, [(40, 60), (600, 900)], 4096, 256, None),
     ("group2_eight_tiles", 16, 8, 128, [(10, 150)], 2048, 0, None),
     ("head_dim256_mha_tile_split", 4, 4, 256, [(50, 250)], 4096, 0, None),
     ("head_dim256_group3_tile_split", 12, 4, 256, [(30, 130)], 2048, 512, None),
+    # Groups that do not divide 16: windows start and end inside tiles (7
+    # heads: 16-pair windows over 10 tiles; 5 heads with contiguous spans and
+    # forced splits; head dim 256, two workgroups per window; 3 heads over
+    # short spans sharing tiles).
+    ("group7_windows_cross_tiles", 28, 4, 128, [(200, 360)], 4096, 0, None),
+    ("group5_windows_cross_tiles_split", 20, 4, 128, [(1000, 1100), (1100, 1164)], 4096, 256, None),
+    ("head_dim256_group7_windows", 28, 4, 256, [(300, 400)], 4096, 0, None),
+    ("group3_short_spans_head_dim64", 12, 4, 64, [(s, s + 8) for s in range(100, 2000, 150)], 4096, 0, None),
 ]
 
 
