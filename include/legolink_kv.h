@@ -407,13 +407,13 @@ typedef struct ll_link_maps_args {
  *   consecutive pairs that share every staged K/V tile (a window may start
  *   or end inside a tile, so groups that do not divide 16 still fill every
  *   item), splits long KV ranges into chunks of
- *   split_tokens keys (a multiple of 64, at most 4096; 0 lets the plan choose
+ *   split_tokens keys (a multiple of 64, at most 7680; 0 lets the plan choose
  *   from a model of the device's workgroup rounds), and writes the item and
  *   combine tables; the caller copies them to the device once and reuses them
  *   for every layer.  Call it with NULL tables to size them.  num_q_heads is
  *   at most 65535.
  *   ll_repair_attention runs one layer; it takes tables made by this plan
- *   (items over more than 4096 keys are not computed) and num_slots < 2^31.
+ *   (items over more than 7680 keys are not computed) and num_slots < 2^31.
  *
  * Replaces the FlashInfer block-sparse repair attention of
  * patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py

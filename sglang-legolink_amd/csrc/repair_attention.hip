@@ -187,7 +187,9 @@ __host__ __device__ constexpr int max_pairs(int d) { return d == 256 ? kMaxPairs
 // 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.  The item's
 // slots are read once into LDS (at most kDmaMaxRange of them).
 constexpr int kDmaStages = 4;
-constexpr int kDmaMaxRange = 4096;   // KV tokens per work item on this path
+// KV tokens per work item: their slots fill the LDS the ring leaves (the
+// 4 x 32 KB ring at head dims 128 and 256, 159 KB in all).
+constexpr int kDmaMaxRange = 7680;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Two 16-byte-per-lane gathers into LDS (global_load_lds_dwordx4: lane l's
@@ -710,13 +712,14 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
   std::sort(item_cost.begin(), item_cost.end(), std::greater<double>());
   double makespan = 0.0;
   if (static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits) {
-    // Many rounds: the last one's imbalance is small against the total.
+    // Many rounds: the last one's imbalance is small against the total; it
+    // leaves about half of the longest item to run alone.
     double total = 0.0, longest = 0.0;
     for (const double cost : item_cost) {
       total += cost;
       longest = cost > longest ? cost : longest;
     }
-    makespan = total * num_kv_heads / kComputeUnits + longest;
+    makespan = total * num_kv_heads / kComputeUnits + 0.5 * longest;
   } else {
     std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
     for (int i = 0; i < kComputeUnits; ++i) free_at.push(0.0);
@@ -1001,7 +1004,8 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     // its key tiles plus a fixed overhead, then the combine pass reading every
     // partial result.  Few long chunks leave CUs idle in the last round; many
     // short ones add overhead and partials.
-    static const int64_t kCandidates[] = {512, 640, 768, 1024, 1280, 1536, 1792, 2048, 2304, 2560, 3072, 3584, 4096};
+    static const int64_t kCandidates[] = {512,  640,  768,  1024, 1280, 1536, 1792, 2048, 2304,
+                                          2560, 3072, 3584, 4096, 4608, 5120, 6144, 7680};
     double best = -1.0;
     for (const int64_t candidate : kCandidates) {
       const double estimate = plan_cost_estimate(
