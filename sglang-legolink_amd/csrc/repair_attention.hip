@@ -355,8 +355,8 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   const int range = load_stop - kv_begin;
   const int tiles = (range + kTile - 1) / kTile;
 
-  for (int i = tid; i < kRangeTiles; i += kM32Threads) tile_valid[i] = 0ull;
-  __syncthreads();
+  // Each wave takes whole 64-token tiles (the workgroup is a whole number of
+  // waves), so a tile's valid-slot bits are one ballot.
   for (int i = tid; i < tiles * kTile; i += kM32Threads) {
     int slot = -1;
     if (i < range) {
@@ -364,7 +364,8 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
     }
     slot_lds[i] = slot;
-    if (slot >= 0) atomicOr(&tile_valid[i / kTile], 1ull << (i % kTile));
+    const unsigned long long bits = __builtin_amdgcn_ballot_w64(slot >= 0);
+    if (lane == 0) tile_valid[i / kTile] = bits;
   }
 
   // B operand of the score MFMAs: the lane's query, dims 16 ks + 8 h .. + 7.
