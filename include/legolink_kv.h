@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 13
+#define LL_ABI_VERSION 14
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -459,7 +459,9 @@ typedef struct ll_repair_attention_args {
   const int32_t *combine;          /* device copy of the plan's combine items, or NULL */
   int64_t num_combine;
   const int32_t *query_positions;  /* device copy of the plan's positions table [num_queries] */
-  float *workspace;                /* device fp32 [workspace_items, num_q_heads, 16, head_dim + 2] */
+  float *workspace;                /* device, 16-byte aligned: workspace_items x num_q_heads blocks of
+                                      8 * head_dim + 32 floats (16 queries' outputs in the KV dtype,
+                                      then 16 fp32 (maximum, sum) pairs) (ABI 14) */
   int64_t workspace_items;
 } ll_repair_attention_args;
 
@@ -480,7 +482,7 @@ int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream
  * of LL_REPAIR_SCRATCH_BYTES that the library holds on every GPU it runs on,
  * from its first use there until the process ends (args->workspace_items
  * still gives the plan's partial count).  A plan whose partials need more --
- * workspace_items * num_q_heads * (16 * head_dim + 32) * 4 bytes -- is
+ * workspace_items * num_q_heads * (8 * head_dim + 32) * 4 bytes -- is
  * rejected with LL_ERR_INVALID_ARGUMENT before any launch.  Nothing needs
  * clearing: every partial the combine reads is written by the same call.
  * Calls that overlap on one GPU (two streams, or two threads) share that

@@ -125,6 +125,9 @@ struct Bf16 {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), __builtin_bit_cast(bf16x2, kOnes),
                                            acc, false);
   }
+  __device__ static f32x2 unpack(uint32_t pair) {  // exact
+    return f32x2{__uint_as_float(pair << 16), __uint_as_float(pair & 0xffff0000u)};
+  }
 };
 
 struct F16 {
@@ -139,6 +142,9 @@ struct F16 {
   __device__ static float dot2_ones(uint32_t pair, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, kOnes), acc, false);
   }
+  __device__ static f32x2 unpack(uint32_t pair) {  // exact
+    return __builtin_convertvector(__builtin_bit_cast(f16x2, pair), f32x2);
+  }
 };
 
 __device__ inline long long slot_at(const AttnParams &p, long long i) {
@@ -146,10 +152,17 @@ __device__ inline long long slot_at(const AttnParams &p, long long i) {
                    : static_cast<long long>(static_cast<const int *>(p.slots)[i]);
 }
 
-// Partial results of item `partial`, query head h: O [16][D] then (m, l) [16][2].
+// Partial result of item `partial`, query head h: the 16 queries' outputs
+// over the item's keys, normalised by their own sums (O / l) and rounded to
+// the KV dtype, [16][D] 16-bit values, then (m, l) [16][2] in fp32: 8 D + 32
+// floats.  Rounding O / l adds at most 2^-9 of the softmax-weighted |V| to
+// the merged output (a convex combination of the partials), half of what
+// rounding the probabilities to the KV dtype already allows.
+template <int D>
+__host__ __device__ constexpr int partial_floats() { return kQueries * D / 2 + 2 * kQueries; }
 template <int D>
 __device__ inline float *partial_block(const AttnParams &p, int partial, int h) {
-  return p.ws + (static_cast<long long>(partial) * p.hq + h) * (kQueries * D + 2 * kQueries);
+  return p.ws + (static_cast<long long>(partial) * p.hq + h) * partial_floats<D>();
 }
 
 // v_permlane32_swap a, b exchanges the upper half of a with the lower half of
@@ -593,32 +606,26 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     l = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
   }
   if (!mine.computes) return;
+  // The output row, or the partial result's row: O / l in the KV dtype.
   // Register r of dim block b holds dim 32 b + 8 (r / 4) + 4 h + r % 4.
-  if (mine.partial < 0) {
-    if (!q_ok) return;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t *dst = p.out + (static_cast<long long>(mine.q_index + qc) * p.hq + mine.hq) * D + 4 * h;
+  if (!q_ok) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float *block = mine.partial < 0 ? nullptr : partial_block<D>(p, mine.partial, mine.hq);
+  uint16_t *dst = block == nullptr
+                      ? p.out + (static_cast<long long>(mine.q_index + qc) * p.hq + mine.hq) * D + 4 * h
+                      : reinterpret_cast<uint16_t *>(block) + qc * D + 4 * h;
 #pragma unroll
-    for (int b = 0; b < kDimBlocks; ++b)
+  for (int b = 0; b < kDimBlocks; ++b)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        u32x2 packed;
-        packed[0] = E::pack(o[b][4 * rr] * inv, o[b][4 * rr + 1] * inv);
-        packed[1] = E::pack(o[b][4 * rr + 2] * inv, o[b][4 * rr + 3] * inv);
-        *reinterpret_cast<u32x2 *>(dst + 32 * b + 8 * rr) = packed;
-      }
-  } else {
-    float *block = partial_block<D>(p, mine.partial, mine.hq);
-#pragma unroll
-    for (int b = 0; b < kDimBlocks; ++b)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        *reinterpret_cast<f32x4 *>(block + qc * D + 32 * b + 8 * rr + 4 * h) =
-            f32x4{o[b][4 * rr], o[b][4 * rr + 1], o[b][4 * rr + 2], o[b][4 * rr + 3]};
-    if (h == 0) {
-      block[kQueries * D + 2 * qc] = m * scale_log2;
-      block[kQueries * D + 2 * qc + 1] = l;
+    for (int rr = 0; rr < 4; ++rr) {
+      u32x2 packed;
+      packed[0] = E::pack(o[b][4 * rr] * inv, o[b][4 * rr + 1] * inv);
+      packed[1] = E::pack(o[b][4 * rr + 2] * inv, o[b][4 * rr + 3] * inv);
+      *reinterpret_cast<u32x2 *>(dst + 32 * b + 8 * rr) = packed;
     }
+  if (block != nullptr && h == 0) {
+    block[kQueries * D / 2 + 2 * qc] = m * scale_log2;
+    block[kQueries * D / 2 + 2 * qc + 1] = l;
   }
 }
 
@@ -639,7 +646,8 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
   if (c >= q_count) return;
   // One pass in batches of kBatch partials whose loads are all in flight
   // together; the running maximum rescales what is summed when a batch
-  // raises it.
+  // raises it.  A partial's weight is its sum l times 2^(m - max): its
+  // normalised output O / l then contributes exactly O.
   constexpr int kBatch = 8;
   float run_max = -INFINITY;
   float total = 0.f;
@@ -648,14 +656,15 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
   for (int d = 0; d < kPer / 4; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < count; s0 += kBatch) {
     float ms[kBatch], ls[kBatch];
-    f32x4 rows[kBatch][kPer / 4];
+    u32x2 rows[kBatch][kPer / 4];  // kPer 16-bit values: kPer / 4 pairs of words
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int s = min(s0 + i, count - 1);  // past the end: the last partial again, unused
       const float *block = partial_block<D>(p, first + s, h);
-      ms[i] = block[kQueries * D + 2 * c];
-      ls[i] = block[kQueries * D + 2 * c + 1];
-      const f32x4 *row = reinterpret_cast<const f32x4 *>(block + c * D + part * kPer);
+      ms[i] = block[kQueries * D / 2 + 2 * c];
+      ls[i] = block[kQueries * D / 2 + 2 * c + 1];
+      const u32x2 *row = reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(block) + c * D +
+                                                         part * kPer);
 #pragma unroll
       for (int d = 0; d < kPer / 4; ++d) rows[i][d] = row[d];
     }
@@ -672,10 +681,14 @@ __global__ void __launch_bounds__(256) repair_combine_kernel(const AttnParams p)
     }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const float w = s0 + i >= count || ms[i] == -INFINITY ? 0.f : exp2f(ms[i] - run_max);
-      total += ls[i] * w;
+      const float w = s0 + i >= count || ms[i] == -INFINITY ? 0.f : exp2f(ms[i] - run_max) * ls[i];
+      total += w;
 #pragma unroll
-      for (int d = 0; d < kPer / 4; ++d) acc[d] += w * rows[i][d];
+      for (int d = 0; d < kPer / 4; ++d) {  // values 4 d .. 4 d + 3
+        const f32x2 v0 = E::unpack(rows[i][d][0]);
+        const f32x2 v1 = E::unpack(rows[i][d][1]);
+        acc[d] += w * f32x4{v0[0], v0[1], v1[0], v1[1]};
+      }
     }
   }
   const float inv = total > 0.f ? 1.f / total : 0.f;
@@ -1131,7 +1144,7 @@ int ll_repair_attention_noalloc(const ll_repair_attention_args *a, ll_stream_t s
   // a (maximum, sum) pair per query, in fp32.
   // workspace_items is bounded before the product, which then stays below
   // 2^56 (num_q_heads <= 65535 and head_dim <= 256 were checked).
-  const long long block_floats = 16 * a->head_dim + 32;
+  const long long block_floats = 8 * a->head_dim + 32;
   if (a->workspace_items > kScratchBytes ||
       a->workspace_items * a->num_q_heads * block_floats * 4 > kScratchBytes)
     return fail(LL_ERR_INVALID_ARGUMENT, "the plan's %lld split partials (%lld query heads, %lld bytes each) "

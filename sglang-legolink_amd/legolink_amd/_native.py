@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1

@@ -109,7 +109,7 @@ class RepairAttentionPlan:
         self.items = self._tables[: items.size]
         self.combine = self._tables[items.size : items.size + combine.size]
         self.positions = self._tables[items.size + combine.size :]
-        per_item = self.num_q_heads * (16 * self.head_dim + 32)
+        per_item = self.num_q_heads * (8 * self.head_dim + 32)  # 16 x head_dim 16-bit values, 16 (m, l) pairs
         self.allocation_free = bool(allocation_free)
         self.workspace = (torch.empty(info.workspace_items * per_item, dtype=torch.float32, device=device)
                           if info.workspace_items and not self.allocation_free else None)

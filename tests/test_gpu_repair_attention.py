@@ -5,8 +5,9 @@ torch fp32 restatement.
 Tolerance, elementwise: |got - ref| <= 2^-7 * (sum_j w_j |v_j| + |ref|) + 1e-5,
 where w are the softmax weights.  The kernel rounds each probability to bf16
 for the value product (relative error <= 2^-8, so the output moves by at most
-2^-8 * sum_j w_j |v_j|) and the output to bf16 (<= 2^-8 * |ref|); the bound
-takes twice that.  fp16 inputs round to fp16 instead (2^-11) and keep the same
+2^-8 * sum_j w_j |v_j|), a split range's partial output O / l to bf16 (the
+merge is a convex combination of the partials: at most 2^-9 * sum_j w_j |v_j|
+more) and the output to bf16 (<= 2^-9 * |ref|); the bound is above the sum.  fp16 inputs round to fp16 instead (2^-11) and keep the same
 bound.  The reference's own FlashInfer check is atol = rtol = 3e-2
 (tests/pic/test_sparse_attention_reference.py:103).  Short KVs, a sharp
 softmax (scale 1) and zero queries make an off-by-one mask or a dropped key

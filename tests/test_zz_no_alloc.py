@@ -76,14 +76,14 @@ def test_allocation_free_attention_without_split_items(gpu_device):
 
 
 def test_allocation_free_attention_rejects_plans_beyond_the_scratch(gpu_device):
-    """Checked on the host before any launch: 300+ partials of 28 heads at head
-    dim 128 need more than 64 MiB."""
+    """Checked on the host before any launch: more than 567 partials of 28
+    heads at head dim 128 (4,224 bytes per head) need more than 64 MiB."""
 
     rng = np.random.default_rng(9)
     spans = _spans(gpu_device, rng, requests=1, spans_per_request=40, span=16, gap=260, pool=16384)
     plan = RepairAttentionPlan(spans, num_q_heads=28, num_kv_heads=4, head_dim=128, pool_size=16384,
                                split_tokens=64, allocation_free=True)
-    needed = plan.info["workspace_items"] * 28 * (16 * 128 + 32) * 4
+    needed = plan.info["workspace_items"] * 28 * (8 * 128 + 32) * 4
     assert needed > _native.repair_scratch_bytes()
     key = torch.zeros(16384, 4, 128, dtype=torch.bfloat16, device=gpu_device)
     query = torch.zeros(plan.num_queries, 28, 128, dtype=torch.bfloat16, device=gpu_device)
