@@ -73,7 +73,12 @@ def _check(plan_spans, query, key_pool, value_pool, got, scale):
         worst = max(worst, float((err / bound).max()))
         bad = err > bound
         assert not bad.any(), f"span [{start}, {end}): {int(bad.sum())} elements off, max err {err.max():.3g}"
-        assert (np.abs(part - fp32) <= bound + 2.0 ** -8 * np.abs(fp32)).all()
+        # A query that sees no valid key (its only keys' slots invalid) outputs
+        # zeros, as the oracle defines it; torch's softmax over an all -inf row
+        # is NaN, so the fp32 restatement is compared on the other rows.
+        seen = visible.any(axis=1)
+        assert (part[~seen] == 0).all()
+        assert (np.abs(part - fp32) <= bound + 2.0 ** -8 * np.abs(fp32))[seen].all()
         cursor += n
     report(f"largest error / bound vs fp64: {worst:.3f}")
 
@@ -161,15 +166,16 @@ def test_fp16_matches_oracle(gpu_device, case):
     _check(plan_spans, query, key_pool, value_pool, got, scale if scale is not None else 1.0 / math.sqrt(dim))
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(96))
 def test_random_configurations(gpu_device, seed):
     """Seeded random shapes: GQA group, head dim, dtype, slot dtype, several
-    requests and spans (partial tiles, seams near chunk edges), chunk length,
-    scale and a few invalid slots; checked against the fp64 oracle."""
+    requests and spans (partial tiles, seams near chunk edges, long spans whose
+    work windows cross many tiles), chunk length, scale and a few invalid
+    slots; checked against the fp64 oracle."""
 
     rng = np.random.default_rng(1000 + seed)
     hkv = int(rng.choice([1, 2, 4, 8]))
-    group = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 20]))
+    group = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 15, 16, 20]))
     hq = hkv * group
     dim = int(rng.choice([64, 128, 256]))
     dtype = torch.float16 if rng.random() < 0.4 else torch.bfloat16
@@ -193,7 +199,8 @@ def test_random_configurations(gpu_device, seed):
             slots[int(rng.integers(0, length))] = -1
         for _ in range(int(rng.integers(1, 4))):
             end = int(rng.integers(1, length + 1))
-            start = max(0, end - int(rng.integers(1, 40)))
+            longest = 300 if rng.random() < 0.25 else 40
+            start = max(0, end - int(rng.integers(1, longest)))
             spans.append((slots, start, end))
     report(f"seed {seed}: hq={hq} hkv={hkv} d={dim} {dtype} split={split} scale={scale:.3f} "
            f"spans={[(s, e) for _, s, e in spans]}")
