@@ -722,10 +722,11 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
     }
     partials += group_partials;
   });
-  // The plan dispatches its items longest first (see the ordering below).
-  std::sort(item_cost.begin(), item_cost.end(), std::greater<double>());
   double makespan = 0.0;
-  if (static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits) {
+  const bool many_rounds = static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits;
+  // The plan dispatches its items longest first (see the ordering below).
+  if (!many_rounds) std::sort(item_cost.begin(), item_cost.end(), std::greater<double>());
+  if (many_rounds) {
     // Many rounds: the last one's imbalance is small against the total; it
     // leaves about half of the longest item to run alone.
     double total = 0.0, longest = 0.0;
@@ -734,6 +735,18 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
       longest = cost > longest ? cost : longest;
     }
     makespan = total * num_kv_heads / kComputeUnits + 0.5 * longest;
+  } else if (static_cast<int64_t>(item_cost.size()) * num_kv_heads <= 2 * kComputeUnits) {
+    // At most two rounds: the workgroups beyond the first 256 start when the
+    // first round has ended (measured on c2: its 4 extra workgroups started
+    // 72 us into an 82 us kernel, not when the first short items freed their
+    // CUs), so the rounds' longest items add up.
+    const int64_t n = static_cast<int64_t>(item_cost.size());
+    double second = 0.0;
+    for (int64_t g = kComputeUnits; g < n * num_kv_heads; ++g) {
+      const double cost = item_cost[static_cast<size_t>(g % n)];  // grid order: items, then KV heads
+      second = cost > second ? cost : second;
+    }
+    makespan = item_cost.front() + second;
   } else {
     std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
     for (int i = 0; i < kComputeUnits; ++i) free_at.push(0.0);
@@ -746,9 +759,10 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
       }
     }
   }
-  if (partials > 0)
+  if (partials > 0)  // 16 queries' 16-bit outputs (head dim 128) and fp32 (max, sum) per partial and head
     makespan += kCombineLaunchTiles +
-                static_cast<double>(partials) * num_q_heads * (kQueries * 128 + 2 * kQueries) * 4 / kPartialBytesPerTile;
+                static_cast<double>(partials) * num_q_heads * (kQueries * 128 * 2 + 2 * kQueries * 4) /
+                    kPartialBytesPerTile;
   return makespan;
 }
 
@@ -1017,26 +1031,40 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     // workgroups dispatched in grid order to the first free CU, each costing
     // its key tiles plus a fixed overhead, then the combine pass reading every
     // partial result.  Few long chunks leave CUs idle in the last round; many
-    // short ones add overhead and partials.
-    static const int64_t kCandidates[] = {512,  640,  768,  1024, 1280, 1536, 1792, 2048, 2304,
-                                          2560, 3072, 3584, 4096, 4608, 5120, 6144, 7680};
+    // short ones add overhead and partials.  A coarse pass over lengths from
+    // 512 to the maximum, then every multiple of the key tile within 256 of
+    // the best: one tile more per item can save a round (c2: 2,112 keys make
+    // 64 items, one round of 4 KV heads on 256 CUs, where 2,048 make 65).
+    auto estimate = [&](int64_t candidate) {
+      return plan_cost_estimate(candidate, num_kv_heads, num_q_heads, [&](auto &&visit) {
+        int64_t next_tile = 0;  // a tile's partials count with the first window that holds it
+        for (const Window &w : windows) {
+          int64_t partials = 0;
+          for (int64_t t = w.first > next_tile ? w.first : next_tile; t < w.last; ++t) {
+            const int64_t chunks = (tiles[t].needed + candidate - 1) / candidate;
+            partials += chunks > 1 ? chunks : 0;
+          }
+          next_tile = w.last > next_tile ? w.last : next_tile;
+          visit(window_needed(w), partials);
+        }
+      });
+    };
+    static const int64_t kCoarse[] = {512,  640,  768,  1024, 1280, 1536, 1792, 2048, 2304,
+                                      2560, 3072, 3584, 4096, 4608, 5120, 6144, 7680};
     double best = -1.0;
-    for (const int64_t candidate : kCandidates) {
-      const double estimate = plan_cost_estimate(
-          candidate, num_kv_heads, num_q_heads, [&](auto &&visit) {
-            int64_t next_tile = 0;  // a tile's partials count with the first window that holds it
-            for (const Window &w : windows) {
-              int64_t partials = 0;
-              for (int64_t t = w.first > next_tile ? w.first : next_tile; t < w.last; ++t) {
-                const int64_t chunks = (tiles[t].needed + candidate - 1) / candidate;
-                partials += chunks > 1 ? chunks : 0;
-              }
-              next_tile = w.last > next_tile ? w.last : next_tile;
-              visit(window_needed(w), partials);
-            }
-          });
-      if (best < 0.0 || estimate <= best) {
-        best = estimate;
+    for (const int64_t candidate : kCoarse) {
+      const double cost = estimate(candidate);
+      if (best < 0.0 || cost <= best) {
+        best = cost;
+        split = candidate;
+      }
+    }
+    const int64_t coarse = split;
+    for (int64_t candidate = coarse - 256; candidate <= coarse + 256; candidate += kTile) {
+      if (candidate < 512 || candidate > kDmaMaxRange || candidate == coarse) continue;
+      const double cost = estimate(candidate);
+      if (cost < best || (cost == best && candidate > split)) {
+        best = cost;
         split = candidate;
       }
     }
