@@ -290,6 +290,14 @@ def _range_bounds(ranges: Sequence[Mapping[str, Any]]) -> np.ndarray:
     return flat.reshape(-1, 2)
 
 
+def _exclusive_offsets(sizes: np.ndarray) -> np.ndarray:
+    """int64 offset of every entry in the concatenation of ``sizes``."""
+
+    offsets = np.zeros(sizes.size, dtype=np.int64)
+    np.cumsum(sizes[:-1], out=offsets[1:])
+    return offsets
+
+
 def _index_array(values: Any) -> np.ndarray:
     """imp_indices as a flat int64 array: a Python list (the reference's plan
     format) through array.array, the cheapest conversion (about 17 ns per
@@ -642,6 +650,62 @@ class KVLinkExecutor:
                         repair_positions=repair, prefix_token_count=int(counts[0]) if identity else 0,
                         max_position=int(max_position), leading_blocks=leading)
 
+    def build_batch_link_maps(self, requests: Sequence[tuple[torch.Tensor, Mapping[str, Any]]],
+                              *, device: torch.device) -> LinkMaps:
+        """``LinkMaps.batch`` of every request's ``build_link_maps``, with one
+        registry lookup, one record gather and vectorised range checks for the
+        whole batch.  A batch with any fault is rebuilt request by request, so
+        the error raised is the one that request's own link raises."""
+
+        def one_by_one() -> LinkMaps:
+            return LinkMaps.batch([self.build_link_maps(slots, plan, device=device) for slots, plan in requests])
+
+        if not requests:
+            raise LinkRuntimeError("PIC batched link has no requests.")
+        if len(requests) == 1:
+            return one_by_one()
+        range_lists, key_lists, repair_lists = [], [], []
+        for _, plan in requests:
+            ranges = plan.get("block_ranges") or plan.get("attention_ranges")
+            cache_keys = plan.get("cache_keys")
+            if (not isinstance(ranges, list) or not isinstance(cache_keys, list)
+                    or len(ranges) != len(cache_keys) or not cache_keys):
+                return one_by_one()
+            range_lists.append(ranges)
+            key_lists.append(cache_keys)
+            repair_lists.append(plan.get("imp_indices"))
+        block_counts = np.fromiter(map(len, key_lists), dtype=np.int64, count=len(key_lists))
+        handles, unavailable = self.registry.link_handles(
+            [str(key) for key in itertools.chain.from_iterable(key_lists)])
+        if unavailable:
+            return one_by_one()
+        slot_tensors = [slots if slots.device == device and slots.dtype == torch.int64
+                        else slots.to(device=device, dtype=torch.int64) for slots, _ in requests]
+        sizes = np.fromiter((int(slots.numel()) for slots in slot_tensors), dtype=np.int64, count=len(requests))
+        bases = _exclusive_offsets(sizes)
+        records = self.registry.link_records(handles, device)
+        bounds = _range_bounds(list(itertools.chain.from_iterable(range_lists)))
+        starts, ends = bounds[:, 0].copy(), bounds[:, 1]
+        counts = records[:, 0].copy()
+        totals = np.repeat(sizes, block_counts)
+        if ((ends - starts != counts) | (ends > totals) | (starts < 0)).any():
+            return one_by_one()
+        firsts = _exclusive_offsets(block_counts)
+        leading = np.zeros(len(handles), dtype=bool)
+        leading[firsts] = [not _needs_rope_remap(handles[first], start)
+                           for first, start in zip(firsts.tolist(), starts[firsts].tolist())]
+        blocks = link_maps.BlockTable(starts=starts, counts=counts, source_ptrs=records[:, 1].copy(),
+                                      local_ptrs=records[:, 2].copy(), local_starts=records[:, 3].copy(),
+                                      sets=records[:, 4].copy(), destination_bases=np.repeat(bases, block_counts))
+        # Per request, the largest position is max(end - 1, largest local
+        # position); over the batch that is the maximum of both columns.
+        max_position = int(max(int(ends.max()) - 1, int(records[:, 5].max())))
+        repair = np.concatenate([_index_array(values) + base
+                                 for values, base in zip(repair_lists, bases.tolist())]).astype(np.int64)
+        return LinkMaps(request_slots=torch.cat(slot_tensors), blocks=blocks, handles=handles,
+                        repair_positions=repair, prefix_token_count=int(counts[leading].sum()),
+                        max_position=max_position, leading_blocks=leading, request_count=len(requests))
+
     # -- link ---------------------------------------------------------------
     def _layer_groups(self, layers: list[int], max_position: int,
                       device: torch.device) -> list[tuple[list[int], RotarySpec]]:
@@ -702,7 +766,7 @@ class KVLinkExecutor:
         if boundary_repair_aware is None:
             boundary_repair_aware = _env_flag("SGLANG_PIC_TRITON_BOUNDARY_REPAIR_AWARE", "0")
         device = pool.get_key_buffer(self.start_layer).device
-        maps = LinkMaps.batch([self.build_link_maps(slots, plan, device=device) for slots, plan in requests])
+        maps = self.build_batch_link_maps(requests, device=device)
         groups = self._layer_groups(self.layers, maps.max_position, device)
         prepared = PreparedLink(
             pool=pool, layers=self.layers, maps=maps, groups=groups,
