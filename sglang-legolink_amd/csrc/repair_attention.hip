@@ -410,15 +410,24 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     g_kchunk[j] = (chunk_index % kChunksPerRow) ^ m32_k_swizzle<D>(g_token[j]);
     g_vchunk[j] = (chunk_index % kChunksPerRow) ^ m32_v_swizzle<D>(g_token[j]);
   }
-  auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
+  auto gather_slots = [&](int t, int *slots) {
+#pragma unroll
+    for (int j = 0; j < kGathers; ++j) slots[j] = slot_lds[t * kTile + g_token[j]];
+  };
+  auto gather_from = [&](const int *slots, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
 #pragma unroll
     for (int j = 0; j < kGathers; ++j) {
-      const int slot = max(slot_lds[t * kTile + g_token[j]], 0);
+      const int slot = max(slots[j], 0);
       const long long row = slot * row_stride + hk * D;
       const int offset = (kGathers * wave + j) * kWave * 16;
       dma_pair(p.k + row + g_kchunk[j] * 8, k_dst + offset, p.v + row + g_vchunk[j] * 8, v_dst + offset);
     }
+  };
+  auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
+    int slots[kGathers];
+    gather_slots(t, slots);
+    gather_from(slots, k_dst, v_dst);
   };
 
   float m = kScoreFloor;
@@ -452,16 +461,21 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   for (int t = 0; t < tiles; ++t) {
     const unsigned char *k_stage = k_ring + (t % kStages) * kStageBytes;
     unsigned char *v_stage = v_ring + (t % kStages) * kStageBytes;
+    // The slots of the gather issued after the barrier and the tile's
+    // validity bits are read before it, so that their LDS latency passes
+    // while the waves meet (both tables are written only before the loop).
+    int next_slots[kGathers];
+    if (t + kLead < tiles) gather_slots(t + kLead, next_slots);
+    const unsigned long long valid_bits_lds = tile_valid[t];
     if (kLead >= 3 && t + 2 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (4 * kGathers));
     else if (kLead >= 2 && t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kGathers));
     else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
     workgroup_barrier();
     if (t + kLead < tiles)
-      gather(t + kLead, k_ring + ((t + kLead) % kStages) * kStageBytes,
-             v_ring + ((t + kLead) % kStages) * kStageBytes);
+      gather_from(next_slots, k_ring + ((t + kLead) % kStages) * kStageBytes,
+                  v_ring + ((t + kLead) % kStages) * kStageBytes);
     // readfirstlane returns int: each half goes through unsigned so that the
     // low half is not sign-extended into the high one.
-    const unsigned long long valid_bits_lds = tile_valid[t];
     const unsigned valid_lo =
         static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(valid_bits_lds))));
     const unsigned valid_hi = static_cast<unsigned>(
