@@ -1182,8 +1182,8 @@ int ll_repair_attention_noalloc(const ll_repair_attention_args *a, ll_stream_t s
     return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be NULL: the partial results go to the "
                 "library's scratch array");
   if (a->num_items == 0) return LL_OK;
-  // Every (partial, query head) block holds 16 queries x (head_dim outputs) and
-  // a (maximum, sum) pair per query, in fp32.
+  // Every (partial, query head) block holds 16 queries x head_dim 16-bit
+  // outputs and an fp32 (maximum, sum) pair per query: 8 head_dim + 32 floats.
   // workspace_items is bounded before the product, which then stays below
   // 2^56 (num_q_heads <= 65535 and head_dim <= 256 were checked).
   const long long block_floats = 8 * a->head_dim + 32;
