@@ -415,11 +415,6 @@ def kv_link_describe(args: LinkArgs) -> LaunchInfo:
     return info
 
 
-def kv_scatter_rows(args: ScatterArgs, stream: int) -> None:
-    args.struct_size = ctypes.sizeof(ScatterArgs)
-    _check(load_library().ll_kv_scatter_rows(ctypes.byref(args), _ptr(int(stream))))
-
-
 def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
     args.struct_size = ctypes.sizeof(LinkMapsArgs)
     _check(load_library().ll_kv_build_link_maps(ctypes.byref(args), _ptr(int(stream))))

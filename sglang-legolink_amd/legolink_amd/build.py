@@ -55,13 +55,6 @@ def _flags() -> list[str]:
     ]
 
 
-def compile_command(output: Path, sources=SOURCES) -> list[str]:
-    """One hipcc call that compiles and links ``sources`` into ``output``."""
-
-    sources = [sources] if isinstance(sources, Path) else list(sources)
-    return [hipcc_path(), *_flags(), "-shared", "-o", str(output), *[str(source) for source in sources]]
-
-
 def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path:
     """Compile every translation unit in parallel, then link the library; the
     output is replaced atomically.  ``sanitize_host`` builds the host-sanitized

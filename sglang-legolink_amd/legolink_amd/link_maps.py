@@ -70,10 +70,12 @@ class SegmentPlan:
     set_prefix: tuple[int, int]  # identity tokens at the head of each set's maps
 
 
-def _exclusive_cumsum(values: np.ndarray) -> np.ndarray:
-    out = np.zeros(values.shape[0], dtype=np.int64)
-    if values.shape[0] > 1:
-        np.cumsum(values[:-1], out=out[1:])
+def exclusive_offsets(sizes: np.ndarray) -> np.ndarray:
+    """int64 offset of every entry in the concatenation of ``sizes``."""
+
+    out = np.zeros(sizes.shape[0], dtype=np.int64)
+    if sizes.shape[0] > 1:
+        np.cumsum(sizes[:-1], out=out[1:])
     return out
 
 

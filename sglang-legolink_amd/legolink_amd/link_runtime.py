@@ -290,14 +290,6 @@ def _range_bounds(ranges: Sequence[Mapping[str, Any]]) -> np.ndarray:
     return flat.reshape(-1, 2)
 
 
-def _exclusive_offsets(sizes: np.ndarray) -> np.ndarray:
-    """int64 offset of every entry in the concatenation of ``sizes``."""
-
-    offsets = np.zeros(sizes.size, dtype=np.int64)
-    np.cumsum(sizes[:-1], out=offsets[1:])
-    return offsets
-
-
 def _index_array(values: Any) -> np.ndarray:
     """imp_indices as a flat int64 array: a Python list (the reference's plan
     format) through array.array, the cheapest conversion (about 17 ns per
@@ -682,7 +674,7 @@ class KVLinkExecutor:
         slot_tensors = [slots if slots.device == device and slots.dtype == torch.int64
                         else slots.to(device=device, dtype=torch.int64) for slots, _ in requests]
         sizes = np.fromiter((int(slots.numel()) for slots in slot_tensors), dtype=np.int64, count=len(requests))
-        bases = _exclusive_offsets(sizes)
+        bases = link_maps.exclusive_offsets(sizes)
         records = self.registry.link_records(handles, device)
         bounds = _range_bounds(list(itertools.chain.from_iterable(range_lists)))
         starts, ends = bounds[:, 0].copy(), bounds[:, 1]
@@ -690,7 +682,7 @@ class KVLinkExecutor:
         totals = np.repeat(sizes, block_counts)
         if ((ends - starts != counts) | (ends > totals) | (starts < 0)).any():
             return one_by_one()
-        firsts = _exclusive_offsets(block_counts)
+        firsts = link_maps.exclusive_offsets(block_counts)
         leading = np.zeros(len(handles), dtype=bool)
         leading[firsts] = [not _needs_rope_remap(handles[first], start)
                            for first, start in zip(firsts.tolist(), starts[firsts].tolist())]
@@ -813,9 +805,6 @@ class KVLinkExecutor:
         )
 
     # -- capture and promotion ------------------------------------------------
-    def _any_rotary(self) -> RotarySpec:
-        return self.rotary_by_layer[self.start_layer]
-
     def _copy_rows(self, *, destination: Any, source: Any, source_slots: torch.Tensor,
                    destination_slots: torch.Tensor, local: torch.Tensor, global_: torch.Tensor,
                    prefix: int, rounding: str = "fused") -> None:
