@@ -212,6 +212,33 @@ def test_random_configurations(gpu_device, seed):
     _check(spans, query, key_pool, value_pool, got, scale)
 
 
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("split", [192, 704, 2112, 4160, 7680])
+def test_chunk_lengths_of_the_plan_search(gpu_device, split, dim):
+    """Key chunks of the lengths the plan's fine search picks (multiples of 64
+    that are not powers of two) up to the 7,680-key maximum, whose slot list
+    fills the LDS the ring leaves: spans of an 8,000-token request ending
+    just before, at and after chunk edges, GQA 7/1 and a 16-query span."""
+
+    generator = torch.Generator(device=gpu_device).manual_seed(split + dim)
+    pool, length = 9000, 8000
+    key_pool = _bf16((pool, 1, dim), generator, gpu_device)
+    value_pool = _bf16((pool, 1, dim), generator, gpu_device)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:length].clone()
+    ends = sorted({min(length, max(16, e)) for e in (split - 1, split, split + 1, 2 * split + 33, length)})
+    spans = [(slots, end - 16, end) for end in ends]
+    report(f"chunk {split}, head dim {dim}: spans {[(s, e) for _, s, e in spans]}")
+    plan = RepairAttentionPlan(spans, num_q_heads=7, num_kv_heads=1, head_dim=dim, split_tokens=split,
+                               pool_size=pool)
+    assert plan.info["split_tokens"] == split
+    assert plan.info["workspace_items"] > 0  # the longest spans are split
+    query = _bf16((plan.num_queries, 7, dim), generator, gpu_device)
+    scale = 1.0 / math.sqrt(dim)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, scale)
+
+
 def test_dtype_checks_follow_the_reference(gpu_device):
     slots = torch.arange(64, device=gpu_device)
     plan = RepairAttentionPlan([(slots, 10, 26)], num_q_heads=8, num_kv_heads=2, head_dim=64)
