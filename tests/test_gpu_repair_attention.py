@@ -324,10 +324,11 @@ def test_one_plan_serves_every_layer(gpu_device):
 
 @pytest.mark.parametrize("name", ["c3", "c5"])
 def test_full_size_workload_sampled(gpu_device, name):
-    """The benchmark workloads at full size (c5: 511 spans over a 32,768-token
-    request, 4,096-key chunks and their combine; c3: 448 eight-query spans of
-    64 requests sharing tiles), every output row of a random sample checked
-    against fp32 torch attention on the device, within the same bound."""
+    """The benchmark workloads at full size with the plan's own chunks (c5:
+    511 spans over a 32,768-token request, 7,680-key chunks and their
+    combine; c3: 448 eight-query spans of 64 requests sharing tiles, 6,208-key
+    chunks), every output row of a random sample checked against fp32 torch
+    attention on the device, within the same bound."""
 
     from legolink_amd.link_plan import contiguous_ranges
     from legolink_amd.workloads import make_workload
