@@ -56,6 +56,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--layer-groups-per-block", type=int, default=0)
     parser.add_argument("--delta-staging", choices=["auto", "per_wave", "workgroup"], default="auto",
                         help="where the link kernel computes its RoPE deltas (same result)")
+    parser.add_argument("--visit-order", choices=["auto", "plan", "source", "destination"], default="auto",
+                        help="order in which the link kernel visits the rotated rows (same result; auto: "
+                             "the executor's choice)")
     parser.add_argument("--repair-rows", choices=["compact", "mask"], default="compact",
                         help="drop repair rows from the link maps (as the executor does) or pass a mask")
     parser.add_argument("--copy-calibration", type=int, default=0,
@@ -595,7 +598,8 @@ def main() -> int:
                               end_layer=shape.layers, num_warps=args.waves_per_block,
                               layers_per_wave=args.layers_per_wave,
                               layer_groups_per_block=args.layer_groups_per_block, arena=arena,
-                              fused_mode=fused_mode, delta_staging=args.delta_staging)
+                              fused_mode=fused_mode, delta_staging=args.delta_staging,
+                              visit_order=None if args.visit_order == "auto" else args.visit_order)
     pool = KVPool(keys, values)
     row_bytes = 2 * shape.kv_heads * shape.head_dim * 2  # one token's K and V row, one layer
     storage = {"mode": args.storage}
@@ -670,7 +674,7 @@ def main() -> int:
     link = prepared.launch
     scatter = prepared.prepare_write_repaired(repaired_k, repaired_v)
     launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows),
-                  rounding=prepared.rounding)
+                  rounding=prepared.rounding, visit_order=prepared.visit_order)
     log(f"setup {setup_s:.1f}s; host prepare {host_prepare_ms:.2f} ms; link launch {launch}")
 
     for _ in range(args.warmup):

@@ -68,6 +68,16 @@ class SegmentPlan:
     repair_offsets: np.ndarray  # int64 [R] concatenation offsets of the repair rows
     block_entries: np.ndarray   # int64 [B] map entries each block contributes
     set_prefix: tuple[int, int]  # identity tokens at the head of each set's maps
+    segment_blocks: Optional[np.ndarray] = None  # int64 [S] block of every run
+
+    def run_entries(self, compact: bool) -> np.ndarray:
+        """Map entries of every run (its tokens, less its repair rows when compacted)."""
+
+        table = self.table
+        entries = table[:, _FIELD["token_count"]]
+        if compact:
+            entries = entries - (table[:, _FIELD["repair_end"]] - table[:, _FIELD["repair_begin"]])
+        return entries
 
 
 def exclusive_offsets(sizes: np.ndarray) -> np.ndarray:
@@ -158,6 +168,7 @@ def plan_segments(blocks: BlockTable, repair_positions: np.ndarray, *, compact: 
         repair_offsets=repair_offsets,
         block_entries=np.bincount(segment_blocks, weights=entries, minlength=count_blocks).astype(np.int64),
         set_prefix=(int(info.set_prefix[0]), int(info.set_prefix[1])),
+        segment_blocks=segment_blocks,
     )
 
 
@@ -170,6 +181,21 @@ class DeviceMaps:
     maps: list[Optional[torch.Tensor]]
     masks: list[Optional[torch.Tensor]]
     repair_destination_slots: torch.Tensor
+
+
+def set_entry_flags(plan: SegmentPlan, source_set: int, run_flags: np.ndarray, *, compact: bool) -> np.ndarray:
+    """A per-run flag spread over the map entries of one set: uint8 ``[n]`` with
+    entry ``o`` holding the flag of the run that writes map entry ``o``."""
+
+    table = plan.table
+    pick = table[:, _FIELD["map_set"]] == source_set
+    offsets = table[pick, _FIELD["map_offset"]]
+    entries = plan.run_entries(compact)[pick]
+    order = np.argsort(offsets, kind="stable")
+    flags = np.repeat(np.asarray(run_flags, dtype=np.uint8)[pick][order], entries[order])
+    if flags.size != plan.map_counts[source_set]:
+        raise AssertionError("the runs of a set do not tile its map entries")
+    return flags
 
 
 def build_device_maps(plan: SegmentPlan, destination_slots: torch.Tensor, *, compact: bool,

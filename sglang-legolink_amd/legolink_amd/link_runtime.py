@@ -203,6 +203,7 @@ class LinkMaps:
     max_position: int                 # largest local or global position of the link
     leading_blocks: Optional[np.ndarray] = None  # bool [B]: identity blocks
     request_count: int = 1
+    block_requests: Optional[np.ndarray] = None  # int64 [B] request of every block (None: one request)
 
     @classmethod
     def batch(cls, maps: Sequence["LinkMaps"]) -> "LinkMaps":
@@ -217,11 +218,25 @@ class LinkMaps:
         leading = np.concatenate([m.leading_blocks if m.leading_blocks is not None
                                   else np.zeros(m.blocks.counts.size, dtype=bool) for m in maps])
         repair = np.concatenate([m.repair_positions + base for m, base in zip(maps, bases)])
+        block_requests, first = [], 0
+        for m in maps:
+            own = m.block_requests if m.block_requests is not None else np.zeros(m.blocks.counts.size, np.int64)
+            block_requests.append(own + first)
+            first += m.request_count
         return cls(request_slots=request_slots, blocks=blocks,
                    handles=[h for m in maps for h in m.handles], repair_positions=repair.astype(np.int64),
                    prefix_token_count=sum(m.prefix_token_count for m in maps),
                    max_position=max(m.max_position for m in maps), leading_blocks=leading,
-                   request_count=sum(m.request_count for m in maps))
+                   request_count=sum(m.request_count for m in maps),
+                   block_requests=np.concatenate(block_requests).astype(np.int64))
+
+    def request_has_clone(self) -> np.ndarray:
+        """bool [requests]: the request holds a block stored in clone mode."""
+
+        clone = self.blocks.sets == 1
+        if self.block_requests is None or self.request_count == 1:
+            return np.array([bool(clone.any())])
+        return np.bincount(self.block_requests, weights=clone, minlength=self.request_count) > 0
 
     @property
     def token_count(self) -> int:
@@ -338,6 +353,23 @@ def _validate_pool(pool: Any) -> None:
         raise LinkRuntimeError("PIC link does not yet support quantized KV cache.")
 
 
+VISIT_ORDERS = ("plan", "source", "destination")
+
+
+def _resolve_visit_order(visit_order: Optional[str], order_by_source: Optional[bool], request_count: int) -> str:
+    """The rows' visit order: ``visit_order`` if given, else "source" /
+    "plan" from the older ``order_by_source`` flag, else "source" for a batch
+    of requests and "destination" for one."""
+
+    if visit_order is not None:
+        if visit_order not in VISIT_ORDERS:
+            raise ValueError(f"visit_order must be one of {VISIT_ORDERS}, got {visit_order!r}")
+        return visit_order
+    if order_by_source is not None:
+        return "source" if order_by_source else "plan"
+    return "source" if request_count > 1 else "destination"
+
+
 class PreparedLink:
     """One link, validated and with its device maps built; ``launch()`` enqueues
     the link kernel(s) on the current stream, ``write_repaired()`` the
@@ -352,7 +384,7 @@ class PreparedLink:
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None,
                  fused_mode: str = "required", delta_staging: str = "auto",
-                 skipped_rows: Optional[torch.Tensor] = None) -> None:
+                 skipped_rows: Optional[torch.Tensor] = None, visit_order: Optional[str] = None) -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -366,7 +398,15 @@ class PreparedLink:
         if has_clone and arena is None:
             raise LinkRuntimeError("PIC link of clone-mode blocks needs the snapshot arena.")
         self.fused_mode = fused_mode
-        self.rounding, self.fallback_reason = link_rounding(fused_mode, has_clone)
+        # Rounding per request, as the reference decides it per link
+        # (pic_runtime.py:5033-5035): a request holding a clone block takes the
+        # torch path's rounding, the others the fused kernel's.
+        request_clone = maps.request_has_clone()
+        decided = [link_rounding(fused_mode, bool(clone)) for clone in request_clone]
+        self.request_roundings = [rounding for rounding, _ in decided]
+        self.fallback_reason = next((reason for _, reason in decided if reason), None)
+        distinct = set(self.request_roundings)
+        self.rounding = distinct.pop() if len(distinct) == 1 else "mixed"
         repair_positions = maps.repair_positions if boundary_repair_aware else np.zeros(0, dtype=np.int64)
         plan = link_maps.plan_segments(maps.blocks, repair_positions, compact=compact_repair_rows,
                                        leading_blocks=maps.leading_blocks)
@@ -379,14 +419,17 @@ class PreparedLink:
         self._links: list[kv_link.PreparedKVLink] = []
         self._kernel_maps: list[torch.Tensor] = []
         index_of = {layer: i for i, layer in enumerate(layers)}
-        # A batch of requests often reads the same catalogue blocks: with the
-        # rotated rows in source-slot order, repeated sources are read close
-        # together and hit in cache (c3: 6.2 -> 7.2 TB/s).  The link's result
-        # does not depend on the order (every destination is written once);
+        # The order in which the kernel visits the rotated rows.  The link's
+        # result does not depend on it (every destination is written once);
         # the identity rows stay first, and `device_maps` keeps plan order.
-        if order_by_source is None:
-            order_by_source = maps.request_count > 1
-        self.order_by_source = bool(order_by_source)
+        # A batch of requests often reads the same catalogue blocks: in
+        # source-slot order, repeated sources are read close together and hit
+        # in cache (c3: 6.2 -> 7.2 TB/s; destination order 6.3-6.4).  A single
+        # request reads each row once, and its scattered writes cost more than
+        # its scattered reads: in destination-slot order c2's link runs 1.8 %
+        # faster (0.7465 -> 0.7334 ms), c4's 1.0 % and c5's 2.4 %.
+        self.visit_order = _resolve_visit_order(visit_order, order_by_source, maps.request_count)
+        self.order_by_source = self.visit_order == "source"
         # A single request reads each source row about once: when its rows are
         # larger than the memory-side cache, non-temporal row loads keep them
         # out of the caches (c2 +2 %, c5 +8 %).  Batched requests share
@@ -396,7 +439,12 @@ class PreparedLink:
                         for buffer in (key_buffers[0], value_buffers[0]))
         self.stream_source_rows = (maps.request_count == 1 and not self.order_by_source
                                    and token_count * len(layers) * row_bytes > MEMORY_SIDE_CACHE_BYTES)
-        # One launch per source: set 0 reads the pool, set 1 the snapshot arena.
+        sort_row = {"source": 0, "destination": 1}.get(self.visit_order)
+        # Under a mixed batch, the pool set's entries of clone-holding requests
+        # are eager, the others fused; the snapshot arena's are always eager.
+        request_eager = np.array([rounding == "eager" for rounding in self.request_roundings])
+        # One launch per source (set 0 reads the pool, set 1 the snapshot arena),
+        # per rounding within it.
         for source_set in (0, 1):
             device_maps = built.maps[source_set]
             if device_maps is None:
@@ -404,40 +452,62 @@ class PreparedLink:
             source_arena = arena if source_set == 1 else None
             prefix = plan.set_prefix[source_set]
             mask = built.masks[source_set] if plan.set_repair_rows[source_set] else None
-            if self.order_by_source and device_maps.shape[1] - prefix > 1:
-                order = torch.argsort(device_maps[0, prefix:], stable=True) + prefix
+            count = int(device_maps.shape[1])
+            eager_entries = None
+            if self.rounding != "mixed":
+                pieces = [(0, count, self.rounding, prefix)]
+            elif source_set == 1:
+                pieces = [(0, count, "eager", prefix)]
+            else:
+                run_eager = request_eager[maps.block_requests[plan.segment_blocks]]
+                eager_entries = link_maps.set_entry_flags(plan, 0, run_eager, compact=compact_repair_rows)
+                # Identity entries are bit copies in either rounding: they stay
+                # at the head, with the fused entries after them.
+                split = prefix + int(np.count_nonzero(eager_entries[prefix:] == 0))
+                pieces = [(0, split, "fused", prefix), (split, count, "eager", 0)]
+            if (sort_row is not None or eager_entries is not None) and count - prefix > 1:
+                key = None
+                if sort_row is not None:
+                    key = device_maps[sort_row, prefix:].clamp(0, (1 << 40) - 1)
+                if eager_entries is not None:
+                    group = torch.from_numpy(eager_entries[prefix:].astype(np.int64)).to(device_maps.device) << 40
+                    key = group if key is None else key + group
+                order = torch.argsort(key, stable=True) + prefix
                 device_maps = torch.cat([device_maps[:, :prefix], device_maps[:, order]], dim=1)
                 if mask is not None:
                     mask = torch.cat([mask[:prefix], mask[order]])
                 self._kernel_maps.append(device_maps)
-            for group_index, (group_layers, rotary) in enumerate(groups):
-                indices = [index_of[layer] for layer in group_layers]
-                self._links.append(kv_link.PreparedKVLink(
-                    key_buffers=[key_buffers[i] for i in indices],
-                    value_buffers=[value_buffers[i] for i in indices],
-                    source_slots=device_maps[0],
-                    destination_slots=device_maps[1],
-                    local_positions=device_maps[2],
-                    global_positions=device_maps[3],
-                    cos_sin_cache=rotary.cos_sin_cache,
-                    prefix_token_count=prefix,
-                    rotary_dim=rotary.rotary_dim,
-                    is_neox_style=rotary.is_neox_style,
-                    repair_mask=mask,
-                    num_warps=num_warps,
-                    layers_per_wave=layers_per_wave,
-                    layer_groups_per_block=layer_groups_per_block,
-                    validate_indices=validate_indices,
-                    source_key_buffers=(None if source_arena is None else
-                                        [source_arena.get_key_buffer(layer) for layer in group_layers]),
-                    source_value_buffers=(None if source_arena is None else
-                                          [source_arena.get_value_buffer(layer) for layer in group_layers]),
-                    stream_source_rows=self.stream_source_rows,
-                    rounding=self.rounding,
-                    delta_staging=delta_staging,
-                    # Each set's tokens are counted once, by its first layer group.
-                    skipped_rows=skipped_rows if group_index == 0 else None,
-                ))
+            for begin, end, rounding, piece_prefix in pieces:
+                if end <= begin:
+                    continue
+                for group_index, (group_layers, rotary) in enumerate(groups):
+                    indices = [index_of[layer] for layer in group_layers]
+                    self._links.append(kv_link.PreparedKVLink(
+                        key_buffers=[key_buffers[i] for i in indices],
+                        value_buffers=[value_buffers[i] for i in indices],
+                        source_slots=device_maps[0, begin:end],
+                        destination_slots=device_maps[1, begin:end],
+                        local_positions=device_maps[2, begin:end],
+                        global_positions=device_maps[3, begin:end],
+                        cos_sin_cache=rotary.cos_sin_cache,
+                        prefix_token_count=min(piece_prefix, end - begin),
+                        rotary_dim=rotary.rotary_dim,
+                        is_neox_style=rotary.is_neox_style,
+                        repair_mask=None if mask is None else mask[begin:end],
+                        num_warps=num_warps,
+                        layers_per_wave=layers_per_wave,
+                        layer_groups_per_block=layer_groups_per_block,
+                        validate_indices=validate_indices,
+                        source_key_buffers=(None if source_arena is None else
+                                            [source_arena.get_key_buffer(layer) for layer in group_layers]),
+                        source_value_buffers=(None if source_arena is None else
+                                              [source_arena.get_value_buffer(layer) for layer in group_layers]),
+                        stream_source_rows=self.stream_source_rows,
+                        rounding=rounding,
+                        delta_staging=delta_staging,
+                        # Each launch's tokens are counted once, by its first layer group.
+                        skipped_rows=skipped_rows if group_index == 0 else None,
+                    ))
         key_row = int(key_buffers[0][0].numel()) * key_buffers[0].element_size()
         value_row = int(value_buffers[0][0].numel()) * value_buffers[0].element_size()
         self.traffic = kv_link.estimate_kv_traffic_bytes(
@@ -493,6 +563,7 @@ class PreparedLink:
             "map_runs": int(self.segment_plan.table.shape[0]),
             "fused_mode": self.fused_mode,
             "rounding": self.rounding,
+            "request_roundings": list(self.request_roundings),
             "fallback_reason": self.fallback_reason,
             **self.traffic,
         }
@@ -505,7 +576,8 @@ class KVLinkExecutor:
                  start_layer: int = 0, end_layer: int, num_warps: Optional[int] = None,
                  layers_per_wave: int = 0, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, fused_mode: Optional[str] = None,
-                 delta_staging: str = "auto", count_skipped_rows: bool = True) -> None:
+                 delta_staging: str = "auto", count_skipped_rows: bool = True,
+                 visit_order: Optional[str] = None) -> None:
         """``rotary`` is a RotarySpec, a model's rotary module, or a mapping of
         layer to either.  ``fused_mode`` ("disabled" / "required" / "auto", or the reference's
         aliases) fixes the link's rounding; None reads
@@ -516,6 +588,9 @@ class KVLinkExecutor:
         tokens its kernel skipped for an out-of-range slot or position
         (``skipped_rows`` / ``check_skipped_rows`` read the count)."""
 
+        if visit_order is not None and visit_order not in VISIT_ORDERS:
+            raise ValueError(f"visit_order must be one of {VISIT_ORDERS}, got {visit_order!r}")
+        self.visit_order = visit_order
         self.registry = registry
         self.fused_mode = None if fused_mode is None else get_fused_kv_link_mode(fused_mode)
         self.delta_staging = delta_staging
@@ -696,7 +771,8 @@ class KVLinkExecutor:
                                  for values, base in zip(repair_lists, bases.tolist())]).astype(np.int64)
         return LinkMaps(request_slots=torch.cat(slot_tensors), blocks=blocks, handles=handles,
                         repair_positions=repair, prefix_token_count=int(counts[leading].sum()),
-                        max_position=max_position, leading_blocks=leading, request_count=len(requests))
+                        max_position=max_position, leading_blocks=leading, request_count=len(requests),
+                        block_requests=np.repeat(np.arange(len(requests), dtype=np.int64), block_counts))
 
     # -- link ---------------------------------------------------------------
     def _layer_groups(self, layers: list[int], max_position: int,
@@ -734,6 +810,7 @@ class KVLinkExecutor:
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, fused_mode=self._fused_mode(),
             delta_staging=self.delta_staging, skipped_rows=self._skip_counter(device),
+            visit_order=self.visit_order,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -768,15 +845,22 @@ class KVLinkExecutor:
             layer_groups_per_block=self.layer_groups_per_block, order_by_source=order_by_source,
             fused_mode=self._fused_mode(), delta_staging=self.delta_staging,
             skipped_rows=self._skip_counter(device),
+            visit_order=None if order_by_source is not None else self.visit_order,
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
 
     def copy_linked_kv(self, pool: Any, destination_slots: torch.Tensor, link_plan: Mapping[str, Any],
-                       **options: Any) -> dict[str, Any]:
+                       *, raise_on_skip: bool = False, **options: Any) -> dict[str, Any]:
         """Link the plan's blocks into ``destination_slots`` (the request's slots
         indexed by request position) on the current stream; returns an
-        accounting record.  Blocks stay pinned while the link is enqueued."""
+        accounting record.  Blocks stay pinned while the link is enqueued.
+
+        The kernel skips a token whose slot or RoPE position is out of range
+        and counts it on the device, where the reference's torch path raises.
+        ``raise_on_skip`` reads the count after the launch (which waits for the
+        stream) and raises ``LinkRuntimeError`` if any token was skipped;
+        without it the caller polls ``check_skipped_rows()``."""
 
         lookup = self.registry.lookup_legolink_blocks(str(key) for key in link_plan.get("cache_keys") or [])
         handles = self.registry.acquire_legolink_blocks(lookup.matched_handles)
@@ -785,6 +869,8 @@ class KVLinkExecutor:
             prepared.launch()
         finally:
             self.registry.release_legolink_blocks(handles)
+        if raise_on_skip:
+            self.check_skipped_rows()
         record = prepared.record()
         record["host_prepare_s"] = prepared.host_prepare_s
         return record

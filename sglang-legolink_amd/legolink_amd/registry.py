@@ -122,7 +122,11 @@ class LegoLinkBlockRegistry:
         self._blocks: dict[str, LegoLinkBlockHandle] = {}
         self._lock = threading.Lock()
         self._generation = 0
+        # Rows of the per-device record tables: a new handle takes an evicted
+        # handle's row before a new one, so the tables stay as large as the
+        # most handles ever registered at once.
         self._rows = 0
+        self._free_rows: list[int] = []
         # Per device: the link records of every handle by row, and which rows are filled.
         self._records: dict[tuple[str, Optional[int]], tuple[np.ndarray, np.ndarray]] = {}
 
@@ -171,11 +175,22 @@ class LegoLinkBlockRegistry:
                 storage_mode=storage_mode,
                 local_start=local_start,
                 max_local_position=max_local,
-                row=self._rows,
+                row=self._take_row(),
             )
-            self._rows += 1
             self._blocks[str(cache_key)] = handle
             return handle
+
+    def _take_row(self) -> int:
+        if self._free_rows:
+            return self._free_rows.pop()
+        self._rows += 1
+        return self._rows - 1
+
+    @property
+    def record_rows(self) -> int:
+        """Rows the per-device record tables hold (live handles at most, at their peak)."""
+
+        return self._rows
 
     def get_legolink_block_tokens(self, cache_key: str) -> Optional[tuple[int, ...]]:
         handle = self._blocks.get(str(cache_key))
@@ -211,9 +226,12 @@ class LegoLinkBlockRegistry:
         gathered from a per-device table (filled once per handle and device),
         so that a link of many blocks reads them with one index."""
 
-        rows = np.fromiter((handle.row for handle in handles), dtype=np.int64, count=len(handles))
         key = (device.type, device.index)
         with self._lock:
+            rows = np.fromiter((handle.row for handle in handles), dtype=np.int64, count=len(handles))
+            if rows.size and int(rows.min()) < 0:
+                stale = next(handle for handle in handles if handle.row < 0)
+                raise ValueError(f"LegoLink block {stale.cache_key} was evicted; it has no link record.")
             table, filled = self._records.get(key, (None, None))
             if table is None or table.shape[0] < self._rows:
                 capacity = max(64, 2 * self._rows)
@@ -255,4 +273,13 @@ class LegoLinkBlockRegistry:
                 return None
             handle.valid = False
             handle.stale_reason = "evicted"
+            # The handle stays (lookups report it stale); its record row and
+            # its per-device copies of the slots and positions are released.
+            if handle.row >= 0:
+                for _, filled in self._records.values():
+                    if handle.row < filled.shape[0]:
+                        filled[handle.row] = False
+                self._free_rows.append(handle.row)
+                handle.row = -1
+            handle._device_tensors.clear()
             return handle

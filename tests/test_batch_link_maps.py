@@ -70,6 +70,8 @@ def _assert_same(a: LinkMaps, b: LinkMaps):
     assert (a.prefix_token_count, a.max_position, a.request_count) == (b.prefix_token_count, b.max_position,
                                                                         b.request_count)
     assert len(a.handles) == len(b.handles) and all(h is g for h, g in zip(a.handles, b.handles))
+    assert np.array_equal(a.block_requests, b.block_requests)
+    assert np.array_equal(a.request_has_clone(), b.request_has_clone())
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -152,3 +154,38 @@ def test_a_stale_block_fails_the_batch():
     registry.evict_legolink_block(stale)
     with pytest.raises(LinkRuntimeError, match=stale):
         executor.build_batch_link_maps(requests, device=CPU)
+
+
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("compact", [True, False])
+def test_entry_flags_follow_each_entrys_request(seed, compact):
+    """set_entry_flags spreads a per-run flag (here: the run's request holds a
+    clone block) over a set's map entries; checked against the entries'
+    requests rebuilt token by token from the plan's own runs."""
+
+    from legolink_amd import link_maps
+
+    rng = np.random.default_rng([5, seed])
+    registry, lengths = _registry(rng)
+    executor = _executor(registry)
+    requests = [_request(rng, lengths) for _ in range(int(rng.integers(2, 6)))]
+    maps = executor.build_batch_link_maps(requests, device=CPU)
+    clone = maps.request_has_clone()
+    for request in range(maps.request_count):
+        own = maps.blocks.sets[maps.block_requests == request]
+        assert bool(clone[request]) == bool((own == 1).any())
+    plan = link_maps.plan_segments(maps.blocks, maps.repair_positions, compact=compact,
+                                   leading_blocks=maps.leading_blocks)
+    run_request = maps.block_requests[plan.segment_blocks]
+    table = plan.table
+    field = link_maps._FIELD
+    for source_set in (0, 1):
+        flags = link_maps.set_entry_flags(plan, source_set, clone[run_request], compact=compact)
+        want = np.full(plan.map_counts[source_set], 255, dtype=np.int64)
+        entries = plan.run_entries(compact)
+        for run in np.flatnonzero(table[:, field["map_set"]] == source_set):
+            offset = table[run, field["map_offset"]]
+            assert (want[offset:offset + entries[run]] == 255).all()  # runs do not overlap
+            want[offset:offset + entries[run]] = clone[run_request[run]]
+        assert (want != 255).all()
+        assert np.array_equal(flags, want.astype(np.uint8))

@@ -205,11 +205,15 @@ def test_random_batches_through_the_executor_match_oracle(gpu_device, seed):
     torch.cuda.synchronize(gpu_device)
     executor.check_skipped_rows()
 
-    rounding = ko.EAGER if prepared.rounding == "eager" else ko.FUSED
+    # Rounding per request, as each request's own link decides it.
+    holds_clone = [any(catalogue[key]["clone"] for key in order) for _, _, order in requests]
+    request_roundings = ["eager" if fused_mode == "disabled" or clone else "fused" for clone in holds_clone]
+    assert prepared.request_roundings == request_roundings
     table = executor.rotary_by_layer[0].cos_sin_cache.cpu().numpy()
     want_k, want_v = before_k, before_v
     repair_destinations = []
-    for destination, plan, order in requests:
+    for (destination, plan, order), request_rounding in zip(requests, request_roundings):
+        rounding = ko.EAGER if request_rounding == "eager" else ko.FUSED
         blocks = []
         for entry, key in zip(plan["block_ranges"], order):
             handle = registry.lookup_legolink_blocks([key]).matched_handles[0]

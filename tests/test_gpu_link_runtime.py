@@ -72,7 +72,7 @@ def test_first_block_remap_cases(gpu_device, case):
                                   ko.f32_to_bf16_bits(compiled.astype(np.float32)))
 
 
-def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="required"):
+def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="required", visit_order=None):
     """Register 5 blocks, derive a plan, link, write repaired rows; the result is
     checked with the oracle of the rounding the fused mode selects."""
 
@@ -103,7 +103,7 @@ def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="require
     linked = resolve_link_plan(registry.get_legolink_block_tokens, host_tokens, plan)
     destination = torch.from_numpy(perm[cursor : cursor + len(linked)]).to(device)
     rotary = RotarySpec.for_theta(2048, dim)
-    executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode=fused_mode)
+    executor = KVLinkExecutor(registry, rotary, end_layer=layers, fused_mode=fused_mode, visit_order=visit_order)
     before_k = [bits(k) for k in pool.k_buffer]
     before_v = [bits(v) for v in pool.v_buffer]
     prepared = executor.prepare_link(pool, destination, plan, boundary_repair_aware=boundary_repair_aware,
@@ -133,6 +133,26 @@ def _flow(device, *, boundary_repair_aware, compact, seed=3, fused_mode="require
         assert np.array_equal(bits(pool.k_buffer[layer]), expected_k[layer]), f"K layer {layer}"
         assert np.array_equal(bits(pool.v_buffer[layer]), expected_v[layer]), f"V layer {layer}"
     return prepared, [bits(k) for k in pool.k_buffer], plan
+
+
+@pytest.mark.parametrize("visit_order", ["plan", "source", "destination"])
+@pytest.mark.parametrize("compact", [True, False])
+def test_visit_orders_match_oracle(gpu_device, visit_order, compact):
+    """The order in which the kernel visits the rotated rows changes nothing:
+    every order, with repair rows compacted or masked, equals the oracle."""
+
+    report(f"visit order {visit_order}, compact {compact}")
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=compact, visit_order=visit_order)
+    assert prepared.visit_order == visit_order
+
+
+def test_single_request_visits_destination_order(gpu_device):
+    prepared, _, _ = _flow(gpu_device, boundary_repair_aware=True, compact=True)
+    assert prepared.visit_order == "destination"
+    maps = prepared._kernel_maps[0]
+    prefix = prepared.segment_plan.set_prefix[0]
+    destinations = maps[1, prefix:].cpu().numpy()
+    assert np.all(np.diff(destinations) > 0)
 
 
 def test_plan_link_repair_flow_matches_oracle(gpu_device):
@@ -251,14 +271,18 @@ def test_prepared_link_replays_in_a_hip_graph(gpu_device):
             assert np.array_equal(a, b), f"replay {replay}"
 
 
+@pytest.mark.parametrize("mix", ["clone_in_every_request", "mixed"])
 @pytest.mark.parametrize("fused_mode", ["disabled", "auto"])
 @pytest.mark.parametrize("order_by_source", [True, False])
-def test_batched_link_equals_request_by_request_links(gpu_device, order_by_source, fused_mode):
+def test_batched_link_equals_request_by_request_links(gpu_device, order_by_source, fused_mode, mix):
     """prepare_links over several requests -- identity first blocks, a request
     behind a chat prefix, a block compiled behind a prefix, clone blocks in
     the snapshot arena, shared blocks, repair rows -- leaves the pool
     bit-identical to linking and repairing each request alone, whether the
-    kernel visits the rows in plan order or in source-slot order."""
+    kernel visits the rows in plan order or in source-slot order.  With
+    "mixed", some requests hold no clone block: under "auto" those link with
+    the fused rounding and the others with the eager one, each as its own
+    link would (pic_runtime.py:5033-5035 decides per request)."""
 
     from legolink_amd.link_runtime import SnapshotArena
 
@@ -298,8 +322,11 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
         return {"cache_keys": list(names), "block_ranges": ranges, "imp_indices": imp}, cursor_
 
     requests = []
-    for names, start in ((["b0", "b1", "b2"], 0), (["b4", "b3"], 5), (["b1", "b5", "b0"], 0),
-                         (["b2", "b4"], 0)):
+    request_names = [(["b0", "b1", "b2"], 0), (["b4", "b3"], 5), (["b1", "b5", "b0"], 0), (["b2", "b4"], 0)]
+    if mix == "mixed":  # requests of reference blocks only, around and between the others
+        request_names = ([(["b3", "b0"], 0)] + request_names[:2] + [(["b5", "b2", "b3"], 7)]
+                         + request_names[2:] + [(["b0", "b5"], 0)])
+    for names, start in request_names:
         plan, total = plan_of(names, start)
         destination = torch.from_numpy(perm[cursor : cursor + total]).to(gpu_device)
         cursor += total
@@ -308,19 +335,26 @@ def test_batched_link_equals_request_by_request_links(gpu_device, order_by_sourc
 
     batched = executor.prepare_links(pool_a, requests, boundary_repair_aware=True, order_by_source=order_by_source)
     assert batched.order_by_source == order_by_source
-    # Every request holds a clone block: the reference's torch path either way.
-    assert batched.rounding == "eager"
+    holds_clone = [any(name in ("b1", "b4") for name in names) for names, _ in request_names]
+    want_roundings = ["eager" if fused_mode == "disabled" or clone else "fused" for clone in holds_clone]
+    assert batched.request_roundings == want_roundings
+    # A request holding a clone block takes the reference's torch path; under
+    # "auto" the other requests keep the fused kernel's rounding.
+    assert batched.rounding == ("mixed" if len(set(want_roundings)) > 1 else "eager")
     assert batched.fallback_reason == (None if fused_mode == "disabled" else "reference_storage_required")
     batched.launch()
     rows = int(batched.repair_offsets.size)
     repaired_k = torch.randn(layers, rows, heads, dim, dtype=torch.bfloat16, device=gpu_device, generator=generator)
     repaired_v = torch.randn_like(repaired_k)
     batched.write_repaired(repaired_k, repaired_v)
-    assert len(batched.launch_info) == 2  # one launch per source: pool, arena
+    # One launch per source (pool, arena); a mixed pool set splits into a
+    # fused and an eager launch.
+    assert len(batched.launch_info) == (3 if batched.rounding == "mixed" else 2)
 
     row = 0
-    for destination, plan in requests:
+    for (destination, plan), rounding in zip(requests, want_roundings):
         single = executor.prepare_link(pool_b, destination, plan, boundary_repair_aware=True)
+        assert single.rounding == rounding
         single.launch()
         count = int(single.repair_offsets.size)
         single.write_repaired(repaired_k[:, row : row + count].contiguous(),

@@ -248,3 +248,45 @@ def test_batched_capture_rejects_before_any_registration():
                                        {"cache_key": "u", "token_ids": [2], "slots": [10]}])
     assert registry.get_legolink_block_tokens("u") is None
     assert registry.get_legolink_block_tokens("r") == (1, 2)  # earlier blocks untouched
+
+
+def test_visit_order_defaults_and_validation():
+    from legolink_amd.link_runtime import _resolve_visit_order
+
+    assert _resolve_visit_order(None, None, 1) == "destination"
+    assert _resolve_visit_order(None, None, 4) == "source"
+    assert _resolve_visit_order(None, False, 4) == "plan"
+    assert _resolve_visit_order(None, True, 1) == "source"
+    assert _resolve_visit_order("plan", True, 4) == "plan"
+    with pytest.raises(ValueError, match="visit_order"):
+        _resolve_visit_order("random", None, 1)
+    with pytest.raises(ValueError, match="visit_order"):
+        KVLinkExecutor(LegoLinkBlockRegistry(), RotarySpec.for_theta(64, 64), end_layer=1, visit_order="sideways")
+
+
+def test_registry_rows_are_reused_after_eviction():
+    """Registering and evicting blocks over and over keeps the per-device record
+    table as large as the most blocks live at once, and an evicted handle's
+    device copies are released."""
+
+    registry = LegoLinkBlockRegistry()
+    cpu = torch.device("cpu")
+    live = []
+    for index in range(2000):
+        handle = registry.register_legolink_block(f"k{index}", range(4), torch.arange(4 * index, 4 * index + 4))
+        records = registry.link_records([handle], cpu)
+        assert records[0, 0] == 4 and records[0, 4] == 0
+        live.append(handle)
+        if len(live) > 5:
+            old = live.pop(0)
+            assert registry.evict_legolink_block(old.cache_key) is old
+            assert old.row == -1 and not old._device_tensors
+    assert registry.record_rows <= 6
+    table, _ = registry._records[(cpu.type, cpu.index)]
+    assert table.shape[0] <= 64
+    # A reused row holds the new handle's record, not the evicted one's.
+    again = registry.register_legolink_block("again", range(9), torch.arange(9))
+    assert registry.link_records([again], cpu)[0, 0] == 9
+    assert registry.lookup_legolink_blocks(["k0"]).stale_blocks == ["k0"]
+    with pytest.raises(ValueError, match="evicted"):
+        registry.link_records([registry._blocks["k0"]], cpu)
