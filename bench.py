@@ -66,6 +66,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--run-sweep", action="store_true",
                         help="time the link kernel on maps whose sources and destinations come in "
                              "contiguous runs of 1..64 slots, for several launch shapes")
+    parser.add_argument("--no-calibration", dest="calibration", action="store_false", default=True,
+                        help="sweep: skip the row calibration (calibration kernels and torch index ops)")
     parser.add_argument("--sweep-detail-run", type=int, default=64,
                         help="run length that gets every launch-shape variant (besides 1)")
     parser.add_argument("--repair-attention", action="store_true",
@@ -206,6 +208,10 @@ def _median_ms(torch, run, steps: int, warmup: int) -> float:
 RUN_LENGTHS = (1, 2, 4, 8, 16, 64)
 
 
+# Orders (at run length 1) on which the sweep also runs the row calibration.
+CALIBRATION_ORDERS = ("random", "sorted_destination", "contiguous")
+
+
 SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", "contiguous",
                 "random_source_contiguous_destination", "contiguous_source_random_destination",
                 "random_in_first_65536_slots", "random_in_first_131072_slots")
@@ -273,6 +279,150 @@ def run_length_maps(workload, run: int, seed: int):
     return src, dst
 
 
+class _RowCalibration:
+    """ctypes binding of liblegolink_calibration.so (csrc/row_calibration.hip):
+    the link's row traffic without the RoPE arithmetic, and its halves."""
+
+    MODES = {"copy": 0, "read_only": 1, "write_only": 2}
+
+    def __init__(self, torch) -> None:
+        import ctypes
+
+        self.ctypes = ctypes
+        path = REPO_ROOT / "sglang-legolink_amd" / "legolink_amd" / "lib" / "liblegolink_calibration.so"
+        if not path.is_file():
+            raise SystemExit(f"{path} is not built (python -c 'import __graft_entry__ as g; g.build()')")
+        self.lib = ctypes.CDLL(str(path))
+        i64, ptr = ctypes.c_int64, ctypes.c_void_p
+
+        class Args(ctypes.Structure):
+            _fields_ = [("struct_size", i64), ("num_layers", i64), ("key_layers", ptr), ("value_layers", ptr),
+                        ("num_slots", i64), ("row_bytes", i64), ("num_tokens", i64), ("source_slots", ptr),
+                        ("destination_slots", ptr), ("mode", i64), ("layer_major", i64),
+                        ("layers_per_wave", i64), ("tokens_per_wave", i64), ("lds_bytes", i64), ("sink", ptr)]
+
+        self.Args = Args
+        self.lib.llc_rows.argtypes = [ctypes.POINTER(Args), ptr]
+        self.lib.llc_rows.restype = ctypes.c_int
+        self.lib.llc_row_args_size.restype = i64
+        self.lib.llc_last_error.restype = ctypes.c_char_p
+        if self.lib.llc_row_args_size() != ctypes.sizeof(Args):
+            raise SystemExit("liblegolink_calibration.so does not match bench.py's argument struct")
+        self.torch = torch
+
+    def prepare(self, keys, values, src, dst, *, mode: str, layer_major: bool, per_wave: int, lds_bytes: int,
+                sink):
+        ctypes = self.ctypes
+        key_table = (ctypes.c_void_p * len(keys))(*[k.data_ptr() for k in keys])
+        value_table = (ctypes.c_void_p * len(values))(*[v.data_ptr() for v in values])
+        args = self.Args(struct_size=ctypes.sizeof(self.Args), num_layers=len(keys),
+                         key_layers=ctypes.addressof(key_table), value_layers=ctypes.addressof(value_table),
+                         num_slots=int(keys[0].shape[0]), row_bytes=int(keys[0][0].numel()) * keys[0].element_size(),
+                         num_tokens=int(src.numel()), source_slots=src.data_ptr(), destination_slots=dst.data_ptr(),
+                         mode=self.MODES[mode], layer_major=1 if layer_major else 0,
+                         layers_per_wave=0 if layer_major else per_wave, tokens_per_wave=per_wave if layer_major else 0,
+                         lds_bytes=lds_bytes, sink=sink.data_ptr())
+        keep = (key_table, value_table, args, keys, values, src, dst, sink)
+        torch = self.torch
+
+        def run() -> None:
+            status = self.lib.llc_rows(ctypes.byref(keep[2]), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if status != 0:
+                raise RuntimeError(f"llc_rows: {self.lib.llc_last_error().decode()}")
+
+        return run
+
+
+# Occupancy limits of the calibration kernels: dynamic LDS per 256-thread
+# workgroup (160 KiB of LDS per CU): none, 40 KiB (4 workgroups per CU), 64 KiB (2).
+CALIBRATION_LDS = (0, 40960, 65536)
+
+
+def calibrate_rows(torch, workload, keys, values, src_t, dst_t, order: str, args) -> list[dict]:
+    """The link's row traffic on these maps, moved by code other than the link
+    kernel: the calibration kernels (copy, read only, write only; token-major
+    4 layers per wave and layer-major 2 tokens per wave; three occupancies)
+    and torch's own index kernels per layer (index_select + index_copy_ as the
+    reference's eager path moves rows, and each half alone: the gather into a
+    contiguous buffer, the scatter from one).  GB/s count the bytes each
+    variant moves: the link's 2 x T x L x (K + V row) for a copy, half of it
+    for a read-only or write-only pass, and the gather's and scatter's own
+    read + write bytes for torch's halves."""
+
+    calibration = _RowCalibration(torch)
+    sink = torch.zeros(65536 * 4, dtype=torch.int32, device=keys[0].device)
+    row = int(keys[0][0].numel()) * keys[0].element_size()
+    one_way = workload.tokens * len(keys) * 2 * row
+    rows = []
+    for mode in ("copy", "read_only", "write_only"):
+        for layer_major, per_wave in ((False, 4), (True, 2)):
+            for lds in CALIBRATION_LDS:
+                run = calibration.prepare(keys, values, src_t, dst_t, mode=mode, layer_major=layer_major,
+                                          per_wave=per_wave, lds_bytes=lds, sink=sink)
+                ms = _median_ms(torch, run, args.steps, args.warmup)
+                moved = 2 * one_way if mode == "copy" else one_way
+                shape = f"{'layer_major_2_tokens' if layer_major else 'token_major_4_layers'}_lds{lds // 1024}k"
+                rows.append({"order": order, "source": "calibration", "mode": mode, "variant": shape,
+                             "ms": round(ms, 5), "bytes": moved, "GBps": round(moved / ms / 1e6, 1)})
+                log(f"calibration {order:18s} {mode:10s} {shape:34s} {ms:.4f} ms {moved / ms / 1e6:8.1f} GB/s")
+    staging_k = torch.empty((workload.tokens,) + tuple(keys[0].shape[1:]), dtype=keys[0].dtype, device=keys[0].device)
+    staging_v = torch.empty_like(staging_k)
+
+    def torch_copy() -> None:
+        for key, value in zip(keys, values):
+            key.index_copy_(0, dst_t, key.index_select(0, src_t))
+            value.index_copy_(0, dst_t, value.index_select(0, src_t))
+
+    def torch_gather() -> None:
+        for key, value in zip(keys, values):
+            torch.index_select(key, 0, src_t, out=staging_k)
+            torch.index_select(value, 0, src_t, out=staging_v)
+
+    def torch_scatter() -> None:
+        for key, value in zip(keys, values):
+            key.index_copy_(0, dst_t, staging_k)
+            value.index_copy_(0, dst_t, staging_v)
+
+    for mode, run in (("copy", torch_copy), ("gather_half", torch_gather), ("scatter_half", torch_scatter)):
+        ms = _median_ms(torch, run, args.steps, args.warmup)
+        moved = 2 * one_way
+        rows.append({"order": order, "source": "torch", "mode": mode,
+                     "variant": {"copy": "index_select + index_copy_ per layer",
+                                 "gather_half": "index_select into a contiguous buffer per layer",
+                                 "scatter_half": "index_copy_ from a contiguous buffer per layer"}[mode],
+                     "ms": round(ms, 5), "bytes": moved, "GBps": round(moved / ms / 1e6, 1)})
+        log(f"torch       {order:18s} {mode:12s} {ms:.4f} ms {moved / ms / 1e6:8.1f} GB/s")
+    return rows
+
+
+def sweep_ceiling(rows: list[dict], calibration: list[dict], link_bytes: int) -> dict:
+    """The fastest valid way to move the workload's own rows (fully fragmented,
+    in any visit order): the link kernel's variants, the calibration copies and
+    torch's copy; and the bound the separately timed halves give when a copy's
+    reads and writes do not slow each other down."""
+
+    own = [r for r in rows if r["run"] == 1 and r["order"] in ("random", "sorted_destination", "sorted_source",
+                                                                "sorted_both")]
+    best_link = max(own, key=lambda r: r["GBps"])
+    fragmented = [c for c in calibration if c["order"] != "contiguous"]
+    copies = [c for c in fragmented if c["mode"] == "copy"]
+    best_copy = max(copies, key=lambda c: c["GBps"])
+    reads = [c for c in fragmented if c["source"] == "calibration" and c["mode"] == "read_only"]
+    writes = [c for c in fragmented if c["source"] == "calibration" and c["mode"] == "write_only"]
+    best_read, best_write = min(reads, key=lambda c: c["ms"]), min(writes, key=lambda c: c["ms"])
+    halves_ms = best_read["ms"] + best_write["ms"]
+    return {
+        "link_kernel_best": {"GBps": best_link["GBps"], "order": best_link["order"], "variant": best_link["variant"]},
+        "independent_copy_best": {"GBps": best_copy["GBps"], "order": best_copy["order"],
+                                  "source": best_copy["source"], "variant": best_copy["variant"]},
+        "read_only_best": {"GBps": best_read["GBps"], "ms": best_read["ms"], "order": best_read["order"],
+                           "variant": best_read["variant"]},
+        "write_only_best": {"GBps": best_write["GBps"], "ms": best_write["ms"], "order": best_write["order"],
+                            "variant": best_write["variant"]},
+        "halves_bound": {"GBps": round(link_bytes / halves_ms / 1e6, 1), "ms": round(halves_ms, 5)},
+    }
+
+
 def run_sweep(args: argparse.Namespace) -> None:
     """The link kernel itself on maps of growing contiguity: how fast the
     kernel moves the workload's rows when sources and destinations come in
@@ -317,7 +467,7 @@ def run_sweep(args: argparse.Namespace) -> None:
         ("staged_deltas_layers_per_wave_2", {"delta_staging": "workgroup", "layers_per_wave": 2}),
         ("staged_deltas_layers_per_wave_7", {"delta_staging": "workgroup", "layers_per_wave": 7}),
     ]
-    rows, schedule, dispatch = [], [], 0
+    rows, schedule, dispatch, calibration, calibration_maps = [], [], 0, [], []
     cases = [(run, "random") for run in RUN_LENGTHS]
     cases += [(1, order) for order in SWEEP_ORDERS if order != "random"]
     for run, order in cases:
@@ -346,8 +496,15 @@ def run_sweep(args: argparse.Namespace) -> None:
                          "frac": round(link_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
                          "launch": prepared.launch})
             log(f"run {run:3d} {order:18s} {name:20s} {ms:.4f} ms  {link_bytes / ms / 1e6:8.1f} GB/s")
-    print(json.dumps({"sweep": rows, "schedule": schedule, "workload": workload.name,
-                      "tokens": workload.tokens, "bytes_per_launch": link_bytes,
+        if args.calibration and run == 1 and order in CALIBRATION_ORDERS:
+            calibration_maps.append((order, src_t, dst_t))
+    # After every link launch, so that the link's dispatches keep their
+    # positions in a counter trace; the calibration's are matched by kernel name.
+    for order, src_t, dst_t in calibration_maps:
+        calibration += calibrate_rows(torch, workload, keys, values, src_t, dst_t, order, args)
+    ceiling = sweep_ceiling(rows, calibration, link_bytes) if calibration else None
+    print(json.dumps({"sweep": rows, "calibration": calibration, "ceiling": ceiling, "schedule": schedule,
+                      "workload": workload.name, "tokens": workload.tokens, "bytes_per_launch": link_bytes,
                       "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 

@@ -22,6 +22,10 @@ SOURCE = PACKAGE_DIR.parent / "csrc" / "legolink_kv.hip"
 SOURCES = (SOURCE, PACKAGE_DIR.parent / "csrc" / "repair_attention.hip")
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
+# The row-access calibration kernels of bench.py's sweep (measurement only,
+# not part of the link's C ABI): their own small library.
+CALIBRATION_SOURCE = PACKAGE_DIR.parent / "csrc" / "row_calibration.hip"
+CALIBRATION_OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_calibration.so"
 # The same library with its host code under AddressSanitizer and
 # UndefinedBehaviorSanitizer (device code unchanged), for the CPU tests of the
 # host entries; never loaded on a GPU.
@@ -58,7 +62,8 @@ def _flags() -> list[str]:
 def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path:
     """Compile every translation unit in parallel, then link the library; the
     output is replaced atomically.  ``sanitize_host`` builds the host-sanitized
-    copy (SANITIZED_OUTPUT) instead."""
+    copy (SANITIZED_OUTPUT) instead.  The unsanitized build also builds the
+    calibration library (CALIBRATION_OUTPUT)."""
 
     output = SANITIZED_OUTPUT if sanitize_host else OUTPUT
     extra = SANITIZE_FLAGS if sanitize_host else []
@@ -70,6 +75,14 @@ def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path
                               stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True), source)
             for source, obj in zip(SOURCES, objects)
         ]
+        calibration = None
+        if not sanitize_host:
+            calibration_tmp = Path(scratch) / CALIBRATION_OUTPUT.name
+            calibration = (subprocess.Popen([hipcc_path(), *_flags(), "-shared", "-o", str(calibration_tmp),
+                                             str(CALIBRATION_SOURCE)],
+                                            stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True),
+                           CALIBRATION_SOURCE)
+            jobs.append(calibration)
         failures = []
         for job, source in jobs:
             printed, _ = job.communicate()
@@ -87,6 +100,8 @@ def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path
         if result.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + "\n".join(_messages(result.stdout + result.stderr)))
         os.replace(temporary, output)
+        if calibration is not None:
+            os.replace(calibration_tmp, CALIBRATION_OUTPUT)
     return output
 
 
