@@ -41,10 +41,28 @@ def make_pool(layers: int, slots: int, heads: int, key_dim: int, value_dim: int,
     return keys, values
 
 
-def row_checksums(buffer: torch.Tensor) -> torch.Tensor:
-    """Per-slot sum of the element bit patterns (int64), computed on the device."""
+_HASH_WEIGHTS: dict = {}
 
-    return buffer.view(torch.int16).sum(dim=(1, 2), dtype=torch.int64)
+
+def row_checksums(buffer: torch.Tensor, chunk: int = 65536) -> torch.Tensor:
+    """Per-slot hash of a row's element bit patterns (int64), on the device:
+    sum_i w_i * bits_i with a distinct pseudo-random weight w_i in
+    [1, 2^20] per element position, so that a stray write that swaps two
+    elements of a row, or copies in a row with the same plain sum, changes
+    it.  |bits| < 2^15 and at most 2^11 elements per row keep the sum below
+    2^46: exact in int64."""
+
+    elements = buffer[0].numel()
+    assert elements <= 2048
+    key = (buffer.device, elements)
+    weights = _HASH_WEIGHTS.get(key)
+    if weights is None:
+        index = torch.arange(elements, dtype=torch.int64)
+        weights = ((index * 2654435761) % (1 << 20) + 1).to(buffer.device)
+        _HASH_WEIGHTS[key] = weights
+    flat = buffer.view(torch.int16).reshape(buffer.shape[0], elements)
+    parts = [(flat[i : i + chunk].to(torch.int64) * weights).sum(dim=1) for i in range(0, flat.shape[0], chunk)]
+    return torch.cat(parts)
 
 
 def _link_through_executor(workload: LinkWorkload, keys, values, table, repaired_k, repaired_v,
@@ -75,7 +93,7 @@ def _link_through_executor(workload: LinkWorkload, keys, values, table, repaired
     assert prepared.linked_token_count == workload.tokens - workload.repair_rows
     assert np.array_equal(prepared.repair_destination_slots.cpu().numpy(), workload.repair_destination_slots)
     launch = dict(prepared.launch_info[0], stream_source_rows=bool(prepared.stream_source_rows),
-                  rounding=prepared.rounding)
+                  rounding=prepared.rounding, visit_order=prepared.visit_order)
     report(f"[{workload.name}] executor link {launch}")
     prepared.launch()
     if with_scatter:

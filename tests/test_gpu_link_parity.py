@@ -436,6 +436,21 @@ def test_full_size_link_as_benched(gpu_device, name):
     assert result["launch"]["stream_source_rows"] and result["launch"]["kernel"] == "vector"
 
 
+def test_full_size_c3_link_as_benched(gpu_device):
+    """c3 as bench.py times it: 64 requests through prepare_links (one map
+    build, the device sort of the rotated rows by source slot, cacheable row
+    loads, per-wave deltas), the write-back of every request's repair rows;
+    16,384 sampled tokens compared with the oracle, and every row outside the
+    destinations checked unchanged."""
+
+    result = check_workload(make_workload("c3"), gpu_device, sample_tokens=16384, via_executor=True,
+                            rounding="fused")
+    assert result["mismatches"] == 0
+    launch = result["launch"]
+    assert launch["kernel"] == "vector" and not launch["stream_source_rows"]
+    assert launch["delta_staging"] == "per_wave" and launch["visit_order"] == "source"
+
+
 @pytest.mark.parametrize("name", ["c2", "c5", "c4"])
 def test_full_size_eager_link(gpu_device, name):
     """The reference's default link (fused mode off: its torch path's rounding)

@@ -100,3 +100,25 @@ def test_workloads_are_deterministic():
     a, b = make_workload("c2"), make_workload("c2")
     assert np.array_equal(a.source_slots, b.source_slots)
     assert np.array_equal(a.local_positions, b.local_positions)
+
+
+def test_row_hash_of_the_gpu_tests_sees_swaps_and_equal_sum_rows():
+    """The untouched-rows check of the GPU parity tests (row_checksums) is a
+    weighted hash: a swap of two elements inside a row, or a row replaced by
+    one with the same plain sum, changes it (checked on CPU tensors)."""
+
+    import torch
+
+    from tests.gpu_helpers import row_checksums
+
+    generator = torch.Generator().manual_seed(3)
+    rows = torch.randn(64, 4, 128, generator=generator).to(torch.bfloat16)
+    base = row_checksums(rows)
+    swapped = rows.clone()
+    swapped[5, 0, 3], swapped[5, 2, 100] = rows[5, 2, 100], rows[5, 0, 3]
+    assert (row_checksums(swapped) != base).tolist() == [i == 5 for i in range(64)]
+    permuted = rows.clone()
+    permuted[9] = rows[9].flip(-1)  # same elements, same plain sum
+    assert rows[9].view(torch.int16).sum() == permuted[9].view(torch.int16).sum()
+    assert row_checksums(permuted)[9] != base[9]
+    assert torch.equal(row_checksums(rows, chunk=7), base)
