@@ -479,9 +479,13 @@ int ll_repair_attention(const ll_repair_attention_args *args, ll_stream_t stream
  *
  * Same arguments, semantics and output as ll_repair_attention, except that
  * args->workspace must be NULL: the split partial results go to a device array
- * of LL_REPAIR_SCRATCH_BYTES that the library holds on every GPU it runs on,
- * from its first use there until the process ends (args->workspace_items
- * still gives the plan's partial count).  A plan whose partials need more --
+ * of LL_REPAIR_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * (args->workspace_items still gives the plan's partial count).  The array
+ * is part of the repair attention's code object: a process is charged
+ * LL_REPAIR_SCRATCH_BYTES of device memory on a GPU from the first repair
+ * attention launch there (through either entry) until it exits; with the
+ * HIP runtime's deferred code-object loading (its default) a process that
+ * only links is not charged.  A plan whose partials need more --
  * workspace_items * num_q_heads * (8 * head_dim + 32) * 4 bytes -- is
  * rejected with LL_ERR_INVALID_ARGUMENT before any launch.  Nothing needs
  * clearing: every partial the combine reads is written by the same call.

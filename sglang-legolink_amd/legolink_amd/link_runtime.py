@@ -129,6 +129,28 @@ class KVPool:
     def get_value_buffer(self, layer_id: int) -> torch.Tensor:
         return self.v_buffer[layer_id - self.start_layer]
 
+    def set_kv_buffer(self, layer: Any, loc: torch.Tensor, cache_k: torch.Tensor, cache_v: torch.Tensor,
+                      k_scale: Optional[float] = None, v_scale: Optional[float] = None) -> None:
+        """K_l[loc[i]] = cache_k[i], V likewise, for ``layer.layer_id`` (the
+        pool's write of SGLang's MHATokenToKVPool, with its signature): rows of
+        another dtype are divided by the layer's scale, when it has one, and
+        cast to the pool's.  One ll_kv_scatter_rows launch on the current stream."""
+
+        layer_id = int(getattr(layer, "layer_id", layer))
+        key_buffer, value_buffer = self.get_key_buffer(layer_id), self.get_value_buffer(layer_id)
+
+        def stored(rows: torch.Tensor, buffer: torch.Tensor, scale: Optional[float]) -> torch.Tensor:
+            rows = rows.reshape(-1, *buffer.shape[1:])
+            if rows.dtype != buffer.dtype:
+                if scale is not None:
+                    rows = rows / scale
+                rows = rows.to(buffer.dtype)
+            return rows.contiguous().unsqueeze(0)
+
+        kv_link.scatter_kv_rows_inplace(key_buffers=[key_buffer], value_buffers=[value_buffer],
+                                        destination_slots=loc, repaired_keys=stored(cache_k, key_buffer, k_scale),
+                                        repaired_values=stored(cache_v, value_buffer, v_scale))
+
 
 class SnapshotArena(KVPool):
     """Storage of clone-mode blocks: the pool's row layout, with a first-fit

@@ -202,3 +202,84 @@ def sparse_repair_attention(query: torch.Tensor, key_buffer: torch.Tensor, value
                                num_kv_heads=int(key_buffer.shape[1]), head_dim=int(key_buffer.shape[2]),
                                pool_size=int(key_buffer.shape[0]))
     return plan.run(query, key_buffer, value_buffer, scale=scale)
+
+
+def _repair_ranges(metadata: dict) -> list[tuple[int, int]]:
+    ranges = metadata.get("repair_ranges")
+    if ranges:
+        return [(int(r["start"]), int(r["end"])) for r in ranges]
+    return [(int(metadata["repair_start"]), int(metadata["repair_end"]))]
+
+
+def try_sparse_repair_attention(q: torch.Tensor, k: Optional[torch.Tensor], v: Optional[torch.Tensor], layer,
+                                forward_batch, save_kv_cache: bool) -> Optional[torch.Tensor]:
+    """The repair pass's attention at the reference's seam:
+    ``try_flashinfer_sparse_attention(q, k, v, layer, forward_batch,
+    save_kv_cache)`` (flashinfer_sparse_repair.py:1944-1972), which
+    ``RadixAttention.forward`` calls for a batch that carries
+    ``pic_sparse_repair_metadata`` (layers/radix_attention.py:125-135).
+
+    Returns None -- the caller's native attention -- when the batch has no
+    repair metadata or its metadata names the native backend
+    (``actual_backend == "native"``, :2023-2024).  Otherwise:
+
+    * the repair rows come from the metadata: ``repair_ranges`` (or
+      ``repair_start`` / ``repair_end``); with several rows in a batch of
+      several requests, row r is request ``req_pool_indices[r]``
+      (_make_flashinfer_row_batch, :1516-1554), else every row is request
+      ``req_pool_indices[0]``; a row's keys are that request's slots
+      ``req_to_token[request, :end]`` (_physical_slot_identity, :1083-1087);
+    * the plan is built at the first layer and kept in the metadata for the
+      later ones (the reference keeps its planned wrapper there, :2193-2200);
+    * with ``save_kv_cache`` the batch's new K/V are written to
+      ``out_cache_loc`` through the pool's ``set_kv_buffer`` before the
+      attention reads the pool (:2235-2239);
+    * the output is ``[tokens, tp_q_head_num * head_dim]`` in q's dtype,
+      with ``layer.scaling`` as the softmax scale.
+    """
+
+    metadata = getattr(forward_batch, "pic_sparse_repair_metadata", None)
+    if not metadata or metadata.get("actual_backend") == "native":
+        return None
+    hq, hkv, dim = int(layer.tp_q_head_num), int(layer.tp_k_head_num), int(layer.head_dim)
+    pool = forward_batch.token_to_kv_pool
+    key_buffer = pool.get_key_buffer(layer.layer_id)
+    value_buffer = pool.get_value_buffer(layer.layer_id)
+    ranges = _repair_ranges(metadata)
+    plan = metadata.get("_hip_repair_plan")
+    plan_key = (str(key_buffer.device), int(key_buffer.shape[0]), hq, hkv, dim, tuple(ranges))
+    if plan is None or metadata.get("_hip_repair_plan_key") != plan_key:
+        requests = forward_batch.req_pool_indices
+        batch_size = int(getattr(forward_batch, "batch_size", 1))
+        per_row = len(ranges) > 1 and batch_size > 1
+        if per_row and len(ranges) != batch_size:
+            raise SparseRepairAttentionError("grouped repair rows must match the batch's requests")
+        table = forward_batch.req_to_token_pool.req_to_token
+        slots: dict[int, torch.Tensor] = {}
+        spans = []
+        for row, (start, end) in enumerate(ranges):
+            request = int(requests[row if per_row else 0])
+            if request not in slots:
+                slots[request] = table[request].to(torch.int32)
+            spans.append((slots[request], start, end))
+        plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim,
+                                   pool_size=int(key_buffer.shape[0]))
+        metadata["_hip_repair_plan"] = plan
+        metadata["_hip_repair_plan_key"] = plan_key
+    else:
+        metadata["plan_reuse_calls"] = int(metadata.get("plan_reuse_calls", 0)) + 1
+    if int(q.numel()) != plan.num_queries * hq * dim:
+        raise SparseRepairAttentionError("query tokens do not match the repair rows")
+    if save_kv_cache and k is not None:
+        pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v, getattr(layer, "k_scale", None),
+                           getattr(layer, "v_scale", None))
+    output = plan.run(q.reshape(plan.num_queries, hq, dim), key_buffer, value_buffer,
+                      scale=float(getattr(layer, "scaling", 1.0 / math.sqrt(dim))))
+    metadata["actual_backend"] = "hip_repair_attention"
+    metadata["layer_calls"] = int(metadata.get("layer_calls", 0)) + 1
+    metadata["run_calls"] = int(metadata.get("run_calls", 0)) + 1
+    return output.view(-1, hq * dim)
+
+
+# The reference's name for the seam, for callers written against it.
+try_flashinfer_sparse_attention = try_sparse_repair_attention
