@@ -54,7 +54,7 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--layers-per-wave", type=int, default=0)
     parser.add_argument("--waves-per-block", type=int, default=4)
     parser.add_argument("--layer-groups-per-block", type=int, default=0)
-    parser.add_argument("--delta-staging", choices=["auto", "per_wave", "workgroup"], default="auto",
+    parser.add_argument("--delta-staging", choices=["auto", "per_wave", "workgroup", "table"], default="auto",
                         help="where the link kernel computes its RoPE deltas (same result)")
     parser.add_argument("--visit-order", choices=["auto", "plan", "source", "destination"], default="auto",
                         help="order in which the link kernel visits the rotated rows (same result; auto: "

@@ -22,8 +22,10 @@
  *   - Device pointers are plain addresses in the device's HIP address space.
  *     Host pointers are marked "host".
  *   - Work is enqueued on `stream` (a hipStream_t) and is asynchronous.  No
- *     entry allocates memory, synchronises or keeps state between calls
- *     other than the thread-local error string.  Entries are reentrant.
+ *     entry allocates device memory, synchronises or keeps state between
+ *     calls other than the thread-local error string and, in
+ *     ll_repair_attention_plan, a thread-local copy of the last plan it
+ *     computed (a cache that no result depends on).  Entries are reentrant.
  *   - A return value of 0 is success; a negative value is one of the LL_ERR_*
  *     codes below, and ll_last_error() then holds a message.
  *   - Rows whose slot index lies outside [0, num_slots) and remapped tokens
@@ -42,7 +44,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 14
+#define LL_ABI_VERSION 15
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -93,6 +95,15 @@ enum {
  *                       two table rows read once per token); neox links
  *                       with full rotary and an fp32 table only, else per
  *                       wave;
+ *   LL_DELTA_TABLE      a first launch writes every token's deltas to a
+ *                       table in delta_workspace; a second, layer-major launch
+ *                       moves two tokens of one layer per wave, reading each
+ *                       token's deltas from that table (the GPU then works on
+ *                       one layer's buffers at a time).  Neox links with full
+ *                       rotary, an fp32 table and rows of a multiple of 1 KiB
+ *                       (num_heads * key_head_dim a multiple of 512), and a
+ *                       workspace of at least num_tokens * rotary_dim * 4
+ *                       bytes, 16-byte aligned; else as LL_DELTA_AUTO;
  *   LL_DELTA_AUTO       workgroup where it fits, the source rows are streamed
  *                       (stream_source_rows) and layer_groups_per_block is 0
  *                       (waves_per_block then sizes per-wave blocks only),
@@ -101,7 +112,8 @@ enum {
 enum {
   LL_DELTA_AUTO = 0,
   LL_DELTA_PER_WAVE = 1,
-  LL_DELTA_WORKGROUP = 2
+  LL_DELTA_WORKGROUP = 2,
+  LL_DELTA_TABLE = 3
 };
 
 /*
@@ -227,6 +239,10 @@ typedef struct ll_kv_link_args {
                                       zeroes it and reads it after the stream's work.  With a
                                       counter, a pool of no rows is rejected (nothing would run
                                       to count) */
+  void *delta_workspace;           /* device scratch of LL_DELTA_TABLE, or NULL (ABI 15): the link
+                                      writes each token's deltas there before it reads them back;
+                                      links that share it must not overlap */
+  int64_t delta_workspace_bytes;   /* its size */
 } ll_kv_link_args;
 
 /*
@@ -508,7 +524,7 @@ typedef struct ll_launch_info {
   int64_t block_threads;
   int64_t layers_per_wave;
   int64_t layer_groups_per_block;
-  int64_t delta_staging;           /* LL_DELTA_PER_WAVE or LL_DELTA_WORKGROUP (vector kernel), else 0 */
+  int64_t delta_staging;           /* LL_DELTA_PER_WAVE, LL_DELTA_WORKGROUP or LL_DELTA_TABLE (vector kernels), else 0 */
 } ll_launch_info;
 
 int ll_kv_link(const ll_kv_link_args *args, ll_stream_t stream);

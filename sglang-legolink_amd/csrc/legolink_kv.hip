@@ -69,6 +69,7 @@ constexpr int kLayerUnroll = LL_LAYER_UNROLL;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // Kernel parameters (passed by value in the kernarg segment; the per-layer
@@ -109,6 +110,7 @@ struct LinkParams {
   int eager;                 // LL_ROUNDING_EAGER: the torch path's rounding points
   int staged;                // vector kernel: deltas staged once per workgroup in LDS
   unsigned long long *skipped;  // tokens skipped for an out-of-range index, or NULL
+  f32x2 *delta_table;        // layer-major kernel: per token and rotary pair (dc, ds)
 };
 
 struct ScatterParams {
@@ -535,6 +537,143 @@ kv_link_vec_kernel(const LinkParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Layer-major link (LL_DELTA_TABLE).  Two launches:
+//
+//   link_delta_table_kernel  entry [t][i] of the delta table = (dc, ds) of
+//                            rotary pair i of token t (one thread per entry,
+//                            consecutive threads on consecutive pairs, so the
+//                            cos/sin rows are read coalesced, once per token);
+//                            (1, 0) where the token keeps its rotation (the
+//                            identity prefix) or a position is out of range.
+//   kv_link_layer_kernel     wave w moves two consecutive tokens of one layer
+//                            (one 1 KiB chunk of their rows per lane group);
+//                            the waves of a launch go through the layers one
+//                            after another, so at any time the GPU reads and
+//                            writes the buffers of about one layer.  Each lane
+//                            reads its 8 pairs' deltas back from the table
+//                            (the table is small and stays in the caches).
+// The arithmetic is the vector kernel's: same delta_pair rounding points, same
+// rotate_neox, same bounds checks, skips and skipped-token count.
+// Requirements (checked on the host): neox, rotary_dim == key_head_dim ==
+// value_head_dim == kD, an fp32 table with unit column stride and 16-byte
+// aligned rows, chunks_per_row a multiple of 64, 16-byte aligned buffers.
+// ---------------------------------------------------------------------------
+constexpr int kLayerMajorWaves = 4;  // waves per workgroup of the layer-major kernel
+
+template <bool kBF16, int kR, typename Index, bool kEager>
+__global__ void __launch_bounds__(256) link_delta_table_kernel(const LinkParams p) {
+  using Round = Rounding<kBF16, 3, kEager>;
+  constexpr int kPairs = kR / 2;
+  const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= p.num_tokens * kPairs) return;
+  const long long t = e / kPairs;
+  const int i = static_cast<int>(e - t * kPairs);
+  float dc = 1.0f, ds = 0.0f;
+  if (t >= p.prefix) {
+    const long long lp = static_cast<long long>(static_cast<const Index *>(p.lpos)[t]);
+    const long long gp = static_cast<long long>(static_cast<const Index *>(p.gpos)[t]);
+    if (lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows) {
+      const float *table = static_cast<const float *>(p.cs);
+      const float lc = table[lp * p.cs_stride_row + i];
+      const float ls = table[lp * p.cs_stride_row + i + kPairs];
+      const float gc = table[gp * p.cs_stride_row + i];
+      const float gs = table[gp * p.cs_stride_row + i + kPairs];
+      delta_pair<Round::kDelta, Round::kCast>(lc, ls, gc, gs, dc, ds);
+    }
+  }
+  f32x2 entry;
+  entry.x = dc;
+  entry.y = ds;
+  p.delta_table[e] = entry;
+}
+
+template <bool kBF16, int kD, typename Index, bool kStream, bool kEager>
+__global__ void __launch_bounds__(kLayerMajorWaves * kWave) kv_link_layer_kernel(const LinkParams p) {
+  constexpr int kChunksPerHead = kD / 8;
+  constexpr int kHalfChunks = kChunksPerHead / 2;  // chunks of a head's first rotate half
+  constexpr int kPairs = kD / 2;                   // rotary pairs of a token (full rotary)
+  using Round = Rounding<kBF16, 3, kEager>;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  // Wave-uniform: the wave's layer, token pair and row part (scalar registers).
+  const long long wave = static_cast<long long>(blockIdx.x) * kLayerMajorWaves +
+                         __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const long long parts = p.chunks_per_row / kWave;
+  const long long pairs = (p.num_tokens + 1) / 2;
+  const long long per_layer = pairs * parts;
+  if (wave >= per_layer * p.num_layers) return;
+  const int layer = static_cast<int>(wave / per_layer);
+  const long long rest = wave - static_cast<long long>(layer) * per_layer;
+  const long long pair = rest / parts;
+  const long long part = rest - pair * parts;
+  const long long c = part * kWave + lane;  // the lane's 16-byte chunk of the row
+  const int q = lane % kChunksPerHead;
+  const bool second_half = q >= kHalfChunks;
+  const int pb = (q % kHalfChunks) * 8;     // the lane's first rotary pair
+
+  u32x4 kin[2], vin[2];
+  long long k_dst[2], v_dst[2], token[2];
+  bool ok[2], remap[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const long long t = 2 * pair + u;
+    const bool in_range = t < p.num_tokens;
+    token[u] = in_range ? t : 2 * pair;
+    const long long tt = token[u];
+    const long long src = static_cast<long long>(static_cast<const Index *>(p.src)[tt]);
+    const long long dst = static_cast<long long>(static_cast<const Index *>(p.dst)[tt]);
+    const long long lp = static_cast<long long>(static_cast<const Index *>(p.lpos)[tt]);
+    const long long gp = static_cast<long long>(static_cast<const Index *>(p.gpos)[tt]);
+    const bool masked = p.mask != nullptr && p.mask[tt] != 0;
+    remap[u] = tt >= p.prefix;
+    const bool positions_ok = lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows;
+    ok[u] = in_range && !masked && src >= 0 && src < p.src_num_slots && dst >= 0 && dst < p.num_slots &&
+            (!remap[u] || positions_ok);
+    // An unmasked token skipped for an out-of-range index is counted once:
+    // by lane 0 of its first row part in layer 0.
+    if (p.skipped != nullptr && in_range && !ok[u] && !masked && layer == 0 && part == 0 && lane == 0)
+      atomicAdd(p.skipped, 1ull);
+    // Unconditional row loads: a token without a valid source reads row 0
+    // (the host launches only when the source pool has rows) and stores nothing.
+    const long long src_row = (src >= 0 && src < p.src_num_slots) ? src : 0;
+    kin[u] = load_row<kStream>(p.sk_layers[layer] + src_row * p.k_row_bytes + c * 16);
+    vin[u] = load_row<kStream>(p.sv_layers[layer] + src_row * p.v_row_bytes + c * 16);
+    k_dst[u] = dst * p.k_row_bytes + c * 16;
+    v_dst[u] = dst * p.v_row_bytes + c * 16;
+  }
+  // The lanes' deltas: 8 consecutive (dc, ds) entries of the token's row of
+  // the table, identity where the token keeps its rotation.
+  f32x4 entries[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const f32x4 *row = reinterpret_cast<const f32x4 *>(p.delta_table + token[u] * kPairs + pb);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) entries[u][k] = row[k];
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float dc[8], dsn[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      dc[2 * k] = entries[u][k][0];
+      dc[2 * k + 1] = entries[u][k][2];
+      const float s0 = entries[u][k][1];
+      const float s1 = entries[u][k][3];
+      dsn[2 * k] = second_half ? s0 : -s0;
+      dsn[2 * k + 1] = second_half ? s1 : -s1;
+    }
+    // Every lane takes part in the exchange (uniform control flow here).
+    const u32x4 partner = xor_lane4<kHalfChunks>(kin[u]);
+    u32x4 kout = kin[u];
+    if (remap[u]) kout = rotate_neox<kBF16, Round::kProd>(kin[u], partner, dc, dsn);
+    if (ok[u]) {
+      store_row_chunk(p.k_layers[layer] + k_dst[u], kout);
+      store_row_chunk(p.v_layers[layer] + v_dst[u], vin[u]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic link kernel: grid.y = layer, blocks stride over tokens, threads over
 // the token's work items (rotary pairs, pass-through K dims, V dims).
 // kKey: 1 = fp16, 2 = bf16.  kCache: 1 = fp16, 2 = bf16, 3 = fp32.
@@ -800,8 +939,9 @@ int validate_link(const ll_kv_link_args *a) {
   if (a->kernel < LL_KERNEL_AUTO || a->kernel > LL_KERNEL_GENERIC)
     return fail(LL_ERR_LAUNCH_CONFIG, "unknown kernel selector %lld",
                 static_cast<long long>(a->kernel));
-  if (a->delta_staging < LL_DELTA_AUTO || a->delta_staging > LL_DELTA_WORKGROUP)
+  if (a->delta_staging < LL_DELTA_AUTO || a->delta_staging > LL_DELTA_TABLE)
     return fail(LL_ERR_LAUNCH_CONFIG, "unknown delta_staging %lld", static_cast<long long>(a->delta_staging));
+  if (a->delta_workspace_bytes < 0) return fail(LL_ERR_INVALID_ARGUMENT, "delta_workspace_bytes is negative");
   if (a->delta_staging == LL_DELTA_WORKGROUP) {
     if (a->waves_per_block < 0 || a->waves_per_block > kMaxWavesPerBlock)
       return fail(LL_ERR_LAUNCH_CONFIG, "waves_per_block must be 0..16 with workgroup-staged deltas");
@@ -852,12 +992,20 @@ struct LinkPlan {
   int layer_groups_per_block;  // vector kernel
   int launches;
   bool staged;  // vector kernel: workgroup-staged deltas
+  bool layer_major;  // delta table + layer-major kernel
 };
 
 // Workgroup-staged deltas need the production shape (neox, full rotary, fp32
 // table) on the vector kernel.
 bool staging_fits(const ll_kv_link_args *a) {
   return a->is_neox_style && a->rotary_dim == a->key_head_dim && a->cos_sin_dtype == LL_DTYPE_FLOAT32;
+}
+
+// The layer-major kernel moves rows in whole 1 KiB chunks per wave and reads
+// each token's deltas from the caller's workspace.
+bool table_fits(const ll_kv_link_args *a) {
+  return staging_fits(a) && (a->num_heads * a->key_head_dim) % 512 == 0 && a->delta_workspace != nullptr &&
+         aligned16(a->delta_workspace) && a->delta_workspace_bytes / 4 / a->rotary_dim >= a->num_tokens;
 }
 
 // Launch shape of the vector kernel.  Short runs of layers per wave keep the
@@ -906,6 +1054,22 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     if (lpw > layers_first) lpw = layers_first;
     plan->layers_per_wave = lpw;
     plan->staged = false;
+    plan->layer_major = false;
+    // The delta table and the layer-major walk on request only: on c2's
+    // random rows a plain copy of one layer's rows at a time moves 3 % more
+    // than a token-major copy, but the link's staged workgroups (all layers of
+    // two tokens) already match the layer-major kernel, and the table's first
+    // launch then costs 1.0-1.4 % (c2 0.7424 against 0.7330 ms, c4, c5).
+    if (a->delta_staging == LL_DELTA_TABLE && table_fits(a)) {
+      const long long pairs = (a->num_tokens + 1) / 2;
+      const long long waves = pairs * (chunks / kWave) * layers_first;
+      plan->layer_major = true;
+      plan->block_threads = kLayerMajorWaves * kWave;
+      plan->grid_x = (waves + kLayerMajorWaves - 1) / kLayerMajorWaves;
+      plan->layers_per_wave = 1;
+      plan->layer_groups_per_block = 1;
+      return plan->grid_x > 0x7fffffffLL ? fail(LL_ERR_LAUNCH_CONFIG, "link too large for one grid") : LL_OK;
+    }
     // By default, staged deltas where they fit and the source rows are
     // streamed (read once, beyond the caches): there they cut the table reads
     // from one per token and layer group to one per token (c2 reads 1.094x ->
@@ -915,7 +1079,8 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     // explicit layer_groups_per_block asks for per-wave deltas.
     const bool want_staged =
         a->delta_staging == LL_DELTA_WORKGROUP ||
-        (a->delta_staging == LL_DELTA_AUTO && a->layer_groups_per_block == 0 && a->stream_source_rows != 0);
+        ((a->delta_staging == LL_DELTA_AUTO || a->delta_staging == LL_DELTA_TABLE) &&
+         a->layer_groups_per_block == 0 && a->stream_source_rows != 0);
     if (want_staged && staging_fits(a)) {
       // Every layer group of a token in one workgroup: G groups of
       // layers_per_wave layers (at most 16, so lpw grows for deep models),
@@ -945,6 +1110,7 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     plan->layers_per_wave = 1;
     plan->layer_groups_per_block = 1;
     plan->staged = false;
+    plan->layer_major = false;
   }
   if (plan->grid_x > 0x7fffffffLL) return fail(LL_ERR_LAUNCH_CONFIG, "link too large for one grid");
   return LL_OK;
@@ -1021,6 +1187,55 @@ void launch_vec(int cache_dtype, int d, dim3 grid, dim3 block, hipStream_t s, co
                 bool neox) {
   if (p.eager) launch_vec_cache<kBF16, true>(cache_dtype, d, grid, block, s, p, neox);
   else launch_vec_cache<kBF16, false>(cache_dtype, d, grid, block, s, p, neox);
+}
+
+// Layer-major link: the delta table once per call, then one kernel per
+// launch of <= 64 layers.
+template <bool kBF16, int kD, typename Index, bool kEager>
+void launch_delta_table_typed(hipStream_t s, const LinkParams &p) {
+  const long long entries = p.num_tokens * (kD / 2);
+  link_delta_table_kernel<kBF16, kD, Index, kEager>
+      <<<dim3(static_cast<unsigned>((entries + 255) / 256)), dim3(256), 0, s>>>(p);
+}
+
+template <bool kBF16, int kD, typename Index, bool kEager>
+void launch_layer_major_typed(dim3 grid, hipStream_t s, const LinkParams &p) {
+  const dim3 block(kLayerMajorWaves * kWave);
+  if (p.stream_rows) kv_link_layer_kernel<kBF16, kD, Index, true, kEager><<<grid, block, 0, s>>>(p);
+  else kv_link_layer_kernel<kBF16, kD, Index, false, kEager><<<grid, block, 0, s>>>(p);
+}
+
+template <bool kBF16, int kD, bool kEager>
+void launch_layer_major_index(bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+  const bool index64 = (p.idx64 & 15) == 15;  // one index type for the four maps (the plan checks)
+  if (table) {
+    if (index64) launch_delta_table_typed<kBF16, kD, long long, kEager>(s, p);
+    else launch_delta_table_typed<kBF16, kD, int, kEager>(s, p);
+  } else {
+    if (index64) launch_layer_major_typed<kBF16, kD, long long, kEager>(grid, s, p);
+    else launch_layer_major_typed<kBF16, kD, int, kEager>(grid, s, p);
+  }
+}
+
+template <bool kBF16, bool kEager>
+void launch_layer_major_dim(bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+  switch (p.kdim) {
+    case 32: launch_layer_major_index<kBF16, 32, kEager>(table, grid, s, p); break;
+    case 64: launch_layer_major_index<kBF16, 64, kEager>(table, grid, s, p); break;
+    case 128: launch_layer_major_index<kBF16, 128, kEager>(table, grid, s, p); break;
+    default: launch_layer_major_index<kBF16, 256, kEager>(table, grid, s, p); break;
+  }
+}
+
+// table: launch the delta table kernel (else the layer-major link kernel).
+void launch_layer_major(bool bf16, bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+  if (bf16) {
+    if (p.eager) launch_layer_major_dim<true, true>(table, grid, s, p);
+    else launch_layer_major_dim<true, false>(table, grid, s, p);
+  } else {
+    if (p.eager) launch_layer_major_dim<false, true>(table, grid, s, p);
+    else launch_layer_major_dim<false, false>(table, grid, s, p);
+  }
 }
 
 template <int kKey, bool kEager>
@@ -1115,7 +1330,10 @@ int ll_kv_link_describe(const ll_kv_link_args *args, ll_launch_info *info) {
   info->block_threads = plan.block_threads;
   info->layers_per_wave = plan.layers_per_wave;
   info->layer_groups_per_block = plan.layer_groups_per_block;
-  info->delta_staging = plan.kernel != LL_KERNEL_VECTOR ? 0 : (plan.staged ? LL_DELTA_WORKGROUP : LL_DELTA_PER_WAVE);
+  info->delta_staging = plan.kernel != LL_KERNEL_VECTOR
+                            ? 0
+                            : (plan.layer_major ? LL_DELTA_TABLE : (plan.staged ? LL_DELTA_WORKGROUP : LL_DELTA_PER_WAVE));
+  if (plan.layer_major) info->grid_y = 1;
   return LL_OK;
 }
 
@@ -1142,6 +1360,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
   p.eager = a->rounding == LL_ROUNDING_EAGER ? 1 : 0;
   p.staged = plan.staged ? 1 : 0;
   p.skipped = reinterpret_cast<unsigned long long *>(a->skipped_rows);
+  p.delta_table = plan.layer_major ? static_cast<f32x2 *>(a->delta_workspace) : nullptr;
   p.cs_rows = a->cos_sin_rows;
   p.cs_stride_row = a->cos_sin_stride_row;
   p.cs_stride_col = a->cos_sin_stride_col;
@@ -1169,6 +1388,11 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
     return LL_OK;
   }
 
+  if (plan.layer_major) {
+    launch_layer_major(bf16, true, dim3(1), s, p);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
   for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
     const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch
                                        ? a->num_layers - base
@@ -1183,7 +1407,12 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
                                                       : a->source_value_layers[base + l]);
     }
     p.num_layers = n;
-    if (plan.kernel == LL_KERNEL_VECTOR) {
+    if (plan.layer_major) {
+      const long long pairs = (p.num_tokens + 1) / 2;
+      const long long waves = pairs * (p.chunks_per_row / kWave) * n;
+      const dim3 grid(static_cast<unsigned>((waves + kLayerMajorWaves - 1) / kLayerMajorWaves));
+      launch_layer_major(bf16, false, grid, s, p);
+    } else if (plan.kernel == LL_KERNEL_VECTOR) {
       const int lpw = plan.layers_per_wave < n ? plan.layers_per_wave : n;
       p.layers_per_wave = lpw;
       p.layer_groups_per_block = plan.layer_groups_per_block;

@@ -929,22 +929,23 @@ int64_t ll_repair_attention_args_size(void) {
   return static_cast<int64_t>(sizeof(ll_repair_attention_args));
 }
 
-int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
-                             int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
-                             int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
-                             int32_t *positions, int64_t positions_capacity,
-                             ll_repair_attention_plan_info *info) {
-  if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
-  if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
-    return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
-  if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0)
-    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be a multiple of num_kv_heads");
-  if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > kDmaMaxRange)
-    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
-                kTile, kDmaMaxRange);
+}  // extern "C"
+
+namespace {
+
+// A plan computed into its own tables.  The last one is kept per thread:
+// the table-sizing call and the table-filling call that follows it with the
+// same rows and heads then compute it once.
+struct RepairPlan {
+  std::vector<ll_repair_row> rows;
+  int64_t num_q_heads = -1, num_kv_heads = -1, split_in = -1;
+  std::vector<int32_t> items, combine, positions;
+  ll_repair_attention_plan_info info{};
+};
+
+int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
+                 int64_t split_tokens, RepairPlan &out) {
   constexpr int64_t kIntMax = 0x7fffffff;
-  if (num_q_heads > 65535)
-    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be at most 65535");
   const int64_t group = num_q_heads / num_kv_heads;
   // 16-query tiles in row order.  Consecutive rows of one request (the next
   // row's queries follow the last one's, same kv_offset) share a tile, so
@@ -961,16 +962,14 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
                   "(query_count >= 1) and fit in int32", static_cast<long long>(r));
     if (row.query_index + row.query_count > num_queries) num_queries = row.query_index + row.query_count;
   }
-  if (positions != nullptr && positions_capacity < num_queries)
-    return fail(LL_ERR_INVALID_ARGUMENT, "positions_capacity %lld is below the %lld queries",
-                static_cast<long long>(positions_capacity), static_cast<long long>(num_queries));
+  out.positions.assign(static_cast<size_t>(num_queries), 0);
+  int32_t *positions = out.positions.data();
   std::vector<Tile> tiles;
   int64_t fill = 0;  // queries in the open tile
   for (int64_t r = 0; r < num_rows; ++r) {
     const ll_repair_row &row = rows[r];
-    if (positions != nullptr)
-      for (int64_t i = 0; i < row.query_count; ++i)
-        positions[row.query_index + i] = static_cast<int32_t>(row.query_start + i);
+    for (int64_t i = 0; i < row.query_count; ++i)
+      positions[row.query_index + i] = static_cast<int32_t>(row.query_start + i);
     const bool continues = fill > 0 && row.kv_offset == tiles.back().kv_offset &&
                            row.query_index == tiles.back().q_index + tiles.back().count;
     if (!continues) fill = 0;
@@ -1087,60 +1086,46 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
   // with more than one.
   int64_t n_items = 0, n_combine = 0, n_partial = 0;
   std::vector<int64_t> chunks(static_cast<size_t>(n_tiles)), base(static_cast<size_t>(n_tiles), -1);
+  out.combine.clear();
   for (int64_t t = 0; t < n_tiles; ++t) {
     chunks[t] = (tiles[t].needed + split - 1) / split;
     if (chunks[t] < 2) continue;
-    if (combine != nullptr) {
-      if (n_combine >= combine_capacity)
-        return fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
-                    static_cast<long long>(combine_capacity));
-      int32_t *ci = combine + n_combine * kCombineInts;
-      ci[0] = static_cast<int32_t>(tiles[t].q_index);
-      ci[1] = static_cast<int32_t>(tiles[t].count);
-      ci[2] = static_cast<int32_t>(n_partial);
-      ci[3] = static_cast<int32_t>(chunks[t]);
-    }
+    out.combine.push_back(static_cast<int32_t>(tiles[t].q_index));
+    out.combine.push_back(static_cast<int32_t>(tiles[t].count));
+    out.combine.push_back(static_cast<int32_t>(n_partial));
+    out.combine.push_back(static_cast<int32_t>(chunks[t]));
     base[t] = n_partial;
     n_partial += chunks[t];
     ++n_combine;
   }
-  int rc = LL_OK;
+  for (const Window &w : windows) n_items += (window_needed(w) + split - 1) / split;
+  if (n_items > kIntMax || n_partial > kIntMax) return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
+  out.items.assign(static_cast<size_t>(n_items * kItemInts), 0);
+  int32_t *items = out.items.data();
+  n_items = 0;
   for (const Window &w : windows) {
     const int64_t needed = window_needed(w);
     const int64_t window_chunks = (needed + split - 1) / split;
-    for (int64_t s = 0; s < window_chunks; ++s) {
-      if (items != nullptr) {
-        if (n_items >= items_capacity) {
-          rc = fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
-                    static_cast<long long>(items_capacity));
-          break;
-        }
-        int32_t *it = items + n_items * kItemInts;
-        for (int i = 0; i < kItemInts; ++i) it[i] = 0;
-        it[0] = static_cast<int32_t>(tiles[w.first].kv_offset);
-        it[1] = static_cast<int32_t>(s * split);
-        it[2] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
-        it[3] = static_cast<int32_t>(w.last - w.first);
-        it[4] = static_cast<int32_t>(w.pair_first);
-        it[5] = static_cast<int32_t>(w.pair_count);
-        for (int64_t t = w.first; t < w.last; ++t) {
-          int32_t *e = it + kItemHeader + kTileInts * (t - w.first);
-          e[0] = static_cast<int32_t>(tiles[t].q_index);
-          e[1] = static_cast<int32_t>(tiles[t].pos);
-          const bool present = s < chunks[t];  // this chunk holds keys the tile sees
-          e[2] = present ? static_cast<int32_t>(tiles[t].count) : 0;
-          e[3] = !present || chunks[t] == 1 ? -1 : static_cast<int32_t>(base[t] + s);
-          e[4] = static_cast<int32_t>(tiles[t].needed);
-        }
+    for (int64_t s = 0; s < window_chunks; ++s, ++n_items) {
+      int32_t *it = items + n_items * kItemInts;  // zeroed by the assign above
+      it[0] = static_cast<int32_t>(tiles[w.first].kv_offset);
+      it[1] = static_cast<int32_t>(s * split);
+      it[2] = static_cast<int32_t>((s + 1) * split < needed ? (s + 1) * split : needed);
+      it[3] = static_cast<int32_t>(w.last - w.first);
+      it[4] = static_cast<int32_t>(w.pair_first);
+      it[5] = static_cast<int32_t>(w.pair_count);
+      for (int64_t t = w.first; t < w.last; ++t) {
+        int32_t *e = it + kItemHeader + kTileInts * (t - w.first);
+        e[0] = static_cast<int32_t>(tiles[t].q_index);
+        e[1] = static_cast<int32_t>(tiles[t].pos);
+        const bool present = s < chunks[t];  // this chunk holds keys the tile sees
+        e[2] = present ? static_cast<int32_t>(tiles[t].count) : 0;
+        e[3] = !present || chunks[t] == 1 ? -1 : static_cast<int32_t>(base[t] + s);
+        e[4] = static_cast<int32_t>(tiles[t].needed);
       }
-      ++n_items;
     }
-    if (rc != LL_OK) break;
   }
-  if (rc != LL_OK) return rc;
-  if (n_items > kIntMax || n_partial > kIntMax)
-    return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
-  if (items != nullptr && n_items > 1) {
+  if (n_items > 1) {
     // Longest key chunks first (the last round then holds the short ones),
     // and among equals the chunks in key order, so that the items running
     // together read the same keys: c5 +7 %, c3 +9 % over plan order.  The
@@ -1158,11 +1143,66 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
              kItemInts * sizeof(int32_t));
     memcpy(items, sorted.data(), sorted.size() * sizeof(int32_t));
   }
-  info->num_items = n_items;
-  info->num_combine = n_combine;
-  info->workspace_items = n_partial;
-  info->split_tokens = split;
-  info->num_queries = num_queries;
+  out.info.num_items = n_items;
+  out.info.num_combine = n_combine;
+  out.info.workspace_items = n_partial;
+  out.info.split_tokens = split;
+  out.info.num_queries = num_queries;
+  return LL_OK;
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_heads,
+                             int64_t num_kv_heads, int64_t split_tokens, int32_t *items,
+                             int64_t items_capacity, int32_t *combine, int64_t combine_capacity,
+                             int32_t *positions, int64_t positions_capacity,
+                             ll_repair_attention_plan_info *info) {
+  if (info == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "info is NULL");
+  if (num_rows < 0 || (num_rows > 0 && rows == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
+  if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be a multiple of num_kv_heads");
+  if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > kDmaMaxRange)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
+                kTile, kDmaMaxRange);
+  if (num_q_heads > 65535)
+    return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be at most 65535");
+  thread_local RepairPlan kept;
+  const bool same_rows =
+      static_cast<int64_t>(kept.rows.size()) == num_rows && kept.num_q_heads == num_q_heads &&
+      kept.num_kv_heads == num_kv_heads &&
+      (split_tokens == kept.split_in || split_tokens == kept.info.split_tokens) &&
+      (num_rows == 0 || memcmp(kept.rows.data(), rows, static_cast<size_t>(num_rows) * sizeof(ll_repair_row)) == 0);
+  if (!same_rows) {
+    kept.num_q_heads = -1;  // invalid until computed
+    const int rc = compute_plan(rows, num_rows, num_q_heads, num_kv_heads, split_tokens, kept);
+    if (rc != LL_OK) return rc;
+    kept.rows.assign(rows, rows + num_rows);
+    kept.num_q_heads = num_q_heads;
+    kept.num_kv_heads = num_kv_heads;
+    kept.split_in = split_tokens;
+  }
+  const ll_repair_attention_plan_info &plan = kept.info;
+  if (positions != nullptr && positions_capacity < plan.num_queries)
+    return fail(LL_ERR_INVALID_ARGUMENT, "positions_capacity %lld is below the %lld queries",
+                static_cast<long long>(positions_capacity), static_cast<long long>(plan.num_queries));
+  if (combine != nullptr && combine_capacity < plan.num_combine)
+    return fail(LL_ERR_INVALID_ARGUMENT, "combine_capacity %lld is too small",
+                static_cast<long long>(combine_capacity));
+  if (items != nullptr && items_capacity < plan.num_items)
+    return fail(LL_ERR_INVALID_ARGUMENT, "items_capacity %lld is too small",
+                static_cast<long long>(items_capacity));
+  if (positions != nullptr && !kept.positions.empty())
+    memcpy(positions, kept.positions.data(), kept.positions.size() * sizeof(int32_t));
+  if (combine != nullptr && !kept.combine.empty())
+    memcpy(combine, kept.combine.data(), kept.combine.size() * sizeof(int32_t));
+  if (items != nullptr && !kept.items.empty())
+    memcpy(items, kept.items.data(), kept.items.size() * sizeof(int32_t));
+  *info = plan;
   return LL_OK;
 }
 

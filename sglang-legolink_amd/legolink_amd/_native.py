@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -37,6 +37,7 @@ ROUNDING_EAGER = 1
 DELTA_AUTO = 0
 DELTA_PER_WAVE = 1
 DELTA_WORKGROUP = 2
+DELTA_TABLE = 3
 
 KERNEL_AUTO = 0
 KERNEL_VECTOR = 1
@@ -117,6 +118,8 @@ class LinkArgs(ctypes.Structure):
         ("rounding", _i64),
         ("delta_staging", _i64),
         ("skipped_rows", _ptr),
+        ("delta_workspace", _ptr),
+        ("delta_workspace_bytes", _i64),
     ]
 
 
@@ -432,11 +435,14 @@ def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_token
     rows_ptr = rows.ctypes.data if rows.size else None
     _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
                                         int(split_tokens), None, 0, None, 0, None, 0, ctypes.byref(info)))
-    items = np.zeros((info.num_items, REPAIR_ITEM_INTS), dtype=np.int32)
-    combine = np.zeros((info.num_combine, REPAIR_COMBINE_INTS), dtype=np.int32)
-    positions = np.zeros(info.num_queries, dtype=np.int32)
+    items = np.empty((info.num_items, REPAIR_ITEM_INTS), dtype=np.int32)
+    combine = np.empty((info.num_combine, REPAIR_COMBINE_INTS), dtype=np.int32)
+    positions = np.empty(info.num_queries, dtype=np.int32)
+    # The sizing call chose the chunk length: the filling call takes it as
+    # given instead of searching again (same plan, half the host time).
+    chosen = int(info.split_tokens)
     _check(lib.ll_repair_attention_plan(rows_ptr, rows.shape[0], int(num_q_heads), int(num_kv_heads),
-                                        int(split_tokens), items.ctypes.data if items.size else None,
+                                        chosen, items.ctypes.data if items.size else None,
                                         info.num_items,
                                         combine.ctypes.data if combine.size else None, info.num_combine,
                                         positions.ctypes.data if positions.size else None, positions.size,

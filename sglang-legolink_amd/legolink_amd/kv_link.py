@@ -61,9 +61,18 @@ ROUNDINGS = {"fused": _native.ROUNDING_FUSED, "eager": _native.ROUNDING_EAGER}
 
 # Where the vector kernel computes each token's RoPE delta (the result is the
 # same): "per_wave" (each wave from the table), "workgroup" (once per workgroup
-# into LDS, the table rows read once per token), "auto" (the library's choice).
+# into LDS, the table rows read once per token), "table" (once per token into
+# a workspace by a first launch, then a layer-major second launch reads them;
+# needs ``delta_workspace``), "auto" (the library's choice).
 DELTA_STAGINGS = {"auto": _native.DELTA_AUTO, "per_wave": _native.DELTA_PER_WAVE,
-                  "workgroup": _native.DELTA_WORKGROUP}
+                  "workgroup": _native.DELTA_WORKGROUP, "table": _native.DELTA_TABLE}
+
+
+def delta_workspace_bytes(token_count: int, rotary_dim: int) -> int:
+    """Bytes of the delta table of a link of ``token_count`` tokens: an fp32
+    (dc, ds) per token and rotary pair."""
+
+    return int(token_count) * int(rotary_dim) * 4
 _DELTA_NAMES = {code: name for name, code in DELTA_STAGINGS.items()}
 
 
@@ -459,6 +468,11 @@ class PreparedKVLink:
     reference's fused operator) or "eager" (its torch path); V and copied K are
     bit copies either way.
 
+    ``delta_workspace`` (a device tensor of at least
+    ``delta_workspace_bytes(tokens, rotary_dim)`` bytes) lets the library
+    compute every token's delta once into a table and walk the rows layer by
+    layer (``delta_staging="table"``); links that share one must not overlap.
+
     ``skipped_rows`` (a one-element int64 device tensor) receives, per call,
     the count of unmasked tokens the kernel skipped because a slot or position
     is out of range; the caller zeroes it and reads it after the stream's work.
@@ -491,6 +505,7 @@ class PreparedKVLink:
         rounding: str = "fused",
         delta_staging: str = "auto",
         skipped_rows: torch.Tensor | None = None,
+        delta_workspace: torch.Tensor | None = None,
     ) -> None:
         key_buffers = list(key_buffers)
         value_buffers = list(value_buffers)
@@ -569,6 +584,11 @@ class PreparedKVLink:
                     or skipped_rows.device != key_buffer.device):
                 raise ValueError("skipped_rows must be a one-element int64 tensor on the link's device")
             self._args.skipped_rows = skipped_rows.data_ptr()
+        if delta_workspace is not None:
+            if not delta_workspace.is_contiguous() or delta_workspace.device != key_buffer.device:
+                raise ValueError("delta_workspace must be a contiguous tensor on the link's device")
+            self._args.delta_workspace = delta_workspace.data_ptr()
+            self._args.delta_workspace_bytes = delta_workspace.numel() * delta_workspace.element_size()
         self._args.struct_size = ctypes.sizeof(_native.LinkArgs)
         # Rows read once (no source repeats within the launch) take non-temporal loads.
         self._args.stream_source_rows = 1 if stream_source_rows else 0
@@ -576,7 +596,7 @@ class PreparedKVLink:
         self._tensors = (
             key_buffers, value_buffers, source_slots, destination_slots,
             local_positions, global_positions, cos_sin_cache, repair_mask,
-            source_key_buffers, source_value_buffers, skipped_rows,
+            source_key_buffers, source_value_buffers, skipped_rows, delta_workspace,
         )
         self.device = key_buffer.device
         try:
@@ -637,6 +657,7 @@ def fused_kv_link_layers_inplace(
     rounding: str = "fused",
     delta_staging: str = "auto",
     skipped_rows: torch.Tensor | None = None,
+    delta_workspace: torch.Tensor | None = None,
 ) -> None:
     """Link every layer in ``key_buffers``/``value_buffers`` with one launch per
     64 layers, on the current stream.  Per layer the result equals
@@ -672,6 +693,7 @@ def fused_kv_link_layers_inplace(
         rounding=rounding,
         delta_staging=delta_staging,
         skipped_rows=skipped_rows,
+        delta_workspace=delta_workspace,
     )
     prepared()
 
@@ -740,6 +762,7 @@ def describe_link_launch(
     rounding: str = "fused",
     delta_staging: str = "auto",
     stream_source_rows: bool = False,
+    delta_workspace: torch.Tensor | None = None,
 ) -> dict[str, Any]:
     """Kernel and launch shape the link would use (no GPU work, no device needed)."""
 
@@ -765,6 +788,9 @@ def describe_link_launch(
         delta_staging=delta_staging,
     )
     args.stream_source_rows = 1 if stream_source_rows else 0
+    if delta_workspace is not None:
+        args.delta_workspace = delta_workspace.data_ptr()
+        args.delta_workspace_bytes = delta_workspace.numel() * delta_workspace.element_size()
     info = _native.kv_link_describe(args)
     del keepalive
     return _launch_record(info)

@@ -13,6 +13,7 @@ lifetime, not link arithmetic, and are not restated.
 
 from __future__ import annotations
 
+import operator
 import threading
 from dataclasses import dataclass, field
 from typing import Any, Iterable, Optional, Sequence
@@ -109,6 +110,9 @@ def _int_array(values: Any) -> np.ndarray:
     if array.size and not np.issubdtype(array.dtype, np.integer):
         array = np.asarray([int(value) for value in values], dtype=np.int64)
     return array.astype(np.int64, copy=False).reshape(-1)
+
+
+_ROW = operator.attrgetter("row")
 
 
 def _int_tuple(values: Any) -> tuple[int, ...]:
@@ -217,7 +221,7 @@ class LegoLinkBlockRegistry:
         reduced to what a link reads, in one pass."""
 
         with self._lock:
-            handles = [self._blocks.get(key) for key in cache_keys]
+            handles = list(map(self._blocks.get, cache_keys))
         unavailable = [str(key) for key, handle in zip(cache_keys, handles) if handle is None or not handle.valid]
         return handles, unavailable
 
@@ -228,7 +232,7 @@ class LegoLinkBlockRegistry:
 
         key = (device.type, device.index)
         with self._lock:
-            rows = np.fromiter((handle.row for handle in handles), dtype=np.int64, count=len(handles))
+            rows = np.fromiter(map(_ROW, handles), dtype=np.int64, count=len(handles))
             if rows.size and int(rows.min()) < 0:
                 stale = next(handle for handle in handles if handle.row < 0)
                 raise ValueError(f"LegoLink block {stale.cache_key} was evicted; it has no link record.")

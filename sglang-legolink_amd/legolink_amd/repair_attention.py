@@ -34,16 +34,6 @@ class SparseRepairAttentionError(RuntimeError):
     """A repair attention request that must not run (flashinfer_sparse_repair.py:65-66)."""
 
 
-def _check_span(slot_ids: torch.Tensor, repair_start: int, repair_end: int) -> None:
-    # The checks and messages of build_explicit_causal_pattern (:1217-1238).
-    if slot_ids.ndim != 1:
-        raise SparseRepairAttentionError("slot_ids must be rank 1")
-    if repair_start < 0 or repair_end <= repair_start:
-        raise SparseRepairAttentionError("invalid repair range")
-    if slot_ids.numel() < repair_end:
-        raise SparseRepairAttentionError("slot_ids is shorter than repair_end")
-
-
 class RepairAttentionPlan:
     """The work of one repair batch: ``spans`` is a list of
     ``(slot_ids, repair_start, repair_end)`` in query order -- the queries of
@@ -72,30 +62,48 @@ class RepairAttentionPlan:
         device = spans[0][0].device
         tables: list[torch.Tensor] = []
         offset_of: dict[int, int] = {}
-        rows = np.empty((len(spans), 4), dtype=np.int64)
+        length_of: dict[int, int] = {}
+        row_list: list[tuple[int, int, int, int]] = []
         cursor = 0
         table_len = 0
         dtype = None
-        for index, (slot_ids, start, end) in enumerate(spans):
-            start, end = int(start), int(end)
-            _check_span(slot_ids, start, end)
-            if slot_ids.device != device:
-                raise SparseRepairAttentionError("repair spans must share one device")
-            if slot_ids.dtype not in (torch.int32, torch.int64):
-                raise SparseRepairAttentionError("slot_ids must be int32 or int64")
+        for slot_ids, start, end in spans:
+            # Spans of one request share its slot tensor: the tensor is checked
+            # once, each span's range every time (the checks and messages of
+            # build_explicit_causal_pattern, :1217-1238).
             key = id(slot_ids)
-            if key not in offset_of:
-                offset_of[key] = table_len
+            base = offset_of.get(key)
+            if base is None:
+                if slot_ids.ndim != 1:
+                    raise SparseRepairAttentionError("slot_ids must be rank 1")
+                if slot_ids.device != device:
+                    raise SparseRepairAttentionError("repair spans must share one device")
+                if slot_ids.dtype not in (torch.int32, torch.int64):
+                    raise SparseRepairAttentionError("slot_ids must be int32 or int64")
+                base = offset_of[key] = table_len
+                length_of[key] = int(slot_ids.numel())
                 tables.append(slot_ids.contiguous())
-                table_len += int(slot_ids.numel())
+                table_len += length_of[key]
                 dtype = slot_ids.dtype if dtype in (None, slot_ids.dtype) else torch.int64
-            rows[index] = (cursor, start, end - start, offset_of[key])
+            start, end = int(start), int(end)
+            if start < 0 or end <= start:
+                raise SparseRepairAttentionError("invalid repair range")
+            if length_of[key] < end:
+                raise SparseRepairAttentionError("slot_ids is shorter than repair_end")
+            row_list.append((cursor, start, end - start, base))
             cursor += end - start
+        rows = np.array(row_list, dtype=np.int64).reshape(-1, 4)
         self.num_queries = cursor
         self.spans = [(int(s), int(e)) for _, s, e in spans]
         table = tables[0] if len(tables) == 1 else torch.cat([t.to(dtype) for t in tables])
         if validate and pool_size is not None:
-            needed = torch.cat([slot_ids[:end] for slot_ids, _, end in spans])
+            # Spans of one request share its slot tensor: each tensor's slots up
+            # to its spans' largest end are checked once.
+            reach: dict[int, int] = {}
+            for slot_ids, _, end in spans:
+                reach[id(slot_ids)] = max(reach.get(id(slot_ids), 0), int(end))
+            needed = [tables[index][: reach[key]] for index, key in enumerate(offset_of)]
+            needed = needed[0] if len(needed) == 1 else torch.cat(needed)
             if bool(((needed < 0) | (needed >= int(pool_size))).any()):
                 raise SparseRepairAttentionError("slot_ids contains invalid KV slots")
         self.kv_slots = table

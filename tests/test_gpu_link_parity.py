@@ -134,8 +134,8 @@ def _run_case(device, case, *, seed=11, mask_dtype=torch.uint8, cache_layout="de
         kernel=kernel, **describe_options,
     )
     assert launch["kernel"] == expected_kernel, launch
-    if link_options.get("delta_staging") == "workgroup":
-        assert launch["delta_staging"] == "workgroup", launch
+    if link_options.get("delta_staging") in ("workgroup", "table"):
+        assert launch["delta_staging"] == link_options["delta_staging"], launch
     kv_link.fused_kv_link_layers_inplace(
         key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
         local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table_dev,
@@ -188,6 +188,98 @@ def test_workgroup_staged_deltas_match_oracle(gpu_device, staged, rounding):
     case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
             mask_fraction, layers, tokens, "vector")
     _run_case(gpu_device, case, rounding=rounding, delta_staging="workgroup", layers_per_wave=lpw)
+
+
+# The delta table and the layer-major walk (neox, full rotary, fp32 table,
+# rows of whole KiB): name, kv dtype, heads, dim, layers, tokens (odd counts
+# leave the last wave one token), prefix (even and odd, so that it ends inside
+# a wave's token pair), mask fraction, index dtype, source pool.
+TABLE_CASES = [
+    ("qwen7b_28_layers", torch.bfloat16, 4, 128, 28, 301, 17, 0.1, torch.int64, "own"),
+    ("qwen7b_even_prefix", torch.bfloat16, 4, 128, 28, 300, 40, 0.0, torch.int32, "own"),
+    ("qwen3_32b_two_parts_per_row", torch.bfloat16, 8, 128, 64, 91, 5, 0.1, torch.int64, "own"),
+    ("seventy_layers_two_launches", torch.bfloat16, 4, 128, 70, 63, 3, 0.1, torch.int64, "own"),
+    ("head_dim_64", torch.float16, 8, 64, 7, 171, 9, 0.1, torch.int64, "own"),
+    ("head_dim_256", torch.bfloat16, 2, 256, 5, 150, 0, 0.1, torch.int32, "own"),
+    ("head_dim_32", torch.bfloat16, 16, 32, 3, 45, 2, 0.1, torch.int64, "own"),
+    ("single_token", torch.bfloat16, 4, 128, 28, 1, 0, 0.0, torch.int64, "own"),
+    ("prefix_is_everything", torch.bfloat16, 4, 128, 6, 100, 100, 0.0, torch.int64, "own"),
+    ("separate_source_pool", torch.bfloat16, 4, 128, 6, 257, 30, 0.1, torch.int64, "separate"),
+]
+
+
+@pytest.mark.parametrize("rounding", ["fused", "eager"])
+@pytest.mark.parametrize("table_case", TABLE_CASES, ids=[case[0] for case in TABLE_CASES])
+def test_delta_table_layer_major_link_matches_oracle(gpu_device, table_case, rounding):
+    name, dtype, heads, dim, layers, tokens, prefix, mask_fraction, index_dtype, source = table_case
+    case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
+            mask_fraction, layers, tokens, "vector")
+    workspace = torch.empty(kv_link.delta_workspace_bytes(tokens, dim) // 4 + 1, dtype=torch.float32,
+                            device=gpu_device)
+    options = {"delta_staging": "table", "delta_workspace": workspace}
+    if source == "separate":
+        _run_separate_source_case(gpu_device, case, rounding=rounding, **options)
+    else:
+        _run_case(gpu_device, case, rounding=rounding, **options)
+
+
+def test_delta_table_without_workspace_falls_back_to_staging(gpu_device):
+    keys, values = make_pool(2, 64, 4, 128, 128, torch.bfloat16, gpu_device, 1)
+    maps = [torch.arange(10, device=gpu_device), torch.arange(20, 30, device=gpu_device),
+            torch.arange(10, device=gpu_device), torch.arange(10, device=gpu_device) + 3]
+    table = build_cos_sin_cache(64, 128).to(gpu_device)
+    common = dict(key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+                  local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table, prefix_token_count=0,
+                  rotary_dim=128, is_neox_style=True, delta_staging="table", stream_source_rows=True)
+    assert kv_link.describe_link_launch(**common)["delta_staging"] == "workgroup"
+    small = torch.empty(10 * 128 - 1, dtype=torch.float32, device=gpu_device)  # one entry short
+    assert kv_link.describe_link_launch(**common, delta_workspace=small)["delta_staging"] == "workgroup"
+    enough = torch.empty(10 * 128, dtype=torch.float32, device=gpu_device)
+    launch = kv_link.describe_link_launch(**common, delta_workspace=enough)
+    assert launch["delta_staging"] == "table" and launch["block_threads"] == 256
+
+
+def _run_separate_source_case(device, case, *, rounding, **link_options):
+    """A link whose sources live in a second pool of the same row layout
+    (the snapshot arena's case), through the delta table."""
+
+    (name, dtype, _, heads, dim, _, rotary, _, _, index_dtype, prefix, mask_fraction, layers, tokens, _) = case
+    report(f"table case {name}: separate source pool, rounding={rounding}")
+    rng = np.random.default_rng(41)
+    slots, arena_slots = 2 * tokens + 9, tokens + 5
+    keys, values = make_pool(layers, slots, heads, dim, dim, dtype, device, 41)
+    arena_k, arena_v = make_pool(layers, arena_slots, heads, dim, dim, dtype, device, 42)
+    src_np = rng.permutation(arena_slots)[:tokens]
+    dst_np = rng.permutation(slots)[:tokens]
+    local_np = rng.integers(0, 9000, size=tokens)
+    global_np = rng.integers(0, 9000, size=tokens)
+    mask_np = (rng.random(tokens) < mask_fraction).astype(np.uint8)
+    table = build_cos_sin_cache(9000, rotary, theta=1e6)
+    expected_k, expected_v = ko.link_pool(
+        [bits(k) for k in keys], [bits(v) for v in values], src_np, dst_np, local_np, global_np, table.numpy(),
+        key_dtype=TORCH_TO_CODE[dtype], cache_dtype=ko.F32, rotary_dim=rotary, neox=True, prefix=prefix,
+        repair_mask=mask_np, source_key_layers=[bits(k) for k in arena_k],
+        source_value_layers=[bits(v) for v in arena_v], rounding=ko.EAGER if rounding == "eager" else ko.FUSED)
+    maps = [torch.from_numpy(a).to(index_dtype).to(device) for a in (src_np, dst_np, local_np, global_np)]
+    kv_link.fused_kv_link_layers_inplace(
+        key_buffers=keys, value_buffers=values, source_slots=maps[0], destination_slots=maps[1],
+        local_positions=maps[2], global_positions=maps[3], cos_sin_cache=table.to(device),
+        prefix_token_count=prefix, rotary_dim=rotary, is_neox_style=True,
+        repair_mask=torch.from_numpy(mask_np).to(device), source_key_buffers=arena_k,
+        source_value_buffers=arena_v, rounding=rounding, **link_options)
+    torch.cuda.synchronize(device)
+    for layer in range(layers):
+        assert np.array_equal(bits(keys[layer]), expected_k[layer]), f"{name}: K layer {layer}"
+        assert np.array_equal(bits(values[layer]), expected_v[layer]), f"{name}: V layer {layer}"
+
+
+@pytest.mark.parametrize("table_case", TABLE_CASES[:4], ids=[case[0] for case in TABLE_CASES[:4]])
+def test_out_of_range_tokens_are_counted_with_the_delta_table(gpu_device, table_case):
+    name, dtype, heads, dim, layers, tokens, prefix, mask_fraction, index_dtype, _ = table_case
+    case = (name, dtype, torch.float32, heads, dim, dim, dim, True, AUTO, index_dtype, prefix,
+            mask_fraction, layers, tokens, "vector")
+    workspace = torch.empty(kv_link.delta_workspace_bytes(tokens, dim), dtype=torch.uint8, device=gpu_device)
+    _run_case(gpu_device, case, delta_staging="table", delta_workspace=workspace, corrupt=0.15, seed=31)
 
 
 SKIP_CASES = [case for case in CASES if case[0] in {

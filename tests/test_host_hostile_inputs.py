@@ -183,7 +183,7 @@ def test_repair_plan_rejects_rows_that_overflow_int32(row):
 def test_link_describe_rejects_hostile_shapes():
     from tests.test_native_abi import _cpu_args
 
-    for field, value in (("num_tokens", 1 << 40), ("prefix_token_count", 9), ("delta_staging", 3),
+    for field, value in (("num_tokens", 1 << 40), ("prefix_token_count", 9), ("delta_staging", 4),
                          ("waves_per_block", 16), ("rounding", 2), ("layers_per_wave", -1),
                          ("num_layers", 0), ("key_head_dim", 300), ("cos_sin_cols", 4)):
         args, keepalive = _cpu_args()

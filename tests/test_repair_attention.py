@@ -329,3 +329,77 @@ def test_attention_entry_validates_before_any_launch():
             _native.repair_attention(args(**overrides), 0)
         assert error.value.reason == reason, overrides
     _native.repair_attention(args(num_items=0), 0)  # nothing to do, no GPU touched
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_plan_filled_with_the_chosen_length_equals_a_searching_fill(seed):
+    """The wrapper sizes the plan with the length search and fills it with the
+    length that search chose; filling while searching again (both calls at 0)
+    gives the same tables."""
+
+    import ctypes
+
+    rng = np.random.default_rng([9, seed])
+    rows, cursor = [], 0
+    for request in range(int(rng.integers(1, 5))):
+        for _ in range(int(rng.integers(1, 60))):
+            count = int(rng.integers(1, 33))
+            rows.append((cursor, int(rng.integers(0, 30000)), count, request * 40000))
+            cursor += count
+    rows = np.asarray(rows, dtype=np.int64)
+    items, combine, positions, info = _native.repair_attention_plan(rows, 28, 4, 0)
+    lib = _native.load_library()
+    again = _native.RepairPlanInfo()
+    items2 = np.zeros_like(items)
+    combine2 = np.zeros_like(combine)
+    positions2 = np.zeros_like(positions)
+    status = lib.ll_repair_attention_plan(
+        rows.ctypes.data, rows.shape[0], 28, 4, 0, items2.ctypes.data if items2.size else None, items2.shape[0],
+        combine2.ctypes.data if combine2.size else None, combine2.shape[0],
+        positions2.ctypes.data if positions2.size else None, positions2.size, ctypes.byref(again))
+    assert status == 0
+    assert again.split_tokens == info.split_tokens and again.num_items == info.num_items
+    assert np.array_equal(items, items2) and np.array_equal(combine, combine2)
+    assert np.array_equal(positions, positions2)
+
+
+def test_kept_plan_never_changes_results():
+    """The planner keeps its last plan per thread; a plan asked again after
+    other plans, with other heads or another chunk length, equals the one
+    computed first, and a changed row is never served from the kept copy."""
+
+    rng = np.random.default_rng(31)
+
+    def random_rows(requests):
+        rows, cursor = [], 0
+        for request in range(requests):
+            for _ in range(int(rng.integers(1, 40))):
+                count = int(rng.integers(1, 33))
+                rows.append((cursor, int(rng.integers(0, 20000)), count, request * 30000))
+                cursor += count
+        return np.asarray(rows, dtype=np.int64)
+
+    a, b = random_rows(3), random_rows(2)
+    first = _native.repair_attention_plan(a, 28, 4, 0)
+    other = _native.repair_attention_plan(b, 28, 4, 0)
+    assert not np.array_equal(first[0], other[0]) or first[0].shape != other[0].shape
+    again = _native.repair_attention_plan(a, 28, 4, 0)
+    for x, y in zip(first[:3], again[:3]):
+        assert np.array_equal(x, y)
+    assert first[3].split_tokens == again[3].split_tokens
+    # Other heads, then an explicit length, on the same rows.
+    grouped = _native.repair_attention_plan(a, 32, 4, 0)
+    fresh_b = _native.repair_attention_plan(b, 28, 4, 0)
+    grouped_again = _native.repair_attention_plan(a, 32, 4, 0)
+    assert np.array_equal(grouped[0], grouped_again[0]) and np.array_equal(fresh_b[0], other[0])
+    explicit = _native.repair_attention_plan(a, 28, 4, 1024)
+    assert explicit[3].split_tokens == 1024
+    _native.repair_attention_plan(b, 28, 4, 0)
+    explicit_again = _native.repair_attention_plan(a, 28, 4, 1024)
+    assert np.array_equal(explicit[0], explicit_again[0]) and np.array_equal(explicit[1], explicit_again[1])
+    # One changed row right after the plan it would otherwise match.
+    changed = a.copy()
+    changed[-1, 1] += 1
+    plan_changed = _native.repair_attention_plan(changed, 28, 4, 0)
+    assert not np.array_equal(plan_changed[2], first[2])
+    assert plan_changed[2][-1] == first[2][-1] + 1
