@@ -551,6 +551,7 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
     import numpy as np
     import torch
 
+    from legolink_amd import _native
     from legolink_amd.link_plan import contiguous_ranges
     from legolink_amd.repair_attention import RepairAttentionPlan
     from legolink_amd.workloads import make_workload
@@ -581,6 +582,9 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
             spans.append((slots, int(start), int(end)))
     plan_times = []
     for _ in range(4):  # the first plan pays torch's first-use costs: report the median of the rest
+        # The planner keeps its last plan per thread; plan other rows first so
+        # that every timed plan is computed, as for a new batch.
+        _native.repair_attention_plan(np.array([[0, 0, 1, 0]], dtype=np.int64), q_heads, shape.kv_heads, 0)
         plan_start = time.perf_counter()
         plan = RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads,
                                    head_dim=shape.head_dim, pool_size=workload.num_slots,

@@ -44,7 +44,6 @@
 #include <algorithm>
 #include <functional>
 #include <mutex>
-#include <queue>
 #include <vector>
 
 #include "legolink_kv.h"
@@ -725,59 +724,90 @@ constexpr int kComputeUnits = 256;          // MI355X
 constexpr double kItemOverheadTiles = 3.0;  // slots, queries, write-out
 constexpr double kPartialBytesPerTile = 12e6;  // partial results the combine reads in one tile's time
 constexpr double kCombineLaunchTiles = 2.0;
+// A plan whose cost provably exceeds `beat` returns early with a lower bound
+// of its cost (still above `beat`).
 template <typename Groups>
-double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_heads, Groups &&groups) {
-  std::vector<double> item_cost;
-  int64_t partials = 0;
+double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_heads, double beat,
+                          Groups &&groups) {
+  // A group of `needed` keys makes needed / split full chunks and one shorter
+  // one.  Costs are whole numbers of tiles, so their sums are exact in double
+  // and do not depend on the order they are added in.
+  const double full_cost = static_cast<double>((split + kTile - 1) / kTile) + kItemOverheadTiles;
+  int64_t partials = 0, count = 0;
+  double total = 0.0, longest = 0.0;
   groups([&](int64_t needed, int64_t group_partials) {
-    for (int64_t begin = 0; begin < needed; begin += split) {
-      const int64_t len = needed - begin < split ? needed - begin : split;
-      item_cost.push_back(static_cast<double>((len + kTile - 1) / kTile) + kItemOverheadTiles);
-    }
-    partials += group_partials;
-  });
-  double makespan = 0.0;
-  const bool many_rounds = static_cast<int64_t>(item_cost.size()) * num_kv_heads > 8 * kComputeUnits;
-  // The plan dispatches its items longest first (see the ordering below).
-  if (!many_rounds) std::sort(item_cost.begin(), item_cost.end(), std::greater<double>());
-  if (many_rounds) {
-    // Many rounds: the last one's imbalance is small against the total; it
-    // leaves about half of the longest item to run alone.
-    double total = 0.0, longest = 0.0;
-    for (const double cost : item_cost) {
+    const int64_t full = needed / split, rest = needed - full * split;
+    count += full + (rest > 0);
+    total += static_cast<double>(full) * full_cost;
+    if (full > 0) longest = full_cost > longest ? full_cost : longest;
+    if (rest > 0) {
+      const double cost = static_cast<double>((rest + kTile - 1) / kTile) + kItemOverheadTiles;
       total += cost;
       longest = cost > longest ? cost : longest;
     }
-    makespan = total * num_kv_heads / kComputeUnits + 0.5 * longest;
-  } else if (static_cast<int64_t>(item_cost.size()) * num_kv_heads <= 2 * kComputeUnits) {
+    partials += group_partials;
+  });
+  double combine_cost = 0.0;
+  if (partials > 0)  // 16 queries' 16-bit outputs (head dim 128) and fp32 (max, sum) per partial and head
+    combine_cost = kCombineLaunchTiles + static_cast<double>(partials) * num_q_heads *
+                                             (kQueries * 128 * 2 + 2 * kQueries * 4) / kPartialBytesPerTile;
+  if (count == 0) return combine_cost;
+  if (count * num_kv_heads > 8 * kComputeUnits) {
+    // Many rounds: the last one's imbalance is small against the total; it
+    // leaves about half of the longest item to run alone.
+    return total * num_kv_heads / kComputeUnits + 0.5 * longest + combine_cost;
+  }
+  // No schedule ends before its longest item or before the CUs have run
+  // every item's work.
+  const double spread = total * static_cast<double>(num_kv_heads) / kComputeUnits;
+  const double bound = (longest > spread ? longest : spread) + combine_cost;
+  if (bound > beat) return bound;
+  double makespan = 0.0;
+  // Item costs in whole tiles, longest first (the order the plan dispatches
+  // its items in, see the ordering below): counted by value, then listed.
+  static_assert(kItemOverheadTiles == 3.0, "the schedule counts whole tiles");
+  constexpr int64_t kOverhead = 3;
+  const int64_t max_cost = (split + kTile - 1) / kTile + kOverhead;
+  std::vector<int64_t> cost_count(static_cast<size_t>(max_cost + 1), 0);
+  groups([&](int64_t needed, int64_t) {
+    const int64_t full = needed / split, rest = needed - full * split;
+    cost_count[static_cast<size_t>(max_cost)] += full;
+    if (rest > 0) ++cost_count[static_cast<size_t>((rest + kTile - 1) / kTile + kOverhead)];
+  });
+  std::vector<int64_t> item_cost;
+  item_cost.reserve(static_cast<size_t>(count));
+  for (int64_t c = max_cost; c > 0; --c) item_cost.insert(item_cost.end(), static_cast<size_t>(cost_count[c]), c);
+  const int64_t n = static_cast<int64_t>(item_cost.size());
+  if (n * num_kv_heads <= 2 * kComputeUnits) {
     // At most two rounds: the workgroups beyond the first 256 start when the
     // first round has ended (measured on c2: its 4 extra workgroups started
     // 72 us into an 82 us kernel, not when the first short items freed their
     // CUs), so the rounds' longest items add up.
-    const int64_t n = static_cast<int64_t>(item_cost.size());
-    double second = 0.0;
+    int64_t second = 0;
     for (int64_t g = kComputeUnits; g < n * num_kv_heads; ++g) {
-      const double cost = item_cost[static_cast<size_t>(g % n)];  // grid order: items, then KV heads
+      const int64_t cost = item_cost[static_cast<size_t>(g % n)];  // grid order: items, then KV heads
       second = cost > second ? cost : second;
     }
-    makespan = item_cost.front() + second;
+    makespan = static_cast<double>(item_cost.front() + second);
   } else {
-    std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
-    for (int i = 0; i < kComputeUnits; ++i) free_at.push(0.0);
+    // Each workgroup starts on the CU that frees first.  Free times are
+    // whole tiles and never earlier than the last start, so the CUs are
+    // counted by free time and the earliest is found by moving forward.
+    std::vector<int32_t> free_from(1, kComputeUnits);
+    int64_t now = 0, last_end = 0;
     for (int64_t h = 0; h < num_kv_heads; ++h) {
-      for (const double cost : item_cost) {
-        const double start = free_at.top();
-        free_at.pop();
-        free_at.push(start + cost);
-        makespan = start + cost > makespan ? start + cost : makespan;
+      for (const int64_t cost : item_cost) {
+        while (free_from[static_cast<size_t>(now)] == 0) ++now;
+        --free_from[static_cast<size_t>(now)];
+        const int64_t end = now + cost;
+        if (end >= static_cast<int64_t>(free_from.size())) free_from.resize(static_cast<size_t>(end + 1), 0);
+        ++free_from[static_cast<size_t>(end)];
+        last_end = end > last_end ? end : last_end;
       }
     }
+    makespan = static_cast<double>(last_end);
   }
-  if (partials > 0)  // 16 queries' 16-bit outputs (head dim 128) and fp32 (max, sum) per partial and head
-    makespan += kCombineLaunchTiles +
-                static_cast<double>(partials) * num_q_heads * (kQueries * 128 * 2 + 2 * kQueries * 4) /
-                    kPartialBytesPerTile;
-  return makespan;
+  return makespan + combine_cost;
 }
 
 bool aligned(const void *ptr, uintptr_t bytes) {
@@ -940,6 +970,7 @@ struct RepairPlan {
   std::vector<ll_repair_row> rows;
   int64_t num_q_heads = -1, num_kv_heads = -1, split_in = -1;
   std::vector<int32_t> items, combine, positions;
+  std::vector<int32_t> sorted;  // reordering space for the items
   ll_repair_attention_plan_info info{};
 };
 
@@ -997,7 +1028,7 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
   struct Window { int64_t first, last, pair_first, pair_count; };
   std::vector<Window> windows;
   std::vector<double> cost;
-  std::vector<int64_t> from;
+  std::vector<int64_t> from, pair_tiles;
   for (int64_t run = 0; run < n_tiles;) {
     int64_t run_end = run + 1;
     while (run_end < n_tiles && tiles[run_end].kv_offset == tiles[run].kv_offset) ++run_end;
@@ -1009,13 +1040,17 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
       const int64_t n = (run_end - run) * group;  // pairs of the run, below 16 per tile
       cost.assign(static_cast<size_t>(n + 1), 0.0);
       from.assign(static_cast<size_t>(n + 1), 0);
+      // Key tiles of each pair's tile (the ceiling of the maximum is the
+      // maximum of the ceilings).
+      pair_tiles.resize(static_cast<size_t>(n));
+      for (int64_t t = run, j = 0; t < run_end; ++t)
+        for (int64_t h = 0; h < group; ++h, ++j) pair_tiles[j] = (tiles[t].needed + kTile - 1) / kTile;
       for (int64_t i = 1; i <= n; ++i) {
         double best = -1.0;
         int64_t furthest = 0;
         for (int64_t j = i - 1; j >= 0 && j >= i - kMaxPairs; --j) {  // window [j, i)
-          const int64_t needed = tiles[run + j / group].needed;
-          furthest = needed > furthest ? needed : furthest;
-          const double c = cost[j] + static_cast<double>((furthest + kTile - 1) / kTile) + kItemOverheadTiles;
+          furthest = pair_tiles[j] > furthest ? pair_tiles[j] : furthest;
+          const double c = cost[j] + static_cast<double>(furthest) + kItemOverheadTiles;
           if (best < 0.0 || c <= best) {  // ties: the longer window
             best = c;
             from[i] = j;
@@ -1032,11 +1067,13 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
     }
     run = run_end;
   }
-  auto window_needed = [&](const Window &w) {
+  std::vector<int64_t> window_keys(windows.size());  // keys of each window's furthest tile
+  for (size_t k = 0; k < windows.size(); ++k) {
     int64_t needed = 0;
-    for (int64_t t = w.first; t < w.last; ++t) needed = tiles[t].needed > needed ? tiles[t].needed : needed;
-    return needed;
-  };
+    for (int64_t t = windows[k].first; t < windows[k].last; ++t)
+      needed = tiles[t].needed > needed ? tiles[t].needed : needed;
+    window_keys[k] = needed;
+  }
   int64_t split = split_tokens;
   if (split == 0) {
     // Pick the chunk length whose plan finishes first on a model of the
@@ -1048,23 +1085,25 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
     // 512 to the maximum, then every multiple of the key tile within 256 of
     // the best: one tile more per item can save a round (c2: 2,112 keys make
     // 64 items, one round of 4 KV heads on 256 CUs, where 2,048 make 65).
+    double best = -1.0;
     auto estimate = [&](int64_t candidate) {
-      return plan_cost_estimate(candidate, num_kv_heads, num_q_heads, [&](auto &&visit) {
+      const double beat = best < 0.0 ? HUGE_VAL : best;
+      return plan_cost_estimate(candidate, num_kv_heads, num_q_heads, beat, [&](auto &&visit) {
         int64_t next_tile = 0;  // a tile's partials count with the first window that holds it
-        for (const Window &w : windows) {
+        for (size_t k = 0; k < windows.size(); ++k) {
+          const Window &w = windows[k];
           int64_t partials = 0;
           for (int64_t t = w.first > next_tile ? w.first : next_tile; t < w.last; ++t) {
             const int64_t chunks = (tiles[t].needed + candidate - 1) / candidate;
             partials += chunks > 1 ? chunks : 0;
           }
           next_tile = w.last > next_tile ? w.last : next_tile;
-          visit(window_needed(w), partials);
+          visit(window_keys[k], partials);
         }
       });
     };
     static const int64_t kCoarse[] = {512,  640,  768,  1024, 1280, 1536, 1792, 2048, 2304,
                                       2560, 3072, 3584, 4096, 4608, 5120, 6144, 7680};
-    double best = -1.0;
     for (const int64_t candidate : kCoarse) {
       const double cost = estimate(candidate);
       if (best < 0.0 || cost <= best) {
@@ -1098,13 +1137,14 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
     n_partial += chunks[t];
     ++n_combine;
   }
-  for (const Window &w : windows) n_items += (window_needed(w) + split - 1) / split;
+  for (const int64_t needed : window_keys) n_items += (needed + split - 1) / split;
   if (n_items > kIntMax || n_partial > kIntMax) return fail(LL_ERR_INVALID_ARGUMENT, "too many work items");
   out.items.assign(static_cast<size_t>(n_items * kItemInts), 0);
   int32_t *items = out.items.data();
   n_items = 0;
-  for (const Window &w : windows) {
-    const int64_t needed = window_needed(w);
+  for (size_t k = 0; k < windows.size(); ++k) {
+    const Window &w = windows[k];
+    const int64_t needed = window_keys[k];
     const int64_t window_chunks = (needed + split - 1) / split;
     for (int64_t s = 0; s < window_chunks; ++s, ++n_items) {
       int32_t *it = items + n_items * kItemInts;  // zeroed by the assign above
@@ -1130,18 +1170,23 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
     // and among equals the chunks in key order, so that the items running
     // together read the same keys: c5 +7 %, c3 +9 % over plan order.  The
     // order is free: every item names its own queries and partial slots.
-    std::vector<int64_t> order(static_cast<size_t>(n_items));
-    for (int64_t i = 0; i < n_items; ++i) order[static_cast<size_t>(i)] = i;
-    std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
-      const int32_t *x = items + a * kItemInts, *y = items + b * kItemInts;
-      const int32_t lx = x[2] - x[1], ly = y[2] - y[1];
-      return lx != ly ? lx > ly : x[1] < y[1];
+    // Keys (longer first, then key begin, then plan order) are distinct, so
+    // an unstable sort of them gives the stable order.
+    struct Key { int32_t neg_len, begin, index; };
+    std::vector<Key> order(static_cast<size_t>(n_items));
+    for (int64_t i = 0; i < n_items; ++i) {
+      const int32_t *x = items + i * kItemInts;
+      order[static_cast<size_t>(i)] = Key{x[1] - x[2], x[1], static_cast<int32_t>(i)};
+    }
+    std::sort(order.begin(), order.end(), [](const Key &a, const Key &b) {
+      return a.neg_len != b.neg_len ? a.neg_len < b.neg_len : a.begin != b.begin ? a.begin < b.begin
+                                                                                 : a.index < b.index;
     });
-    std::vector<int32_t> sorted(static_cast<size_t>(n_items * kItemInts));
+    out.sorted.resize(static_cast<size_t>(n_items * kItemInts));
     for (int64_t i = 0; i < n_items; ++i)
-      memcpy(&sorted[static_cast<size_t>(i * kItemInts)], items + order[static_cast<size_t>(i)] * kItemInts,
+      memcpy(&out.sorted[static_cast<size_t>(i * kItemInts)], items + order[static_cast<size_t>(i)].index * kItemInts,
              kItemInts * sizeof(int32_t));
-    memcpy(items, sorted.data(), sorted.size() * sizeof(int32_t));
+    out.items.swap(out.sorted);
   }
   out.info.num_items = n_items;
   out.info.num_combine = n_combine;
