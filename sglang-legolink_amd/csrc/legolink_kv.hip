@@ -1258,7 +1258,11 @@ void launch_generic(int cache_dtype, dim3 grid, dim3 block, hipStream_t s, const
 // reuse its capacity instead of mapping fresh pages on every call.
 struct PlanScratch {
   struct Seg { int64_t block, a, b, rb, re; };
-  std::vector<int64_t> dstart, offset, positions, by_start, hit_block, hit_offset, bucket, fill, rows, map_offset;
+  struct Run { int64_t first, last; };  // consecutive repair positions, inclusive
+  struct Hit { int64_t begin, end; };   // a block's repair offsets [begin, end)
+  std::vector<int64_t> dstart, offset, positions, by_start, hit_block, bucket, fill, map_offset;
+  std::vector<Run> runs;
+  std::vector<Hit> hits, block_hits;
   std::vector<Seg> segs;
 };
 
@@ -1549,12 +1553,28 @@ int ll_plan_link_runs(const ll_link_block *blocks, int64_t num_blocks, const int
     offset[static_cast<size_t>(b)] = total;
     total += k.token_count;
   }
-  // Repair positions inside blocks, per block, in increasing order.
-  std::vector<int64_t> &positions = w.positions;
-  positions.assign(repair_positions, repair_positions + num_repair_positions);
-  if (!std::is_sorted(positions.begin(), positions.end()))  // plans list them in order
+  // Repair positions as runs of consecutive positions [first, last], sorted
+  // and without duplicates.  Plans list them in increasing order, in runs
+  // (a seam's imp_indices); other inputs are sorted first.
+  std::vector<PlanScratch::Run> &runs = w.runs;
+  auto find_runs = [&runs](const int64_t *p, int64_t n) {  // false where p is not increasing
+    runs.clear();
+    for (int64_t i = 0; i < n;) {
+      int64_t j = i;
+      while (j + 1 < n && p[j] != INT64_MAX && p[j + 1] == p[j] + 1) ++j;
+      if (j + 1 < n && p[j + 1] <= p[j]) return false;
+      runs.push_back(PlanScratch::Run{p[i], p[j]});
+      i = j + 1;
+    }
+    return true;
+  };
+  if (!find_runs(repair_positions, num_repair_positions)) {
+    std::vector<int64_t> &positions = w.positions;
+    positions.assign(repair_positions, repair_positions + num_repair_positions);
     std::sort(positions.begin(), positions.end());
-  positions.erase(std::unique(positions.begin(), positions.end()), positions.end());
+    positions.erase(std::unique(positions.begin(), positions.end()), positions.end());
+    find_runs(positions.data(), static_cast<int64_t>(positions.size()));
+  }
   std::vector<int64_t> &by_start = w.by_start;
   by_start.resize(static_cast<size_t>(num_blocks));
   for (int64_t b = 0; b < num_blocks; ++b) by_start[static_cast<size_t>(b)] = b;
@@ -1565,59 +1585,63 @@ int ll_plan_link_runs(const ll_link_block *blocks, int64_t num_blocks, const int
       return dstart[static_cast<size_t>(x)] < dstart[static_cast<size_t>(y)];
     });
   // Each position belongs to the last block starting at or before it, if it
-  // lies inside that block: one walk over the sorted positions and the blocks
-  // in start order.  Hits are then bucketed by block (counting sort), in
-  // increasing offset order within a block.
-  std::vector<int64_t> &hit_block = w.hit_block, &hit_offset = w.hit_offset;
+  // lies inside that block: block by_start[k] holds the positions of
+  // [its start, min(its end, the next block's start)).  One walk over the
+  // blocks in start order and the runs gives each block's repair runs as
+  // offset ranges [begin, end), increasing.  They are then bucketed by block
+  // (counting sort) when the blocks are not in start order.
+  std::vector<PlanScratch::Hit> &hits = w.hits;
+  std::vector<int64_t> &hit_block = w.hit_block;
+  hits.clear();
   hit_block.clear();
-  hit_offset.clear();
-  size_t k = 0;
-  for (const int64_t position : positions) {
-    while (k + 1 < by_start.size() && dstart[static_cast<size_t>(by_start[k + 1])] <= position) ++k;
-    if (by_start.empty() || dstart[static_cast<size_t>(by_start[k])] > position) continue;
+  size_t r = 0;
+  for (size_t k = 0; k < by_start.size() && r < runs.size(); ++k) {
     const int64_t b = by_start[k];
-    const int64_t inside = position - dstart[static_cast<size_t>(b)];
-    if (inside < blocks[b].token_count) {
+    const int64_t first = dstart[static_cast<size_t>(b)];
+    int64_t owned_end = first + blocks[b].token_count;
+    if (k + 1 < by_start.size()) {
+      const int64_t next = dstart[static_cast<size_t>(by_start[k + 1])];
+      owned_end = next < owned_end ? next : owned_end;
+    }
+    while (r < runs.size() && runs[r].last < first) ++r;
+    for (size_t q = r; q < runs.size() && runs[q].first < owned_end; ++q) {
+      const int64_t lo = runs[q].first > first ? runs[q].first : first;
+      const int64_t hi = runs[q].last < owned_end - 1 ? runs[q].last : owned_end - 1;
+      if (lo > hi) continue;
+      hits.push_back(PlanScratch::Hit{lo - first, hi - first + 1});
       hit_block.push_back(b);
-      hit_offset.push_back(inside);
     }
   }
-  std::vector<int64_t> &bucket = w.bucket, &fill = w.fill, &rows = w.rows;
+  std::vector<int64_t> &bucket = w.bucket, &fill = w.fill;
   bucket.assign(static_cast<size_t>(num_blocks) + 1, 0);
   for (const int64_t b : hit_block) ++bucket[static_cast<size_t>(b) + 1];
   for (size_t b = 0; b < static_cast<size_t>(num_blocks); ++b) bucket[b + 1] += bucket[b];
+  std::vector<PlanScratch::Hit> &block_hits = w.block_hits;
   if (in_order) {
-    rows.swap(hit_offset);  // hits of blocks in position order come grouped by block
+    block_hits.swap(hits);  // hits of blocks in position order come grouped by block
   } else {
-    rows.resize(hit_block.size());  // offsets inside blocks, grouped by block
+    block_hits.resize(hits.size());  // grouped by block, increasing within each
     fill.assign(bucket.begin(), bucket.end() - 1);
-    for (size_t i = 0; i < hit_block.size(); ++i)
-      rows[static_cast<size_t>(fill[static_cast<size_t>(hit_block[i])]++)] = hit_offset[i];
+    for (size_t i = 0; i < hits.size(); ++i)
+      block_hits[static_cast<size_t>(fill[static_cast<size_t>(hit_block[i])]++)] = hits[i];
   }
-  // Segments in plan order: a block's repair rows cut it into runs of
-  // consecutive offsets; segment j of a block spans [first ? 0 : begin_j,
-  // last ? count : begin_{j+1}) and holds repair run j.
+  // Segments in plan order: a block's repair runs cut it; segment j of a
+  // block spans [first ? 0 : begin_j, last ? count : begin_{j+1}) and holds
+  // repair run j.
   std::vector<PlanScratch::Seg> &segs = w.segs;
   segs.clear();
   for (int64_t b = 0; b < num_blocks; ++b) {
-    const int64_t *r = rows.data() + bucket[static_cast<size_t>(b)];
-    const int64_t hits = bucket[static_cast<size_t>(b) + 1] - bucket[static_cast<size_t>(b)];
+    const PlanScratch::Hit *h = block_hits.data() + bucket[static_cast<size_t>(b)];
+    const int64_t count_hits = bucket[static_cast<size_t>(b) + 1] - bucket[static_cast<size_t>(b)];
     const int64_t count = blocks[b].token_count;
-    if (hits == 0) {
+    if (count_hits == 0) {
       if (count > 0) segs.push_back(PlanScratch::Seg{b, 0, count, 0, 0});
       continue;
     }
-    // Runs of consecutive offsets [r[i], r[j]]: segment of run starting at i.
-    int64_t i = 0;
-    bool first_run = true;
-    while (i < hits) {
-      int64_t j = i;
-      while (j + 1 < hits && r[j + 1] == r[j] + 1) ++j;
-      const int64_t a = first_run ? 0 : r[i];
-      const int64_t e = j + 1 == hits ? count : r[j + 1];
-      segs.push_back(PlanScratch::Seg{b, a, e, r[i] - a, r[j] + 1 - a});
-      first_run = false;
-      i = j + 1;
+    for (int64_t i = 0; i < count_hits; ++i) {
+      const int64_t a = i == 0 ? 0 : h[i].begin;
+      const int64_t e = i + 1 == count_hits ? count : h[i + 1].begin;
+      segs.push_back(PlanScratch::Seg{b, a, e, h[i].begin - a, h[i].end - a});
     }
   }
   const int64_t n = static_cast<int64_t>(segs.size());

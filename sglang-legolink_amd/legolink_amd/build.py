@@ -13,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 import tempfile
 from pathlib import Path
 
@@ -26,6 +27,10 @@ OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_kv.so"
 # not part of the link's C ABI): their own small library.
 CALIBRATION_SOURCE = PACKAGE_DIR.parent / "csrc" / "row_calibration.hip"
 CALIBRATION_OUTPUT = PACKAGE_DIR / "lib" / "liblegolink_calibration.so"
+# The CPython module that converts a link plan's lists to int64 arrays
+# (host code only, built with the C compiler against this interpreter).
+HOST_SEQUENCES_SOURCE = PACKAGE_DIR.parent / "csrc" / "host_sequences.c"
+HOST_SEQUENCES_OUTPUT = PACKAGE_DIR / f"_host_sequences{sysconfig.get_config_var('EXT_SUFFIX')}"
 # The same library with its host code under AddressSanitizer and
 # UndefinedBehaviorSanitizer (device code unchanged), for the CPU tests of the
 # host entries; never loaded on a GPU.
@@ -63,7 +68,8 @@ def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path
     """Compile every translation unit in parallel, then link the library; the
     output is replaced atomically.  ``sanitize_host`` builds the host-sanitized
     copy (SANITIZED_OUTPUT) instead.  The unsanitized build also builds the
-    calibration library (CALIBRATION_OUTPUT)."""
+    calibration library (CALIBRATION_OUTPUT) and the host module
+    (HOST_SEQUENCES_OUTPUT)."""
 
     output = SANITIZED_OUTPUT if sanitize_host else OUTPUT
     extra = SANITIZE_FLAGS if sanitize_host else []
@@ -83,12 +89,19 @@ def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path
                                             stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True),
                            CALIBRATION_SOURCE)
             jobs.append(calibration)
+            host_sequences_tmp = Path(scratch) / HOST_SEQUENCES_OUTPUT.name
+            compiler = os.environ.get("CC") or shutil.which("gcc") or "cc"
+            jobs.append((subprocess.Popen([compiler, "-O2", "-shared", "-fPIC", "-Wall",
+                                           f"-I{sysconfig.get_paths()['include']}", "-o", str(host_sequences_tmp),
+                                           str(HOST_SEQUENCES_SOURCE)],
+                                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True),
+                         HOST_SEQUENCES_SOURCE))
         failures = []
         for job, source in jobs:
             printed, _ = job.communicate()
             messages = _messages(printed)
             if job.returncode != 0:
-                failures.append(f"hipcc failed on {source.name}:\n" + "\n".join(messages))
+                failures.append(f"compiling {source.name} failed:\n" + "\n".join(messages))
             elif verbose and messages:
                 print("\n".join(messages), file=sys.stderr)
         if failures:
@@ -102,6 +115,7 @@ def build_library(verbose: bool = False, *, sanitize_host: bool = False) -> Path
         os.replace(temporary, output)
         if calibration is not None:
             os.replace(calibration_tmp, CALIBRATION_OUTPUT)
+            os.replace(host_sequences_tmp, HOST_SEQUENCES_OUTPUT)
     return output
 
 

@@ -39,7 +39,6 @@ Differences from the reference that keep the result identical:
 
 from __future__ import annotations
 
-import array
 import itertools
 import operator
 import os
@@ -53,6 +52,12 @@ import torch
 
 from . import kv_link, link_maps
 from .errors import LinkRuntimeError
+
+try:
+    from . import _host_sequences
+except ImportError as error:  # the C module is built with the library
+    raise ImportError("legolink_amd._host_sequences is not built: run `python -m legolink_amd.build` "
+                      "from sglang-legolink_amd/") from error
 from .registry import LegoLinkBlockHandle, LegoLinkBlockRegistry
 from .rope import RotarySpec
 
@@ -319,18 +324,19 @@ _RANGE_FIELDS = operator.itemgetter("start_token", "end_token")
 def _range_bounds(ranges: Sequence[Mapping[str, Any]]) -> np.ndarray:
     """int64 ``[B, 2]`` (start_token, end_token) of the plan's block ranges."""
 
+    bounds = np.empty((len(ranges), 2), dtype=np.int64)
     try:
-        flat = np.fromiter(itertools.chain.from_iterable(map(_RANGE_FIELDS, ranges)), dtype=np.int64,
-                           count=2 * len(ranges))
-    except (TypeError, ValueError):  # entries that are not plain integers
-        flat = np.array([int(value) for r in ranges for value in _RANGE_FIELDS(r)], dtype=np.int64)
-    return flat.reshape(-1, 2)
+        _host_sequences.fields_from_mappings(ranges, "start_token", "end_token", bounds)
+    except (TypeError, OverflowError):  # fields that are not integers: int() of each, as the reference
+        bounds = np.array([int(value) for r in ranges for value in _RANGE_FIELDS(r)],
+                          dtype=np.int64).reshape(-1, 2)
+    return bounds
 
 
 def _index_array(values: Any) -> np.ndarray:
     """imp_indices as a flat int64 array: a Python list (the reference's plan
-    format) through array.array, the cheapest conversion (about 17 ns per
-    entry against 26 for numpy's); arrays and tensors as they are."""
+    format) or other iterable of integers read item by item in C; arrays and
+    tensors as they are."""
 
     if values is None:
         return np.zeros(0, dtype=np.int64)
@@ -339,8 +345,12 @@ def _index_array(values: Any) -> np.ndarray:
     if isinstance(values, np.ndarray):
         return values.astype(np.int64, copy=False).reshape(-1)
     try:
-        return np.frombuffer(array.array("q", values), dtype=np.int64)
-    except TypeError:  # entries that are not Python ints (numpy scalars, ...)
+        if not isinstance(values, (list, tuple)):
+            values = list(values)  # any other iterable of integers
+        out = np.empty(len(values), dtype=np.int64)
+        _host_sequences.int64_from_sequence(values, out)
+        return out
+    except (TypeError, OverflowError):  # entries that are not integers, or not a sequence
         return np.asarray(values, dtype=np.int64).reshape(-1)
 
 

@@ -106,6 +106,39 @@ def test_run_planner_fuzz_matches_brute_force(seed):
     assert len(covered) == sum(r[1] for r in rows)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_run_planner_matches_brute_force_on_position_runs(seed):
+    """Repair positions in runs (a seam's imp_indices) that start before,
+    cross and end after block boundaries, increasing or shuffled with
+    repeats, and the largest and smallest int64 positions."""
+
+    rng = np.random.default_rng([7, seed])
+    rows, start = [], 0
+    for _ in range(int(rng.integers(1, 14))):
+        count = int(rng.integers(0, 48))
+        rows.append((start, count, 0, int(rng.integers(0, 2)), int(rng.random() < 0.2)))
+        start += count + int(rng.integers(0, 4))
+    if seed % 4 == 3:
+        rows = rows[::-1]
+    blocks = _blocks(rows)
+    runs, cursor = [], int(rng.integers(-6, 6))
+    while cursor < start + 8:
+        length = int(rng.integers(1, 40))
+        runs.extend(range(cursor, cursor + length))
+        cursor += length + int(rng.integers(1, 20))
+    positions = np.array(runs + [(1 << 63) - 1, -(1 << 63)] if seed % 2 else runs, dtype=np.int64)
+    if seed % 3 == 0:
+        positions = np.concatenate([positions, positions[: positions.size // 4]])
+        rng.shuffle(positions)
+    elif seed % 2:
+        positions = np.sort(positions)
+    compact = bool(seed % 5 != 0)
+    table, segment_blocks, repair_offsets, info = _native.plan_link_runs(blocks, positions, compact)
+    entries, expected_repairs = _brute_force(blocks, positions, compact)
+    assert repair_offsets.tolist() == expected_repairs
+    assert _planned_entries(blocks, table, compact) == entries
+
+
 def _raw_plan(blocks, positions, *, segment_capacity, repair_capacity, count=None, positions_count=None):
     lib = _native.load_library()
     blocks = np.ascontiguousarray(blocks, dtype=np.int64)
