@@ -212,7 +212,7 @@ RUN_LENGTHS = (1, 2, 4, 8, 16, 64)
 CALIBRATION_ORDERS = ("random", "sorted_destination", "contiguous")
 
 
-SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", "contiguous",
+SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "bucketed_destination", "sorted_both", "contiguous",
                 "random_source_contiguous_destination", "contiguous_source_random_destination",
                 "random_in_first_65536_slots", "random_in_first_131072_slots")
 
@@ -220,7 +220,9 @@ SWEEP_ORDERS = ("random", "sorted_source", "sorted_destination", "sorted_both", 
 def ordered_maps(workload, run: int, order: str, seed: int):
     """``run_length_maps`` visited in ``order``: "random" (as drawn),
     "sorted_source" / "sorted_destination" (tokens reordered so that one map
-    increases; positions move with their tokens), "sorted_both" (each map
+    increases; positions move with their tokens), "bucketed_destination"
+    (destination slots increasing by bucket of 2^shift slots, as the
+    executor orders a single request's rows), "sorted_both" (each map
     sorted on its own: the same slots, both increasing), "contiguous" (sources
     [0, T), destinations [T, 2T)).  Returns src, dst, local, global."""
 
@@ -251,6 +253,14 @@ def ordered_maps(workload, run: int, order: str, seed: int):
         return src[index], dst[index], local[index], glob[index]
     if order == "sorted_destination":
         index = np.argsort(dst, kind="stable")
+        return src[index], dst[index], local[index], glob[index]
+    if order == "bucketed_destination":
+        # The executor's destination order: by bucket of 2^shift slots (16,384
+        # buckets over the pool), in no fixed order within a bucket (here: as drawn).
+        shift = 0
+        while ((workload.num_slots - 1) >> shift) >= 16384:
+            shift += 1
+        index = np.argsort(dst >> shift, kind="stable")
         return src[index], dst[index], local[index], glob[index]
     if order == "sorted_both":
         return np.sort(src), np.sort(dst), local, glob

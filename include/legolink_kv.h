@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 15
+#define LL_ABI_VERSION 16
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -393,7 +393,53 @@ typedef struct ll_link_maps_args {
   uint8_t *repair_mask[2];         /* device uint8 [map_capacity[s]], or NULL: compacted set */
   int64_t *repair_destination_slots; /* device int64 [repair_capacity], or NULL */
   int64_t repair_capacity;
+  const ll_link_segment *device_segments; /* device copy of segments[0, num_segments), or NULL (ABI 16):
+                                      with it the builder is one launch that reads the runs
+                                      there (each run re-checked on the device, a run that
+                                      fails is left out); without it the runs travel in
+                                      kernel arguments, 56 per launch.  `segments` is
+                                      validated either way. */
 } ll_link_maps_args;
+
+/*
+ * Destination order of a map set.  No counterpart in the reference, whose torch
+ * path writes the rows in plan order: the kernel's result does not depend on
+ * the order it visits the map entries in (every destination row is written
+ * once), and a single request's scattered row writes run faster in
+ * destination-slot order.  This reorders the entries [prefix, count) of a map
+ * set by destination slot into out_maps (and the mask with them), keeping
+ * entries [0, prefix) (the identity rows) first, in two launches: a count of
+ * the entries per bucket of 2^shift consecutive slots (16,384 buckets over
+ * [0, num_slots); slots outside go to the first or last bucket), whose last
+ * workgroup turns the counts into bucket offsets, and a scatter.  Entries of
+ * one bucket are placed in no fixed order; with num_slots <= 16,384 buckets
+ * hold one slot each.  out_maps is a permutation of the entries for any
+ * input, duplicate or out-of-range slots included.
+ *
+ * The workspace (LL_ORDER_WORKSPACE_BYTES, device, 4-byte aligned) must be
+ * zero before its first use; every call leaves it so.  Calls that share a
+ * workspace must not overlap (one stream).
+ */
+#define LL_ORDER_BUCKETS 16384
+#define LL_ORDER_WORKSPACE_BYTES (8 * LL_ORDER_BUCKETS + 256)
+
+typedef struct ll_order_maps_args {
+  int64_t struct_size;             /* sizeof(ll_order_maps_args) */
+  const int64_t *maps;             /* device int64 [4, capacity]: source slots, destination slots,
+                                      local positions, global positions */
+  const uint8_t *mask;             /* device uint8 [capacity], or NULL */
+  int64_t capacity;                /* row stride of maps and out_maps; count <= capacity < 2^31 */
+  int64_t count;                   /* entries */
+  int64_t prefix;                  /* 0 <= prefix <= count: entries kept in place */
+  int64_t num_slots;               /* destination pool rows (>= 1) */
+  int64_t *out_maps;               /* device int64 [4, capacity], not overlapping maps */
+  uint8_t *out_mask;               /* device uint8 [capacity] (NULL iff mask is NULL) */
+  void *workspace;
+  int64_t workspace_bytes;
+} ll_order_maps_args;
+
+int ll_order_link_maps(const ll_order_maps_args *args, ll_stream_t stream);
+int64_t ll_order_maps_args_size(void);
 
 /*
  * Sparse repair attention: the attention of the repair pass over the linked KV.

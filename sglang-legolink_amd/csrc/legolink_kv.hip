@@ -835,8 +835,8 @@ struct MapSegment {
   int set;
 };
 
-struct MapParams {
-  MapSegment seg[kMaxSegmentsPerLaunch];
+// Where the maps go (shared by every run of a launch).
+struct MapTargets {
   const void *dst;
   long long *maps[2];
   long long cap[2];
@@ -845,8 +845,12 @@ struct MapParams {
   int dst64;
 };
 
-__global__ void __launch_bounds__(256) build_link_maps_kernel(const MapParams p) {
-  const MapSegment &sg = p.seg[blockIdx.x];
+struct MapParams {
+  MapSegment seg[kMaxSegmentsPerLaunch];
+  MapTargets t;
+};
+
+__device__ __forceinline__ void map_run_tokens(const MapSegment &sg, const MapTargets &p) {
   const int first = static_cast<int>(blockIdx.y) * kMapTokensPerBlock;
   const int end = min(sg.count, first + kMapTokensPerBlock);
   unsigned char *mask = p.mask[sg.set];
@@ -867,6 +871,132 @@ __global__ void __launch_bounds__(256) build_link_maps_kernel(const MapParams p)
     m[2 * cap + o] = sg.local != nullptr ? sg.local[i] : sg.local_start + i;
     m[3 * cap + o] = pos;
     if (mask != nullptr) mask[o] = repair ? 1 : 0;
+  }
+}
+
+__global__ void __launch_bounds__(256) build_link_maps_kernel(const MapParams p) {
+  map_run_tokens(p.seg[blockIdx.x], p.t);
+}
+
+// The same, with the runs read from a device copy of the run table: one
+// launch for any number of runs.  The host validated its own copy of the
+// table; each block checks its run again against the launch's bounds (the
+// checks of ll_kv_build_link_maps), so a device table that differs from the
+// host's cannot send a write out of range: such a run is left out.
+__global__ void __launch_bounds__(256) build_link_maps_table_kernel(const MapTargets p,
+                                                                    const ll_link_segment *runs,
+                                                                    long long num_destination_slots,
+                                                                    long long repair_capacity) {
+  const ll_link_segment g = runs[blockIdx.x];
+  constexpr long long kIntMax = 0x7fffffff;
+  if (g.token_count <= 0 || g.token_count > kIntMax || g.source_slots == nullptr) return;
+  if (g.map_set != 0 && g.map_set != 1) return;
+  if (g.destination_start < 0 || g.destination_start > num_destination_slots - g.token_count) return;
+  if (g.repair_begin < 0 || g.repair_begin > g.repair_end || g.repair_end > g.token_count) return;
+  const int set = static_cast<int>(g.map_set);
+  const long long repair_rows = g.repair_end - g.repair_begin;
+  const long long entries = g.token_count - (p.mask[set] == nullptr ? repair_rows : 0);
+  if (entries > 0 && (p.maps[set] == nullptr || g.map_offset < 0 || g.map_offset > p.cap[set] - entries)) return;
+  if (g.repair_offset < -1) return;
+  const bool record = repair_rows > 0 && g.repair_offset >= 0;
+  if (record && (p.repair_dst == nullptr || g.repair_offset > repair_capacity - repair_rows)) return;
+  MapSegment sg;
+  sg.src = reinterpret_cast<const long long *>(g.source_slots);
+  sg.local = reinterpret_cast<const long long *>(g.local_positions);
+  sg.start = g.start_token;
+  sg.dst_start = g.destination_start;
+  sg.local_start = g.local_start;
+  sg.count = static_cast<int>(g.token_count);
+  sg.map_offset = static_cast<int>(g.map_offset);
+  sg.repair_begin = static_cast<int>(g.repair_begin);
+  sg.repair_end = static_cast<int>(g.repair_end);
+  sg.repair_offset = record ? static_cast<int>(g.repair_offset) : -1;
+  sg.set = set;
+  map_run_tokens(sg, p);
+}
+
+// ---------------------------------------------------------------------------
+// Destination order of a map set: a counting sort over buckets of 2^shift
+// consecutive destination slots.  The count launch adds every entry to its
+// bucket's counter (device-scope atomics); the workgroup that finishes last
+// (an arrival counter) turns the counts into exclusive offsets, clears the
+// counters and the arrival counter for the next call.  The scatter launch
+// takes each entry's place with an atomic increment of its bucket's offset.
+// Every wave of both launches exits: no workgroup waits for another.
+// ---------------------------------------------------------------------------
+constexpr int kOrderBuckets = LL_ORDER_BUCKETS;
+constexpr int kOrderThreads = 1024;
+static_assert(kOrderBuckets % kOrderThreads == 0, "whole bucket runs per thread");
+
+struct OrderParams {
+  const long long *maps;
+  const unsigned char *mask;
+  long long cap, count, prefix, num_slots;
+  int shift;
+  long long *out;
+  unsigned char *out_mask;
+  int *counts;            // [kOrderBuckets]: zero between calls
+  int *offsets;           // [kOrderBuckets]
+  unsigned int *arrived;  // zero between calls
+};
+
+__device__ __forceinline__ int order_bucket(long long slot, const OrderParams &p) {
+  if (slot < 0) return 0;
+  if (slot >= p.num_slots) return kOrderBuckets - 1;
+  return static_cast<int>(slot >> p.shift);  // below kOrderBuckets by the choice of shift
+}
+
+__global__ void __launch_bounds__(kOrderThreads) order_count_kernel(const OrderParams p) {
+  const long long n = p.count - p.prefix;
+  const long long *dst = p.maps + p.cap + p.prefix;
+  for (long long i = static_cast<long long>(blockIdx.x) * kOrderThreads + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * kOrderThreads)
+    atomicAdd(&p.counts[order_bucket(dst[i], p)], 1);
+  __shared__ int last;
+  __shared__ int sums[kOrderThreads];
+  __threadfence();  // this workgroup's counts before its arrival
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicAdd(p.arrived, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  constexpr int kPer = kOrderBuckets / kOrderThreads;
+  int own[kPer];
+  int total = 0;
+  for (int k = 0; k < kPer; ++k) {
+    own[k] = __hip_atomic_load(&p.counts[threadIdx.x * kPer + k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    total += own[k];
+  }
+  sums[threadIdx.x] = total;
+  __syncthreads();
+  for (int step = 1; step < kOrderThreads; step <<= 1) {  // inclusive scan of the per-thread totals
+    const int add = threadIdx.x >= static_cast<unsigned>(step) ? sums[threadIdx.x - step] : 0;
+    __syncthreads();
+    sums[threadIdx.x] += add;
+    __syncthreads();
+  }
+  int offset = sums[threadIdx.x] - total;
+  for (int k = 0; k < kPer; ++k) {
+    p.offsets[threadIdx.x * kPer + k] = offset;
+    offset += own[k];
+    p.counts[threadIdx.x * kPer + k] = 0;
+  }
+  if (threadIdx.x == 0) *p.arrived = 0u;
+}
+
+__global__ void __launch_bounds__(256) order_scatter_kernel(const OrderParams p) {
+  const long long n = p.count - p.prefix;
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < p.count;
+       i += static_cast<long long>(gridDim.x) * 256) {
+    long long o = i;
+    if (i >= p.prefix) {
+      const long long place = atomicAdd(&p.offsets[order_bucket(p.maps[p.cap + i], p)], 1);
+      if (place < 0 || place >= n) continue;  // only if the workspace was shared by overlapping calls
+      o = p.prefix + place;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p.out[r * p.cap + o] = p.maps[r * p.cap + i];
+    if (p.mask != nullptr) p.out_mask[o] = p.mask[i];
   }
 }
 
@@ -1777,15 +1907,31 @@ int ll_kv_build_link_maps(const ll_link_maps_args *a, ll_stream_t stream) {
 
   MapParams p;
   memset(&p, 0, sizeof(p));
-  p.dst = a->destination_slots;
-  p.dst64 = a->destination_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
+  p.t.dst = a->destination_slots;
+  p.t.dst64 = a->destination_slots_dtype == LL_DTYPE_INT64 ? 1 : 0;
   for (int s = 0; s < 2; ++s) {
-    p.maps[s] = reinterpret_cast<long long *>(a->maps[s]);
-    p.cap[s] = a->map_capacity[s];
-    p.mask[s] = a->repair_mask[s];
+    p.t.maps[s] = reinterpret_cast<long long *>(a->maps[s]);
+    p.t.cap[s] = a->map_capacity[s];
+    p.t.mask[s] = a->repair_mask[s];
   }
-  p.repair_dst = reinterpret_cast<long long *>(a->repair_destination_slots);
+  p.t.repair_dst = reinterpret_cast<long long *>(a->repair_destination_slots);
   hipStream_t stream_h = reinterpret_cast<hipStream_t>(stream);
+  if (a->device_segments != nullptr) {
+    // One launch over the device copy of the runs.
+    int64_t longest = 0;
+    for (int64_t k = 0; k < a->num_segments; ++k)
+      longest = a->segments[k].token_count > longest ? a->segments[k].token_count : longest;
+    if (longest == 0) return LL_OK;
+    if (a->num_segments > kIntMax)
+      return fail(LL_ERR_INVALID_ARGUMENT, "num_segments must be below 2^31 with device_segments");
+    const dim3 grid(static_cast<unsigned>(a->num_segments),
+                    static_cast<unsigned>((longest + kMapTokensPerBlock - 1) / kMapTokensPerBlock));
+    build_link_maps_table_kernel<<<grid, dim3(256), 0, stream_h>>>(p.t, a->device_segments,
+                                                                    a->num_destination_slots, a->repair_capacity);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return LL_OK;
+  }
   int n = 0;
   int64_t longest = 0;
   auto launch = [&]() -> int {
@@ -1823,6 +1969,68 @@ int ll_kv_build_link_maps(const ll_link_maps_args *a, ll_stream_t stream) {
     }
   }
   return launch();
+}
+
+int64_t ll_order_maps_args_size(void) { return static_cast<int64_t>(sizeof(ll_order_maps_args)); }
+
+int ll_order_link_maps(const ll_order_maps_args *a, ll_stream_t stream) {
+  if (a == nullptr) return fail(LL_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->struct_size != static_cast<int64_t>(sizeof(ll_order_maps_args)))
+    return fail(LL_ERR_INVALID_ARGUMENT, "struct_size %lld != %zu",
+                static_cast<long long>(a->struct_size), sizeof(ll_order_maps_args));
+  constexpr int64_t kIntMax = 0x7fffffff;
+  if (a->capacity < 0 || a->capacity > kIntMax || a->count < 0 || a->count > a->capacity || a->prefix < 0 ||
+      a->prefix > a->count)
+    return fail(LL_ERR_INVALID_ARGUMENT, "need 0 <= prefix <= count <= capacity < 2^31");
+  if (a->num_slots < 1) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots must be >= 1");
+  if (a->count == 0) return LL_OK;
+  if (a->maps == nullptr || a->out_maps == nullptr)
+    return fail(LL_ERR_INVALID_ARGUMENT, "maps and out_maps must be device arrays");
+  if ((a->mask == nullptr) != (a->out_mask == nullptr))
+    return fail(LL_ERR_INVALID_ARGUMENT, "mask and out_mask must both be given or both be NULL");
+  const uintptr_t in_begin = reinterpret_cast<uintptr_t>(a->maps);
+  const uintptr_t out_begin = reinterpret_cast<uintptr_t>(a->out_maps);
+  const uintptr_t bytes = static_cast<uintptr_t>(4 * a->capacity) * sizeof(int64_t);
+  if ((in_begin & 7u) != 0 || (out_begin & 7u) != 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "maps and out_maps must be 8-byte aligned");
+  if (in_begin < out_begin + bytes && out_begin < in_begin + bytes)
+    return fail(LL_ERR_INVALID_ARGUMENT, "out_maps overlaps maps");
+  if (a->mask != nullptr) {
+    const uintptr_t m = reinterpret_cast<uintptr_t>(a->mask), o = reinterpret_cast<uintptr_t>(a->out_mask);
+    if (m < o + static_cast<uintptr_t>(a->capacity) && o < m + static_cast<uintptr_t>(a->capacity))
+      return fail(LL_ERR_INVALID_ARGUMENT, "out_mask overlaps mask");
+  }
+  if (a->workspace == nullptr || a->workspace_bytes < LL_ORDER_WORKSPACE_BYTES ||
+      (reinterpret_cast<uintptr_t>(a->workspace) & 3u) != 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be a 4-byte aligned device array of at least %d bytes",
+                LL_ORDER_WORKSPACE_BYTES);
+  OrderParams p;
+  p.maps = reinterpret_cast<const long long *>(a->maps);
+  p.mask = a->mask;
+  p.cap = a->capacity;
+  p.count = a->count;
+  p.prefix = a->prefix;
+  p.num_slots = a->num_slots;
+  p.shift = 0;
+  while (((a->num_slots - 1) >> p.shift) >= kOrderBuckets) ++p.shift;
+  p.out = reinterpret_cast<long long *>(a->out_maps);
+  p.out_mask = a->out_mask;
+  p.counts = static_cast<int *>(a->workspace);
+  p.offsets = p.counts + kOrderBuckets;
+  p.arrived = reinterpret_cast<unsigned int *>(p.offsets + kOrderBuckets);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t tail = a->count - a->prefix;
+  if (tail > 0) {
+    const int64_t blocks = (tail + kOrderThreads - 1) / kOrderThreads;
+    order_count_kernel<<<dim3(static_cast<unsigned>(blocks < 1024 ? blocks : 1024)), dim3(kOrderThreads), 0, s>>>(p);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  const int64_t blocks = (a->count + 255) / 256;
+  order_scatter_kernel<<<dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s>>>(p);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return LL_OK;
 }
 
 }  // extern "C"

@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -62,6 +62,8 @@ EXPORTED_SYMBOLS = (
     "ll_kv_scatter_args_size",
     "ll_kv_build_link_maps",
     "ll_link_maps_args_size",
+    "ll_order_link_maps",
+    "ll_order_maps_args_size",
     "ll_repair_attention_plan",
     "ll_repair_attention",
     "ll_repair_attention_args_size",
@@ -215,6 +217,30 @@ class LinkMapsArgs(ctypes.Structure):
         ("repair_mask", _ptr * 2),
         ("repair_destination_slots", _ptr),
         ("repair_capacity", _i64),
+        ("device_segments", _ptr),
+    ]
+
+
+# Destination order of a map set (ll_order_link_maps).
+ORDER_BUCKETS = 16384
+ORDER_WORKSPACE_BYTES = 8 * ORDER_BUCKETS + 256
+
+
+class OrderMapsArgs(ctypes.Structure):
+    """Mirror of ``ll_order_maps_args``."""
+
+    _fields_ = [
+        ("struct_size", _i64),
+        ("maps", _ptr),
+        ("mask", _ptr),
+        ("capacity", _i64),
+        ("count", _i64),
+        ("prefix", _i64),
+        ("num_slots", _i64),
+        ("out_maps", _ptr),
+        ("out_mask", _ptr),
+        ("workspace", _ptr),
+        ("workspace_bytes", _i64),
     ]
 
 
@@ -350,6 +376,10 @@ def load_library() -> ctypes.CDLL:
         lib.ll_kv_build_link_maps.restype = ctypes.c_int
         lib.ll_link_maps_args_size.argtypes = []
         lib.ll_link_maps_args_size.restype = _i64
+        lib.ll_order_link_maps.argtypes = [ctypes.POINTER(OrderMapsArgs), _ptr]
+        lib.ll_order_link_maps.restype = ctypes.c_int
+        lib.ll_order_maps_args_size.argtypes = []
+        lib.ll_order_maps_args_size.restype = _i64
         lib.ll_repair_attention_plan.argtypes = [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64,
                                                  _ptr, _i64, ctypes.POINTER(RepairPlanInfo)]
         lib.ll_repair_attention_plan.restype = ctypes.c_int
@@ -371,6 +401,7 @@ def load_library() -> ctypes.CDLL:
         if (lib.ll_kv_link_args_size() != ctypes.sizeof(LinkArgs)
                 or lib.ll_kv_scatter_args_size() != ctypes.sizeof(ScatterArgs)
                 or lib.ll_link_maps_args_size() != ctypes.sizeof(LinkMapsArgs)
+                or lib.ll_order_maps_args_size() != ctypes.sizeof(OrderMapsArgs)
                 or lib.ll_repair_attention_args_size() != ctypes.sizeof(RepairAttentionArgs)):
             raise NativeLibraryUnavailable(f"{LIB_PATH} struct layout differs; rebuild it")
         _lib = lib
@@ -421,6 +452,11 @@ def kv_link_describe(args: LinkArgs) -> LaunchInfo:
 def kv_build_link_maps(args: LinkMapsArgs, stream: int) -> None:
     args.struct_size = ctypes.sizeof(LinkMapsArgs)
     _check(load_library().ll_kv_build_link_maps(ctypes.byref(args), _ptr(int(stream))))
+
+
+def order_link_maps(args: OrderMapsArgs, stream: int) -> None:
+    args.struct_size = ctypes.sizeof(OrderMapsArgs)
+    _check(load_library().ll_order_link_maps(ctypes.byref(args), _ptr(int(stream))))
 
 
 def repair_attention_plan(rows, num_q_heads: int, num_kv_heads: int, split_tokens: int = 0):

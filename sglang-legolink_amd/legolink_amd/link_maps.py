@@ -181,6 +181,7 @@ class DeviceMaps:
     maps: list[Optional[torch.Tensor]]
     masks: list[Optional[torch.Tensor]]
     repair_destination_slots: torch.Tensor
+    run_table: Optional[torch.Tensor] = None  # the device copy of the runs the builder read
 
 
 def set_entry_flags(plan: SegmentPlan, source_set: int, run_flags: np.ndarray, *, compact: bool) -> np.ndarray:
@@ -196,6 +197,11 @@ def set_entry_flags(plan: SegmentPlan, source_set: int, run_flags: np.ndarray, *
     if flags.size != plan.map_counts[source_set]:
         raise AssertionError("the runs of a set do not tile its map entries")
     return flags
+
+
+# Above this many runs the map builder reads them from a device copy of the
+# run table (one launch) instead of its kernel arguments (56 runs a launch).
+DEVICE_TABLE_RUNS = 56
 
 
 def build_device_maps(plan: SegmentPlan, destination_slots: torch.Tensor, *, compact: bool,
@@ -231,8 +237,46 @@ def build_device_maps(plan: SegmentPlan, destination_slots: torch.Tensor, *, com
     args.repair_capacity = plan.repair_count
     if stream is None:
         stream = torch.cuda.current_stream(device)
+    device_table = None
+    if args.num_segments > DEVICE_TABLE_RUNS:
+        # Many runs: one copy of the run table to the device and one launch,
+        # where the kernel arguments would take a launch per 56 runs.  The
+        # copy is ordered before the builder on its stream.
+        with torch.cuda.stream(stream):
+            device_table = torch.from_numpy(table).pin_memory().to(device, non_blocking=True)
+        args.device_segments = device_table.data_ptr()
     _native.kv_build_link_maps(args, stream.cuda_stream)
-    return DeviceMaps(maps=maps, masks=masks, repair_destination_slots=repair)
+    return DeviceMaps(maps=maps, masks=masks, repair_destination_slots=repair, run_table=device_table)
+
+
+def order_by_destination(maps: torch.Tensor, mask: Optional[torch.Tensor], *, prefix: int, num_slots: int,
+                         workspace: torch.Tensor,
+                         stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """A map set's entries [prefix, n) in destination-slot order (slots in
+    buckets of 2^shift over the pool, 16,384 buckets; one slot per bucket up
+    to a 16,384-row pool), entries [0, prefix) first and in place; the mask
+    follows its entries.  ``workspace`` is a zeroed uint8 device tensor of
+    ``_native.ORDER_WORKSPACE_BYTES`` that calls on one stream may share
+    (``ll_order_link_maps``)."""
+
+    n = int(maps.shape[1])
+    out = torch.empty_like(maps)
+    out_mask = None if mask is None else torch.empty_like(mask)
+    args = _native.OrderMapsArgs()
+    args.maps = maps.data_ptr()
+    args.mask = None if mask is None else mask.data_ptr()
+    args.capacity = n
+    args.count = n
+    args.prefix = int(prefix)
+    args.num_slots = int(num_slots)
+    args.out_maps = out.data_ptr()
+    args.out_mask = None if out_mask is None else out_mask.data_ptr()
+    args.workspace = workspace.data_ptr()
+    args.workspace_bytes = int(workspace.numel())
+    if stream is None:
+        stream = torch.cuda.current_stream(maps.device)
+    _native.order_link_maps(args, stream.cuda_stream)
+    return out, out_mask
 
 
 def block_table(starts: Sequence[int], counts: Sequence[int], source_ptrs: Sequence[int],

@@ -50,7 +50,7 @@ from typing import Any, Mapping, Optional, Sequence
 import numpy as np
 import torch
 
-from . import kv_link, link_maps
+from . import _native, kv_link, link_maps
 from .errors import LinkRuntimeError
 
 try:
@@ -422,7 +422,8 @@ class PreparedLink:
                  validate_indices: bool, arena: Optional[SnapshotArena] = None,
                  layer_groups_per_block: int = 0, order_by_source: Optional[bool] = None,
                  fused_mode: str = "required", delta_staging: str = "auto",
-                 skipped_rows: Optional[torch.Tensor] = None, visit_order: Optional[str] = None) -> None:
+                 skipped_rows: Optional[torch.Tensor] = None, visit_order: Optional[str] = None,
+                 order_workspace: Optional[torch.Tensor] = None) -> None:
         self.pool = pool
         self.layers = layers
         self.maps = maps
@@ -479,6 +480,9 @@ class PreparedLink:
         self.stream_source_rows = (maps.request_count == 1 and not self.order_by_source
                                    and token_count * len(layers) * row_bytes > MEMORY_SIDE_CACHE_BYTES)
         sort_row = {"source": 0, "destination": 1}.get(self.visit_order)
+        if sort_row == 1 and order_workspace is None:
+            order_workspace = torch.zeros(_native.ORDER_WORKSPACE_BYTES, dtype=torch.uint8,
+                                          device=key_buffers[0].device)
         # delta_staging "table": a first launch writes every token's RoPE delta
         # to a table and a second walks the rows layer by layer (measured
         # 1.0-1.4 % slower than the default staged deltas on c2, c4, c5); the
@@ -515,7 +519,14 @@ class PreparedLink:
                 # at the head, with the fused entries after them.
                 split = prefix + int(np.count_nonzero(eager_entries[prefix:] == 0))
                 pieces = [(0, split, "fused", prefix), (split, count, "eager", 0)]
-            if (sort_row is not None or eager_entries is not None) and count - prefix > 1:
+            if sort_row == 1 and eager_entries is None and count - prefix > 1:
+                # Destination order by the library's bucketed counting sort
+                # (two launches, where torch's argsort takes about ten).
+                device_maps, mask = link_maps.order_by_destination(
+                    device_maps, mask.view(torch.uint8) if mask is not None else None, prefix=prefix,
+                    num_slots=int(key_buffers[0].shape[0]), workspace=order_workspace)
+                self._kernel_maps.append(device_maps)
+            elif (sort_row is not None or eager_entries is not None) and count - prefix > 1:
                 tail = device_maps[:, prefix:]
                 key = None if sort_row is None else tail[sort_row]
                 if eager_entries is not None:
@@ -668,6 +679,7 @@ class KVLinkExecutor:
         self.arena = arena
         self.count_skipped_rows = bool(count_skipped_rows)
         self._skip_counters: dict[torch.device, torch.Tensor] = {}
+        self._order_workspaces: dict[torch.device, torch.Tensor] = {}
 
     @property
     def layers(self) -> list[int]:
@@ -682,6 +694,17 @@ class KVLinkExecutor:
             counter = torch.zeros(1, dtype=torch.int64, device=device)
             self._skip_counters[device] = counter
         return counter
+
+    def _order_workspace(self, device: torch.device) -> torch.Tensor:
+        """The zeroed workspace of the destination ordering on ``device``,
+        shared by this executor's links (prepared on one stream)."""
+
+        device = torch.device(device)
+        workspace = self._order_workspaces.get(device)
+        if workspace is None:
+            workspace = torch.zeros(_native.ORDER_WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+            self._order_workspaces[device] = workspace
+        return workspace
 
     def skipped_rows(self, *, reset: bool = True) -> int:
         """Tokens the links so far skipped because a slot or position was out
@@ -860,7 +883,7 @@ class KVLinkExecutor:
             validate_indices=validate_indices, arena=self.arena,
             layer_groups_per_block=self.layer_groups_per_block, fused_mode=self._fused_mode(),
             delta_staging=self.delta_staging, skipped_rows=self._skip_counter(device),
-            visit_order=self.visit_order,
+            visit_order=self.visit_order, order_workspace=self._order_workspace(device),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared
@@ -896,6 +919,7 @@ class KVLinkExecutor:
             fused_mode=self._fused_mode(), delta_staging=self.delta_staging,
             skipped_rows=self._skip_counter(device),
             visit_order=None if order_by_source is not None else self.visit_order,
+            order_workspace=self._order_workspace(device),
         )
         prepared.host_prepare_s = time.perf_counter() - started
         return prepared

@@ -27,11 +27,22 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from . import _native
+from . import _host_sequences, _native
 
 
 class SparseRepairAttentionError(RuntimeError):
     """A repair attention request that must not run (flashinfer_sparse_repair.py:65-66)."""
+
+
+def _int64_values(values: Sequence) -> np.ndarray:
+    """Span bounds as int64: integers read in C, anything else through int()."""
+
+    out = np.empty(len(values), dtype=np.int64)
+    try:
+        _host_sequences.int64_from_sequence(values, out)
+    except (TypeError, OverflowError):
+        out = np.array([int(value) for value in values], dtype=np.int64)
+    return out
 
 
 class RepairAttentionPlan:
@@ -60,51 +71,59 @@ class RepairAttentionPlan:
         self.num_kv_heads = int(num_kv_heads)
         self.head_dim = int(head_dim)
         device = spans[0][0].device
-        tables: list[torch.Tensor] = []
-        offset_of: dict[int, int] = {}
-        length_of: dict[int, int] = {}
-        row_list: list[tuple[int, int, int, int]] = []
-        cursor = 0
-        table_len = 0
-        dtype = None
-        for slot_ids, start, end in spans:
-            # Spans of one request share its slot tensor: the tensor is checked
-            # once, each span's range every time (the checks and messages of
-            # build_explicit_causal_pattern, :1217-1238).
-            key = id(slot_ids)
-            base = offset_of.get(key)
-            if base is None:
-                if slot_ids.ndim != 1:
-                    raise SparseRepairAttentionError("slot_ids must be rank 1")
-                if slot_ids.device != device:
-                    raise SparseRepairAttentionError("repair spans must share one device")
-                if slot_ids.dtype not in (torch.int32, torch.int64):
-                    raise SparseRepairAttentionError("slot_ids must be int32 or int64")
-                base = offset_of[key] = table_len
-                length_of[key] = int(slot_ids.numel())
-                tables.append(slot_ids.contiguous())
-                table_len += length_of[key]
-                dtype = slot_ids.dtype if dtype in (None, slot_ids.dtype) else torch.int64
-            start, end = int(start), int(end)
-            if start < 0 or end <= start:
-                raise SparseRepairAttentionError("invalid repair range")
-            if length_of[key] < end:
-                raise SparseRepairAttentionError("slot_ids is shorter than repair_end")
-            row_list.append((cursor, start, end - start, base))
-            cursor += end - start
-        rows = np.array(row_list, dtype=np.int64).reshape(-1, 4)
-        self.num_queries = cursor
-        self.spans = [(int(s), int(e)) for _, s, e in spans]
+        tensors, starts, ends = zip(*spans)
+        starts, ends = _int64_values(starts), _int64_values(ends)
+        # Spans of one request share its slot tensor: each distinct tensor is
+        # checked once, each span's range every time (the checks and messages
+        # of build_explicit_causal_pattern, :1217-1238), and the error raised
+        # is the one the first failing span meets, tensor checks first.
+        ids = list(map(id, tensors))
+        # Distinct tensors in order of first use, and the span that first uses each.
+        first_use = dict(zip(reversed(ids), range(len(ids) - 1, -1, -1)))
+        first_spans = [first_use[key] for key in dict.fromkeys(ids)]
+        distinct = [tensors[index] for index in first_spans]
+        position_of = {ids[index]: position for position, index in enumerate(first_spans)}
+        span_tensor = np.fromiter(map(position_of.__getitem__, ids), dtype=np.int64, count=len(ids))
+        failures = []  # (span index, message)
+        for index, slot_ids in zip(first_spans, distinct):
+            if slot_ids.ndim != 1:
+                failures.append((index, "slot_ids must be rank 1"))
+            elif slot_ids.device != device:
+                failures.append((index, "repair spans must share one device"))
+            elif slot_ids.dtype not in (torch.int32, torch.int64):
+                failures.append((index, "slot_ids must be int32 or int64"))
+        lengths = np.fromiter((int(t.numel()) for t in distinct), dtype=np.int64, count=len(distinct))
+        bad_range = np.flatnonzero((starts < 0) | (ends <= starts))
+        if bad_range.size:
+            failures.append((int(bad_range[0]), "invalid repair range"))
+        short = np.flatnonzero(lengths[span_tensor] < ends)
+        if short.size:
+            failures.append((int(short[0]), "slot_ids is shorter than repair_end"))
+        if failures:
+            raise SparseRepairAttentionError(min(failures, key=lambda failure: failure[0])[1])
+        tables = [t.contiguous() for t in distinct]
+        bases = np.zeros(len(distinct), dtype=np.int64)
+        np.cumsum(lengths[:-1], out=bases[1:])
+        counts = ends - starts
+        rows = np.empty((len(ids), 4), dtype=np.int64)
+        rows[0, 0] = 0
+        np.cumsum(counts[:-1], out=rows[1:, 0])
+        rows[:, 1] = starts
+        rows[:, 2] = counts
+        rows[:, 3] = bases[span_tensor]
+        self.num_queries = int(counts.sum())
+        self.span_starts, self.span_ends = starts, ends
+        dtype = distinct[0].dtype if all(t.dtype == distinct[0].dtype for t in distinct) else torch.int64
         table = tables[0] if len(tables) == 1 else torch.cat([t.to(dtype) for t in tables])
         if validate and pool_size is not None:
-            # Spans of one request share its slot tensor: each tensor's slots up
-            # to its spans' largest end are checked once.
-            reach: dict[int, int] = {}
-            for slot_ids, _, end in spans:
-                reach[id(slot_ids)] = max(reach.get(id(slot_ids), 0), int(end))
-            needed = [tables[index][: reach[key]] for index, key in enumerate(offset_of)]
-            needed = needed[0] if len(needed) == 1 else torch.cat(needed)
-            if bool(((needed < 0) | (needed >= int(pool_size))).any()):
+            # Each tensor's slots up to its spans' largest end are checked
+            # once: the smallest and largest with one reduction.
+            reach = np.zeros(len(distinct), dtype=np.int64)
+            np.maximum.at(reach, span_tensor, ends)
+            needed = [t[: int(r)] for t, r in zip(tables, reach.tolist())]
+            needed = needed[0] if len(needed) == 1 else torch.cat([t.to(dtype) for t in needed])
+            low, high = torch.aminmax(needed)
+            if int(low) < 0 or int(high) >= int(pool_size):
                 raise SparseRepairAttentionError("slot_ids contains invalid KV slots")
         self.kv_slots = table
         self.rows = rows
@@ -126,7 +145,8 @@ class RepairAttentionPlan:
     def algorithmic_flops(self) -> int:
         """4 * head_dim flops per (query, visible key) pair and query head."""
 
-        pairs = sum((end - start) * (start + end + 1) // 2 for start, end in self.spans)
+        starts, ends = self.span_starts.tolist(), self.span_ends.tolist()
+        pairs = sum((end - start) * (start + end + 1) // 2 for start, end in zip(starts, ends))
         return 4 * self.head_dim * self.num_q_heads * pairs
 
     @property

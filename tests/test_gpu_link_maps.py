@@ -52,9 +52,15 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("run_table", ["kernel_arguments", "device_table"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_device_maps_match_oracle(gpu_device, case):
+def test_device_maps_match_oracle(gpu_device, case, run_table, monkeypatch):
+    """Both ways the runs reach the builder: in kernel arguments (56 runs a
+    launch) and from a device copy of the run table (one launch)."""
+
+    monkeypatch.setattr(link_maps, "DEVICE_TABLE_RUNS", 0 if run_table == "device_table" else 1 << 30)
     name, seed, count, max_len, compact, slot_dtype = case
+    name = f"{name}/{run_table}"
     rng = np.random.default_rng(seed)
     for trial in range(4):
         blocks, request_slots, imp = _random_plan(rng, blocks=count, max_len=max_len)
@@ -64,6 +70,7 @@ def test_device_maps_match_oracle(gpu_device, case):
                f"maps {plan.map_counts}, repair rows {plan.repair_count}")
         slots_device = torch.from_numpy(request_slots).to(slot_dtype).to(gpu_device)
         built = link_maps.build_device_maps(plan, slots_device, compact=compact)
+        assert (built.run_table is not None) == (run_table == "device_table")
         torch.cuda.synchronize(gpu_device)
         expected = lmo.device_maps(blocks, request_slots, imp, compact=compact)
         assert np.array_equal(built.repair_destination_slots.cpu().numpy(),
@@ -116,3 +123,69 @@ def test_batched_device_maps_match_oracle(gpu_device):
             if not compact:
                 assert np.array_equal(built.masks[s].cpu().numpy(), expected[f"mask{s}"])
         del keep
+
+
+def test_device_table_runs_are_checked_again_on_the_device(gpu_device):
+    """A device run table that differs from the host's (map offsets past the
+    capacity, a destination range past the request, a repair range past its
+    capacity) loses those runs; the others are built.  The buffers are
+    allocated larger than the sizes passed, so a read or write past one would
+    still land inside them, and the test checks that no write did."""
+
+    from legolink_amd import _native
+
+    rng = np.random.default_rng(11)
+    blocks, request_slots, imp = _random_plan(rng, blocks=12, max_len=30)
+    table, keep = _device_table(blocks, gpu_device)
+    plan = link_maps.plan_segments(table, np.asarray(imp, dtype=np.int64), compact=True)
+    runs = np.ascontiguousarray(plan.table).copy()
+    field = {name: i for i, name in enumerate(_native.SEGMENT_FIELDS)}
+    guard = 4096
+    slot_buffer = torch.zeros(request_slots.size + guard, dtype=torch.int64, device=gpu_device)
+    slots = slot_buffer[: request_slots.size]
+    slots.copy_(torch.from_numpy(request_slots))
+    capacity = [plan.map_counts[0], plan.map_counts[1]]
+    maps = [torch.full((4 * c + guard,), -7, dtype=torch.int64, device=gpu_device) for c in capacity]
+    repair = torch.full((plan.repair_count + guard,), -7, dtype=torch.int64, device=gpu_device)
+    corrupt = runs.copy()
+    nonempty = np.flatnonzero(corrupt[:, field["token_count"]] > 0)
+    bad = nonempty[:3]
+    corrupt[bad[0], field["map_offset"]] = capacity[int(corrupt[bad[0], field["map_set"]])]
+    corrupt[bad[1], field["destination_start"]] = request_slots.size
+    with_repair = [k for k in nonempty if corrupt[k, field["repair_end"]] > corrupt[k, field["repair_begin"]]]
+    if with_repair:
+        corrupt[with_repair[-1], field["repair_offset"]] = plan.repair_count
+    device_runs = torch.from_numpy(corrupt).to(gpu_device)
+    args = _native.LinkMapsArgs()
+    args.num_segments = runs.shape[0]
+    args.segments = runs.ctypes.data
+    args.destination_slots = slots.data_ptr()
+    args.destination_slots_dtype = _native.DTYPE_INT64
+    args.num_destination_slots = slots.numel()
+    for s in (0, 1):
+        args.maps[s] = maps[s].data_ptr() if capacity[s] else None
+        args.map_capacity[s] = capacity[s]
+    args.repair_destination_slots = repair.data_ptr() if plan.repair_count else None
+    args.repair_capacity = plan.repair_count
+    args.device_segments = device_runs.data_ptr()
+    report(f"device table re-check: {runs.shape[0]} runs, corrupted {bad.tolist()}")
+    _native.kv_build_link_maps(args, torch.cuda.current_stream(gpu_device).cuda_stream)
+    torch.cuda.synchronize(gpu_device)
+    for s in (0, 1):
+        assert (maps[s][4 * capacity[s]:] == -7).all(), "a write past the map capacity"
+    assert (repair[plan.repair_count:] == -7).all(), "a write past the repair capacity"
+    # The runs left intact are built as the host table says.
+    expected = link_maps.build_device_maps(plan, slots, compact=True)
+    torch.cuda.synchronize(gpu_device)
+    skipped = set(bad[:2].tolist()) | ({with_repair[-1]} if with_repair else set())
+    for k in range(runs.shape[0]):
+        s = int(runs[k, field["map_set"]])
+        count = int(runs[k, field["token_count"]])
+        if k in skipped or count == 0 or expected.maps[s] is None:
+            continue
+        rb, re = int(runs[k, field["repair_begin"]]), int(runs[k, field["repair_end"]])
+        begin = int(runs[k, field["map_offset"]])
+        entries = count - (re - rb)
+        got = maps[s][: 4 * capacity[s]].view(4, capacity[s])[:, begin : begin + entries]
+        assert torch.equal(got, expected.maps[s][:, begin : begin + entries]), k
+    del keep

@@ -318,3 +318,41 @@ def test_map_builder_struct_checks():
     assert lib.ll_kv_build_link_maps(ctypes.byref(args), None) == _native.LL_ERR_INVALID_ARGUMENT
     empty = _native.LinkMapsArgs()
     _native.kv_build_link_maps(empty, 0)  # no runs: nothing to do, no GPU touched
+
+
+def test_order_entry_rejects_bad_arguments_before_any_launch():
+    """ll_order_link_maps checks its arguments on the host (no GPU here: every
+    case returns before a launch)."""
+
+    lib = _native.load_library()
+    assert lib.ll_order_link_maps(None, None) == _native.LL_ERR_INVALID_ARGUMENT
+
+    def args(**fields):
+        a = _native.OrderMapsArgs()
+        a.struct_size = ctypes.sizeof(a)
+        a.maps, a.out_maps, a.workspace = 0x100000, 0x200000, 0x300000
+        a.capacity = a.count = 100
+        a.prefix, a.num_slots = 10, 1000
+        a.workspace_bytes = _native.ORDER_WORKSPACE_BYTES
+        for key, value in fields.items():
+            setattr(a, key, value)
+        return a
+
+    for fields, message in [
+        (dict(struct_size=8), "struct_size"),
+        (dict(count=101), "prefix <= count <= capacity"),
+        (dict(prefix=101), "prefix <= count"),
+        (dict(capacity=1 << 31, count=1 << 31), "2^31"),
+        (dict(num_slots=0), "num_slots"),
+        (dict(maps=None), "device arrays"),
+        (dict(mask=0x400000), "both"),
+        (dict(out_maps=0x100000 + 8 * 399), "overlaps"),
+        (dict(maps=0x100004), "aligned"),
+        (dict(mask=0x400000, out_mask=0x400000 + 50), "out_mask overlaps"),
+        (dict(workspace_bytes=_native.ORDER_WORKSPACE_BYTES - 1), "workspace"),
+        (dict(workspace=None), "workspace"),
+    ]:
+        status = lib.ll_order_link_maps(ctypes.byref(args(**fields)), None)
+        assert status == _native.LL_ERR_INVALID_ARGUMENT, fields
+        assert message in lib.ll_last_error().decode(), (fields, lib.ll_last_error())
+    assert lib.ll_order_link_maps(ctypes.byref(args(count=0, prefix=0)), None) == _native.LL_OK  # nothing to do

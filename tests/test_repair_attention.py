@@ -403,3 +403,65 @@ def test_kept_plan_never_changes_results():
     plan_changed = _native.repair_attention_plan(changed, 28, 4, 0)
     assert not np.array_equal(plan_changed[2], first[2])
     assert plan_changed[2][-1] == first[2][-1] + 1
+
+
+def test_plan_span_checks_report_the_first_failing_span():
+    """The checks of build_explicit_causal_pattern (flashinfer_sparse_repair.py:
+    1217-1238) in span order: the first span that fails decides the message,
+    its tensor's checks before its range checks."""
+
+    import torch
+
+    from legolink_amd.repair_attention import RepairAttentionPlan, SparseRepairAttentionError
+
+    good = torch.arange(10, dtype=torch.int64)
+    rank2 = torch.arange(10, dtype=torch.int64).view(2, 5)
+    floats = torch.arange(10, dtype=torch.float32)
+    meta = torch.empty(10, dtype=torch.int64, device="meta")
+    cases = [
+        ([(good, 0, 4), (floats, 0, 2)], "int32 or int64"),
+        ([(good, 3, 3), (rank2, 0, 1)], "invalid repair range"),
+        ([(rank2, 0, 1), (good, 3, 3)], "rank 1"),
+        ([(good, 0, 4), (good, 5, 11)], "shorter than repair_end"),
+        ([(good, 5, 11), (good, -1, 2)], "shorter than repair_end"),
+        ([(good, 0, 4), (good, -1, 2), (floats, 0, 1)], "invalid repair range"),
+        ([(good, 0, 4), (meta, 0, 2)], "share one device"),
+    ]
+    for spans, message in cases:
+        with pytest.raises(SparseRepairAttentionError, match=message):
+            RepairAttentionPlan(spans, num_q_heads=8, num_kv_heads=2, head_dim=64, pool_size=100)
+    with pytest.raises(SparseRepairAttentionError, match="no repair spans"):
+        RepairAttentionPlan([], num_q_heads=8, num_kv_heads=2, head_dim=64)
+    # Slots outside the pool, up to the spans' largest end only.
+    slots = torch.tensor([3, 7, 99, 100, -1], dtype=torch.int64)
+    RepairAttentionPlan([(slots, 1, 3)], num_q_heads=8, num_kv_heads=2, head_dim=64, pool_size=100)
+    for end, size in ((4, 100), (3, 99)):
+        with pytest.raises(SparseRepairAttentionError, match="invalid KV slots"):
+            RepairAttentionPlan([(slots, 1, end)], num_q_heads=8, num_kv_heads=2, head_dim=64, pool_size=size)
+    RepairAttentionPlan([(slots, 0, 5)], num_q_heads=8, num_kv_heads=2, head_dim=64, validate=False,
+                        pool_size=100)
+
+
+def test_plan_rows_and_slot_table_of_shared_and_mixed_tensors():
+    import torch
+
+    from legolink_amd.repair_attention import RepairAttentionPlan
+
+    a = torch.arange(100, 140, dtype=torch.int64)
+    b = torch.arange(500, 520, dtype=torch.int32)
+    spans = [(a, 4, 9), (b, 2, 3), (a, 20, 36), (b, 10, 20), (a, 39, 40)]
+    plan = RepairAttentionPlan(spans, num_q_heads=28, num_kv_heads=4, head_dim=128, pool_size=1000)
+    # One table: a's slots, then b's (as int64); rows (query index, start, count, table offset).
+    assert plan.kv_slots.dtype == torch.int64
+    assert plan.kv_slots.tolist() == list(range(100, 140)) + list(range(500, 520))
+    expected, cursor = [], 0
+    for tensor, start, end in spans:
+        expected.append([cursor, start, end - start, 0 if tensor is a else 40])
+        cursor += end - start
+    assert plan.rows.tolist() == expected and plan.num_queries == cursor
+    # Bounds given as numpy integers or 0-dim tensors read the same.
+    odd = [(a, np.int64(4), torch.tensor(9)), (b, 2, np.int32(3))]
+    plan2 = RepairAttentionPlan(odd, num_q_heads=28, num_kv_heads=4, head_dim=128)
+    assert plan2.rows.tolist() == [[0, 4, 5, 0], [5, 2, 1, 40]]
+    pairs = sum((e - s) * (s + e + 1) // 2 for _, s, e in spans)
+    assert plan.algorithmic_flops == 4 * 128 * 28 * pairs
