@@ -66,6 +66,10 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--run-sweep", action="store_true",
                         help="time the link kernel on maps whose sources and destinations come in "
                              "contiguous runs of 1..64 slots, for several launch shapes")
+    parser.add_argument("--calibration-only", action="store_true",
+                        help="only the sweep's row calibration (calibration kernels and torch's index "
+                             "kernels) on the workload's random, destination-sorted and contiguous maps: "
+                             "a short run for hardware counters")
     parser.add_argument("--no-calibration", dest="calibration", action="store_false", default=True,
                         help="sweep: skip the row calibration (calibration kernels and torch index ops)")
     parser.add_argument("--sweep-detail-run", type=int, default=64,
@@ -412,7 +416,7 @@ def sweep_ceiling(rows: list[dict], calibration: list[dict], link_bytes: int) ->
     reads and writes do not slow each other down."""
 
     own = [r for r in rows if r["run"] == 1 and r["order"] in ("random", "sorted_destination", "sorted_source",
-                                                                "sorted_both")]
+                                                                "sorted_both", "bucketed_destination")]
     best_link = max(own, key=lambda r: r["GBps"])
     fragmented = [c for c in calibration if c["order"] != "contiguous"]
     copies = [c for c in fragmented if c["mode"] == "copy"]
@@ -518,6 +522,36 @@ def run_sweep(args: argparse.Namespace) -> None:
                       "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 
+def calibration_only(args: argparse.Namespace) -> None:
+    """The sweep's calibration leg alone (no link launches): the same pool and
+    maps, every calibration variant and torch's index kernels, in a fixed
+    dispatch order that the JSON line lists (for matching counter rows)."""
+
+    import torch
+
+    from legolink_amd.workloads import make_workload
+
+    device = torch.device("cuda", 0)
+    workload = make_workload(args.workload)
+    shape = workload.shape
+    generator = torch.Generator(device=device).manual_seed(20260824)
+    keys = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                        device=device, generator=generator) for _ in range(shape.layers)]
+    values = [torch.randn(workload.num_slots, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                          device=device, generator=generator) for _ in range(shape.layers)]
+    rows = []
+    for order in CALIBRATION_ORDERS:
+        src, dst, _, _ = ordered_maps(workload, 1, order, seed=20260824 + 1)
+        src_t = torch.from_numpy(src).to(device)
+        dst_t = torch.from_numpy(dst).to(device)
+        rows += calibrate_rows(torch, workload, keys, values, src_t, dst_t, order, args)
+    print(json.dumps({"calibration": rows, "workload": workload.name, "tokens": workload.tokens,
+                      "layers": shape.layers, "steps": args.steps, "warmup": args.warmup,
+                      "dispatch_order": "per row: (warmup + steps) launches of its kernels; calibration "
+                                        "rows one launch each, torch rows 4 launches per layer (copy: "
+                                        "index_select + index_copy_ for K and V) or 2 (a half)"}), flush=True)
+
+
 def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
     """HBM bytes per link launch from the committed rocprofv3 counter summary of
     this workload; None when there is none, or when it was taken on a launch
@@ -536,18 +570,27 @@ def load_traffic(workload_name: str, link_launch_bytes: int) -> float | None:
 
 
 def load_pattern_ceiling(workload_name: str) -> dict | None:
-    """The committed run-length sweep's ceiling for this workload's access
-    pattern (the fastest link variant on its fully fragmented rows, and on
-    contiguous rows), or None when there is none."""
+    """The committed sweep's ceiling for this workload's access pattern: the
+    fastest independent copy of the workload's own fragmented rows (the
+    row-calibration kernels and torch's index kernels), the bound of its
+    read-only and write-only halves, and the link as the executor launches
+    it, all measured in one process; None when there is none."""
 
     path = PROFILES / f"pattern_ceiling_kv_link_{workload_name}.json"
     if not path.is_file():
         return None
     data = json.loads(path.read_text())
-    best = data["fragmented_rows_best"]["GBps"]
-    return {"GBps": best, "frac": round(best / HBM_PEAK_GBPS, 4),
-            "what": data["fragmented_rows_best"]["what"],
-            "contiguous_rows_GBps": data["contiguous_rows_best"]["GBps"], "source": data["source"]}
+    try:
+        best = data["independent_copy_best"]
+        return {"GBps": best["GBps"], "frac": round(best["GBps"] / HBM_PEAK_GBPS, 4),
+                "what": f"fastest independent copy of the same rows ({best['source']} {best['variant']}, "
+                        f"{best['order']} order)",
+                "halves_bound_GBps": data["halves_bound"]["GBps"],
+                "link_in_same_run_GBps": data["link_as_run"]["GBps"],
+                "link_over_ceiling_in_same_run": data["link_over_independent_copy"],
+                "source": f"profiles/{path.name}: {data['command']}"}
+    except (KeyError, TypeError):
+        return None
 
 
 def repair_attention_bench(args: argparse.Namespace) -> None:
@@ -715,6 +758,9 @@ def main() -> int:
         return 0
     if args.run_sweep:
         run_sweep(args)
+        return 0
+    if args.calibration_only:
+        calibration_only(args)
         return 0
     if args.repair_attention:
         repair_attention_bench(args)
