@@ -522,6 +522,37 @@ def run_sweep(args: argparse.Namespace) -> None:
                       "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 
+def time_attention_plan(workload, requests, device) -> float | None:
+    """Host time of the repair pass's attention plan for this link's repair
+    spans (built once per batch, shared by every layer; Qwen's 7 query heads
+    per KV head, Qwen3-32B's 8): median of 5 after a first, each computed
+    afresh.  None when the link has no repair rows."""
+
+    import numpy as np
+    import torch
+
+    from legolink_amd import _native
+    from legolink_amd.link_plan import contiguous_ranges
+    from legolink_amd.repair_attention import RepairAttentionPlan
+
+    spans = [(slots, int(start), int(end)) for slots, plan in requests
+             for start, end in contiguous_ranges(plan.get("imp_indices") or [])]
+    if not spans:
+        return None
+    shape = workload.shape
+    q_heads = (7 if shape.kv_heads == 4 else 8) * shape.kv_heads
+    times = []
+    for _ in range(6):
+        _native.repair_attention_plan(np.array([[0, 0, 1, 0]], dtype=np.int64), q_heads, shape.kv_heads, 0)
+        torch.cuda.synchronize(device)
+        start = time.perf_counter()
+        RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads, head_dim=shape.head_dim,
+                            pool_size=workload.num_slots)
+        torch.cuda.synchronize(device)
+        times.append((time.perf_counter() - start) * 1e3)
+    return float(np.median(times[1:]))
+
+
 def calibration_only(args: argparse.Namespace) -> None:
     """The sweep's calibration leg alone (no link launches): the same pool and
     maps, every calibration variant and torch's index kernels, in a fixed
@@ -638,6 +669,7 @@ def repair_attention_bench(args: argparse.Namespace) -> None:
         # The planner keeps its last plan per thread; plan other rows first so
         # that every timed plan is computed, as for a new batch.
         _native.repair_attention_plan(np.array([[0, 0, 1, 0]], dtype=np.int64), q_heads, shape.kv_heads, 0)
+        torch.cuda.synchronize(device)  # earlier device work is not the plan's
         plan_start = time.perf_counter()
         plan = RepairAttentionPlan(spans, num_q_heads=q_heads, num_kv_heads=shape.kv_heads,
                                    head_dim=shape.head_dim, pool_size=workload.num_slots,
@@ -885,6 +917,7 @@ def main() -> int:
         prepare_ms.append((time.perf_counter() - prepare_start) * 1e3)
     torch.cuda.synchronize(device)
     host_prepare_ms = float(np.median(prepare_ms[1:]))  # the first pays first-use costs
+    attention_plan_ms = time_attention_plan(workload, requests, device)
     if (prepared.linked_token_count != workload.tokens - workload.repair_rows
             or int(prepared.repair_offsets.size) != workload.repair_rows):
         raise RuntimeError("prepared link does not match the workload's token and repair-row counts")
@@ -1002,6 +1035,7 @@ def main() -> int:
         "scatter_kernel_ms": round(float(np.mean(scatter_ms)), 5),
         "event_ms_per_step": round(gpu_ms, 5),
         "host_prepare_ms": round(host_prepare_ms, 3),
+        "host_attention_plan_ms": None if attention_plan_ms is None else round(attention_plan_ms, 3),
         "end_to_end_link_ms": round(end_to_end_link_ms, 3),
         "repair_rows_mode": args.repair_rows,
         "storage": storage,

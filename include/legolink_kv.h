@@ -408,15 +408,15 @@ typedef struct ll_link_maps_args {
  * once), and a single request's scattered row writes run faster in
  * destination-slot order.  This reorders the entries [prefix, count) of a map
  * set by destination slot into out_maps (and the mask with them), keeping
- * entries [0, prefix) (the identity rows) first, in two launches: a count of
- * the entries per bucket of 2^shift consecutive slots (16,384 buckets over
- * [0, num_slots); slots outside go to the first or last bucket), whose last
- * workgroup turns the counts into bucket offsets, and a scatter.  Entries of
+ * entries [0, prefix) (the identity rows) first, in three launches: a count
+ * of the entries per bucket of 2^shift consecutive slots (16,384 buckets over
+ * [0, num_slots); slots outside go to the first or last bucket), one
+ * workgroup turning the counts into bucket offsets, and a scatter.  Entries of
  * one bucket are placed in no fixed order; with num_slots <= 16,384 buckets
  * hold one slot each.  out_maps is a permutation of the entries for any
  * input, duplicate or out-of-range slots included.
  *
- * The workspace (LL_ORDER_WORKSPACE_BYTES, device, 4-byte aligned) must be
+ * The workspace (LL_ORDER_WORKSPACE_BYTES, device, 16-byte aligned) must be
  * zero before its first use; every call leaves it so.  Calls that share a
  * workspace must not overlap (one stream).
  */

@@ -917,12 +917,12 @@ __global__ void __launch_bounds__(256) build_link_maps_table_kernel(const MapTar
 
 // ---------------------------------------------------------------------------
 // Destination order of a map set: a counting sort over buckets of 2^shift
-// consecutive destination slots.  The count launch adds every entry to its
-// bucket's counter (device-scope atomics); the workgroup that finishes last
-// (an arrival counter) turns the counts into exclusive offsets, clears the
-// counters and the arrival counter for the next call.  The scatter launch
-// takes each entry's place with an atomic increment of its bucket's offset.
-// Every wave of both launches exits: no workgroup waits for another.
+// consecutive destination slots, in three launches.  The count adds every
+// entry to its bucket's counter (atomics); one workgroup turns the counts
+// into exclusive offsets and clears the counters for the next call; the
+// scatter takes each entry's place with an atomic increment of its bucket's
+// offset.  The launches' boundaries order them: no fences, and no workgroup
+// waits for another.
 // ---------------------------------------------------------------------------
 constexpr int kOrderBuckets = LL_ORDER_BUCKETS;
 constexpr int kOrderThreads = 1024;
@@ -935,9 +935,8 @@ struct OrderParams {
   int shift;
   long long *out;
   unsigned char *out_mask;
-  int *counts;            // [kOrderBuckets]: zero between calls
-  int *offsets;           // [kOrderBuckets]
-  unsigned int *arrived;  // zero between calls
+  int *counts;   // [kOrderBuckets]: zero between calls
+  int *offsets;  // [kOrderBuckets]
 };
 
 __device__ __forceinline__ int order_bucket(long long slot, const OrderParams &p) {
@@ -946,42 +945,55 @@ __device__ __forceinline__ int order_bucket(long long slot, const OrderParams &p
   return static_cast<int>(slot >> p.shift);  // below kOrderBuckets by the choice of shift
 }
 
-__global__ void __launch_bounds__(kOrderThreads) order_count_kernel(const OrderParams p) {
+__global__ void __launch_bounds__(256) order_count_kernel(const OrderParams p) {
   const long long n = p.count - p.prefix;
   const long long *dst = p.maps + p.cap + p.prefix;
-  for (long long i = static_cast<long long>(blockIdx.x) * kOrderThreads + threadIdx.x; i < n;
-       i += static_cast<long long>(gridDim.x) * kOrderThreads)
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * 256)
     atomicAdd(&p.counts[order_bucket(dst[i], p)], 1);
-  __shared__ int last;
-  __shared__ int sums[kOrderThreads];
-  __threadfence();  // this workgroup's counts before its arrival
-  __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(p.arrived, 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
+}
+
+__global__ void __launch_bounds__(kOrderThreads) order_offsets_kernel(const OrderParams p) {
+  // Thread t owns buckets [16 t, 16 t + 16): 64 contiguous bytes, read and
+  // written as four 16-byte vectors.  Scan: within each wave by shuffles,
+  // then across the 16 waves through LDS.
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
   constexpr int kPer = kOrderBuckets / kOrderThreads;
-  int own[kPer];
+  static_assert(kPer == 16, "four 16-byte vectors per thread");
+  __shared__ int wave_totals[kOrderThreads / 64];
+  i32x4 *counts = reinterpret_cast<i32x4 *>(p.counts) + threadIdx.x * (kPer / 4);
+  i32x4 *offsets = reinterpret_cast<i32x4 *>(p.offsets) + threadIdx.x * (kPer / 4);
+  i32x4 own[kPer / 4];
   int total = 0;
-  for (int k = 0; k < kPer; ++k) {
-    own[k] = __hip_atomic_load(&p.counts[threadIdx.x * kPer + k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    total += own[k];
+#pragma unroll
+  for (int k = 0; k < kPer / 4; ++k) {
+    own[k] = counts[k];
+    total += own[k][0] + own[k][1] + own[k][2] + own[k][3];
   }
-  sums[threadIdx.x] = total;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  int inclusive = total;
+#pragma unroll
+  for (int step = 1; step < 64; step <<= 1) {
+    const int up = __shfl_up(inclusive, step, 64);
+    if (lane >= step) inclusive += up;
+  }
+  if (lane == 63) wave_totals[wave] = inclusive;
   __syncthreads();
-  for (int step = 1; step < kOrderThreads; step <<= 1) {  // inclusive scan of the per-thread totals
-    const int add = threadIdx.x >= static_cast<unsigned>(step) ? sums[threadIdx.x - step] : 0;
-    __syncthreads();
-    sums[threadIdx.x] += add;
-    __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wave_totals[w];
+  int offset = before + inclusive - total;
+  const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < kPer / 4; ++k) {
+    i32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[e] = offset;
+      offset += own[k][e];
+    }
+    offsets[k] = out;
+    counts[k] = zero;
   }
-  int offset = sums[threadIdx.x] - total;
-  for (int k = 0; k < kPer; ++k) {
-    p.offsets[threadIdx.x * kPer + k] = offset;
-    offset += own[k];
-    p.counts[threadIdx.x * kPer + k] = 0;
-  }
-  if (threadIdx.x == 0) *p.arrived = 0u;
 }
 
 __global__ void __launch_bounds__(256) order_scatter_kernel(const OrderParams p) {
@@ -2001,8 +2013,8 @@ int ll_order_link_maps(const ll_order_maps_args *a, ll_stream_t stream) {
       return fail(LL_ERR_INVALID_ARGUMENT, "out_mask overlaps mask");
   }
   if (a->workspace == nullptr || a->workspace_bytes < LL_ORDER_WORKSPACE_BYTES ||
-      (reinterpret_cast<uintptr_t>(a->workspace) & 3u) != 0)
-    return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be a 4-byte aligned device array of at least %d bytes",
+      (reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "workspace must be a 16-byte aligned device array of at least %d bytes",
                 LL_ORDER_WORKSPACE_BYTES);
   OrderParams p;
   p.maps = reinterpret_cast<const long long *>(a->maps);
@@ -2017,13 +2029,15 @@ int ll_order_link_maps(const ll_order_maps_args *a, ll_stream_t stream) {
   p.out_mask = a->out_mask;
   p.counts = static_cast<int *>(a->workspace);
   p.offsets = p.counts + kOrderBuckets;
-  p.arrived = reinterpret_cast<unsigned int *>(p.offsets + kOrderBuckets);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t tail = a->count - a->prefix;
   if (tail > 0) {
-    const int64_t blocks = (tail + kOrderThreads - 1) / kOrderThreads;
-    order_count_kernel<<<dim3(static_cast<unsigned>(blocks < 1024 ? blocks : 1024)), dim3(kOrderThreads), 0, s>>>(p);
-    const hipError_t err = hipGetLastError();
+    const int64_t blocks = (tail + 255) / 256;
+    order_count_kernel<<<dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s>>>(p);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    order_offsets_kernel<<<dim3(1), dim3(kOrderThreads), 0, s>>>(p);
+    err = hipGetLastError();
     if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   }
   const int64_t blocks = (a->count + 255) / 256;

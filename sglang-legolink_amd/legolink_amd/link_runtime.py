@@ -521,7 +521,7 @@ class PreparedLink:
                 pieces = [(0, split, "fused", prefix), (split, count, "eager", 0)]
             if sort_row == 1 and eager_entries is None and count - prefix > 1:
                 # Destination order by the library's bucketed counting sort
-                # (two launches, where torch's argsort takes about ten).
+                # (three launches, where torch's argsort takes about ten).
                 device_maps, mask = link_maps.order_by_destination(
                     device_maps, mask.view(torch.uint8) if mask is not None else None, prefix=prefix,
                     num_slots=int(key_buffers[0].shape[0]), workspace=order_workspace)

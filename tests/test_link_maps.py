@@ -351,6 +351,7 @@ def test_order_entry_rejects_bad_arguments_before_any_launch():
         (dict(mask=0x400000, out_mask=0x400000 + 50), "out_mask overlaps"),
         (dict(workspace_bytes=_native.ORDER_WORKSPACE_BYTES - 1), "workspace"),
         (dict(workspace=None), "workspace"),
+        (dict(workspace=0x300008), "16-byte aligned"),
     ]:
         status = lib.ll_order_link_maps(ctypes.byref(args(**fields)), None)
         assert status == _native.LL_ERR_INVALID_ARGUMENT, fields
