@@ -197,9 +197,9 @@ __host__ __device__ constexpr int max_pairs(int d) { return d == 256 ? kMaxPairs
 // returns to lane i, element e, element i % 4 of the 8 bytes that lane
 // 4 e + i / 4 addressed (checked on the device), so lanes addressing 4 dims of
 // 4 tokens receive 4 tokens of one dim -- the MFMA's A layout.  The item's
-// slots are read once into LDS (at most kDmaMaxRange of them).
+// slots are read into LDS kDmaMaxRange at a time.
 constexpr int kDmaStages = 4;
-// KV tokens per work item: their slots fill the LDS the ring leaves (the
+// KV tokens per slot-list refill: the slots fill the LDS the ring leaves (the
 // 4 x 32 KB ring at head dims 128 and 256, 159 KB in all).
 constexpr int kDmaMaxRange = 7680;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -306,7 +306,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   const int wg_first = pair_first + static_cast<int>(blockIdx.y % p.pair_chunks) * kPairs;
   const int wg_end = min(pair_first + pair_count, wg_first + kPairs);
   if (n_tiles < 1 || n_tiles > kMaxTiles || kv_off < 0 || kv_begin < 0 || kv_begin > kv_end ||
-      kv_end - kv_begin > kDmaMaxRange || static_cast<long long>(kv_off) + kv_end > p.slots_len ||
+      static_cast<long long>(kv_off) + kv_end > p.slots_len ||
       hk >= p.hkv || pair_first < 0 || pair_first >= p.group || pair_count < 1 || pair_count > kMaxPairs ||
       wg_first >= wg_end || (wg_end - 1) / p.group >= n_tiles)
     return;
@@ -364,22 +364,6 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     const int *e = it + kItemHeader + kTileInts * t;
     if (e[2] >= 1) load_stop = max(load_stop, min(kv_end, e[4]));
   }
-  const int range = load_stop - kv_begin;
-  const int tiles = (range + kTile - 1) / kTile;
-
-  // Each wave takes whole 64-token tiles (the workgroup is a whole number of
-  // waves), so a tile's valid-slot bits are one ballot.
-  for (int i = tid; i < tiles * kTile; i += kM32Threads) {
-    int slot = -1;
-    if (i < range) {
-      const long long s = slot_at(p, static_cast<long long>(kv_off) + kv_begin + i);
-      if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
-    }
-    slot_lds[i] = slot;
-    const unsigned long long bits = __builtin_amdgcn_ballot_w64(slot >= 0);
-    if (lane == 0) tile_valid[i / kTile] = bits;
-  }
-
   // B operand of the score MFMAs: the lane's query, dims 16 ks + 8 h .. + 7.
   frag qf[kKSteps];
   {
@@ -391,8 +375,6 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       qf[ks] = __builtin_bit_cast(frag, bits);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): queries and slots are in
-  __syncthreads();
 
   // Gather of tile t: D / 8 K and D / 8 V instructions of 64 lanes; wave w
   // issues instructions kGathers w .. kGathers w + kGathers - 1 of each.
@@ -454,6 +436,28 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   // A wave's 2 kGathers loads of tile t are complete when at most those of
   // tiles t + 1 .. t + kLead - 1 are outstanding (loads count down in issue
   // order).
+  // The keys go in chunks of at most kDmaMaxRange, the slot list's capacity:
+  // per chunk the slot list is refilled (the ring drained at the chunk's end
+  // and restarted), while the softmax state carries over, so one workgroup
+  // takes a key range of any length.
+  for (int chunk_begin = kv_begin; chunk_begin < load_stop; chunk_begin += kDmaMaxRange) {
+  const int range = min(load_stop - chunk_begin, kDmaMaxRange);
+  const int tiles = (range + kTile - 1) / kTile;
+  if (chunk_begin != kv_begin) __syncthreads();  // every wave is done with the previous chunk's slots and stages
+  // Each wave takes whole 64-token tiles (the workgroup is a whole number of
+  // waves), so a tile's valid-slot bits are one ballot.
+  for (int i = tid; i < tiles * kTile; i += kM32Threads) {
+    int slot = -1;
+    if (i < range) {
+      const long long s = slot_at(p, static_cast<long long>(kv_off) + chunk_begin + i);
+      if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
+    }
+    slot_lds[i] = slot;
+    const unsigned long long bits = __builtin_amdgcn_ballot_w64(slot >= 0);
+    if (lane == 0) tile_valid[i / kTile] = bits;
+  }
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): the slots (and, in the first chunk, the queries) are in
+  __syncthreads();
 #pragma unroll
   for (int t = 0; t < kLead; ++t)
     if (t < tiles) gather(t, k_ring + t * kStageBytes, v_ring + t * kStageBytes);
@@ -488,7 +492,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       workgroup_barrier();
     }
-    const int t0 = kv_begin + t * kTile;
+    const int t0 = chunk_begin + t * kTile;
     if (!wave_computes || t0 >= wave_stop) continue;
     int k_addr = k_lane;
     int v_addr = v_lane;
@@ -612,6 +616,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       for (int b = 0; b < kDimBlocks; ++b) o[b] = E::mfma32(vf[step % 2][b], pb[step], o[b]);
     }
   }
+  }  // key chunks
   // The column's other half (lane l ^ 32) summed the other tokens.
   {
     unsigned a = __builtin_bit_cast(unsigned, l), b = a;
@@ -724,6 +729,7 @@ constexpr int kComputeUnits = 256;          // MI355X
 constexpr double kItemOverheadTiles = 3.0;  // slots, queries, write-out
 constexpr double kPartialBytesPerTile = 12e6;  // partial results the combine reads in one tile's time
 constexpr double kCombineLaunchTiles = 2.0;
+constexpr int64_t kRefillTiles = 2;  // an item's slot-list refill (every kDmaMaxRange keys): drain and restart
 // A plan whose cost provably exceeds `beat` returns early with a lower bound
 // of its cost (still above `beat`).
 template <typename Groups>
@@ -732,7 +738,11 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
   // A group of `needed` keys makes needed / split full chunks and one shorter
   // one.  Costs are whole numbers of tiles, so their sums are exact in double
   // and do not depend on the order they are added in.
-  const double full_cost = static_cast<double>((split + kTile - 1) / kTile) + kItemOverheadTiles;
+  auto tiles_of = [](int64_t keys) {  // an item's cost in whole tiles
+    return (keys + kTile - 1) / kTile + static_cast<int64_t>(kItemOverheadTiles) +
+           kRefillTiles * ((keys - 1) / kDmaMaxRange);
+  };
+  const double full_cost = static_cast<double>(tiles_of(split));
   int64_t partials = 0, count = 0;
   double total = 0.0, longest = 0.0;
   groups([&](int64_t needed, int64_t group_partials) {
@@ -741,7 +751,7 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
     total += static_cast<double>(full) * full_cost;
     if (full > 0) longest = full_cost > longest ? full_cost : longest;
     if (rest > 0) {
-      const double cost = static_cast<double>((rest + kTile - 1) / kTile) + kItemOverheadTiles;
+      const double cost = static_cast<double>(tiles_of(rest));
       total += cost;
       longest = cost > longest ? cost : longest;
     }
@@ -766,13 +776,12 @@ double plan_cost_estimate(int64_t split, int64_t num_kv_heads, int64_t num_q_hea
   // Item costs in whole tiles, longest first (the order the plan dispatches
   // its items in, see the ordering below): counted by value, then listed.
   static_assert(kItemOverheadTiles == 3.0, "the schedule counts whole tiles");
-  constexpr int64_t kOverhead = 3;
-  const int64_t max_cost = (split + kTile - 1) / kTile + kOverhead;
+  const int64_t max_cost = tiles_of(split);
   std::vector<int64_t> cost_count(static_cast<size_t>(max_cost + 1), 0);
   groups([&](int64_t needed, int64_t) {
     const int64_t full = needed / split, rest = needed - full * split;
     cost_count[static_cast<size_t>(max_cost)] += full;
-    if (rest > 0) ++cost_count[static_cast<size_t>((rest + kTile - 1) / kTile + kOverhead)];
+    if (rest > 0) ++cost_count[static_cast<size_t>(tiles_of(rest))];
   });
   std::vector<int64_t> item_cost;
   item_cost.reserve(static_cast<size_t>(count));
@@ -1102,9 +1111,18 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
         }
       });
     };
+    // Beyond 7,680 keys the lengths grow by half up to the longest window's
+    // keys, which leaves every window whole (no partials, no combine).
     static const int64_t kCoarse[] = {512,  640,  768,  1024, 1280, 1536, 1792, 2048, 2304,
                                       2560, 3072, 3584, 4096, 4608, 5120, 6144, 7680};
-    for (const int64_t candidate : kCoarse) {
+    int64_t longest = kTile;
+    for (const int64_t keys : window_keys) longest = keys > longest ? keys : longest;
+    longest = (longest + kTile - 1) / kTile * kTile;
+    std::vector<int64_t> candidates(std::begin(kCoarse), std::end(kCoarse));
+    for (int64_t c = kCoarse[16] * 3 / 2 / kTile * kTile; c < longest; c = c * 3 / 2 / kTile * kTile)
+      candidates.push_back(c);
+    if (longest > kCoarse[16]) candidates.push_back(longest);
+    for (const int64_t candidate : candidates) {
       const double cost = estimate(candidate);
       if (best < 0.0 || cost <= best) {
         best = cost;
@@ -1113,7 +1131,7 @@ int compute_plan(const ll_repair_row *rows, int64_t num_rows, int64_t num_q_head
     }
     const int64_t coarse = split;
     for (int64_t candidate = coarse - 256; candidate <= coarse + 256; candidate += kTile) {
-      if (candidate < 512 || candidate > kDmaMaxRange || candidate == coarse) continue;
+      if (candidate < 512 || candidate == coarse) continue;
       const double cost = estimate(candidate);
       if (cost < best || (cost == best && candidate > split)) {
         best = cost;
@@ -1211,9 +1229,9 @@ int ll_repair_attention_plan(const ll_repair_row *rows, int64_t num_rows, int64_
     return fail(LL_ERR_INVALID_ARGUMENT, "rows must be a host array of num_rows >= 0 entries");
   if (num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads != 0)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be a multiple of num_kv_heads");
-  if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > kDmaMaxRange)
-    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d, at most %d",
-                kTile, kDmaMaxRange);
+  if (split_tokens < 0 || split_tokens % kTile != 0 || split_tokens > 0x7fffffc0)
+    return fail(LL_ERR_INVALID_ARGUMENT, "split_tokens must be 0 or a positive multiple of %d below 2^31",
+                kTile);
   if (num_q_heads > 65535)
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "num_q_heads must be at most 65535");
   thread_local RepairPlan kept;

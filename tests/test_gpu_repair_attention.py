@@ -239,6 +239,38 @@ def test_chunk_lengths_of_the_plan_search(gpu_device, split, dim):
     _check(spans, query, key_pool, value_pool, got, scale)
 
 
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("split", [7744, 15360, 20032])
+def test_items_longer_than_one_slot_list(gpu_device, split, dim):
+    """Work items over more keys than the slot list holds (7,680): the
+    workgroup refills it every 7,680 keys, carrying the softmax state, so an
+    item may span a whole request (20,032: every item whole).  A
+    20,000-token request with invalid slots on both sides of each refill
+    boundary; spans ending just before, at and after the boundaries."""
+
+    generator = torch.Generator(device=gpu_device).manual_seed(split + dim + 5)
+    pool, length = 21000, 20000
+    key_pool = _bf16((pool, 1, dim), generator, gpu_device)
+    value_pool = _bf16((pool, 1, dim), generator, gpu_device)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:length].clone()
+    for edge in (7680, 15360):
+        slots[edge - 1] = -1
+        slots[edge] = pool + 3  # outside the pool: an invisible key too
+    ends = [7679, 7680, 7681, 15359, 15361, 19000, 20000]
+    spans = [(slots, end - 16, end) for end in ends] + [(slots, 7600, 7700)]
+    report(f"long items, split {split}, head dim {dim}: spans {[(s, e) for _, s, e in spans]}")
+    plan = RepairAttentionPlan(spans, num_q_heads=7, num_kv_heads=1, head_dim=dim, split_tokens=split,
+                               validate=False)
+    assert plan.info["split_tokens"] == split
+    if split >= length:
+        assert plan.info["workspace_items"] == 0, plan.info  # whole items, no combine
+    query = _bf16((plan.num_queries, 7, dim), generator, gpu_device)
+    scale = 1.0 / math.sqrt(dim)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, scale)
+
+
 def test_dtype_checks_follow_the_reference(gpu_device):
     slots = torch.arange(64, device=gpu_device)
     plan = RepairAttentionPlan([(slots, 10, 26)], num_q_heads=8, num_kv_heads=2, head_dim=64)

@@ -286,8 +286,9 @@ def test_plan_rejects_bad_rows():
         _plan([(0, 5, 3, 0), (3, -1, 3, 0)])
     with pytest.raises(_native.NativeCallError, match="multiple of 64"):
         _plan([(0, 5, 3, 0)], split=100)
-    with pytest.raises(_native.NativeCallError, match="at most 7680"):
-        _plan([(0, 5, 3, 0)], split=7744)
+    with pytest.raises(_native.NativeCallError, match="below 2"):
+        _plan([(0, 5, 3, 0)], split=1 << 31)
+    _plan([(0, 5, 3, 0)], split=7744)  # items longer than one slot-list fill run whole
     with pytest.raises(_native.NativeCallError) as error:
         _plan([(0, 5, 3, 0)], q_heads=30, kv_heads=4)  # not a multiple
     assert error.value.reason == "kv_head_layout_mismatch"
