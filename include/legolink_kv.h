@@ -469,13 +469,15 @@ int64_t ll_order_maps_args_size(void);
  *   consecutive pairs that share every staged K/V tile (a window may start
  *   or end inside a tile, so groups that do not divide 16 still fill every
  *   item), splits long KV ranges into chunks of
- *   split_tokens keys (a multiple of 64, at most 7680; 0 lets the plan choose
- *   from a model of the device's workgroup rounds), and writes the item and
+ *   split_tokens keys (a multiple of 64 below 2^31; 0 lets the plan choose
+ *   from a model of the device's workgroup rounds, which may leave a range
+ *   whole: no partials, no combine), and writes the item and
  *   combine tables; the caller copies them to the device once and reuses them
  *   for every layer.  Call it with NULL tables to size them.  num_q_heads is
  *   at most 65535.
  *   ll_repair_attention runs one layer; it takes tables made by this plan
- *   (items over more than 7680 keys are not computed) and num_slots < 2^31.
+ *   and num_slots < 2^31.  A workgroup reads its item's slots into LDS 7,680
+ *   at a time, so items of any key length run in one workgroup.
  *
  * Replaces the FlashInfer block-sparse repair attention of
  * patched_sglang_files/python/sglang/srt/flashinfer_sparse_repair.py

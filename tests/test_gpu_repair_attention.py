@@ -216,7 +216,7 @@ def test_random_configurations(gpu_device, seed):
 @pytest.mark.parametrize("split", [192, 704, 2112, 4160, 7680])
 def test_chunk_lengths_of_the_plan_search(gpu_device, split, dim):
     """Key chunks of the lengths the plan's fine search picks (multiples of 64
-    that are not powers of two) up to the 7,680-key maximum, whose slot list
+    that are not powers of two) up to 7,680 keys, whose slot list
     fills the LDS the ring leaves: spans of an 8,000-token request ending
     just before, at and after chunk edges, GQA 7/1 and a 16-query span."""
 
@@ -357,9 +357,10 @@ def test_one_plan_serves_every_layer(gpu_device):
 @pytest.mark.parametrize("name", ["c3", "c5"])
 def test_full_size_workload_sampled(gpu_device, name):
     """The benchmark workloads at full size with the plan's own chunks (c5:
-    511 spans over a 32,768-token request, 7,680-key chunks and their
-    combine; c3: 448 eight-query spans of 64 requests sharing tiles, 6,208-key
-    chunks): the last row of every span (the one that sees the most keys) and
+    511 spans over a 32,768-token request, whole key ranges of up to 32,768
+    keys (four slot-list refills), no combine; c3: 448 eight-query spans of 64
+    requests sharing tiles, 6,208-key chunks and their combine): the last row
+    of every span (the one that sees the most keys) and
     64 random rows, each checked against fp32 torch attention on the device,
     within the same bound."""
 
