@@ -816,7 +816,7 @@ class KVLinkExecutor:
             repair_lists.append(plan.get("imp_indices"))
         block_counts = np.fromiter(map(len, key_lists), dtype=np.int64, count=len(key_lists))
         handles, unavailable = self.registry.link_handles(
-            [str(key) for key in itertools.chain.from_iterable(key_lists)])
+            list(map(str, itertools.chain.from_iterable(key_lists))))
         if unavailable:
             return one_by_one()
         slot_tensors = [slots if slots.device == device and slots.dtype == torch.int64
@@ -840,8 +840,15 @@ class KVLinkExecutor:
         # Per request, the largest position is max(end - 1, largest local
         # position); over the batch that is the maximum of both columns.
         max_position = int(max(int(ends.max()) - 1, int(records[:, 5].max())))
-        repair = np.concatenate([_index_array(values) + base
-                                 for values, base in zip(repair_lists, bases.tolist())]).astype(np.int64)
+        repair_lists = [[] if values is None else values for values in repair_lists]
+        if all(type(values) is list for values in repair_lists):
+            # The reference's plan format: one conversion of every request's
+            # list, then each request's base added.
+            lengths = np.fromiter(map(len, repair_lists), dtype=np.int64, count=len(repair_lists))
+            repair = _index_array(list(itertools.chain.from_iterable(repair_lists))) + np.repeat(bases, lengths)
+        else:
+            repair = np.concatenate([_index_array(values) + base
+                                     for values, base in zip(repair_lists, bases.tolist())]).astype(np.int64)
         return LinkMaps(request_slots=torch.cat(slot_tensors), blocks=blocks, handles=handles,
                         repair_positions=repair, prefix_token_count=int(counts[leading].sum()),
                         max_position=max_position, leading_blocks=leading, request_count=len(requests),
