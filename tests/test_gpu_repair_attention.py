@@ -212,6 +212,46 @@ def test_random_configurations(gpu_device, seed):
     _check(spans, query, key_pool, value_pool, got, scale)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_long_requests(gpu_device, seed):
+    """Seeded random long requests (8,000-24,000 keys), so that work items
+    cross one or more slot-list refills (every 7,680 keys): chunk lengths
+    beyond the refill size or automatic, invalid slots on refill edges, GQA
+    groups 1-8, head dims 64 and 128."""
+
+    rng = np.random.default_rng(5000 + seed)
+    hkv = int(rng.choice([1, 2]))
+    group = int(rng.choice([1, 3, 4, 7, 8]))
+    hq = hkv * group
+    dim = int(rng.choice([64, 128]))
+    dtype = torch.float16 if rng.random() < 0.3 else torch.bfloat16
+    length = int(rng.integers(8000, 24000))
+    pool = length + int(rng.integers(16, 2000))
+    split = int(rng.choice([0, 0, 8960, 16384, 24576]))
+    generator = torch.Generator(device=gpu_device).manual_seed(seed + 77)
+    key_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=dtype)
+    value_pool = _bf16((pool, hkv, dim), generator, gpu_device, dtype=dtype)
+    slots = torch.randperm(pool, generator=generator, device=gpu_device)[:length].clone()
+    for edge in range(7680, length, 7680):
+        if rng.random() < 0.5:
+            slots[edge - int(rng.integers(0, 2))] = -1
+    if rng.random() < 0.5:
+        slots = slots.to(torch.int32)
+    spans = []
+    for _ in range(int(rng.integers(1, 3))):
+        end = int(rng.integers(length // 3, length + 1))
+        spans.append((slots, max(0, end - int(rng.integers(1, 24))), end))
+    report(f"long seed {seed}: hq={hq} hkv={hkv} d={dim} {dtype} length={length} split={split} "
+           f"spans={[(s, e) for _, s, e in spans]}")
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, split_tokens=split,
+                               validate=False)
+    scale = 1.0 / math.sqrt(dim)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device, dtype=dtype)
+    got = plan.run(query, key_pool, value_pool, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    _check(spans, query, key_pool, value_pool, got, scale)
+
+
 @pytest.mark.parametrize("dim", [64, 128, 256])
 @pytest.mark.parametrize("split", [192, 704, 2112, 4160, 7680])
 def test_chunk_lengths_of_the_plan_search(gpu_device, split, dim):
