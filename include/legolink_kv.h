@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define LL_ABI_VERSION 16
+#define LL_ABI_VERSION 17
 
 /* hipStream_t, declared without pulling in the HIP headers. */
 struct ihipStream_t;
@@ -402,19 +402,22 @@ typedef struct ll_link_maps_args {
 } ll_link_maps_args;
 
 /*
- * Destination order of a map set.  No counterpart in the reference, whose torch
- * path writes the rows in plan order: the kernel's result does not depend on
- * the order it visits the map entries in (every destination row is written
- * once), and a single request's scattered row writes run faster in
- * destination-slot order.  This reorders the entries [prefix, count) of a map
- * set by destination slot into out_maps (and the mask with them), keeping
- * entries [0, prefix) (the identity rows) first, in three launches: a count
- * of the entries per bucket of 2^shift consecutive slots (16,384 buckets over
- * [0, num_slots); slots outside go to the first or last bucket), one
- * workgroup turning the counts into bucket offsets, and a scatter.  Entries of
- * one bucket are placed in no fixed order; with num_slots <= 16,384 buckets
- * hold one slot each.  out_maps is a permutation of the entries for any
- * input, duplicate or out-of-range slots included.
+ * Visit order of a map set.  No counterpart in the reference, whose torch path
+ * writes the rows in plan order: the kernel's result does not depend on the
+ * order it visits the map entries in (every destination row is written once).
+ * A single request's scattered row writes run faster in destination-slot
+ * order; a batch whose requests share catalogue blocks reads repeated source
+ * rows from cache in source-slot order.  This reorders the entries
+ * [prefix, count) of a map set by the slots of map row key_row (0: source
+ * slots, 1: destination slots) into out_maps (and the mask with them),
+ * keeping entries [0, prefix) (the identity rows) first, in three launches: a
+ * count of the entries per bucket of 2^shift consecutive slots (16,384
+ * buckets over [0, num_slots), the key pool's rows; slots outside go to the
+ * first or last bucket), one workgroup turning the counts into bucket
+ * offsets, and a scatter.  Entries of one bucket are placed in no fixed order;
+ * with num_slots <= 16,384 buckets hold one slot each.  out_maps is a
+ * permutation of the entries for any input, duplicate or out-of-range slots
+ * included.
  *
  * The workspace (LL_ORDER_WORKSPACE_BYTES, device, 16-byte aligned) must be
  * zero before its first use; every call leaves it so.  Calls that share a
@@ -431,11 +434,12 @@ typedef struct ll_order_maps_args {
   int64_t capacity;                /* row stride of maps and out_maps; count <= capacity < 2^31 */
   int64_t count;                   /* entries */
   int64_t prefix;                  /* 0 <= prefix <= count: entries kept in place */
-  int64_t num_slots;               /* destination pool rows (>= 1) */
+  int64_t num_slots;               /* rows of the pool the key slots index (>= 1) */
   int64_t *out_maps;               /* device int64 [4, capacity], not overlapping maps */
   uint8_t *out_mask;               /* device uint8 [capacity] (NULL iff mask is NULL) */
   void *workspace;
   int64_t workspace_bytes;
+  int64_t key_row;                 /* 0: order by source slots, 1: by destination slots (ABI 17) */
 } ll_order_maps_args;
 
 int ll_order_link_maps(const ll_order_maps_args *args, ll_stream_t stream);

@@ -916,8 +916,8 @@ __global__ void __launch_bounds__(256) build_link_maps_table_kernel(const MapTar
 }
 
 // ---------------------------------------------------------------------------
-// Destination order of a map set: a counting sort over buckets of 2^shift
-// consecutive destination slots, in three launches.  The count adds every
+// Visit order of a map set: a counting sort over buckets of 2^shift
+// consecutive slots of one map row (source or destination), in three launches.  The count adds every
 // entry to its bucket's counter (atomics); one workgroup turns the counts
 // into exclusive offsets and clears the counters for the next call; the
 // scatter takes each entry's place with an atomic increment of its bucket's
@@ -930,6 +930,7 @@ static_assert(kOrderBuckets % kOrderThreads == 0, "whole bucket runs per thread"
 
 struct OrderParams {
   const long long *maps;
+  const long long *key;  // the map row ordered by: maps + key_row * cap
   const unsigned char *mask;
   long long cap, count, prefix, num_slots;
   int shift;
@@ -947,7 +948,7 @@ __device__ __forceinline__ int order_bucket(long long slot, const OrderParams &p
 
 __global__ void __launch_bounds__(256) order_count_kernel(const OrderParams p) {
   const long long n = p.count - p.prefix;
-  const long long *dst = p.maps + p.cap + p.prefix;
+  const long long *dst = p.key + p.prefix;
   for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n;
        i += static_cast<long long>(gridDim.x) * 256)
     atomicAdd(&p.counts[order_bucket(dst[i], p)], 1);
@@ -1002,7 +1003,7 @@ __global__ void __launch_bounds__(256) order_scatter_kernel(const OrderParams p)
        i += static_cast<long long>(gridDim.x) * 256) {
     long long o = i;
     if (i >= p.prefix) {
-      const long long place = atomicAdd(&p.offsets[order_bucket(p.maps[p.cap + i], p)], 1);
+      const long long place = atomicAdd(&p.offsets[order_bucket(p.key[i], p)], 1);
       if (place < 0 || place >= n) continue;  // only if the workspace was shared by overlapping calls
       o = p.prefix + place;
     }
@@ -1995,6 +1996,8 @@ int ll_order_link_maps(const ll_order_maps_args *a, ll_stream_t stream) {
       a->prefix > a->count)
     return fail(LL_ERR_INVALID_ARGUMENT, "need 0 <= prefix <= count <= capacity < 2^31");
   if (a->num_slots < 1) return fail(LL_ERR_INVALID_ARGUMENT, "num_slots must be >= 1");
+  if (a->key_row != 0 && a->key_row != 1)
+    return fail(LL_ERR_INVALID_ARGUMENT, "key_row must be 0 (source slots) or 1 (destination slots)");
   if (a->count == 0) return LL_OK;
   if (a->maps == nullptr || a->out_maps == nullptr)
     return fail(LL_ERR_INVALID_ARGUMENT, "maps and out_maps must be device arrays");
@@ -2018,6 +2021,7 @@ int ll_order_link_maps(const ll_order_maps_args *a, ll_stream_t stream) {
                 LL_ORDER_WORKSPACE_BYTES);
   OrderParams p;
   p.maps = reinterpret_cast<const long long *>(a->maps);
+  p.key = p.maps + a->key_row * a->capacity;
   p.mask = a->mask;
   p.cap = a->capacity;
   p.count = a->count;

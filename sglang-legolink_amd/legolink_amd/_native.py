@@ -21,7 +21,7 @@ LIB_DIR = Path(__file__).resolve().parent / "lib"
 # LEGOLINK_KV_LIBRARY names another build of the library (the host-sanitized
 # one of the CPU sanitizer test).
 LIB_PATH = Path(os.environ.get("LEGOLINK_KV_LIBRARY") or LIB_DIR / "liblegolink_kv.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 # Element type codes (include/legolink_kv.h).
 DTYPE_FLOAT16 = 1
@@ -221,7 +221,7 @@ class LinkMapsArgs(ctypes.Structure):
     ]
 
 
-# Destination order of a map set (ll_order_link_maps).
+# Visit order of a map set (ll_order_link_maps).
 ORDER_BUCKETS = 16384
 ORDER_WORKSPACE_BYTES = 8 * ORDER_BUCKETS + 256
 
@@ -241,6 +241,7 @@ class OrderMapsArgs(ctypes.Structure):
         ("out_mask", _ptr),
         ("workspace", _ptr),
         ("workspace_bytes", _i64),
+        ("key_row", _i64),
     ]
 
 

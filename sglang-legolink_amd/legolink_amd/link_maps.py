@@ -249,16 +249,19 @@ def build_device_maps(plan: SegmentPlan, destination_slots: torch.Tensor, *, com
     return DeviceMaps(maps=maps, masks=masks, repair_destination_slots=repair, run_table=device_table)
 
 
-def order_by_destination(maps: torch.Tensor, mask: Optional[torch.Tensor], *, prefix: int, num_slots: int,
-                         workspace: torch.Tensor,
-                         stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """A map set's entries [prefix, n) in destination-slot order (slots in
-    buckets of 2^shift over the pool, 16,384 buckets; one slot per bucket up
-    to a 16,384-row pool), entries [0, prefix) first and in place; the mask
-    follows its entries.  ``workspace`` is a zeroed uint8 device tensor of
-    ``_native.ORDER_WORKSPACE_BYTES`` that calls on one stream may share
-    (``ll_order_link_maps``)."""
+def order_link_maps(maps: torch.Tensor, mask: Optional[torch.Tensor], *, key_row: int, prefix: int,
+                    num_slots: int, workspace: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """A map set's entries [prefix, n) ordered by the slots of map row
+    ``key_row`` (0: source slots, 1: destination slots), in buckets of 2^shift
+    slots (16,384 buckets over the ``num_slots`` rows of the pool those slots
+    index; one slot per bucket up to 16,384 rows); entries [0, prefix) stay
+    first and in place, and the mask follows its entries.  ``workspace`` is a
+    zeroed uint8 device tensor of ``_native.ORDER_WORKSPACE_BYTES`` that calls
+    on one stream may share (``ll_order_link_maps``)."""
 
+    if key_row not in (0, 1):
+        raise ValueError("key_row must be 0 (source slots) or 1 (destination slots)")
     n = int(maps.shape[1])
     out = torch.empty_like(maps)
     out_mask = None if mask is None else torch.empty_like(mask)
@@ -273,10 +276,20 @@ def order_by_destination(maps: torch.Tensor, mask: Optional[torch.Tensor], *, pr
     args.out_mask = None if out_mask is None else out_mask.data_ptr()
     args.workspace = workspace.data_ptr()
     args.workspace_bytes = int(workspace.numel())
+    args.key_row = int(key_row)
     if stream is None:
         stream = torch.cuda.current_stream(maps.device)
     _native.order_link_maps(args, stream.cuda_stream)
     return out, out_mask
+
+
+def order_by_destination(maps: torch.Tensor, mask: Optional[torch.Tensor], *, prefix: int, num_slots: int,
+                         workspace: torch.Tensor,
+                         stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """``order_link_maps`` by destination slot."""
+
+    return order_link_maps(maps, mask, key_row=1, prefix=prefix, num_slots=num_slots, workspace=workspace,
+                           stream=stream)
 
 
 def block_table(starts: Sequence[int], counts: Sequence[int], source_ptrs: Sequence[int],

@@ -1,9 +1,9 @@
-"""GPU checks of the destination ordering of a map set (ll_order_link_maps):
-the output is a permutation of the input entries that keeps the identity
-prefix in place and lists the rest by destination bucket (by slot where the
-pool has at most 16,384 rows); masks follow their entries; duplicate and
-out-of-range slots still give a permutation; the shared workspace is zero
-again after every call."""
+"""GPU checks of the visit ordering of a map set (ll_order_link_maps), by
+destination or by source slot: the output is a permutation of the input
+entries that keeps the identity prefix in place and lists the rest by bucket
+of the key slots (by slot where the pool has at most 16,384 rows); masks
+follow their entries; duplicate and out-of-range slots still give a
+permutation; the shared workspace is zero again after every call."""
 
 from __future__ import annotations
 
@@ -53,20 +53,23 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("key_row", [1, 0], ids=["by_destination", "by_source"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_destination_order_is_a_bucketed_permutation(gpu_device, case):
+def test_order_is_a_bucketed_permutation(gpu_device, case, key_row):
     name, n, prefix, num_slots, duplicates, outside, with_mask = case
-    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + key_row)
     workspace = torch.zeros(_native.ORDER_WORKSPACE_BYTES, dtype=torch.uint8, device=gpu_device)
     for call in range(2):  # the second call reuses the workspace the first left
         entries = n if call == 0 else max(prefix, n // 3)
         host = _maps(rng, entries, num_slots, duplicates=duplicates, outside=outside)
+        if key_row == 0:  # the slots to order by in the source row
+            host = host[[1, 0, 2, 3]].copy()
         mask_host = rng.integers(0, 2, size=entries).astype(np.uint8) if with_mask else None
         maps = torch.from_numpy(host).to(gpu_device)
         mask = torch.from_numpy(mask_host).to(gpu_device) if with_mask else None
         report(f"order {name} call {call}: {entries} entries, prefix {prefix}, pool {num_slots}")
-        out, out_mask = link_maps.order_by_destination(maps, mask, prefix=prefix, num_slots=num_slots,
-                                                       workspace=workspace)
+        out, out_mask = link_maps.order_link_maps(maps, mask, key_row=key_row, prefix=prefix,
+                                                  num_slots=num_slots, workspace=workspace)
         torch.cuda.synchronize(gpu_device)
         got = out.cpu().numpy()
         assert np.array_equal(got[:, :prefix], host[:, :prefix])
@@ -74,10 +77,10 @@ def test_destination_order_is_a_bucketed_permutation(gpu_device, case):
         order = np.argsort(host[3, prefix:])
         got_order = np.argsort(got[3, prefix:])
         assert np.array_equal(host[:, prefix:][:, order], got[:, prefix:][:, got_order])
-        buckets = _bucket(got[1, prefix:], num_slots)
+        buckets = _bucket(got[key_row, prefix:], num_slots)
         assert (np.diff(buckets) >= 0).all(), "tail not in bucket order"
         if num_slots <= _native.ORDER_BUCKETS and not outside:
-            assert (np.diff(got[1, prefix:]) >= 0).all()
+            assert (np.diff(got[key_row, prefix:]) >= 0).all()
         if with_mask:
             by_position = dict(zip(host[3].tolist(), mask_host.tolist()))
             assert out_mask.cpu().numpy().tolist() == [by_position[g] for g in got[3].tolist()]

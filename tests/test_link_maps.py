@@ -334,6 +334,7 @@ def test_order_entry_rejects_bad_arguments_before_any_launch():
         a.capacity = a.count = 100
         a.prefix, a.num_slots = 10, 1000
         a.workspace_bytes = _native.ORDER_WORKSPACE_BYTES
+        a.key_row = 1
         for key, value in fields.items():
             setattr(a, key, value)
         return a
@@ -352,6 +353,8 @@ def test_order_entry_rejects_bad_arguments_before_any_launch():
         (dict(workspace_bytes=_native.ORDER_WORKSPACE_BYTES - 1), "workspace"),
         (dict(workspace=None), "workspace"),
         (dict(workspace=0x300008), "16-byte aligned"),
+        (dict(key_row=2), "key_row"),
+        (dict(key_row=-1), "key_row"),
     ]:
         status = lib.ll_order_link_maps(ctypes.byref(args(**fields)), None)
         assert status == _native.LL_ERR_INVALID_ARGUMENT, fields
