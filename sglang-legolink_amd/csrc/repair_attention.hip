@@ -105,6 +105,7 @@ struct AttnParams {
   int group;
   int pair_chunks;   // workgroups per (item, KV head): 16 / (pairs per workgroup)
   int slots64;
+  unsigned pool_bytes;  // bytes of the K (and of the V) buffer, when they fit 32-bit offsets; else 0
   float scale_log2;
 };
 
@@ -231,6 +232,44 @@ __device__ inline void dma_pair(const void *src0, void *lds0, const void *src1, 
       : "memory");
 }
 
+// The same with 32-bit byte offsets into the K and V buffers (buffer loads:
+// one multiply-add per address instead of 64-bit address arithmetic), for
+// pools whose K and V buffers each fit in 4 GiB.  The resources hold the
+// buffer's base and size (loads past it would read zeros; the offsets used
+// stay inside).
+typedef int i32x4r __attribute__((ext_vector_type(4)));
+__device__ inline i32x4r buffer_resource(const void *base, unsigned bytes) {
+  const unsigned long long address = reinterpret_cast<unsigned long long>(base);
+  i32x4r r;
+  r[0] = static_cast<int>(static_cast<unsigned>(address));
+  r[1] = static_cast<int>(static_cast<unsigned>(address >> 32) & 0xffffu);  // stride 0
+  r[2] = static_cast<int>(bytes);
+  r[3] = 0x00020000;  // raw 32-bit dwords
+  return r;
+}
+
+__device__ inline void dma_pair_buffer(unsigned off0, void *lds0, i32x4r res0, unsigned off1, void *lds1,
+                                       i32x4r res1) {
+  const unsigned base0 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds0)));
+  const unsigned base1 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds1)));
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+      "s_mov_b32 m0, %4\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %6, 0 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off0), "v"(off1), "s"(base0), "s"(base1), "s"(res0), "s"(res1)
+      : "memory");
+}
+
 // s_barrier without __syncthreads()'s wait for all outstanding memory
 // operations (which would drain the gathers in flight); the empty asm keeps
 // the compiler from moving LDS accesses across it.
@@ -276,7 +315,7 @@ __host__ __device__ constexpr int m32_k_swizzle(int t) { return D >= 128 ? t % 1
 template <int D>
 __host__ __device__ constexpr int m32_v_swizzle(int t) { return D >= 128 ? 4 * (t % 4) : 4 * ((t / 2) % 2); }
 
-template <int D, typename E>
+template <int D, typename E, bool kOffsets>
 __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(const AttnParams p) {
   typedef typename E::frag frag;
   static_assert(D == 64 || D == 128 || D == 256, "head dims 64, 128 and 256");
@@ -384,25 +423,37 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   const long long row_stride = static_cast<long long>(p.hkv) * D;
   const bool have_slots = p.num_slots > 0;
   int g_token[kGathers], g_kchunk[kGathers], g_vchunk[kGathers];
+  unsigned g_koff[kGathers], g_voff[kGathers];  // kOffsets: the lane's bytes within a token's row
 #pragma unroll
   for (int j = 0; j < kGathers; ++j) {
     const int chunk_index = (kGathers * wave + j) * kWave + lane;
     g_token[j] = chunk_index / kChunksPerRow;
     g_kchunk[j] = (chunk_index % kChunksPerRow) ^ m32_k_swizzle<D>(g_token[j]);
     g_vchunk[j] = (chunk_index % kChunksPerRow) ^ m32_v_swizzle<D>(g_token[j]);
+    g_koff[j] = static_cast<unsigned>(hk * D * 2 + g_kchunk[j] * 16);
+    g_voff[j] = static_cast<unsigned>(hk * D * 2 + g_vchunk[j] * 16);
   }
+  const i32x4r k_res = buffer_resource(p.k, p.pool_bytes);
+  const i32x4r v_res = buffer_resource(p.v, p.pool_bytes);
   auto gather_slots = [&](int t, int *slots) {
 #pragma unroll
     for (int j = 0; j < kGathers; ++j) slots[j] = slot_lds[t * kTile + g_token[j]];
   };
+  // The slot list holds slots, or with kOffsets the byte offset of each
+  // token's row (row 0 for a token without a valid slot).
   auto gather_from = [&](const int *slots, unsigned char *k_dst, unsigned char *v_dst) {
     if (!have_slots) return;
 #pragma unroll
     for (int j = 0; j < kGathers; ++j) {
-      const int slot = max(slots[j], 0);
-      const long long row = slot * row_stride + hk * D;
       const int offset = (kGathers * wave + j) * kWave * 16;
-      dma_pair(p.k + row + g_kchunk[j] * 8, k_dst + offset, p.v + row + g_vchunk[j] * 8, v_dst + offset);
+      if constexpr (kOffsets) {
+        const unsigned row = static_cast<unsigned>(slots[j]);
+        dma_pair_buffer(row + g_koff[j], k_dst + offset, k_res, row + g_voff[j], v_dst + offset, v_res);
+      } else {
+        const int slot = max(slots[j], 0);
+        const long long row = slot * row_stride + hk * D;
+        dma_pair(p.k + row + g_kchunk[j] * 8, k_dst + offset, p.v + row + g_vchunk[j] * 8, v_dst + offset);
+      }
     }
   };
   auto gather = [&](int t, unsigned char *k_dst, unsigned char *v_dst) {
@@ -452,7 +503,10 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       const long long s = slot_at(p, static_cast<long long>(kv_off) + chunk_begin + i);
       if (s >= 0 && s < p.num_slots) slot = static_cast<int>(s);
     }
-    slot_lds[i] = slot;
+    if constexpr (kOffsets)
+      slot_lds[i] = static_cast<int>(static_cast<unsigned>(slot >= 0 ? slot : 0) * static_cast<unsigned>(2 * row_stride));
+    else
+      slot_lds[i] = slot;
     const unsigned long long bits = __builtin_amdgcn_ballot_w64(slot >= 0);
     if (lane == 0) tile_valid[i / kTile] = bits;
   }
@@ -487,7 +541,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     if (valid_bits != ~0ull) {
       // Zero the V rows of tokens without a valid slot (0 * Inf would be NaN).
       for (int c = tid; c < kTile * kChunksPerRow; c += kM32Threads)
-        if (slot_lds[t * kTile + c / kChunksPerRow] < 0)
+        if (((valid_bits >> (c / kChunksPerRow)) & 1ull) == 0)
           *reinterpret_cast<u32x4 *>(v_stage + c * 16) = u32x4{0u, 0u, 0u, 0u};
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       workgroup_barrier();
@@ -899,6 +953,12 @@ int check_attention_args(const ll_repair_attention_args *a) {
   return LL_OK;
 }
 
+template <int D, bool kOffsets>
+void launch_m32(bool f16, dim3 grid, hipStream_t s, const AttnParams &p) {
+  if (f16) repair_attention_m32_kernel<D, F16, kOffsets><<<grid, dim3(m32_threads<D>()), 0, s>>>(p);
+  else repair_attention_m32_kernel<D, Bf16, kOffsets><<<grid, dim3(m32_threads<D>()), 0, s>>>(p);
+}
+
 // Launches the attention (and the combine of split items) with the partial
 // results in `ws` (ws_items partial slots); the arguments are checked.
 int launch_attention(const ll_repair_attention_args *a, float *ws, long long ws_items, hipStream_t s) {
@@ -930,15 +990,18 @@ int launch_attention(const ll_repair_attention_args *a, float *ws, long long ws_
     return fail(LL_ERR_KV_HEAD_LAYOUT_MISMATCH, "too many KV heads for the grid");
   const dim3 grid(static_cast<unsigned>(a->num_items), static_cast<unsigned>(a->num_kv_heads * p.pair_chunks));
   const bool f16 = a->kv_dtype == LL_DTYPE_FLOAT16;
-  if (a->head_dim == 128) {
-    if (f16) repair_attention_m32_kernel<128, F16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<128, Bf16><<<grid, dim3(m32_threads<128>()), 0, s>>>(p);
-  } else if (a->head_dim == 64) {
-    if (f16) repair_attention_m32_kernel<64, F16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<64, Bf16><<<grid, dim3(m32_threads<64>()), 0, s>>>(p);
+  // 32-bit row offsets where every row of the K (and V) buffer is below 4 GiB.
+  const unsigned long long pool_bytes =
+      static_cast<unsigned long long>(a->num_slots) * a->num_kv_heads * a->head_dim * 2;
+  p.pool_bytes = pool_bytes <= 0xffffffffull ? static_cast<unsigned>(pool_bytes) : 0u;
+  if (p.pool_bytes != 0 || a->num_slots == 0) {
+    if (a->head_dim == 128) launch_m32<128, true>(f16, grid, s, p);
+    else if (a->head_dim == 64) launch_m32<64, true>(f16, grid, s, p);
+    else launch_m32<256, true>(f16, grid, s, p);
   } else {
-    if (f16) repair_attention_m32_kernel<256, F16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
-    else repair_attention_m32_kernel<256, Bf16><<<grid, dim3(m32_threads<256>()), 0, s>>>(p);
+    if (a->head_dim == 128) launch_m32<128, false>(f16, grid, s, p);
+    else if (a->head_dim == 64) launch_m32<64, false>(f16, grid, s, p);
+    else launch_m32<256, false>(f16, grid, s, p);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));

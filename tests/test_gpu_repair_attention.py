@@ -394,6 +394,43 @@ def test_one_plan_serves_every_layer(gpu_device):
         _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
 
 
+@pytest.mark.parametrize("pool", [(1 << 22) - 1, 4_500_000], ids=["top_rows_of_a_4gib_buffer", "beyond_4gib"])
+def test_pools_at_and_beyond_32_bit_row_offsets(gpu_device, pool):
+    """K and V buffers of up to 4 GiB (1 KiB rows: 4,194,303 slots) are
+    gathered with 32-bit byte offsets, larger ones with 64-bit addresses.
+    Slots at the top of each pool give the same output, bit for bit, as the
+    same rows gathered from a small pool, and match the oracle."""
+
+    generator = torch.Generator(device=gpu_device).manual_seed(8)
+    hq, hkv, dim = 28, 4, 128
+    key_pool = torch.empty((pool, hkv, dim), dtype=torch.bfloat16, device=gpu_device)
+    value_pool = torch.empty_like(key_pool)
+    # 3,000 distinct slots: most in the pool's top 64 Ki rows (past 4 GiB in
+    # the larger pool), a few at the bottom.
+    top = pool - 1 - torch.randperm(1 << 16, generator=generator, device=gpu_device)[:2900]
+    slots = torch.cat([top, torch.randperm(1 << 12, generator=generator, device=gpu_device)[:100]])
+    slots = slots[torch.randperm(slots.numel(), generator=generator, device=gpu_device)]
+    rows_k = _bf16((slots.numel(), hkv, dim), generator, gpu_device)
+    rows_v = _bf16((slots.numel(), hkv, dim), generator, gpu_device)
+    key_pool[slots] = rows_k
+    value_pool[slots] = rows_v
+    spans = [(slots, 1200, 1232), (slots, 2900, 2916), (slots, 2990, 3000)]
+    report(f"pool of {pool} slots ({pool * hkv * dim * 2 / 2**30:.2f} GiB per buffer), top slot {int(slots.max())}")
+    plan = RepairAttentionPlan(spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim, pool_size=pool)
+    query = _bf16((plan.num_queries, hq, dim), generator, gpu_device)
+    got = plan.run(query, key_pool, value_pool)
+    # The same rows at slots 0 .. 2,999 of a small pool.
+    small = torch.arange(slots.numel(), device=gpu_device)
+    small_spans = [(small, start, end) for _, start, end in spans]
+    small_plan = RepairAttentionPlan(small_spans, num_q_heads=hq, num_kv_heads=hkv, head_dim=dim,
+                                     pool_size=slots.numel())
+    want = small_plan.run(query, rows_k, rows_v)
+    torch.cuda.synchronize(gpu_device)
+    assert torch.equal(got, want)
+    del key_pool, value_pool
+    _check(small_spans, query, rows_k, rows_v, want, 1.0 / math.sqrt(dim))
+
+
 @pytest.mark.parametrize("name", ["c3", "c5"])
 def test_full_size_workload_sampled(gpu_device, name):
     """The benchmark workloads at full size with the plan's own chunks (c5:
