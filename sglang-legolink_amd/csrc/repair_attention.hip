@@ -44,6 +44,7 @@
 #include <algorithm>
 #include <functional>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "legolink_kv.h"
@@ -481,6 +482,26 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
   const int vu = li / 4;
   const int v_lane = (4 * h + vu) * kRowBytes + (2 * ((lane / 16) % 2) + (li % 4) / 2) * 16 + 8 * (li % 2);
   const int k_lane = col * kRowBytes;
+  // The lane's byte offsets within a stage: K per 16-dim step ks (its
+  // swizzled chunk), V per 32-dim block b.  Kept in registers (the empty asm
+  // stops the compiler from recomputing them per tile), so that with the
+  // stage a constant every fragment read is one register plus an immediate.
+  int k_off[kKSteps];
+#pragma unroll
+  for (int ks = 0; ks < kKSteps; ++ks) {
+    k_off[ks] = k_lane + ((2 * ks + h) ^ m32_k_swizzle<D>(col)) * 16;
+    asm volatile("" : "+v"(k_off[ks]));
+  }
+  // V offsets carry the V ring's LDS address (beyond the 16-bit immediate
+  // of the reads), so that the stage and step offsets stay immediates.
+  const unsigned v_ring_lds =
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)v_ring));
+  unsigned v_off[kDimBlocks];
+#pragma unroll
+  for (int b = 0; b < kDimBlocks; ++b) {
+    v_off[b] = v_ring_lds + v_lane + ((b ^ (m32_v_swizzle<D>(vu) / 4)) << 6);
+    asm volatile("" : "+v"(v_off[b]));
+  }
 
   // Tiles are gathered kLead ahead: tile t + kLead goes into the stage of
   // tile t - 1 once every wave is past it (the barrier at the top of tile t).
@@ -515,9 +536,14 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
 #pragma unroll
   for (int t = 0; t < kLead; ++t)
     if (t < tiles) gather(t, k_ring + t * kStageBytes, v_ring + t * kStageBytes);
-  for (int t = 0; t < tiles; ++t) {
-    const unsigned char *k_stage = k_ring + (t % kStages) * kStageBytes;
-    unsigned char *v_stage = v_ring + (t % kStages) * kStageBytes;
+  static_assert(kStages == 2 || kStages == 4, "the tile loop is unrolled over the ring's stages");
+  // One tile; the ring stage (t % kStages) is a compile-time constant, so
+  // that the stage offsets of the LDS reads are immediates.
+  auto tile_step = [&](const int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_tag)::value;  // t % kStages
+    constexpr int lead_stage = (stage + kLead) % kStages;
+    const unsigned char *k_stage = k_ring + stage * kStageBytes;
+    unsigned char *v_stage = v_ring + stage * kStageBytes;
     // The slots of the gather issued after the barrier and the tile's
     // validity bits are read before it, so that their LDS latency passes
     // while the waves meet (both tables are written only before the loop).
@@ -529,8 +555,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
     workgroup_barrier();
     if (t + kLead < tiles)
-      gather_from(next_slots, k_ring + ((t + kLead) % kStages) * kStageBytes,
-                  v_ring + ((t + kLead) % kStages) * kStageBytes);
+      gather_from(next_slots, k_ring + lead_stage * kStageBytes, v_ring + lead_stage * kStageBytes);
     // readfirstlane returns int: each half goes through unsigned so that the
     // low half is not sign-extended into the high one.
     const unsigned valid_lo =
@@ -547,10 +572,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       workgroup_barrier();
     }
     const int t0 = chunk_begin + t * kTile;
-    if (!wave_computes || t0 >= wave_stop) continue;
-    int k_addr = k_lane;
-    int v_addr = v_lane;
-    asm volatile("" : "+v"(k_addr), "+v"(v_addr));
+    if (!wave_computes || t0 >= wave_stop) return;
 
     f32x16 s[2];
 #pragma unroll
@@ -564,10 +586,9 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     auto load_k = [&](int batch, frag *dst) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int chunk = (2 * (2 * batch + j) + h) ^ m32_k_swizzle<D>(col);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
-          dst[2 * j + kb] = *reinterpret_cast<const frag *>(k_stage + k_addr + kb * 32 * kRowBytes + chunk * 16);
+          dst[2 * j + kb] = *reinterpret_cast<const frag *>(k_stage + k_off[2 * batch + j] + kb * 32 * kRowBytes);
       }
     };
     load_k(0, kf[0]);
@@ -651,9 +672,10 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       const int token_base = 16 * step * kRowBytes;
 #pragma unroll
       for (int b = 0; b < kDimBlocks; ++b) {
-        const unsigned char *lo = v_stage + v_addr + token_base + ((b ^ (m32_v_swizzle<D>(vu) / 4)) << 6);
-        const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)lo);
-        const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lo + 8 * kRowBytes));
+        const unsigned lo = v_off[b] + stage * kStageBytes + token_base;
+        const i16x4 a_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(static_cast<uintptr_t>(lo)));
+        const i16x4 a_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            reinterpret_cast<lds_i16x4 *>(static_cast<uintptr_t>(lo + 8 * kRowBytes)));
         u32x4 va;
         va[0] = __builtin_bit_cast(u32x2, a_lo)[0];
         va[1] = __builtin_bit_cast(u32x2, a_lo)[1];
@@ -668,6 +690,14 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       if (step + 1 < 4) load_v(step + 1, vf[(step + 1) % 2]);
 #pragma unroll
       for (int b = 0; b < kDimBlocks; ++b) o[b] = E::mfma32(vf[step % 2][b], pb[step], o[b]);
+    }
+  };
+  for (int tb = 0; tb < tiles; tb += kStages) {
+    tile_step(tb, std::integral_constant<int, 0>{});
+    if (tb + 1 < tiles) tile_step(tb + 1, std::integral_constant<int, 1>{});
+    if constexpr (kStages == 4) {
+      if (tb + 2 < tiles) tile_step(tb + 2, std::integral_constant<int, 2>{});
+      if (tb + 3 < tiles) tile_step(tb + 3, std::integral_constant<int, 3>{});
     }
   }
   }  // key chunks
