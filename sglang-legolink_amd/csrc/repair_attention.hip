@@ -554,8 +554,17 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
     else if (kLead >= 2 && t + 1 < tiles) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kGathers));
     else __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
     workgroup_barrier();
-    if (t + kLead < tiles)
+    // The gathers of tile t + kLead go to the stage every wave left before
+    // this barrier.  Waves issue them at different points of the tile (wave w
+    // after score batch w % 4), so that the workgroup's 32 loads do not all
+    // queue for the texture unit at once while every wave waits in order
+    // behind its own.
+    const bool gather_due = t + kLead < tiles;
+    auto issue_gathers = [&]() {
       gather_from(next_slots, k_ring + lead_stage * kStageBytes, v_ring + lead_stage * kStageBytes);
+    };
+    constexpr int kIssuePoints = kKSteps / 2;  // score batches of a tile
+    const int issue_point = wave % kIssuePoints;
     // readfirstlane returns int: each half goes through unsigned so that the
     // low half is not sign-extended into the high one.
     const unsigned valid_lo =
@@ -572,7 +581,10 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       workgroup_barrier();
     }
     const int t0 = chunk_begin + t * kTile;
-    if (!wave_computes || t0 >= wave_stop) return;
+    if (!wave_computes || t0 >= wave_stop) {
+      if (gather_due) issue_gathers();
+      return;
+    }
 
     f32x16 s[2];
 #pragma unroll
@@ -599,6 +611,7 @@ __global__ void __launch_bounds__(m32_threads<D>()) repair_attention_m32_kernel(
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) s[kb] = E::mfma32(kf[batch % 2][2 * j + kb], qf[2 * batch + j], s[kb]);
+      if (gather_due && issue_point == batch) issue_gathers();
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first batch's 4 LDS reads
 #pragma unroll
