@@ -394,15 +394,19 @@ def test_one_plan_serves_every_layer(gpu_device):
         _check(spans, query, key_pool, value_pool, got, 1.0 / math.sqrt(dim))
 
 
-@pytest.mark.parametrize("pool", [(1 << 22) - 1, 4_500_000], ids=["top_rows_of_a_4gib_buffer", "beyond_4gib"])
-def test_pools_at_and_beyond_32_bit_row_offsets(gpu_device, pool):
-    """K and V buffers of up to 4 GiB (1 KiB rows: 4,194,303 slots) are
-    gathered with 32-bit byte offsets, larger ones with 64-bit addresses.
-    Slots at the top of each pool give the same output, bit for bit, as the
-    same rows gathered from a small pool, and match the oracle."""
+@pytest.mark.parametrize("dim,pool", [(128, (1 << 22) - 1), (128, 4_500_000), (256, (1 << 21) - 1),
+                                      (256, 2_200_000), (64, (1 << 23) - 1), (64, 9_000_000)],
+                         ids=["d128_top_rows_of_a_4gib_buffer", "d128_beyond_4gib", "d256_top_rows_of_a_4gib_buffer",
+                              "d256_beyond_4gib", "d64_top_rows_of_a_4gib_buffer", "d64_beyond_4gib"])
+def test_pools_at_and_beyond_32_bit_row_offsets(gpu_device, dim, pool):
+    """K and V buffers of up to 4 GiB (4 KV heads: 4,194,303 slots of 1 KiB
+    rows at head dim 128, 2,097,151 at 256, 8,388,607 at 64) are gathered
+    with 32-bit byte offsets, larger ones with 64-bit addresses.  Slots at
+    the top of each pool give the same output, bit for bit, as the same rows
+    gathered from a small pool, and match the oracle."""
 
     generator = torch.Generator(device=gpu_device).manual_seed(8)
-    hq, hkv, dim = 28, 4, 128
+    hq, hkv = 28, 4
     key_pool = torch.empty((pool, hkv, dim), dtype=torch.bfloat16, device=gpu_device)
     value_pool = torch.empty_like(key_pool)
     # 3,000 distinct slots: most in the pool's top 64 Ki rows (past 4 GiB in
