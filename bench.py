@@ -466,7 +466,10 @@ def run_sweep(args: argparse.Namespace) -> None:
     link_bytes = workload.tokens * shape.bytes_per_token
     # (name, launch keywords); the first is the executor's choice for a single request.
     default = {"num_warps": 4, "layers_per_wave": 0, "stream_source_rows": True}
-    variants = [("default", {}), ("staged_deltas", {"delta_staging": "workgroup"})]
+    table_workspace = torch.empty(kv_link.delta_workspace_bytes(workload.tokens, workload.rotary_dim),
+                                  dtype=torch.uint8, device=device)
+    variants = [("default", {}), ("staged_deltas", {"delta_staging": "workgroup"}),
+                ("delta_table", {"delta_staging": "table", "delta_workspace": table_workspace})]
     detailed = {1, int(args.sweep_detail_run)}
     extra = [
         ("cached_loads", {"stream_source_rows": False}),
@@ -484,6 +487,8 @@ def run_sweep(args: argparse.Namespace) -> None:
     rows, schedule, dispatch, calibration, calibration_maps = [], [], 0, [], []
     cases = [(run, "random") for run in RUN_LENGTHS]
     cases += [(1, order) for order in SWEEP_ORDERS if order != "random"]
+    # The runs again in the executor's visit order (destination buckets).
+    cases += [(run, "bucketed_destination") for run in RUN_LENGTHS if run > 1]
     for run, order in cases:
         src, dst, local_np, global_np = ordered_maps(workload, run, order, seed=20260824 + run)
         src_t = torch.from_numpy(src).to(device)

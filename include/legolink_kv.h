@@ -95,11 +95,12 @@ enum {
  *                       two table rows read once per token); neox links
  *                       with full rotary and an fp32 table only, else per
  *                       wave;
- *   LL_DELTA_TABLE      a first launch writes every token's deltas to a
- *                       table in delta_workspace; a second, layer-major launch
- *                       moves two tokens of one layer per wave, reading each
- *                       token's deltas from that table (the GPU then works on
- *                       one layer's buffers at a time).  Neox links with full
+ *   LL_DELTA_TABLE      two layer-major launches (two tokens of one layer per
+ *                       wave, the GPU working on one layer's buffers at a
+ *                       time): the first moves the V rows and writes every
+ *                       token's deltas to a table in delta_workspace, the
+ *                       second moves the K rows, reading each token's deltas
+ *                       from that table.  Neox links with full
  *                       rotary, an fp32 table and rows of a multiple of 1 KiB
  *                       (num_heads * key_head_dim a multiple of 512), and a
  *                       workspace of at least num_tokens * rotary_dim * 4

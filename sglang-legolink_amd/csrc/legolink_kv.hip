@@ -111,6 +111,7 @@ struct LinkParams {
   int staged;                // vector kernel: deltas staged once per workgroup in LDS
   unsigned long long *skipped;  // tokens skipped for an out-of-range index, or NULL
   f32x2 *delta_table;        // layer-major kernel: per token and rotary pair (dc, ds)
+  int write_table;           // layer-major value pass: layer 0 writes the delta table
 };
 
 struct ScatterParams {
@@ -537,58 +538,33 @@ kv_link_vec_kernel(const LinkParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Layer-major link (LL_DELTA_TABLE).  Two launches:
+// Layer-major link (LL_DELTA_TABLE).  Two launches of kv_link_layer_kernel,
+// each a walk of the layers one after another (wave w moves two consecutive
+// tokens of one layer, one 1 KiB chunk of their rows per lane group), so that
+// at any time the GPU reads and writes about one buffer of one layer:
 //
-//   link_delta_table_kernel  entry [t][i] of the delta table = (dc, ds) of
-//                            rotary pair i of token t (one thread per entry,
-//                            consecutive threads on consecutive pairs, so the
-//                            cos/sin rows are read coalesced, once per token);
-//                            (1, 0) where the token keeps its rotation (the
-//                            identity prefix) or a position is out of range.
-//   kv_link_layer_kernel     wave w moves two consecutive tokens of one layer
-//                            (one 1 KiB chunk of their rows per lane group);
-//                            the waves of a launch go through the layers one
-//                            after another, so at any time the GPU reads and
-//                            writes the buffers of about one layer.  Each lane
-//                            reads its 8 pairs' deltas back from the table
-//                            (the table is small and stays in the caches).
-// The arithmetic is the vector kernel's: same delta_pair rounding points, same
-// rotate_neox, same bounds checks, skips and skipped-token count.
+//   value pass  the V rows (bit copies); with write_table, the waves of
+//               layer 0 also write the delta table: entry [t][i] = (dc, ds)
+//               of rotary pair i of token t (consecutive lanes on
+//               consecutive pairs, so the cos/sin rows are read coalesced,
+//               once per token), (1, 0) where the token keeps its rotation
+//               (the identity prefix) or a position is out of range;
+//   key pass    the K rows, each lane rotating its chunk with its 8 pairs'
+//               deltas read back from the table (the table is small and
+//               stays in the caches).
+// The second launch is ordered after the first on the stream, so the table
+// is complete when the key pass reads it.  The arithmetic is the vector
+// kernel's: same delta_pair rounding points, same rotate_neox, same bounds
+// checks, skips and skipped-token count (counted by the value pass).
 // Requirements (checked on the host): neox, rotary_dim == key_head_dim ==
 // value_head_dim == kD, an fp32 table with unit column stride and 16-byte
 // aligned rows, chunks_per_row a multiple of 64, 16-byte aligned buffers.
 // ---------------------------------------------------------------------------
 constexpr int kLayerMajorWaves = 4;  // waves per workgroup of the layer-major kernel
 
-template <bool kBF16, int kR, typename Index, bool kEager>
-__global__ void __launch_bounds__(256) link_delta_table_kernel(const LinkParams p) {
-  using Round = Rounding<kBF16, 3, kEager>;
-  constexpr int kPairs = kR / 2;
-  const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= p.num_tokens * kPairs) return;
-  const long long t = e / kPairs;
-  const int i = static_cast<int>(e - t * kPairs);
-  float dc = 1.0f, ds = 0.0f;
-  if (t >= p.prefix) {
-    const long long lp = static_cast<long long>(static_cast<const Index *>(p.lpos)[t]);
-    const long long gp = static_cast<long long>(static_cast<const Index *>(p.gpos)[t]);
-    if (lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows) {
-      const float *table = static_cast<const float *>(p.cs);
-      const float lc = table[lp * p.cs_stride_row + i];
-      const float ls = table[lp * p.cs_stride_row + i + kPairs];
-      const float gc = table[gp * p.cs_stride_row + i];
-      const float gs = table[gp * p.cs_stride_row + i + kPairs];
-      delta_pair<Round::kDelta, Round::kCast>(lc, ls, gc, gs, dc, ds);
-    }
-  }
-  f32x2 entry;
-  entry.x = dc;
-  entry.y = ds;
-  p.delta_table[e] = entry;
-}
-
-template <bool kBF16, int kD, typename Index, bool kStream, bool kEager>
+template <bool kBF16, int kD, typename Index, bool kStream, bool kEager, bool kKeys>
 __global__ void __launch_bounds__(kLayerMajorWaves * kWave) kv_link_layer_kernel(const LinkParams p) {
+  constexpr bool kValues = !kKeys;
   constexpr int kChunksPerHead = kD / 8;
   constexpr int kHalfChunks = kChunksPerHead / 2;  // chunks of a head's first rotate half
   constexpr int kPairs = kD / 2;                   // rotary pairs of a token (full rotary)
@@ -612,8 +588,8 @@ __global__ void __launch_bounds__(kLayerMajorWaves * kWave) kv_link_layer_kernel
   const int pb = (q % kHalfChunks) * 8;     // the lane's first rotary pair
 
   u32x4 kin[2], vin[2];
-  long long k_dst[2], v_dst[2], token[2];
-  bool ok[2], remap[2];
+  long long k_dst[2], v_dst[2], token[2], lpos[2], gpos[2];
+  bool ok[2], remap[2], use[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const long long t = 2 * pair + u;
@@ -629,17 +605,53 @@ __global__ void __launch_bounds__(kLayerMajorWaves * kWave) kv_link_layer_kernel
     const bool positions_ok = lp >= 0 && lp < p.cs_rows && gp >= 0 && gp < p.cs_rows;
     ok[u] = in_range && !masked && src >= 0 && src < p.src_num_slots && dst >= 0 && dst < p.num_slots &&
             (!remap[u] || positions_ok);
+    use[u] = remap[u] && positions_ok;
+    lpos[u] = use[u] ? lp : 0;
+    gpos[u] = use[u] ? gp : 0;
     // An unmasked token skipped for an out-of-range index is counted once:
     // by lane 0 of its first row part in layer 0.
-    if (p.skipped != nullptr && in_range && !ok[u] && !masked && layer == 0 && part == 0 && lane == 0)
+    if (kValues && p.skipped != nullptr && in_range && !ok[u] && !masked && layer == 0 && part == 0 &&
+        lane == 0)
       atomicAdd(p.skipped, 1ull);
     // Unconditional row loads: a token without a valid source reads row 0
     // (the host launches only when the source pool has rows) and stores nothing.
     const long long src_row = (src >= 0 && src < p.src_num_slots) ? src : 0;
-    kin[u] = load_row<kStream>(p.sk_layers[layer] + src_row * p.k_row_bytes + c * 16);
-    vin[u] = load_row<kStream>(p.sv_layers[layer] + src_row * p.v_row_bytes + c * 16);
-    k_dst[u] = dst * p.k_row_bytes + c * 16;
-    v_dst[u] = dst * p.v_row_bytes + c * 16;
+    if constexpr (kKeys) {
+      kin[u] = load_row<kStream>(p.sk_layers[layer] + src_row * p.k_row_bytes + c * 16);
+      k_dst[u] = dst * p.k_row_bytes + c * 16;
+    } else {
+      vin[u] = load_row<kStream>(p.sv_layers[layer] + src_row * p.v_row_bytes + c * 16);
+      v_dst[u] = dst * p.v_row_bytes + c * 16;
+    }
+  }
+  if constexpr (!kKeys) {
+    // Layer 0 of the value pass writes the delta table: entry (token, pair)
+    // = (dc, ds), identity where the token keeps its rotation.
+    if (p.write_table && layer == 0 && part == 0) {
+      const float *cs = static_cast<const float *>(p.cs);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (2 * pair + u >= p.num_tokens) continue;
+        for (int i = lane; i < kPairs; i += kWave) {
+          float dc = 1.0f, ds = 0.0f;
+          if (use[u]) {
+            const float lc = cs[lpos[u] * p.cs_stride_row + i];
+            const float ls = cs[lpos[u] * p.cs_stride_row + i + kPairs];
+            const float gc = cs[gpos[u] * p.cs_stride_row + i];
+            const float gs = cs[gpos[u] * p.cs_stride_row + i + kPairs];
+            delta_pair<Round::kDelta, Round::kCast>(lc, ls, gc, gs, dc, ds);
+          }
+          f32x2 entry;
+          entry.x = dc;
+          entry.y = ds;
+          p.delta_table[token[u] * kPairs + i] = entry;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (ok[u]) store_row_chunk(p.v_layers[layer] + v_dst[u], vin[u]);
+    return;
   }
   // The lanes' deltas: 8 consecutive (dc, ds) entries of the token's row of
   // the table, identity where the token keeps its rotation.
@@ -666,10 +678,7 @@ __global__ void __launch_bounds__(kLayerMajorWaves * kWave) kv_link_layer_kernel
     const u32x4 partner = xor_lane4<kHalfChunks>(kin[u]);
     u32x4 kout = kin[u];
     if (remap[u]) kout = rotate_neox<kBF16, Round::kProd>(kin[u], partner, dc, dsn);
-    if (ok[u]) {
-      store_row_chunk(p.k_layers[layer] + k_dst[u], kout);
-      store_row_chunk(p.v_layers[layer] + v_dst[u], vin[u]);
-    }
+    if (ok[u]) store_row_chunk(p.k_layers[layer] + k_dst[u], kout);
   }
 }
 
@@ -1198,11 +1207,10 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     plan->layers_per_wave = lpw;
     plan->staged = false;
     plan->layer_major = false;
-    // The delta table and the layer-major walk on request only: on c2's
-    // random rows a plain copy of one layer's rows at a time moves 3 % more
-    // than a token-major copy, but the link's staged workgroups (all layers of
-    // two tokens) already match the layer-major kernel, and the table's first
-    // launch then costs 1.0-1.4 % (c2 0.7424 against 0.7330 ms, c4, c5).
+    // The delta table and the layer-major passes on request only: on c2's
+    // fully fragmented rows in destination order they gain 0.6-1.1 % over
+    // the staged workgroups and on contiguous rows 12 %, but lose 0.3-2.1 %
+    // on rows in runs of 4-64 slots.
     if (a->delta_staging == LL_DELTA_TABLE && table_fits(a)) {
       const long long pairs = (a->num_tokens + 1) / 2;
       const long long waves = pairs * (chunks / kWave) * layers_first;
@@ -1332,52 +1340,44 @@ void launch_vec(int cache_dtype, int d, dim3 grid, dim3 block, hipStream_t s, co
   else launch_vec_cache<kBF16, false>(cache_dtype, d, grid, block, s, p, neox);
 }
 
-// Layer-major link: the delta table once per call, then one kernel per
-// launch of <= 64 layers.
-template <bool kBF16, int kD, typename Index, bool kEager>
-void launch_delta_table_typed(hipStream_t s, const LinkParams &p) {
-  const long long entries = p.num_tokens * (kD / 2);
-  link_delta_table_kernel<kBF16, kD, Index, kEager>
-      <<<dim3(static_cast<unsigned>((entries + 255) / 256)), dim3(256), 0, s>>>(p);
-}
-
+// Layer-major link: per launch of <= 64 layers, the value pass (the first
+// one also writing the delta table) and then the key pass.
 template <bool kBF16, int kD, typename Index, bool kEager>
 void launch_layer_major_typed(dim3 grid, hipStream_t s, const LinkParams &p) {
   const dim3 block(kLayerMajorWaves * kWave);
-  if (p.stream_rows) kv_link_layer_kernel<kBF16, kD, Index, true, kEager><<<grid, block, 0, s>>>(p);
-  else kv_link_layer_kernel<kBF16, kD, Index, false, kEager><<<grid, block, 0, s>>>(p);
+  if (p.stream_rows) {
+    kv_link_layer_kernel<kBF16, kD, Index, true, kEager, false><<<grid, block, 0, s>>>(p);
+    kv_link_layer_kernel<kBF16, kD, Index, true, kEager, true><<<grid, block, 0, s>>>(p);
+  } else {
+    kv_link_layer_kernel<kBF16, kD, Index, false, kEager, false><<<grid, block, 0, s>>>(p);
+    kv_link_layer_kernel<kBF16, kD, Index, false, kEager, true><<<grid, block, 0, s>>>(p);
+  }
 }
 
 template <bool kBF16, int kD, bool kEager>
-void launch_layer_major_index(bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+void launch_layer_major_index(dim3 grid, hipStream_t s, const LinkParams &p) {
   const bool index64 = (p.idx64 & 15) == 15;  // one index type for the four maps (the plan checks)
-  if (table) {
-    if (index64) launch_delta_table_typed<kBF16, kD, long long, kEager>(s, p);
-    else launch_delta_table_typed<kBF16, kD, int, kEager>(s, p);
-  } else {
-    if (index64) launch_layer_major_typed<kBF16, kD, long long, kEager>(grid, s, p);
-    else launch_layer_major_typed<kBF16, kD, int, kEager>(grid, s, p);
-  }
+  if (index64) launch_layer_major_typed<kBF16, kD, long long, kEager>(grid, s, p);
+  else launch_layer_major_typed<kBF16, kD, int, kEager>(grid, s, p);
 }
 
 template <bool kBF16, bool kEager>
-void launch_layer_major_dim(bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+void launch_layer_major_dim(dim3 grid, hipStream_t s, const LinkParams &p) {
   switch (p.kdim) {
-    case 32: launch_layer_major_index<kBF16, 32, kEager>(table, grid, s, p); break;
-    case 64: launch_layer_major_index<kBF16, 64, kEager>(table, grid, s, p); break;
-    case 128: launch_layer_major_index<kBF16, 128, kEager>(table, grid, s, p); break;
-    default: launch_layer_major_index<kBF16, 256, kEager>(table, grid, s, p); break;
+    case 32: launch_layer_major_index<kBF16, 32, kEager>(grid, s, p); break;
+    case 64: launch_layer_major_index<kBF16, 64, kEager>(grid, s, p); break;
+    case 128: launch_layer_major_index<kBF16, 128, kEager>(grid, s, p); break;
+    default: launch_layer_major_index<kBF16, 256, kEager>(grid, s, p); break;
   }
 }
 
-// table: launch the delta table kernel (else the layer-major link kernel).
-void launch_layer_major(bool bf16, bool table, dim3 grid, hipStream_t s, const LinkParams &p) {
+void launch_layer_major(bool bf16, dim3 grid, hipStream_t s, const LinkParams &p) {
   if (bf16) {
-    if (p.eager) launch_layer_major_dim<true, true>(table, grid, s, p);
-    else launch_layer_major_dim<true, false>(table, grid, s, p);
+    if (p.eager) launch_layer_major_dim<true, true>(grid, s, p);
+    else launch_layer_major_dim<true, false>(grid, s, p);
   } else {
-    if (p.eager) launch_layer_major_dim<false, true>(table, grid, s, p);
-    else launch_layer_major_dim<false, false>(table, grid, s, p);
+    if (p.eager) launch_layer_major_dim<false, true>(grid, s, p);
+    else launch_layer_major_dim<false, false>(grid, s, p);
   }
 }
 
@@ -1535,11 +1535,7 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
     return LL_OK;
   }
 
-  if (plan.layer_major) {
-    launch_layer_major(bf16, true, dim3(1), s, p);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return fail(LL_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-  }
+  p.write_table = plan.layer_major ? 1 : 0;
   for (int64_t base = 0; base < a->num_layers; base += kMaxLayersPerLaunch) {
     const int n = static_cast<int>(a->num_layers - base < kMaxLayersPerLaunch
                                        ? a->num_layers - base
@@ -1558,7 +1554,8 @@ int ll_kv_link(const ll_kv_link_args *a, ll_stream_t stream) {
       const long long pairs = (p.num_tokens + 1) / 2;
       const long long waves = pairs * (p.chunks_per_row / kWave) * n;
       const dim3 grid(static_cast<unsigned>((waves + kLayerMajorWaves - 1) / kLayerMajorWaves));
-      launch_layer_major(bf16, false, grid, s, p);
+      launch_layer_major(bf16, grid, s, p);
+      p.write_table = 0;  // the first launch's value pass wrote it
     } else if (plan.kernel == LL_KERNEL_VECTOR) {
       const int lpw = plan.layers_per_wave < n ? plan.layers_per_wave : n;
       p.layers_per_wave = lpw;
