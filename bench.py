@@ -313,7 +313,8 @@ class _RowCalibration:
             _fields_ = [("struct_size", i64), ("num_layers", i64), ("key_layers", ptr), ("value_layers", ptr),
                         ("num_slots", i64), ("row_bytes", i64), ("num_tokens", i64), ("source_slots", ptr),
                         ("destination_slots", ptr), ("mode", i64), ("layer_major", i64),
-                        ("layers_per_wave", i64), ("tokens_per_wave", i64), ("lds_bytes", i64), ("sink", ptr)]
+                        ("layers_per_wave", i64), ("tokens_per_wave", i64), ("lds_bytes", i64), ("sink", ptr),
+                        ("buffers", i64)]
 
         self.Args = Args
         self.lib.llc_rows.argtypes = [ctypes.POINTER(Args), ptr]
@@ -325,7 +326,7 @@ class _RowCalibration:
         self.torch = torch
 
     def prepare(self, keys, values, src, dst, *, mode: str, layer_major: bool, per_wave: int, lds_bytes: int,
-                sink):
+                sink, buffers: int = 3):
         ctypes = self.ctypes
         key_table = (ctypes.c_void_p * len(keys))(*[k.data_ptr() for k in keys])
         value_table = (ctypes.c_void_p * len(values))(*[v.data_ptr() for v in values])
@@ -335,7 +336,7 @@ class _RowCalibration:
                          num_tokens=int(src.numel()), source_slots=src.data_ptr(), destination_slots=dst.data_ptr(),
                          mode=self.MODES[mode], layer_major=1 if layer_major else 0,
                          layers_per_wave=0 if layer_major else per_wave, tokens_per_wave=per_wave if layer_major else 0,
-                         lds_bytes=lds_bytes, sink=sink.data_ptr())
+                         lds_bytes=lds_bytes, sink=sink.data_ptr(), buffers=buffers)
         keep = (key_table, value_table, args, keys, values, src, dst, sink)
         torch = self.torch
 
@@ -356,7 +357,8 @@ def calibrate_rows(torch, workload, keys, values, src_t, dst_t, order: str, args
     """The link's row traffic on these maps, moved by code other than the link
     kernel: the calibration kernels (copy, read only, write only; token-major
     4 layers per wave and layer-major 2 tokens per wave; three occupancies)
-    and torch's own index kernels per layer (index_select + index_copy_ as the
+    and in two layer-major passes (K rows, then V rows), and torch's own index
+    kernels per layer (index_select + index_copy_ as the
     reference's eager path moves rows, and each half alone: the gather into a
     contiguous buffer, the scatter from one).  GB/s count the bytes each
     variant moves: the link's 2 x T x L x (K + V row) for a copy, half of it
@@ -379,6 +381,23 @@ def calibrate_rows(torch, workload, keys, values, src_t, dst_t, order: str, args
                 rows.append({"order": order, "source": "calibration", "mode": mode, "variant": shape,
                              "ms": round(ms, 5), "bytes": moved, "GBps": round(moved / ms / 1e6, 1)})
                 log(f"calibration {order:18s} {mode:10s} {shape:34s} {ms:.4f} ms {moved / ms / 1e6:8.1f} GB/s")
+    # The copy in two layer-major passes (all K rows, then all V rows), as the
+    # delta-table link moves them.
+    for per_wave in (2, 4):
+        key_pass = calibration.prepare(keys, values, src_t, dst_t, mode="copy", layer_major=True,
+                                       per_wave=per_wave, lds_bytes=0, sink=sink, buffers=1)
+        value_pass = calibration.prepare(keys, values, src_t, dst_t, mode="copy", layer_major=True,
+                                         per_wave=per_wave, lds_bytes=0, sink=sink, buffers=2)
+
+        def two_passes(key_pass=key_pass, value_pass=value_pass) -> None:
+            key_pass()
+            value_pass()
+
+        ms = _median_ms(torch, two_passes, args.steps, args.warmup)
+        shape = f"layer_major_{per_wave}_tokens_two_passes"
+        rows.append({"order": order, "source": "calibration", "mode": "copy", "variant": shape,
+                     "ms": round(ms, 5), "bytes": 2 * one_way, "GBps": round(2 * one_way / ms / 1e6, 1)})
+        log(f"calibration {order:18s} {'copy':10s} {shape:34s} {ms:.4f} ms {2 * one_way / ms / 1e6:8.1f} GB/s")
     staging_k = torch.empty((workload.tokens,) + tuple(keys[0].shape[1:]), dtype=keys[0].dtype, device=keys[0].device)
     staging_v = torch.empty_like(staging_k)
 

@@ -1207,10 +1207,10 @@ int plan_link(const ll_kv_link_args *a, LinkPlan *plan) {
     plan->layers_per_wave = lpw;
     plan->staged = false;
     plan->layer_major = false;
-    // The delta table and the layer-major passes on request only: on c2's
-    // fully fragmented rows in destination order they gain 0.6-1.1 % over
-    // the staged workgroups and on contiguous rows 12 %, but lose 0.3-2.1 %
-    // on rows in runs of 4-64 slots.
+    // The delta table and the layer-major passes on request only: against
+    // the staged workgroups they gain 12 % on contiguous rows, but lose
+    // 1.4-2.0 % on the executor's own c2, c4 and c5 maps and 0.3-2.1 % on
+    // rows in runs of 4-64 slots.
     if (a->delta_staging == LL_DELTA_TABLE && table_fits(a)) {
       const long long pairs = (a->num_tokens + 1) / 2;
       const long long waves = pairs * (chunks / kWave) * layers_first;

@@ -13,7 +13,9 @@
 // token-major (a wave walks `layers_per_wave` layers of one token, the link
 // kernel's order) and layer-major (a wave moves `tokens_per_wave` tokens of
 // one layer; the grid walks the layers one after another).  A dynamic LDS
-// allocation per workgroup limits how many workgroups share a CU.
+// allocation per workgroup limits how many workgroups share a CU.  A launch
+// may move the K rows only or the V rows only (two such launches: a copy in
+// two passes, one buffer of one layer at a time).
 //
 // Built as liblegolink_calibration.so, separate from the link library: it is
 // measurement infrastructure and no part of the link's C ABI.
@@ -42,6 +44,7 @@ typedef struct llc_row_args {
   int64_t tokens_per_wave;       // layer-major: divides num_tokens
   int64_t lds_bytes;             // dynamic LDS per 256-thread workgroup, 0..65536 (occupancy limit)
   uint32_t *sink;                // device [4 * 65536] words: read-only mode's (never taken) output
+  int64_t buffers;               // 1 K rows only, 2 V rows only, 3 (or 0) both
 } llc_row_args;
 
 int llc_rows(const llc_row_args *args, hipStream_t stream);
@@ -71,6 +74,7 @@ struct RowParams {
   int num_layers;
   int layer_major;
   int per_wave;           // layers (token-major) or tokens (layer-major) per wave
+  int buffers;            // bit 0 K rows, bit 1 V rows
 };
 
 thread_local std::string g_error;
@@ -98,8 +102,9 @@ __device__ __forceinline__ void item_of(const RowParams &p, long long w, int i, 
   }
 }
 
-template <int kMode>
+template <int kMode, int kBuffers>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave) row_calibration_kernel(const RowParams p) {
+  constexpr bool kK = (kBuffers & 1) != 0, kV = (kBuffers & 2) != 0;
   extern __shared__ char occupancy[];
   const int lane = threadIdx.x & (kWave - 1);
   const long long w = static_cast<long long>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
@@ -122,8 +127,9 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) row_calibration_kernel
       const long long so = (ok[u] ? s : 0) * p.row_bytes + offset;
       d[u] = (ok[u] ? t : 0) * p.row_bytes + offset;
       if constexpr (kMode != 2) {
-        kin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p.k[layer[u]] + so));
-        vin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p.v[layer[u]] + so));
+        kin[u] = vin[u] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (kK) kin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p.k[layer[u]] + so));
+        if constexpr (kV) vin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p.v[layer[u]] + so));
       } else {
         kin[u] = u32x4{static_cast<uint32_t>(token), static_cast<uint32_t>(layer[u]), static_cast<uint32_t>(lane), 1u};
         vin[u] = u32x4{static_cast<uint32_t>(token), static_cast<uint32_t>(layer[u]), static_cast<uint32_t>(lane), 2u};
@@ -135,8 +141,8 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) row_calibration_kernel
         acc ^= kin[u];
         acc ^= vin[u];
       } else if (ok[u]) {
-        __builtin_nontemporal_store(kin[u], reinterpret_cast<u32x4 *>(p.k[layer[u]] + d[u]));
-        __builtin_nontemporal_store(vin[u], reinterpret_cast<u32x4 *>(p.v[layer[u]] + d[u]));
+        if constexpr (kK) __builtin_nontemporal_store(kin[u], reinterpret_cast<u32x4 *>(p.k[layer[u]] + d[u]));
+        if constexpr (kV) __builtin_nontemporal_store(vin[u], reinterpret_cast<u32x4 *>(p.v[layer[u]] + d[u]));
       }
     }
   }
@@ -193,15 +199,25 @@ extern "C" int llc_rows(const llc_row_args *a, hipStream_t stream) {
   p.num_tokens = a->num_tokens;
   p.num_layers = static_cast<int>(a->num_layers);
   p.layer_major = a->layer_major ? 1 : 0;
+  if (a->buffers < 0 || a->buffers > 3) return fail("buffers must be 0..3");
+  p.buffers = a->buffers == 0 ? 3 : static_cast<int>(a->buffers);
   p.per_wave = per_wave;
   p.waves = groups * p.chunks;
   const long long blocks = (p.waves + kWavesPerBlock - 1) / kWavesPerBlock;
   if (blocks > 0x7fffffffLL) return fail("too many rows for one grid");
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWavesPerBlock * kWave);
   const size_t lds = static_cast<size_t>(a->lds_bytes);
-  if (a->mode == 0) row_calibration_kernel<0><<<grid, block, lds, stream>>>(p);
-  else if (a->mode == 1) row_calibration_kernel<1><<<grid, block, lds, stream>>>(p);
-  else row_calibration_kernel<2><<<grid, block, lds, stream>>>(p);
+  if (a->mode == 0) {
+    if (p.buffers == 1) row_calibration_kernel<0, 1><<<grid, block, lds, stream>>>(p);
+    else if (p.buffers == 2) row_calibration_kernel<0, 2><<<grid, block, lds, stream>>>(p);
+    else row_calibration_kernel<0, 3><<<grid, block, lds, stream>>>(p);
+  } else if (a->mode == 1) {
+    if (p.buffers != 3) return fail("read only moves both buffers");
+    row_calibration_kernel<1, 3><<<grid, block, lds, stream>>>(p);
+  } else {
+    if (p.buffers != 3) return fail("write only moves both buffers");
+    row_calibration_kernel<2, 3><<<grid, block, lds, stream>>>(p);
+  }
   const hipError_t error = hipGetLastError();
   if (error != hipSuccess) {
     g_error = std::string("launch failed: ") + hipGetErrorString(error);

@@ -483,10 +483,11 @@ class PreparedLink:
         if sort_row == 1 and order_workspace is None:
             order_workspace = torch.zeros(_native.ORDER_WORKSPACE_BYTES, dtype=torch.uint8,
                                           device=key_buffers[0].device)
-        # delta_staging "table": a first launch writes every token's RoPE delta
-        # to a table and a second walks the rows layer by layer (measured
-        # 1.0-1.4 % slower than the default staged deltas on c2, c4, c5); the
-        # launches run one after another on one stream and share one workspace.
+        # delta_staging "table": a layer-major value pass writes every token's
+        # RoPE delta to a table and a layer-major key pass reads it back
+        # (measured 1.4-2.0 % slower than the default staged deltas on c2,
+        # c4, c5); the launches run one after another on one stream and share
+        # one workspace.
         self.delta_workspace = None
         if (delta_staging == "table"
                 and int(key_buffers[0].shape[1]) * int(key_buffers[0].shape[2]) % 512 == 0):
