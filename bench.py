@@ -546,6 +546,68 @@ def run_sweep(args: argparse.Namespace) -> None:
                       "steps": args.steps, "warmup": args.warmup, "peak_GBps": HBM_PEAK_GBPS}), flush=True)
 
 
+def same_maps_ceiling(torch, prepared, keys, values, link_bytes: int, args) -> dict | None:
+    """The fastest independent copy of exactly the rows this link moves: the
+    row-calibration kernels (copy, read only, write only) on the link's own
+    device maps, timed in this process alternately with the link itself
+    (three rounds, median of 20 launches each).  None where the calibration
+    does not apply (several map sets, rows not a multiple of 1 KiB, or the
+    calibration library not built)."""
+
+    import numpy as np
+
+    maps = prepared.kernel_maps
+    row = int(keys[0][0].numel()) * keys[0].element_size()
+    if len(maps) != 1 or row % 1024 or int(maps[0].shape[1]) % 2:
+        return None
+    try:
+        calibration = _RowCalibration(torch)
+    except SystemExit:
+        return None
+    src, dst = maps[0][0].contiguous(), maps[0][1].contiguous()
+    sink = torch.zeros(65536 * 4, dtype=torch.int32, device=keys[0].device)
+    shapes = {"layer_major_2_tokens": (True, 2), "token_major_4_layers": (False, 4)}
+    runs = {"link": prepared.launch}
+    moved = {"link": link_bytes}
+    for mode in ("copy", "read_only", "write_only"):
+        for shape, (layer_major, per_wave) in shapes.items():
+            if not layer_major and len(keys) % per_wave:
+                continue
+            runs[f"{mode} {shape}"] = calibration.prepare(keys, values, src, dst, mode=mode, layer_major=layer_major,
+                                                          per_wave=per_wave, lds_bytes=0, sink=sink)
+            moved[f"{mode} {shape}"] = link_bytes if mode == "copy" else link_bytes // 2
+    key_pass = calibration.prepare(keys, values, src, dst, mode="copy", layer_major=True, per_wave=2,
+                                   lds_bytes=0, sink=sink, buffers=1)
+    value_pass = calibration.prepare(keys, values, src, dst, mode="copy", layer_major=True, per_wave=2,
+                                     lds_bytes=0, sink=sink, buffers=2)
+
+    def two_passes() -> None:
+        key_pass()
+        value_pass()
+
+    runs["copy layer_major_2_tokens_two_passes"] = two_passes
+    moved["copy layer_major_2_tokens_two_passes"] = link_bytes
+    times = {name: [] for name in runs}
+    for _ in range(3):
+        for name, run in runs.items():
+            times[name].append(_median_ms(torch, run, 20, 3))
+    gbps = {name: moved[name] / float(np.median(ms)) / 1e6 for name, ms in times.items()}
+    copies = {name: value for name, value in gbps.items() if name.startswith("copy ")}
+    best = max(copies, key=copies.get)
+    reads = [float(np.median(times[n])) for n in times if n.startswith("read_only")]
+    writes = [float(np.median(times[n])) for n in times if n.startswith("write_only")]
+    halves = link_bytes / (min(reads) + min(writes)) / 1e6 if reads and writes else None
+    log(f"same-maps ceiling: link {gbps['link']:.1f} GB/s, best copy {copies[best]:.1f} GB/s ({best}), "
+        f"ratio {gbps['link'] / copies[best]:.4f}")
+    return {"GBps": round(copies[best], 1), "frac": round(copies[best] / HBM_PEAK_GBPS, 4),
+            "what": f"fastest independent copy of this link's own rows (the executor's maps of this run), "
+                    f"calibration {best.split(' ', 1)[1]}, timed in this process alternately with the link",
+            "halves_bound_GBps": None if halves is None else round(halves, 1),
+            "link_in_same_run_GBps": round(gbps["link"], 1),
+            "link_over_ceiling_in_same_run": round(gbps["link"] / copies[best], 4),
+            "variants_GBps": {name: round(value, 1) for name, value in gbps.items() if name != "link"}}
+
+
 def time_attention_plan(workload, requests, device) -> float | None:
     """Host time of the repair pass's attention plan for this link's repair
     spans (built once per batch, shared by every layer; Qwen's 7 query heads
@@ -1021,6 +1083,15 @@ def main() -> int:
     executor.check_skipped_rows()
 
     bytes_info = workload.algorithmic_bytes()
+    ceiling = None
+    if args.tp == 1 and not clone:
+        ceiling = same_maps_ceiling(torch, prepared, keys, values, bytes_info["link_bytes"], args)
+    if args.tp == 1:
+        committed = load_pattern_ceiling(workload.name)
+        if ceiling is None:
+            ceiling = committed
+        elif committed is not None:
+            ceiling["synthetic_sweep"] = committed
     total_bytes = bytes_info["total_bytes"]
     value = total_bytes / (ms_per_step / 1e3) / 1e9
     link_avg_ms = float(np.mean(link_ms))
@@ -1073,7 +1144,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic if not clone else None,
             "algorithmic_bytes_per_launch": bytes_info["link_bytes"],
-            "pattern_ceiling": load_pattern_ceiling(workload.name) if args.tp == 1 else None,
+            "pattern_ceiling": ceiling,
         },
         "cpu_baseline": None,
     }

@@ -585,6 +585,14 @@ class PreparedLink:
         self.algorithmic_link_bytes = self.linked_token_count * (key_row + value_row) * 2 * len(layers)
 
     @property
+    def kernel_maps(self) -> list[torch.Tensor]:
+        """The device maps the link kernels read, one [4, N] int64 tensor per
+        source (source slot, destination slot, local and global position per
+        token, in the visit order)."""
+
+        return list(self._kernel_maps)
+
+    @property
     def launch_info(self) -> list[dict[str, int]]:
         return [link.launch for link in self._links]
 
