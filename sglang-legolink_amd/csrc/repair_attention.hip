@@ -30,7 +30,8 @@
 //
 // Every head dim (64, 128, 256) runs repair_attention_m32_kernel: two pairs
 // per wave on v_mfma_f32_32x32x16, rows gathered into an LDS ring by
-// global_load_lds.
+// LDS-DMA loads (buffer_load ... lds with 32-bit row offsets where the pool
+// fits them, else global_load_lds).
 //
 // Roofline: MFMA-bound in principle.  Algorithmic work per (query, visible
 // key) pair and query head: 4 * head_dim flops (QK and PV); KV bytes are read
@@ -192,7 +193,7 @@ constexpr float kScoreFloor = -1e30f;  // initial softmax maximum (raw score uni
 // needs twice the registers and LDS per wave, so its workgroups hold 4 waves.
 __host__ __device__ constexpr int max_pairs(int d) { return d == 256 ? kMaxPairs / 2 : kMaxPairs; }
 
-// K and V rows are gathered straight into an LDS ring with global_load_lds,
+// K and V rows are gathered straight into an LDS ring with LDS-DMA loads,
 // up to three tiles ahead of the MFMAs, so no registers stage them.  Rows are
 // stored token-major with their 16-byte chunks XOR-swizzled by token, which keeps the fragment reads free of bank conflicts.  V^T
 // fragments come from ds_read_b64_tr_b16: within a group of 16 lanes it
@@ -303,7 +304,9 @@ __device__ inline void workgroup_barrier() {
 //   row): K c ^ (t % 16), V c ^ 4 (t % 4);
 //   head dim 64 (128-byte rows, two per bank row): K c ^ ((t / 2) % 8),
 //   V c ^ 4 ((t / 2) % 2).
-// Each wave issues an equal share of a tile's K and V gathers.
+// Each wave issues an equal share of a tile's K and V gathers, after its
+// score batch w % 4 of the tile before (so that they do not all queue at
+// once).
 // Head dims 64 and 128: 8 waves and a four-stage ring; head dim 256 (twice the
 // registers and LDS per tile): 4 waves, one per SIMD, and a two-stage ring.
 template <int D>
