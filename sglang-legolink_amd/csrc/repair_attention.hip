@@ -304,9 +304,9 @@ __device__ inline void workgroup_barrier() {
 //   row): K c ^ (t % 16), V c ^ 4 (t % 4);
 //   head dim 64 (128-byte rows, two per bank row): K c ^ ((t / 2) % 8),
 //   V c ^ 4 ((t / 2) % 2).
-// Each wave issues an equal share of a tile's K and V gathers, after its
-// score batch w % 4 of the tile before (so that they do not all queue at
-// once).
+// Each wave issues an equal share of a tile's K and V gathers, during the
+// tile kLead earlier, after that tile's score batch w % 4 (so that the
+// workgroup's loads do not all queue at once).
 // Head dims 64 and 128: 8 waves and a four-stage ring; head dim 256 (twice the
 // registers and LDS per tile): 4 waves, one per SIMD, and a two-stage ring.
 template <int D>
